@@ -1,0 +1,152 @@
+/*
+ * mlxq.h — C ABI of the MI355X (gfx950) quantized-matmul library.
+ *
+ * Drop-in replacement for the MLX primitives behind mlxcel's quantized
+ * linear layers and MoE experts:
+ *   mlxq_quantized_matmul  <- ffi::quantized_matmul   (src/lib/mlxcel-core/src/lib.rs:1391-1400,
+ *                             cpp/mlx_cxx_bridge.cpp:3782-3814 -> mlx::core::quantized_matmul,
+ *                             overlays/rocm/mlx/ops.cpp:4955-5008)
+ *   mlxq_gather_qmm        <- ffi::gather_qmm         (lib.rs:1374-1388, mlx_cxx_bridge.cpp:3745-3780
+ *                             -> mlx::core::gather_qmm, ops.cpp:5841-5948)
+ *   mlxq_dequantize        <- ffi::dequantize         (lib.rs:1409-1416, mlx_cxx_bridge.cpp:3816-3878
+ *                             -> mlx::core::dequantize, ops.cpp:5753-5805)
+ *   mlxq_quantize          <- ffi::quantize_weights_* (mlx_cxx_bridge.cpp:7867-7900
+ *                             -> mlx::core::quantize, ops.cpp:5454-5492)
+ *
+ * Conventions (differences from the reference are deliberate and listed):
+ *   - Eager and stream-ordered: work is enqueued on `stream` (a hipStream_t,
+ *     NULL = the default stream) and the call returns without waiting.  The
+ *     reference builds a lazy graph node; the node's eval is what this does.
+ *   - Caller-allocated output: `out` must already have the shape and dtype
+ *     the reference would give the result (query it with the *_shape
+ *     functions).  All `data` pointers are device pointers.
+ *   - Errors are status codes, never exceptions.  Argument errors return
+ *     MLXQ_EINVAL with the reference's exception text in mlxq_last_error();
+ *     valid combinations this library does not implement return
+ *     MLXQ_EUNSUPPORTED so the caller can fall back.
+ *   - group_size / bits <= 0 select the mode's default (the reference's
+ *     std::nullopt), as in quantization_params_from_mode (ops.cpp:4846-4870).
+ *   - Thread-safe and re-entrant.  Index values outside the expert or batch
+ *     range are clamped to the last valid entry instead of reading out of
+ *     bounds.
+ */
+#ifndef MLXQ_H
+#define MLXQ_H
+
+#include <stdbool.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MLXQ_MAX_DIMS 8
+
+typedef enum mlxq_status {
+  MLXQ_OK = 0,
+  MLXQ_EINVAL = 1,       /* argument rejected; message = the reference's std::invalid_argument text */
+  MLXQ_EUNSUPPORTED = 2, /* valid for MLX but not implemented here (caller falls back) */
+  MLXQ_EHIP = 3,         /* HIP runtime error (launch failure, no device) */
+  MLXQ_ENOMEM = 4        /* device workspace allocation failed */
+} mlxq_status;
+
+/* Same order as mlx::core::Dtype::Val. */
+typedef enum mlxq_dtype {
+  MLXQ_BOOL = 0,
+  MLXQ_UINT8 = 1,
+  MLXQ_UINT16 = 2,
+  MLXQ_UINT32 = 3,
+  MLXQ_UINT64 = 4,
+  MLXQ_INT8 = 5,
+  MLXQ_INT16 = 6,
+  MLXQ_INT32 = 7,
+  MLXQ_INT64 = 8,
+  MLXQ_FLOAT16 = 9,
+  MLXQ_FLOAT32 = 10,
+  MLXQ_FLOAT64 = 11,
+  MLXQ_BFLOAT16 = 12,
+  MLXQ_COMPLEX64 = 13
+} mlxq_dtype;
+
+/* A strided view of device memory (strides in elements, like mlx::core::array). */
+typedef struct mlxq_array {
+  void* data;
+  int32_t dtype; /* mlxq_dtype */
+  int32_t ndim;  /* 0 .. MLXQ_MAX_DIMS */
+  int64_t shape[MLXQ_MAX_DIMS];
+  int64_t strides[MLXQ_MAX_DIMS];
+} mlxq_array;
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* mlxq_last_error(void);
+
+/* Library version string, e.g. "mlxq 0.1.0 gfx950". */
+const char* mlxq_version(void);
+
+/* y = x @ dequantize(w, scales, biases)^T  (transpose=true), or without the
+ * transpose.  Shapes/dtypes exactly as mlx::core::quantized_matmul
+ * (ops.cpp:4955-5008): out.shape = x.shape[:-1] + [N], out dtype =
+ * promote(x, scales, biases) for affine and x.dtype for fp modes.
+ * Implemented: transpose=true; mode "affine" with bits 4 or 8 and
+ * group_size 32/64/128; mode "mxfp4"; bfloat16 activations; w 2-D, or
+ * batched with the same batch shape as x.  Row-contiguous inputs. */
+mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w,
+                                  const mlxq_array* scales, const mlxq_array* biases,
+                                  bool transpose, int32_t group_size, int32_t bits,
+                                  const char* mode, mlxq_array* out, void* stream);
+
+/* Output shape/dtype the reference would give quantized_matmul, after the same
+ * validation (no device work). */
+mlxq_status mlxq_quantized_matmul_shape(const mlxq_array* x, const mlxq_array* w,
+                                        const mlxq_array* scales, const mlxq_array* biases,
+                                        bool transpose, int32_t group_size, int32_t bits,
+                                        const char* mode, int32_t* out_ndim,
+                                        int64_t* out_shape, int32_t* out_dtype);
+
+/* out[i] = x[lhs[i]] @ dequantize(w[rhs[i]])^T over the broadcast index
+ * shape, as mlx::core::gather_qmm (ops.cpp:5841-5948): out.shape =
+ * broadcast(lhs, rhs).shape + [x.shape[-2], N].  NULL lhs/rhs default to
+ * arange over the batch dims of x/w; both NULL is quantized_matmul.
+ * `sorted_indices` is the reference's hint that rhs is sorted; results do
+ * not depend on it.  `global_scale` (nvfp4 only in the reference) must be
+ * NULL.  Index arrays may be any integer dtype and any strides
+ * (broadcasting included). */
+mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w,
+                            const mlxq_array* scales, const mlxq_array* biases,
+                            const mlxq_array* lhs_indices, const mlxq_array* rhs_indices,
+                            bool transpose, int32_t group_size, int32_t bits,
+                            bool sorted_indices, const char* mode,
+                            const mlxq_array* global_scale, mlxq_array* out, void* stream);
+
+mlxq_status mlxq_gather_qmm_shape(const mlxq_array* x, const mlxq_array* w,
+                                  const mlxq_array* scales, const mlxq_array* biases,
+                                  const mlxq_array* lhs_indices,
+                                  const mlxq_array* rhs_indices, bool transpose,
+                                  int32_t group_size, int32_t bits, const char* mode,
+                                  int32_t* out_ndim, int64_t* out_shape,
+                                  int32_t* out_dtype);
+
+/* w_hat = dequantize(w, scales, biases), as mlx::core::dequantize
+ * (ops.cpp:5753-5805).  Affine output is bit-exact to the MLX CPU graph
+ * (ops.cpp:5531-5573): bf16(bf16(q*s) + b).  mxfp4 output is
+ * LUT[q] * 2^(s-127) (exact; s == 255 gives NaN, ops.cpp:5692-5695).
+ * `dtype` < 0 selects the reference default (scales' dtype for affine,
+ * bfloat16 for fp modes); only bfloat16 output is implemented. */
+mlxq_status mlxq_dequantize(const mlxq_array* w, const mlxq_array* scales,
+                            const mlxq_array* biases, int32_t group_size, int32_t bits,
+                            const char* mode, int32_t dtype, mlxq_array* out, void* stream);
+
+/* (wq, scales[, biases]) = quantize(w), as mlx::core::quantize
+ * (ops.cpp:5454-5492).  Affine follows the MLX CPU quantizer
+ * (overlays/cpu/.../quantized.cpp:1233-1305) bit-exactly; mxfp4 follows the
+ * graph quantizer (ops.cpp:5364-5431).  `biases_out` is ignored for fp
+ * modes.  Implemented for bfloat16 w. */
+mlxq_status mlxq_quantize(const mlxq_array* w, int32_t group_size, int32_t bits,
+                          const char* mode, mlxq_array* wq_out, mlxq_array* scales_out,
+                          mlxq_array* biases_out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLXQ_H */

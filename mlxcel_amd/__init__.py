@@ -1,0 +1,10 @@
+"""mlxcel_amd — MI355X (gfx950) quantized-matmul hot path for mlxcel / MLX.
+
+The product is the C-ABI library ``libmlxq.so`` (``include/mlxq.h``); this
+package holds its HIP sources (``csrc/``), the build script, and a Python
+mirror of the reference operator interface (``ops``).
+"""
+from .ops import dequantize, gather_qmm, quantize, quantized_matmul  # noqa: F401
+from ._lib import LIB_PATH, load as load_library  # noqa: F401
+
+__all__ = ["quantized_matmul", "gather_qmm", "dequantize", "quantize", "load_library", "LIB_PATH"]

@@ -1,0 +1,946 @@
+// api.cpp — the C ABI declared in include/mlxq.h.
+//
+// Validation restates the reference op layer so callers see the same accept /
+// reject decisions and the same messages (overlays/rocm/mlx/ops.cpp):
+//   validate_quantized_input / extract_quantized_matmul_dims   ops.cpp:111-179
+//   quantization_params_from_mode / validate_mode_with_type    ops.cpp:4846-4925
+//   quantized_matmul                                            ops.cpp:4955-5008
+//   quantize / affine_quantize / fp_quantize checks             ops.cpp:5277-5290, 5340-5358, 5454-5492
+//   dequantize / affine_dequantize / fp_dequantize checks       ops.cpp:5494-5530, 5596-5640, 5753-5805
+//   gather_qmm / indices_or_default                             ops.cpp:5841-5948, 79-109
+//   string_to_quantization_mode                                 overlays/rocm/mlx/primitives.cpp:3617-3635
+// The eval side (what the reference's QuantizedMatmul/GatherQMM::eval_gpu do,
+// overlays/rocm/mlx/backend/rocm/quantized/qmm.hip:3550, 6590) is replaced by
+// the dispatch at the bottom of this file.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "../../include/mlxq.h"
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace {
+
+using Shape = std::vector<int64_t>;
+
+thread_local std::string g_last_error;
+
+struct Error {
+  mlxq_status code;
+  std::string msg;
+};
+
+[[noreturn]] void fail(mlxq_status code, const std::string& msg) { throw Error{code, msg}; }
+[[noreturn]] void invalid(const std::ostringstream& os) { fail(MLXQ_EINVAL, os.str()); }
+[[noreturn]] void unsupported(const std::string& msg) { fail(MLXQ_EUNSUPPORTED, "[mlxq] " + msg); }
+
+void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) fail(MLXQ_EHIP, std::string("[mlxq] ") + what + ": " + hipGetErrorString(e));
+}
+
+template <typename F>
+mlxq_status guarded(F&& f) {
+  try {
+    f();
+    g_last_error.clear();
+    return MLXQ_OK;
+  } catch (const Error& e) {
+    g_last_error = e.msg;
+    return e.code;
+  } catch (const std::exception& e) {
+    g_last_error = std::string("[mlxq] internal error: ") + e.what();
+    return MLXQ_EHIP;
+  }
+}
+
+// ---- dtype facts (mlx::core::Dtype order) ----------------------------------
+
+const char* dtype_name(int d) {
+  static const char* names[] = {"bool",  "uint8",   "uint16",  "uint32",  "uint64",
+                                "int8",  "int16",   "int32",   "int64",   "float16",
+                                "float32", "float64", "bfloat16", "complex64"};
+  return (d >= 0 && d <= 13) ? names[d] : "unknown";
+}
+bool is_floating(int d) { return d == MLXQ_FLOAT16 || d == MLXQ_FLOAT32 || d == MLXQ_FLOAT64 || d == MLXQ_BFLOAT16; }
+bool is_integral(int d) { return d >= MLXQ_BOOL + 1 && d <= MLXQ_INT64; }
+int dtype_size(int d) {
+  static const int sz[] = {1, 1, 2, 4, 8, 1, 2, 4, 8, 2, 4, 8, 2, 8};
+  return (d >= 0 && d <= 13) ? sz[d] : 0;
+}
+
+// Upstream MLX promote_types for the floating types this op layer meets
+// (jax-style lattice: f16+bf16 -> f32, anything with f32/f64 -> the wider).
+int promote(int a, int b) {
+  if (a == b) return a;
+  if (!is_floating(a) && !is_floating(b)) return a < b ? b : a;  // stays integral
+  if (a == MLXQ_FLOAT64 || b == MLXQ_FLOAT64) return MLXQ_FLOAT64;
+  if (is_floating(a) && !is_floating(b)) return a;
+  if (is_floating(b) && !is_floating(a)) return b;
+  return MLXQ_FLOAT32;  // f16/bf16/f32 mixes
+}
+
+// ---- array views -------------------------------------------------------------
+
+struct View {
+  const mlxq_array* a = nullptr;
+  int64_t dim(int i) const { return a->shape[i < 0 ? i + a->ndim : i]; }
+  int ndim() const { return a->ndim; }
+  Shape shape() const { return Shape(a->shape, a->shape + a->ndim); }
+  int dtype() const { return a->dtype; }
+  int64_t size() const {
+    int64_t s = 1;
+    for (int i = 0; i < a->ndim; i++) s *= a->shape[i];
+    return s;
+  }
+  bool row_contiguous() const {
+    int64_t st = 1;
+    for (int i = a->ndim - 1; i >= 0; i--) {
+      if (a->shape[i] != 1 && a->strides[i] != st) return false;
+      st *= a->shape[i];
+    }
+    return true;
+  }
+};
+
+std::string fmt_shape(const Shape& s) {
+  std::ostringstream os;
+  os << "(";
+  for (size_t i = 0; i < s.size(); i++) os << s[i] << (i + 1 == s.size() ? "" : ",");
+  os << ")";
+  return os.str();
+}
+
+void check_array(const mlxq_array* a, const char* name) {
+  if (!a) fail(MLXQ_EINVAL, std::string("[mlxq] ") + name + " must not be NULL");
+  if (a->ndim < 0 || a->ndim > MLXQ_MAX_DIMS)
+    fail(MLXQ_EINVAL, std::string("[mlxq] ") + name + " has an invalid ndim");
+  for (int i = 0; i < a->ndim; i++)
+    if (a->shape[i] < 0) fail(MLXQ_EINVAL, std::string("[mlxq] ") + name + " has a negative dimension");
+}
+
+Shape broadcast_shapes(const Shape& s1, const Shape& s2) {
+  const size_t nd = std::max(s1.size(), s2.size());
+  Shape out(nd);
+  for (size_t i = 0; i < nd; i++) {
+    const int64_t a = i < nd - s1.size() ? 1 : s1[i - (nd - s1.size())];
+    const int64_t b = i < nd - s2.size() ? 1 : s2[i - (nd - s2.size())];
+    if (a == b || b == 1) out[i] = a;
+    else if (a == 1) out[i] = b;
+    else {
+      std::ostringstream os;
+      os << "[broadcast_shapes] Shapes " << fmt_shape(s1) << " and " << fmt_shape(s2) << " cannot be broadcast.";
+      invalid(os);
+    }
+  }
+  return out;
+}
+
+// ---- mode / params (ops.cpp:4846-4925, primitives.cpp:3617-3635) ----------
+
+enum Mode { AFFINE = 0, MXFP4_M = 1, MXFP8_M = 2, NVFP4_M = 3 };
+
+Mode parse_mode(const char* mode, const char* tag) {
+  const std::string m = mode ? mode : "affine";
+  if (m == "affine") return AFFINE;
+  if (m == "mxfp4") return MXFP4_M;
+  if (m == "mxfp8") return MXFP8_M;
+  if (m == "nvfp4") return NVFP4_M;
+  std::ostringstream os;
+  if (tag && *tag) os << "[" << tag << "]";
+  os << " Invalid quantization mode '" << m << "'.";
+  invalid(os);
+}
+
+void params_from_mode(Mode mode, int32_t& gs, int32_t& bits) {
+  int dgs = 64, dbits = 4;
+  if (mode == NVFP4_M) dgs = 16;
+  if (mode == MXFP4_M) dgs = 32;
+  if (mode == MXFP8_M) { dgs = 32; dbits = 8; }
+  if (gs <= 0) gs = dgs;
+  if (bits <= 0) bits = dbits;
+}
+
+// returns the output dtype
+int validate_mode_with_type(const char* tag, const mlxq_array* scales, const mlxq_array* biases,
+                            int out_type, Mode mode, const char* mode_str) {
+  if (out_type >= 0 && !is_floating(out_type)) {
+    std::ostringstream os;
+    os << "[" << tag << "] Only real floating types are supported but output dtype == " << dtype_name(out_type)
+       << ".";
+    invalid(os);
+  }
+  if (mode == AFFINE) {
+    if (!biases) {
+      std::ostringstream os;
+      os << "[" << tag << "] Biases must be provided for affine quantization.";
+      invalid(os);
+    }
+    const int dt = promote(scales->dtype, biases->dtype);
+    if (!is_floating(dt)) {
+      std::ostringstream os;
+      os << "[" << tag << "] Only real floating types are supported but scales.dtype() == "
+         << dtype_name(scales->dtype) << " and biases.dtype() == " << dtype_name(biases->dtype) << ".";
+      invalid(os);
+    }
+    return out_type >= 0 ? out_type : dt;
+  } else if (scales->dtype != MLXQ_UINT8) {
+    std::ostringstream os;
+    os << "[" << tag << "] Scale type must be uint8 but received type " << dtype_name(scales->dtype) << ".";
+    invalid(os);
+  }
+  if (biases) {
+    std::ostringstream os;
+    os << "[" << tag << "] Biases must be null for quantization mode '" << (mode_str ? mode_str : "") << "'.";
+    invalid(os);
+  }
+  return out_type >= 0 ? out_type : (int)MLXQ_BFLOAT16;
+}
+
+void validate_quantized_input(const char* tag, View w, View scales, int gs, int bits, const mlxq_array* biases) {
+  if (w.dtype() != MLXQ_UINT32) {
+    std::ostringstream os;
+    os << "[" << tag << "] The weight matrix should be uint32 but received " << dtype_name(w.dtype());
+    invalid(os);
+  }
+  if (biases && View{biases}.shape() != scales.shape()) {
+    std::ostringstream os;
+    os << "[" << tag << "] Scales and biases should have the same shape. Received scales with shape "
+       << fmt_shape(scales.shape()) << " and biases with " << fmt_shape(View{biases}.shape());
+    invalid(os);
+  }
+  if (w.ndim() < 2 || scales.ndim() < 1) {
+    std::ostringstream os;
+    os << "[" << tag << "] The weight matrix must have at least 2 dimensions but received shape "
+       << fmt_shape(w.shape()) << ".";
+    invalid(os);
+  }
+  bool batch_eq = scales.ndim() >= w.ndim() - 2;
+  for (int i = 0; batch_eq && i < w.ndim() - 2; i++) batch_eq = w.dim(i) == scales.dim(i);
+  if (!batch_eq) {
+    std::ostringstream os;
+    os << "[" << tag << "] Weight and scales should have the same batch shape. Received weight with shape "
+       << fmt_shape(w.shape()) << ", scales with " << fmt_shape(scales.shape()) << ".";
+    invalid(os);
+  }
+  if (w.dim(-1) * 32 / bits != scales.dim(-1) * gs) {
+    std::ostringstream os;
+    os << "[" << tag << "] The shapes of the weight and scales are incompatible based on bits and group_size. "
+       << "w.shape() == " << fmt_shape(w.shape()) << " and scales.shape() == " << fmt_shape(scales.shape())
+       << " with group_size=" << gs << " and bits=" << bits;
+    invalid(os);
+  }
+}
+
+// returns {w_inner, w_outer}
+std::pair<int64_t, int64_t> extract_dims(const char* tag, View x, View w, View scales, const mlxq_array* biases,
+                                         bool transpose, int gs, int bits) {
+  validate_quantized_input(tag, w, scales, gs, bits, biases);
+  if (x.ndim() < 1) {
+    std::ostringstream os;
+    os << "[" << tag << "] The input must have at least 1 dimension.";
+    invalid(os);
+  }
+  const int64_t x_inner = x.dim(-1);
+  const int64_t w_inner = transpose ? w.dim(-1) * 32 / bits : w.dim(-2);
+  const int64_t w_outer = transpose ? w.dim(-2) : w.dim(-1) * 32 / bits;
+  if (w_inner != x_inner) {
+    std::ostringstream os;
+    os << "[" << tag << "] Last dimension of first input with shape (..., " << x_inner
+       << ") does not match the expanded quantized matrix (" << w_inner << ", " << w_outer
+       << ") computed from shape " << fmt_shape(w.shape()) << " with group_size=" << gs << ", bits=" << bits
+       << " and transpose=" << (transpose ? "true" : "false");
+    invalid(os);
+  }
+  return {w_inner, w_outer};
+}
+
+// ---- quantized_matmul validation (ops.cpp:4955-5008) ------------------------
+
+struct QmmSpec {
+  Mode mode;
+  int gs, bits;
+  int64_t K, N;
+  int out_dtype;
+  Shape out_shape;
+};
+
+QmmSpec spec_quantized_matmul(const mlxq_array* xa, const mlxq_array* wa, const mlxq_array* sa,
+                              const mlxq_array* ba, bool transpose, int32_t gs, int32_t bits,
+                              const char* mode_str) {
+  check_array(xa, "x");
+  check_array(wa, "w");
+  check_array(sa, "scales");
+  if (ba) check_array(ba, "biases");
+  const char* tag = "quantized_matmul";
+  QmmSpec sp;
+  sp.mode = parse_mode(mode_str, tag);
+  int dtype = validate_mode_with_type(tag, sa, ba, -1, sp.mode, mode_str);
+  params_from_mode(sp.mode, gs, bits);
+  sp.gs = gs;
+  sp.bits = bits;
+  View x{xa}, w{wa}, s{sa};
+  auto [wi, wo] = extract_dims(tag, x, w, s, ba, transpose, gs, bits);
+  sp.K = wi;
+  sp.N = wo;
+  dtype = sp.mode == AFFINE ? promote(x.dtype(), dtype) : x.dtype();
+  if (!is_floating(dtype)) {
+    std::ostringstream os;
+    os << "[quantized_matmul] Only real floating types are supported but x.dtype() == " << dtype_name(x.dtype())
+       << ".";
+    invalid(os);
+  }
+  sp.out_dtype = dtype;
+  Shape xs = x.shape();
+  if (x.ndim() > 2 && w.ndim() > 2) {
+    const Shape wsh = w.shape();
+    Shape xb(xs.begin(), xs.end() - 2), wb(wsh.begin(), wsh.end() - 2);
+    Shape bb = broadcast_shapes(xb, wb);
+    bb.push_back(xs[xs.size() - 2]);
+    bb.push_back(xs.back());
+    xs = bb;
+  }
+  xs.back() = wo;
+  sp.out_shape = xs;
+  return sp;
+}
+
+// ---- gather_qmm validation (ops.cpp:5841-5948) -------------------------------
+
+struct GatherSpec {
+  QmmSpec q;
+  Shape idx_shape;  // broadcast index shape
+};
+
+void check_indices(const mlxq_array* idx, View base) {
+  if (base.ndim() < 2) {
+    std::ostringstream os;
+    os << "[gather_qmm] Input must have at least two dimensions but got input with shape "
+       << fmt_shape(base.shape()) << ".";
+    invalid(os);
+  }
+  if (idx && !is_integral(idx->dtype)) {
+    std::ostringstream os;
+    os << "[gather_qmm] Got indices with invalid dtype. Indices must be integral.";
+    invalid(os);
+  }
+}
+
+Shape default_index_shape(View base) { return Shape(base.a->shape, base.a->shape + base.ndim() - 2); }
+
+GatherSpec spec_gather(const mlxq_array* xa, const mlxq_array* wa, const mlxq_array* sa, const mlxq_array* ba,
+                       const mlxq_array* lhs, const mlxq_array* rhs, bool transpose, int32_t gs, int32_t bits,
+                       const char* mode_str, const mlxq_array* global_scale) {
+  check_array(xa, "x");
+  check_array(wa, "w");
+  check_array(sa, "scales");
+  if (ba) check_array(ba, "biases");
+  if (lhs) check_array(lhs, "lhs_indices");
+  if (rhs) check_array(rhs, "rhs_indices");
+  const char* tag = "gather_qmm";
+  GatherSpec g;
+  QmmSpec& sp = g.q;
+  sp.mode = parse_mode(mode_str, tag);
+  int out_type = validate_mode_with_type(tag, sa, ba, -1, sp.mode, mode_str);
+  params_from_mode(sp.mode, gs, bits);
+  sp.gs = gs;
+  sp.bits = bits;
+  View x{xa}, w{wa}, s{sa};
+  auto [wi, wo] = extract_dims(tag, x, w, s, ba, transpose, gs, bits);
+  sp.K = wi;
+  sp.N = wo;
+  if (global_scale && sp.mode != NVFP4_M) {
+    std::ostringstream os;
+    os << "[gather_qmm] Global scale is only supported for 'nvfp4' quantization mode.";
+    invalid(os);
+  }
+  out_type = sp.mode == AFFINE ? promote(x.dtype(), out_type) : x.dtype();
+  if (!is_floating(out_type)) {
+    std::ostringstream os;
+    os << "[gather_qmm] Only real floating types are supported but x.dtype() == " << dtype_name(x.dtype()) << ".";
+    invalid(os);
+  }
+  sp.out_dtype = out_type;
+  check_indices(lhs, x);
+  check_indices(rhs, w);
+  Shape ls = lhs ? View{lhs}.shape() : default_index_shape(x);
+  Shape rs = rhs ? View{rhs}.shape() : default_index_shape(w);
+  g.idx_shape = broadcast_shapes(ls, rs);
+  sp.out_shape = g.idx_shape;
+  sp.out_shape.push_back(x.dim(-2));
+  sp.out_shape.push_back(wo);
+  return g;
+}
+
+void write_shape(const Shape& s, int dtype, int32_t* ndim, int64_t* shape, int32_t* out_dtype) {
+  if ((int)s.size() > MLXQ_MAX_DIMS) fail(MLXQ_EUNSUPPORTED, "[mlxq] result has too many dimensions");
+  if (ndim) *ndim = (int32_t)s.size();
+  if (shape)
+    for (size_t i = 0; i < s.size(); i++) shape[i] = s[i];
+  if (out_dtype) *out_dtype = dtype;
+}
+
+void check_out(const mlxq_array* out, const Shape& shape, int dtype, const char* tag) {
+  check_array(out, "out");
+  if (View{out}.shape() != shape || out->dtype != dtype) {
+    std::ostringstream os;
+    os << "[" << tag << "] out must have shape " << fmt_shape(shape) << " and dtype " << dtype_name(dtype)
+       << " but has shape " << fmt_shape(View{out}.shape()) << " and dtype " << dtype_name(out->dtype) << ".";
+    invalid(os);
+  }
+  if (!View{out}.row_contiguous()) unsupported(std::string(tag) + ": out must be row-contiguous");
+}
+
+void require_contiguous(const mlxq_array* a, const char* name) {
+  if (a && !View{a}.row_contiguous())
+    unsupported(std::string(name) + " must be row-contiguous (make a contiguous copy first)");
+  if (a && a->data && (reinterpret_cast<uintptr_t>(a->data) & 15u) != 0 && View{a}.size() > 0)
+    unsupported(std::string(name) + " must be 16-byte aligned");
+}
+
+// ---- per-device facts and per-stream workspace -------------------------------
+
+struct DevInfo {
+  int cus = 256;
+};
+
+std::mutex g_mu;
+std::map<int, DevInfo> g_dev;
+
+struct Workspace {
+  void* data = nullptr;
+  size_t bytes = 0;
+  unsigned* counters = nullptr;
+  size_t ncounters = 0;
+};
+std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+
+int current_device() {
+  int dev = 0;
+  hip_check(hipGetDevice(&dev), "hipGetDevice");
+  return dev;
+}
+
+DevInfo device_info(int dev) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_dev.find(dev);
+  if (it != g_dev.end()) return it->second;
+  DevInfo d;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0) d.cus = cus;
+  g_dev[dev] = d;
+  return d;
+}
+
+// Scratch that stays allocated for the stream's lifetime; grows (after a
+// stream synchronize) when a call needs more.  Counters are zeroed once at
+// allocation and every kernel that uses them leaves them zero.
+Workspace& workspace(int dev, hipStream_t stream, size_t bytes, size_t ncounters) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  Workspace& w = g_ws[{dev, stream}];
+  if (w.bytes < bytes) {
+    if (w.data) {
+      hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+      hip_check(hipFree(w.data), "hipFree");
+      w.data = nullptr;
+      w.bytes = 0;
+    }
+    size_t sz = 1 << 20;
+    while (sz < bytes) sz <<= 1;
+    if (hipMalloc(&w.data, sz) != hipSuccess) fail(MLXQ_ENOMEM, "[mlxq] workspace allocation failed");
+    w.bytes = sz;
+  }
+  if (w.ncounters < ncounters) {
+    if (w.counters) {
+      hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+      hip_check(hipFree(w.counters), "hipFree");
+      w.counters = nullptr;
+      w.ncounters = 0;
+    }
+    size_t n = 4096;
+    while (n < ncounters) n <<= 1;
+    if (hipMalloc(reinterpret_cast<void**>(&w.counters), n * sizeof(unsigned)) != hipSuccess)
+      fail(MLXQ_ENOMEM, "[mlxq] counter allocation failed");
+    hip_check(hipMemsetAsync(w.counters, 0, n * sizeof(unsigned), stream), "hipMemsetAsync");
+    w.ncounters = n;
+  }
+  return w;
+}
+
+}  // namespace
+
+
+namespace {
+
+// Broadcast strides of an index array (or of the default arange over `dshape`)
+// against the broadcast shape `b`.
+void bstrides_for(const mlxq_array* idx, const Shape& dshape, const Shape& b, int64_t* out) {
+  const int bnd = (int)b.size();
+  Shape sh;
+  std::vector<int64_t> st;
+  if (idx) {
+    sh = View{idx}.shape();
+    st.assign(idx->strides, idx->strides + idx->ndim);
+  } else {
+    sh = dshape;
+    st.assign(sh.size(), 0);
+    int64_t acc = 1;
+    for (int i = (int)sh.size() - 1; i >= 0; i--) {
+      st[i] = acc;
+      acc *= sh[i];
+    }
+  }
+  const int off = bnd - (int)sh.size();
+  for (int d = 0; d < bnd; d++) {
+    const int sd = d - off;
+    out[d] = (sd < 0 || sh[sd] == 1) ? 0 : st[sd];
+  }
+}
+
+int fmt_of(Mode m, int bits) {
+  if (m == MXFP4_M) return mlxq::MXFP4;
+  return bits == 8 ? mlxq::AFF8 : mlxq::AFF4;
+}
+
+void require_kernel_support(const QmmSpec& sp, bool transpose, const char* tag) {
+  if (sp.mode == NVFP4_M || sp.mode == MXFP8_M)
+    unsupported(std::string(tag) + ": mode '" + (sp.mode == NVFP4_M ? "nvfp4" : "mxfp8") + "' is not implemented");
+  if (sp.mode == MXFP4_M && (sp.gs != 32 || sp.bits != 4))
+    unsupported(std::string(tag) + ": mxfp4 needs group_size 32 and bits 4");
+  if (sp.mode == AFFINE && sp.bits != 4 && sp.bits != 8)
+    unsupported(std::string(tag) + ": affine bits " + std::to_string(sp.bits) + " is not implemented (4 and 8 are)");
+  if (sp.mode == AFFINE && sp.gs != 32 && sp.gs != 64 && sp.gs != 128)
+    unsupported(std::string(tag) + ": group_size must be 32, 64 or 128");
+  if (!transpose) unsupported(std::string(tag) + ": transpose=false is not implemented");
+  if (sp.out_dtype != MLXQ_BFLOAT16)
+    unsupported(std::string(tag) + ": only bfloat16 compute is implemented (result dtype " +
+                dtype_name(sp.out_dtype) + ")");
+  if (sp.K % 32 != 0) unsupported(std::string(tag) + ": K must be a multiple of 32");
+  if (sp.K > (int64_t)1 << 30 || sp.N > (int64_t)1 << 30) unsupported(std::string(tag) + ": dimension too large");
+}
+
+void require_dtype(const mlxq_array* a, int dt, const char* name, const char* tag) {
+  if (a && a->dtype != dt)
+    unsupported(std::string(tag) + ": " + name + " must be " + dtype_name(dt) + " (got " + dtype_name(a->dtype) +
+                ")");
+}
+
+// Launch the skinny kernel over `nseg` mode-A segments.
+void run_qmv(const QmmSpec& sp, mlxq::QmvArgs a, int nseg, int max_rows, hipStream_t stream) {
+  const int fmt = fmt_of(sp.mode, sp.bits);
+  const int dev = current_device();
+  const DevInfo di = device_info(dev);
+  const int mt = mlxq::qmv_tile_mt(fmt, sp.gs, max_rows);
+  a.rows_lds = max_rows;
+  mlxq::QmvPlan p = mlxq::qmv_plan(fmt, sp.gs, sp.N, sp.K, max_rows, nseg, di.cus);
+  a.ks = p.ks;
+  a.kst_per_wg = p.kst_per_wg;
+  if (p.ks > 1) {
+    const size_t ws_bytes = (size_t)p.ks * a.out_rows * sp.N * sizeof(float);
+    Workspace& w = workspace(dev, stream, ws_bytes, (size_t)nseg * p.tiles);
+    a.ws = reinterpret_cast<float*>(w.data);
+    a.counters = w.counters;
+  }
+  if (nseg > 65535) unsupported("too many segments for one launch");
+  hip_check(mlxq::qmv_launch(fmt, sp.gs, mt, a, nseg, p, stream), "qmv launch");
+}
+
+}  // namespace
+
+// ===========================================================================
+extern "C" {
+
+const char* mlxq_last_error(void) { return g_last_error.c_str(); }
+
+const char* mlxq_version(void) { return "mlxq 0.1.0 gfx950"; }
+
+mlxq_status mlxq_quantized_matmul_shape(const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+                                        const mlxq_array* biases, bool transpose, int32_t group_size,
+                                        int32_t bits, const char* mode, int32_t* out_ndim, int64_t* out_shape,
+                                        int32_t* out_dtype) {
+  return guarded([&] {
+    QmmSpec sp = spec_quantized_matmul(x, w, scales, biases, transpose, group_size, bits, mode);
+    write_shape(sp.out_shape, sp.out_dtype, out_ndim, out_shape, out_dtype);
+  });
+}
+
+mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+                                  const mlxq_array* biases, bool transpose, int32_t group_size, int32_t bits,
+                                  const char* mode, mlxq_array* out, void* stream_) {
+  return guarded([&] {
+    const char* tag = "quantized_matmul";
+    QmmSpec sp = spec_quantized_matmul(x, w, scales, biases, transpose, group_size, bits, mode);
+    check_out(out, sp.out_shape, sp.out_dtype, tag);
+    require_kernel_support(sp, transpose, tag);
+    require_dtype(x, MLXQ_BFLOAT16, "x", tag);
+    if (sp.mode == AFFINE) {
+      require_dtype(scales, MLXQ_BFLOAT16, "scales", tag);
+      require_dtype(biases, MLXQ_BFLOAT16, "biases", tag);
+    }
+    require_contiguous(x, "x");
+    require_contiguous(w, "w");
+    require_contiguous(scales, "scales");
+    require_contiguous(biases, "biases");
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    const int64_t rows_total = View{out}.size() / std::max<int64_t>(sp.N, 1);
+    if (rows_total == 0 || sp.N == 0) return;
+    if (sp.K == 0) unsupported("quantized_matmul: K == 0");
+
+    mlxq::QmvArgs a{};
+    a.x = static_cast<const uint16_t*>(x->data);
+    a.w = static_cast<const uint32_t*>(w->data);
+    a.scales = scales->data;
+    a.biases = biases ? static_cast<const uint16_t*>(biases->data) : nullptr;
+    a.out = static_cast<uint16_t*>(out->data);
+    a.N = (int)sp.N;
+    a.K = (int)sp.K;
+    a.out_rows = (int)rows_total;
+    const int fmt = fmt_of(sp.mode, sp.bits);
+    const int cap = mlxq::qmv_max_rows(fmt, sp.gs);
+    View wv{w}, xv{x};
+    if (wv.ndim() == 2) {
+      // every leading dim of x folds into rows (qmm.hip:3606-3620 does the same fold)
+      a.E = 1;
+      a.X = 1;
+      a.w_expert_stride = 0;
+      a.s_expert_stride = 0;
+      const int rps = (int)std::min<int64_t>(rows_total, cap);
+      a.rps = rps;
+      a.total_rows = (int)rows_total;
+      a.X = (int)((rows_total + rps - 1) / rps);
+      const int nseg = a.X;
+      run_qmv(sp, a, nseg, rps, stream);
+    } else {
+      // batched weights: each batch element is a segment of x.shape[-2] rows
+      const Shape wsh = wv.shape(), xsh = xv.shape();
+      Shape wb(wsh.begin(), wsh.end() - 2);
+      Shape ob(sp.out_shape.begin(), sp.out_shape.end() - 2);
+      Shape xb = xv.ndim() > 2 ? Shape(xsh.begin(), xsh.end() - 2) : Shape{};
+      if (xv.ndim() <= 2 || wb != ob || xb != ob)
+        unsupported("quantized_matmul: batched w needs x with the same batch shape (use gather_qmm to broadcast)");
+      const int64_t M = xv.dim(-2);
+      if (M > cap) unsupported("quantized_matmul: batched w with more than " + std::to_string(cap) + " rows per batch");
+      int64_t nb = 1;
+      for (auto d : wb) nb *= d;
+      a.E = (int)nb;
+      a.X = (int)nb;
+      a.w_expert_stride = wv.dim(-2) * wv.dim(-1);
+      a.s_expert_stride = View{scales}.dim(-2) * View{scales}.dim(-1);
+      a.rps = (int)M;
+      a.total_rows = (int)rows_total;
+      run_qmv(sp, a, (int)nb, (int)M, stream);
+    }
+  });
+}
+
+mlxq_status mlxq_gather_qmm_shape(const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+                                  const mlxq_array* biases, const mlxq_array* lhs_indices,
+                                  const mlxq_array* rhs_indices, bool transpose, int32_t group_size, int32_t bits,
+                                  const char* mode, int32_t* out_ndim, int64_t* out_shape, int32_t* out_dtype) {
+  if (!lhs_indices && !rhs_indices)
+    return mlxq_quantized_matmul_shape(x, w, scales, biases, transpose, group_size, bits, mode, out_ndim,
+                                       out_shape, out_dtype);
+  return guarded([&] {
+    GatherSpec g = spec_gather(x, w, scales, biases, lhs_indices, rhs_indices, transpose, group_size, bits, mode,
+                               nullptr);
+    write_shape(g.q.out_shape, g.q.out_dtype, out_ndim, out_shape, out_dtype);
+  });
+}
+
+mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+                            const mlxq_array* biases, const mlxq_array* lhs_indices, const mlxq_array* rhs_indices,
+                            bool transpose, int32_t group_size, int32_t bits, bool sorted_indices, const char* mode,
+                            const mlxq_array* global_scale, mlxq_array* out, void* stream_) {
+  (void)sorted_indices;  // results never depend on it
+  if (!lhs_indices && !rhs_indices) {
+    if (global_scale) {
+      g_last_error = "[gather_qmm] Global scale is not supported without indices.";
+      return MLXQ_EINVAL;
+    }
+    return mlxq_quantized_matmul(x, w, scales, biases, transpose, group_size, bits, mode, out, stream_);
+  }
+  return guarded([&] {
+    const char* tag = "gather_qmm";
+    GatherSpec g = spec_gather(x, w, scales, biases, lhs_indices, rhs_indices, transpose, group_size, bits, mode,
+                               global_scale);
+    QmmSpec& sp = g.q;
+    check_out(out, sp.out_shape, sp.out_dtype, tag);
+    require_kernel_support(sp, transpose, tag);
+    if (global_scale) unsupported("gather_qmm: global_scale (nvfp4) is not implemented");
+    require_dtype(x, MLXQ_BFLOAT16, "x", tag);
+    if (sp.mode == AFFINE) {
+      require_dtype(scales, MLXQ_BFLOAT16, "scales", tag);
+      require_dtype(biases, MLXQ_BFLOAT16, "biases", tag);
+    }
+    require_contiguous(x, "x");
+    require_contiguous(w, "w");
+    require_contiguous(scales, "scales");
+    require_contiguous(biases, "biases");
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    View xv{x}, wv{w}, sv{scales};
+    const int64_t M = xv.dim(-2);
+    int64_t B = 1;
+    for (auto d : g.idx_shape) B *= d;
+    if (B == 0 || M == 0 || sp.N == 0) return;
+    if ((int)g.idx_shape.size() > MLXQ_MAX_DIMS) unsupported("gather_qmm: index rank too large");
+    const int fmt = fmt_of(sp.mode, sp.bits);
+    const int cap = mlxq::qmv_max_rows(fmt, sp.gs);
+    if (M > cap) unsupported("gather_qmm: more than " + std::to_string(cap) + " rows per gathered matrix");
+    if (B > 65535) unsupported("gather_qmm: more than 65535 index entries");
+    const int64_t X = xv.size() / std::max<int64_t>(M * sp.K, 1);
+    const int64_t E = wv.size() / std::max<int64_t>(wv.dim(-2) * wv.dim(-1), 1);
+
+    // flat uint32 lhs/rhs over the broadcast index shape, in the workspace tail
+    mlxq::IdxPrepArgs ip{};
+    ip.bnd = (int)g.idx_shape.size();
+    for (int d = 0; d < ip.bnd; d++) ip.bshape[d] = g.idx_shape[d];
+    ip.B = B;
+    const mlxq_array* idx[2] = {lhs_indices, rhs_indices};
+    const Shape dsh[2] = {default_index_shape(xv), default_index_shape(wv)};
+    for (int s = 0; s < 2; s++) {
+      ip.data[s] = idx[s] ? idx[s]->data : nullptr;
+      ip.dtype[s] = idx[s] ? idx[s]->dtype : MLXQ_UINT32;
+      bstrides_for(idx[s], dsh[s], g.idx_shape, ip.bstrides[s]);
+    }
+    ip.clamp[0] = std::max<int64_t>(X, 1);
+    ip.clamp[1] = std::max<int64_t>(E, 1);
+
+    const int dev = current_device();
+    const DevInfo di = device_info(dev);
+    const int mt = mlxq::qmv_tile_mt(fmt, sp.gs, (int)M);
+    mlxq::QmvPlan p = mlxq::qmv_plan(fmt, sp.gs, sp.N, sp.K, (int)M, (int)B, di.cus);
+    const size_t idx_bytes = ((size_t)B * 2 * sizeof(uint32_t) + 255) & ~(size_t)255;
+    const size_t part_bytes = p.ks > 1 ? (size_t)p.ks * B * M * sp.N * sizeof(float) : 0;
+    Workspace& ws = workspace(dev, stream, idx_bytes + part_bytes, (size_t)B * p.tiles);
+    uint32_t* flat = reinterpret_cast<uint32_t*>(ws.data);
+    ip.out[0] = flat;
+    ip.out[1] = flat + B;
+    hip_check(mlxq::launch_index_prep(ip, stream), "index_prep launch");
+
+    mlxq::QmvArgs a{};
+    a.x = static_cast<const uint16_t*>(x->data);
+    a.w = static_cast<const uint32_t*>(w->data);
+    a.scales = scales->data;
+    a.biases = biases ? static_cast<const uint16_t*>(biases->data) : nullptr;
+    a.out = static_cast<uint16_t*>(out->data);
+    a.lhs = flat;
+    a.rhs = flat + B;
+    a.N = (int)sp.N;
+    a.K = (int)sp.K;
+    a.E = (int)E;
+    a.X = (int)X;
+    a.w_expert_stride = wv.dim(-2) * wv.dim(-1);
+    a.s_expert_stride = sv.dim(-2) * sv.dim(-1);
+    a.rps = (int)M;
+    a.total_rows = (int)(B * M);
+    a.out_rows = (int)(B * M);
+    a.rows_lds = (int)M;
+    a.ks = p.ks;
+    a.kst_per_wg = p.kst_per_wg;
+    if (p.ks > 1) {
+      a.ws = reinterpret_cast<float*>(static_cast<char*>(ws.data) + idx_bytes);
+      a.counters = ws.counters;
+    }
+    hip_check(mlxq::qmv_launch(fmt, sp.gs, mt, a, (int)B, p, stream), "gather qmv launch");
+  });
+}
+
+mlxq_status mlxq_dequantize(const mlxq_array* w, const mlxq_array* scales, const mlxq_array* biases,
+                            int32_t group_size, int32_t bits, const char* mode_str, int32_t dtype,
+                            mlxq_array* out, void* stream_) {
+  return guarded([&] {
+    check_array(w, "w");
+    check_array(scales, "scales");
+    if (biases) check_array(biases, "biases");
+    const char* tag = "dequantize";
+    Mode mode = parse_mode(mode_str, tag);
+    const int out_type = validate_mode_with_type(tag, scales, biases, dtype, mode, mode_str);
+    params_from_mode(mode, group_size, bits);
+    if (bits <= 0) {
+      std::ostringstream os;
+      os << "[dequantize] Invalid value for bits: " << bits;
+      invalid(os);
+    }
+    if (group_size <= 0) {
+      std::ostringstream os;
+      os << "[dequantize] Invalid value for group_size: " << group_size;
+      invalid(os);
+    }
+    View wv{w}, sv{scales};
+    if (w->dtype != MLXQ_UINT32) fail(MLXQ_EINVAL, "[dequantize] The matrix should be given as a uint32");
+    if (wv.ndim() < 2) {
+      std::ostringstream os;
+      os << "[dequantize] The matrix to be dequantized must have at least 2 dimension but it has only " << wv.ndim()
+         << ".";
+      invalid(os);
+    }
+    if (mode == AFFINE) {
+      View bv{biases};
+      if (wv.ndim() != sv.ndim() || wv.ndim() != bv.ndim())
+        fail(MLXQ_EINVAL, "[dequantize] Shape of scales and biases does not match the matrix");
+      Shape a = wv.shape(), b = sv.shape(), c = bv.shape();
+      a.back() = b.back() = c.back() = -1;
+      if (a != b || a != c) fail(MLXQ_EINVAL, "[dequantize] Shape of scales and biases does not match the matrix");
+      // Stricter than ops.cpp:5512-5515, which lets the biases' last dim differ
+      // from the scales' and then reads past the biases: rejected here.
+      if (bv.shape() != sv.shape())
+        fail(MLXQ_EINVAL, "[dequantize] Shape of scales and biases does not match the matrix");
+      if (wv.dim(-1) * 32 / bits != sv.dim(-1) * group_size) {
+        std::ostringstream os;
+        os << "[dequantize] Shape of scales and biases does not match the matrix given the quantization parameters. "
+           << "Provided matrix of shape " << fmt_shape(wv.shape()) << " and scales/biases of shape "
+           << fmt_shape(sv.shape()) << " with group_size=" << group_size << " and bits=" << bits << ".";
+        invalid(os);
+      }
+    } else {
+      const int egs = mode == NVFP4_M ? 16 : 32, ebits = mode == MXFP8_M ? 8 : 4;
+      const char* mname = mode == NVFP4_M ? "nvfp4" : (mode == MXFP8_M ? "mxfp8" : "mxfp4");
+      if (group_size != egs) {
+        std::ostringstream os;
+        os << "[dequantize] " << mname << " quantization requires group size " << egs << " but got " << group_size
+           << ".";
+        invalid(os);
+      }
+      if (bits != ebits) {
+        std::ostringstream os;
+        os << "[dequantize] " << mname << " quantization requires bits to be " << ebits << " but got " << bits << ".";
+        invalid(os);
+      }
+      if (wv.ndim() != sv.ndim()) fail(MLXQ_EINVAL, "[dequantize] Shape of scales does not match the matrix");
+      Shape a = wv.shape(), b = sv.shape();
+      a.back() = b.back() = -1;
+      if (a != b) fail(MLXQ_EINVAL, "[dequantize] Shape of scales does not match the matrix");
+      if (wv.dim(-1) * 32 / bits != sv.dim(-1) * group_size) {
+        std::ostringstream os;
+        os << "[dequantize] Shape of scales does not match the matrix given the quantization parameters. "
+           << "Provided matrix of shape " << fmt_shape(wv.shape()) << " and scales of shape " << fmt_shape(sv.shape())
+           << ".";
+        invalid(os);
+      }
+    }
+    Shape oshape = wv.shape();
+    oshape.back() = wv.dim(-1) * 32 / bits;
+    check_out(out, oshape, out_type, tag);
+    if (mode == NVFP4_M || mode == MXFP8_M) unsupported("dequantize: only affine and mxfp4 are implemented");
+    if (mode == AFFINE && bits != 2 && bits != 4 && bits != 8)
+      unsupported("dequantize: affine bits 2, 4 and 8 are implemented");
+    if (out_type != MLXQ_BFLOAT16) unsupported("dequantize: only bfloat16 output is implemented");
+    if (mode == AFFINE) {
+      require_dtype(scales, MLXQ_BFLOAT16, "scales", tag);
+      require_dtype(biases, MLXQ_BFLOAT16, "biases", tag);
+    }
+    require_contiguous(w, "w");
+    require_contiguous(scales, "scales");
+    require_contiguous(biases, "biases");
+    const int64_t K = oshape.back();
+    const int64_t rows = View{out}.size() / std::max<int64_t>(K, 1);
+    if (rows == 0 || K == 0) return;
+    if (K % group_size) unsupported("dequantize: K must be a multiple of group_size");
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    if (mode == AFFINE) {
+      hip_check(mlxq::launch_affine_dequantize(static_cast<const uint32_t*>(w->data),
+                                               static_cast<const uint16_t*>(scales->data),
+                                               static_cast<const uint16_t*>(biases->data),
+                                               static_cast<uint16_t*>(out->data), rows, K, group_size, bits, stream),
+                "dequantize launch");
+    } else {
+      hip_check(mlxq::launch_mxfp4_dequantize(static_cast<const uint32_t*>(w->data),
+                                              static_cast<const uint8_t*>(scales->data),
+                                              static_cast<uint16_t*>(out->data), rows, K, stream),
+                "dequantize launch");
+    }
+  });
+}
+
+mlxq_status mlxq_quantize(const mlxq_array* w, int32_t group_size, int32_t bits, const char* mode_str,
+                          mlxq_array* wq_out, mlxq_array* scales_out, mlxq_array* biases_out, void* stream_) {
+  return guarded([&] {
+    check_array(w, "w");
+    const char* tag = "quantize";
+    Mode mode = parse_mode(mode_str, tag);
+    params_from_mode(mode, group_size, bits);
+    View wv{w};
+    if (!is_floating(w->dtype)) {
+      std::ostringstream os;
+      os << "[quantize] Only real floating types can be quantized but w has type " << dtype_name(w->dtype) << ".";
+      invalid(os);
+    }
+    if (wv.ndim() < 2) {
+      std::ostringstream os;
+      os << "[quantize] The matrix to be quantized must have at least 2 dimension but it has only " << wv.ndim()
+         << ".";
+      invalid(os);
+    }
+    if (wv.dim(-1) % group_size != 0) {
+      std::ostringstream os;
+      os << "[quantize] The last dimension of the matrix needs to be divisible by the quantization group size "
+         << group_size << ". However the provided  matrix has shape " << fmt_shape(wv.shape());
+      invalid(os);
+    }
+    if (mode == AFFINE) {
+      if (group_size != 32 && group_size != 64 && group_size != 128) {
+        std::ostringstream os;
+        os << "[quantize] The requested group size " << group_size
+           << " is not supported. The supported group sizes are 32, 64, and 128.";
+        invalid(os);
+      }
+      if (bits < 1 || bits > 8 || bits == 7) {
+        std::ostringstream os;
+        os << "[quantize] The requested number of bits " << bits
+           << " is not supported. The supported bits are 1, 2, 3, 4, 5, 6 and 8.";
+        invalid(os);
+      }
+    } else {
+      const int egs = mode == NVFP4_M ? 16 : 32, ebits = mode == MXFP8_M ? 8 : 4;
+      const char* mname = mode == NVFP4_M ? "nvfp4" : (mode == MXFP8_M ? "mxfp8" : "mxfp4");
+      if (group_size != egs) {
+        std::ostringstream os;
+        os << "[quantize] " << mname << " quantization requires group size " << egs << " but got " << group_size
+           << ".";
+        invalid(os);
+      }
+      if (bits != ebits) {
+        std::ostringstream os;
+        os << "[quantize] " << mname << " quantization requires bits to be " << ebits << " but got " << bits << ".";
+        invalid(os);
+      }
+    }
+    Shape qs = wv.shape(), ss = wv.shape();
+    qs.back() = wv.dim(-1) * bits / 32;
+    ss.back() = wv.dim(-1) / group_size;
+    check_out(wq_out, qs, MLXQ_UINT32, tag);
+    check_out(scales_out, ss, mode == AFFINE ? w->dtype : (int)MLXQ_UINT8, tag);
+    if (mode == AFFINE) check_out(biases_out, ss, w->dtype, tag);
+    if (mode == NVFP4_M || mode == MXFP8_M) unsupported("quantize: only affine and mxfp4 are implemented");
+    if (mode == AFFINE && bits != 2 && bits != 4 && bits != 8)
+      unsupported("quantize: affine bits 2, 4 and 8 are implemented");
+    if (w->dtype != MLXQ_BFLOAT16) unsupported("quantize: only bfloat16 weights are implemented");
+    require_contiguous(w, "w");
+    const int64_t K = wv.dim(-1);
+    const int64_t rows = wv.size() / std::max<int64_t>(K, 1);
+    if (rows == 0 || K == 0) return;
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    if (mode == AFFINE) {
+      hip_check(mlxq::launch_affine_quantize(static_cast<const uint16_t*>(w->data),
+                                             static_cast<uint32_t*>(wq_out->data),
+                                             static_cast<uint16_t*>(scales_out->data),
+                                             static_cast<uint16_t*>(biases_out->data), rows, K, group_size, bits,
+                                             stream),
+                "quantize launch");
+    } else {
+      hip_check(mlxq::launch_mxfp4_quantize(static_cast<const uint16_t*>(w->data),
+                                            static_cast<uint32_t*>(wq_out->data),
+                                            static_cast<uint8_t*>(scales_out->data), rows, K, stream),
+                "quantize launch");
+    }
+  });
+}
+
+}  // extern "C"

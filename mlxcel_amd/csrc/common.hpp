@@ -1,0 +1,114 @@
+// common.hpp — shared device helpers for the gfx950 quantized-matmul kernels.
+//
+// Weight formats handled by every kernel (MLX packing, low bits first inside
+// each uint32, overlays/rocm/mlx/ops.cpp:5231-5238):
+//   AFF4  : affine 4-bit codes, 8 per word, bf16 scale and bias per group
+//   AFF8  : affine 8-bit codes, 4 per word, bf16 scale and bias per group
+//   MXFP4 : e2m1 codes, 8 per word, e8m0 (uint8) scale per group of 32
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mlxq {
+
+enum Fmt : int { AFF4 = 0, AFF8 = 1, MXFP4 = 2 };
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ---- bf16 <-> f32 (bit exact; round to nearest even, NaN -> 0x7FC0, which is
+// MLX's `_MLX_BFloat16(float)`) ---------------------------------------------
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// e8m0 scale as float: 2^(s-127); s == 0 -> 2^-127 (float subnormal, as the
+// bf16 0x0040 of overlays/cpu/.../quantized.cpp:97-101), s == 255 -> NaN.
+__device__ __forceinline__ float e8m0_to_f32(uint32_t s) {
+  uint32_t bits = (s == 0u) ? 0x00400000u : (s == 255u ? 0x7FC00000u : (s << 23));
+  return __uint_as_float(bits);
+}
+
+// ---- MFMA ------------------------------------------------------------------
+// v_mfma_f32_16x16x32_bf16: D[16x16] += A[16x32] * B[32x16], fp32 accumulate.
+// Lane i holds A row (i % 16), B column (i % 16), both over the 8 k-slots
+// 8*(i/16) .. 8*(i/16)+7; D rows 4*(i/16) .. +3 of column (i % 16).
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// ---- unpack one 32-bit word of codes into an MFMA bf16 operand fragment ----
+//
+// AFF4: 8 nibbles -> 8 bf16 "128 + q" (0x4300 | q is exactly 128+q in bf16),
+// two per VGPR with a single and-or: VGPR p = (nibble p, nibble p+4).  The
+// matching activation fragment is stored permuted the same way
+// ([x0,x4,x1,x5,x2,x6,x3,x7]); the caller removes the 128*sum(x) offset.
+__device__ __forceinline__ void unpack_aff4(uint32_t w, uint32_t (&v)[4]) {
+  v[0] = (w & 0x000F000Fu) | 0x43004300u;
+  v[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
+  v[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
+  v[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+}
+
+// MXFP4: 8 e2m1 codes -> 8 bf16 in natural order using the gfx950 FP4
+// conversion (scale 1.0 keeps the code points exact: 0, .5, 1, 1.5, 2, 3, 4, 6).
+__device__ __forceinline__ void unpack_mxfp4(uint32_t w, uint32_t (&v)[4]) {
+  bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 0);
+  bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 1);
+  bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 2);
+  bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 3);
+  v[0] = __builtin_bit_cast(uint32_t, p0);
+  v[1] = __builtin_bit_cast(uint32_t, p1);
+  v[2] = __builtin_bit_cast(uint32_t, p2);
+  v[3] = __builtin_bit_cast(uint32_t, p3);
+}
+
+// AFF8: two words = 8 byte codes -> 8 bf16 (exact: codes are < 256), natural order.
+__device__ __forceinline__ uint32_t pack_bf16x2_exact(float lo, float hi) {
+  // Both inputs are integers below 256, so truncation is exact.
+  return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+}
+
+__device__ __forceinline__ void unpack_aff8(uint32_t w0, uint32_t w1, uint32_t (&v)[4]) {
+  v[0] = pack_bf16x2_exact((float)(w0 & 0xFFu), (float)((w0 >> 8) & 0xFFu));
+  v[1] = pack_bf16x2_exact((float)((w0 >> 16) & 0xFFu), (float)(w0 >> 24));
+  v[2] = pack_bf16x2_exact((float)(w1 & 0xFFu), (float)((w1 >> 8) & 0xFFu));
+  v[3] = pack_bf16x2_exact((float)((w1 >> 16) & 0xFFu), (float)(w1 >> 24));
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const uint32_t (&v)[4]) {
+  u32x4 t = {v[0], v[1], v[2], v[3]};
+  return __builtin_bit_cast(bf16x8, t);
+}
+
+// Permute 8 consecutive bf16 (4 words, natural order) into the AFF4 operand
+// order [x0,x4,x1,x5,x2,x6,x3,x7].
+__device__ __forceinline__ u32x4 perm_aff4(u32x4 x) {
+  u32x4 r;
+  r[0] = (x[0] & 0xFFFFu) | (x[2] << 16);
+  r[1] = (x[0] >> 16) | (x[2] & 0xFFFF0000u);
+  r[2] = (x[1] & 0xFFFFu) | (x[3] << 16);
+  r[3] = (x[1] >> 16) | (x[3] & 0xFFFF0000u);
+  return r;
+}
+
+__device__ __forceinline__ float sum_bf16x8(u32x4 x) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; i++) s += bf16_bits_to_f32(x[i] & 0xFFFFu) + bf16_bits_to_f32(x[i] >> 16);
+  return s;
+}
+
+}  // namespace mlxq

@@ -1,0 +1,298 @@
+// dequant.hip — load-time conversions on gfx950: dequantize and quantize.
+//
+// Bit-exact to the MLX CPU definitions (built with -ffp-contract=off):
+//  * affine dequantize: the CPU graph fallback, overlays/rocm/mlx/ops.cpp:5531-5573,
+//    where uint32 x bf16 promotes to bf16 so each op rounds: bf16(bf16(q*s) + b).
+//  * mxfp4 dequantize: ops.cpp:5646-5695, LUT[q] * 2^(s-127), s == 255 -> NaN;
+//    built from integer fields so bf16 subnormal results are exact whatever the
+//    hardware's float denormal mode.
+//  * affine quantize: overlays/cpu/mlx/backend/cpu/quantized.cpp:1233-1305
+//    (`quantize<bfloat16_t, uint32_t>`), including the edge snapping and the
+//    codes computed with the unrounded float scale/bias.
+//  * mxfp4 quantize: the graph fallback ops.cpp:5364-5431, every op rounded to
+//    bf16 as MLX evaluates it; the shared exponent is the smallest e with
+//    2^e >= bf16(max|w| / 6), which is what round(log2) + the round-up step
+//    produce for every normal scale.
+// All four are HBM-bound streaming kernels (one word or one group per lane group).
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace mlxq {
+
+__device__ __forceinline__ float bfr(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+// ---- affine dequantize ------------------------------------------------------
+
+template <int BITS>
+__global__ __launch_bounds__(256) void affine_dequant_kernel(const uint32_t* __restrict__ w,
+                                                             const uint16_t* __restrict__ scales,
+                                                             const uint16_t* __restrict__ biases,
+                                                             uint16_t* __restrict__ out,
+                                                             int64_t nwords, int64_t Kw, int gs) {
+  constexpr int PER = 32 / BITS;  // codes per word
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nwords) return;
+  const int64_t row = i / Kw;
+  const int64_t col = i - row * Kw;
+  const int64_t k0 = col * PER;
+  const int64_t G = Kw * PER / gs;
+  const int64_t gi = row * G + k0 / gs;
+  const float s = bf16_bits_to_f32(scales[gi]);
+  const float b = bf16_bits_to_f32(biases[gi]);
+  const uint32_t word = __builtin_nontemporal_load(w + i);
+  uint32_t packed[PER / 2];
+#pragma unroll
+  for (int p = 0; p < PER; p += 2) {
+    const float q0 = (float)((word >> (p * BITS)) & ((1u << BITS) - 1u));
+    const float q1 = (float)((word >> ((p + 1) * BITS)) & ((1u << BITS) - 1u));
+    const uint32_t h0 = f32_to_bf16_bits(bfr(q0 * s) + b);
+    const uint32_t h1 = f32_to_bf16_bits(bfr(q1 * s) + b);
+    packed[p / 2] = h0 | (h1 << 16);
+  }
+  uint32_t* dst = reinterpret_cast<uint32_t*>(out + row * (Kw * PER) + k0);
+#pragma unroll
+  for (int p = 0; p < PER / 2; p++) dst[p] = packed[p];
+}
+
+hipError_t launch_affine_dequantize(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                                    uint16_t* out, int64_t rows, int64_t K, int gs, int bits,
+                                    hipStream_t stream) {
+  const int64_t Kw = K * bits / 32;
+  const int64_t nwords = rows * Kw;
+  if (nwords == 0) return hipSuccess;
+  const unsigned blocks = (unsigned)((nwords + 255) / 256);
+  switch (bits) {
+    case 2:
+      hipLaunchKernelGGL(affine_dequant_kernel<2>, dim3(blocks), dim3(256), 0, stream, w, scales, biases,
+                         out, nwords, Kw, gs);
+      break;
+    case 4:
+      hipLaunchKernelGGL(affine_dequant_kernel<4>, dim3(blocks), dim3(256), 0, stream, w, scales, biases,
+                         out, nwords, Kw, gs);
+      break;
+    default:
+      hipLaunchKernelGGL(affine_dequant_kernel<8>, dim3(blocks), dim3(256), 0, stream, w, scales, biases,
+                         out, nwords, Kw, gs);
+      break;
+  }
+  return hipGetLastError();
+}
+
+// ---- mxfp4 dequantize -------------------------------------------------------
+
+// bf16 bits of LUT[code] * 2^(s-127), exact (see file header).
+__device__ __forceinline__ uint32_t mxfp4_value_bits(uint32_t code, uint32_t s) {
+  if (s == 255u) return 0x7FC0u;
+  const uint32_t sign = (code & 8u) << 12;
+  const uint32_t mag = code & 7u;
+  if (mag == 0u) return sign;
+  // mag 1..7 -> 0.5, 1, 1.5, 2, 3, 4, 6 = m * 2^ex with m in {1, 1.5}
+  const int ex = (mag == 1u) ? -1 : (int)((mag - 2u) >> 1);
+  const uint32_t half = (mag >= 3u && (mag & 1u)) ? 1u : 0u;  // m == 1.5
+  const int E = ex + (int)s;                                   // biased bf16 exponent
+  if (E >= 255) return sign | 0x7F80u;                         // overflow to inf
+  if (E >= 1) return sign | ((uint32_t)E << 7) | (half << 6);
+  // subnormal: value = m * 2^(E-127) = mant * 2^-133
+  const uint32_t mant = (half ? 3u : 2u) << (E + 5);           // (2 or 3) * 2^(E+6) / 2
+  return sign | mant;
+}
+
+__global__ __launch_bounds__(256) void mxfp4_dequant_kernel(const uint32_t* __restrict__ w,
+                                                            const uint8_t* __restrict__ scales,
+                                                            uint16_t* __restrict__ out,
+                                                            int64_t nwords) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nwords) return;
+  const uint32_t word = __builtin_nontemporal_load(w + i);
+  const uint32_t s = scales[i >> 2];  // 4 words (32 codes) per scale
+  u32x4 o;
+#pragma unroll
+  for (int p = 0; p < 4; p++) {
+    const uint32_t lo = mxfp4_value_bits((word >> (8 * p)) & 15u, s);
+    const uint32_t hi = mxfp4_value_bits((word >> (8 * p + 4)) & 15u, s);
+    o[p] = lo | (hi << 16);
+  }
+  *reinterpret_cast<u32x4*>(out + i * 8) = o;
+}
+
+hipError_t launch_mxfp4_dequantize(const uint32_t* w, const uint8_t* scales, uint16_t* out,
+                                   int64_t rows, int64_t K, hipStream_t stream) {
+  const int64_t nwords = rows * (K / 8);
+  if (nwords == 0) return hipSuccess;
+  hipLaunchKernelGGL(mxfp4_dequant_kernel, dim3((unsigned)((nwords + 255) / 256)), dim3(256), 0, stream, w,
+                     scales, out, nwords);
+  return hipGetLastError();
+}
+
+// ---- affine quantize --------------------------------------------------------
+// GS/8 consecutive lanes own one group; each lane converts 8 consecutive values.
+
+template <int BITS, int GS>
+__global__ __launch_bounds__(256) void affine_quant_kernel(const uint16_t* __restrict__ w,
+                                                           uint32_t* __restrict__ wq,
+                                                           uint16_t* __restrict__ scales,
+                                                           uint16_t* __restrict__ biases,
+                                                           int64_t n_pieces) {
+  constexpr int L = GS / 8;  // lanes per group
+  const int64_t piece = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // 8 values each
+  const bool live = piece < n_pieces;
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (live) v = *reinterpret_cast<const u32x4*>(w + piece * 8);
+  float vals[8];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    vals[2 * i] = bf16_bits_to_f32(v[i] & 0xFFFFu);
+    vals[2 * i + 1] = bf16_bits_to_f32(v[i] >> 16);
+  }
+  // (a < b) ? b : a  /  (b < a) ? b : a  as std::max / std::min
+  float w_max = -INFINITY, w_min = INFINITY;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    w_max = (w_max < vals[i]) ? vals[i] : w_max;
+    w_min = (vals[i] < w_min) ? vals[i] : w_min;
+  }
+#pragma unroll
+  for (int off = 1; off < L; off <<= 1) {
+    const float omax = __shfl_xor(w_max, off);
+    const float omin = __shfl_xor(w_min, off);
+    w_max = (w_max < omax) ? omax : w_max;
+    w_min = (omin < w_min) ? omin : w_min;
+  }
+  const float n_bins = (float)((1 << BITS) - 1);
+  const float eps = 1e-7f;
+  const bool mask = fabsf(w_min) > fabsf(w_max);
+  float scale = (w_max - w_min) / n_bins;
+  scale = (scale < eps) ? eps : scale;
+  scale = mask ? scale : -scale;
+  const float edge = mask ? w_min : w_max;
+  const float q0 = rintf(edge / scale);
+  float bias = 0.0f;
+  if (q0 != 0.0f) {
+    scale = edge / q0;
+    bias = edge;
+  }
+  uint32_t codes = 0;  // 8 codes of BITS bits (BITS == 8: low 4 in `codes`, high 4 in `codes_hi`)
+  uint32_t codes_hi = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    float q = rintf((vals[i] - bias) / scale);
+    q = (q < 0.0f) ? 0.0f : q;
+    q = (n_bins < q) ? n_bins : q;
+    const uint32_t c = (uint32_t)q;
+    if (BITS == 8) {
+      if (i < 4) codes |= c << (8 * i);
+      else codes_hi |= c << (8 * (i - 4));
+    } else {
+      codes |= c << (BITS * i);
+    }
+  }
+  if (BITS == 2) {
+    // two lanes (16 codes) per word
+    const uint32_t other = __shfl_xor(codes, 1);
+    if (live && (piece & 1) == 0) wq[piece >> 1] = codes | (other << 16);
+  } else if (BITS == 4) {
+    if (live) wq[piece] = codes;
+  } else {
+    if (live) *reinterpret_cast<u32x2*>(wq + piece * 2) = u32x2{codes, codes_hi};
+  }
+  if (live && (piece % L) == 0) {
+    scales[piece / L] = (uint16_t)f32_to_bf16_bits(scale);
+    biases[piece / L] = (uint16_t)f32_to_bf16_bits(bias);
+  }
+}
+
+template <int BITS>
+static void launch_aq_bits(const uint16_t* w, uint32_t* wq, uint16_t* s, uint16_t* b, int64_t pieces,
+                           int gs, hipStream_t stream) {
+  const dim3 grid((unsigned)((pieces + 255) / 256));
+  if (gs == 32)
+    hipLaunchKernelGGL((affine_quant_kernel<BITS, 32>), grid, dim3(256), 0, stream, w, wq, s, b, pieces);
+  else if (gs == 64)
+    hipLaunchKernelGGL((affine_quant_kernel<BITS, 64>), grid, dim3(256), 0, stream, w, wq, s, b, pieces);
+  else
+    hipLaunchKernelGGL((affine_quant_kernel<BITS, 128>), grid, dim3(256), 0, stream, w, wq, s, b, pieces);
+}
+
+hipError_t launch_affine_quantize(const uint16_t* w, uint32_t* wq, uint16_t* scales, uint16_t* biases,
+                                  int64_t rows, int64_t K, int gs, int bits, hipStream_t stream) {
+  const int64_t pieces = rows * K / 8;
+  if (pieces == 0) return hipSuccess;
+  if (bits == 2) launch_aq_bits<2>(w, wq, scales, biases, pieces, gs, stream);
+  else if (bits == 4) launch_aq_bits<4>(w, wq, scales, biases, pieces, gs, stream);
+  else launch_aq_bits<8>(w, wq, scales, biases, pieces, gs, stream);
+  return hipGetLastError();
+}
+
+// ---- mxfp4 quantize ---------------------------------------------------------
+// 4 lanes per group of 32 values, 8 values (one output word) per lane.
+
+__device__ __forceinline__ int ceil_log2_pos(float s) {
+  const uint32_t u = __float_as_uint(s);
+  const int e = (int)(u >> 23);
+  const uint32_t mant = u & 0x7FFFFFu;
+  if (e != 0) return (e - 127) + (mant != 0u ? 1 : 0);
+  // subnormal: s = mant * 2^-149
+  return (32 - __clz((int)(mant - 1u))) - 149;
+}
+
+__global__ __launch_bounds__(256) void mxfp4_quant_kernel(const uint16_t* __restrict__ w,
+                                                          uint32_t* __restrict__ wq,
+                                                          uint8_t* __restrict__ scales,
+                                                          int64_t n_pieces) {
+  const float lut[16] = {+0.0f, +0.5f, +1.0f, +1.5f, +2.0f, +3.0f, +4.0f, +6.0f,
+                         -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
+  const int64_t piece = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool live = piece < n_pieces;
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (live) v = *reinterpret_cast<const u32x4*>(w + piece * 8);
+  float vals[8];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    vals[2 * i] = bf16_bits_to_f32(v[i] & 0xFFFFu);
+    vals[2 * i + 1] = bf16_bits_to_f32(v[i] >> 16);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const float a = fabsf(vals[i]);
+    amax = (amax < a) ? a : amax;
+  }
+#pragma unroll
+  for (int off = 1; off < 4; off <<= 1) {
+    const float o = __shfl_xor(amax, off);
+    amax = (amax < o) ? o : amax;
+  }
+  const float s = bfr(amax / 6.0f);
+  const int e = (s == 0.0f) ? 0 : ceil_log2_pos(s);
+  // power(bf16(2), e) in bf16: 2^e is exact in bf16 for e >= -133
+  const float p = bf16_bits_to_f32(e >= -126 ? (uint32_t)(e + 127) << 7 : (0x40u >> (-127 - e)));
+  uint32_t word = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const float x = bfr(vals[i] / p);
+    int best = 0;
+    float best_d = INFINITY;
+#pragma unroll
+    for (int c = 0; c < 16; c++) {
+      const float d = fabsf(bfr(x - lut[c]));
+      if (d < best_d) {
+        best_d = d;
+        best = c;
+      }
+    }
+    word |= (uint32_t)best << (4 * i);
+  }
+  if (live) wq[piece] = word;
+  if (live && (piece & 3) == 0) scales[piece >> 2] = (uint8_t)(e + 127);
+}
+
+hipError_t launch_mxfp4_quantize(const uint16_t* w, uint32_t* wq, uint8_t* scales, int64_t rows,
+                                 int64_t K, hipStream_t stream) {
+  const int64_t pieces = rows * K / 8;
+  if (pieces == 0) return hipSuccess;
+  hipLaunchKernelGGL(mxfp4_quant_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, stream, w,
+                     wq, scales, pieces);
+  return hipGetLastError();
+}
+
+}  // namespace mlxq

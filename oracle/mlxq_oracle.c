@@ -1,0 +1,351 @@
+/*
+ * mlxq_oracle.c — CPU restatement of MLX's quantized matmul, quantize and
+ * dequantize, as built into mlxcel.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the GPU path and the timed
+ * single-core CPU baseline.  The product library never links or calls it.
+ *
+ * Built with -ffp-contract=off so float expressions round exactly as the
+ * reference's scalar loops do on an x86 host without FMA contraction.
+ * Citations: CPUQ = src/lib/mlxcelverse/overlays/cpu/mlx/backend/cpu/quantized.cpp,
+ * ROPS = src/lib/mlxcelverse/overlays/rocm/mlx/ops.cpp,
+ * QAFF = src/lib/mlxcelverse/overlays/rocm/mlx/backend/rocm/quantized/affine_quantize.hip.
+ *
+ * Parity pins (tests/test_oracle.py): hand-computed known answers, torch's
+ * independent bf16 arithmetic for both dequantize roundings, exhaustive
+ * mxfp4 table vs ldexp, f64 matmul of the dequantized weights (the
+ * reference's own test method, cpu_qmm_accum_tests.rs:237-287), one-hot and
+ * all-ones activations with exact closed forms, and quantizer invariants.
+ * Unpinned beyond invariants: the exact bits of MLX's bf16 log2 inside the
+ * mxfp4 graph quantizer (shown not to change the chosen exponent for normal
+ * scales), and MLX's NaN sign on conversion.
+ */
+#include "mlxq_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- bf16 (MLX `_MLX_BFloat16`: RNE, NaN -> 0x7FC0) ------------------------ */
+
+uint16_t oracle_f32_to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if (isnan(f)) return 0x7FC0;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+float oracle_bf16_to_f32(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+void oracle_f32_to_bf16_n(const float* in, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; i++) out[i] = oracle_f32_to_bf16(in[i]);
+}
+
+void oracle_bf16_to_f32_n(const uint16_t* in, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; i++) out[i] = oracle_bf16_to_f32(in[i]);
+}
+
+/* bf16 binary op as MLX evaluates it on the CPU: widen, operate in float,
+ * round the float result to bf16. */
+static inline float bf(float f) { return oracle_bf16_to_f32(oracle_f32_to_bf16(f)); }
+
+/* std::max / std::min on floats: (a < b) ? b : a  and  (b < a) ? b : a. */
+static inline float std_max(float a, float b) { return (a < b) ? b : a; }
+static inline float std_min(float a, float b) { return (b < a) ? b : a; }
+
+static int pow2_bits(int bits) { return bits == 1 || bits == 2 || bits == 4 || bits == 8; }
+static int valid_gs(int gs) { return gs == 32 || gs == 64 || gs == 128; }
+
+/* Code i of a packed row: power-of-two widths pack 32/bits codes per uint32,
+ * low bits first (CPUQ:1283-1290; ROPS:5231-5238). */
+static inline uint32_t code_at(const uint32_t* row, int bits, int64_t i) {
+  int per = 32 / bits;
+  return (row[i / per] >> ((i % per) * bits)) & ((1u << bits) - 1u);
+}
+
+/* ---- affine quantize: CPUQ:1233-1305 ------------------------------------ */
+
+int oracle_affine_quantize(const uint16_t* w, int64_t rows, int64_t K, int group_size,
+                           int bits, uint32_t* wq, uint16_t* scales, uint16_t* biases) {
+  if (!pow2_bits(bits) || !valid_gs(group_size) || K % group_size) return -1;
+  const float n_bins = (float)((1 << bits) - 1);
+  const float eps = 1e-7f;
+  const int el_per_int = 32 / bits;
+  const int64_t int_per_group = (int64_t)group_size * bits / 32;
+  const int64_t n_groups = rows * (K / group_size);
+
+  for (int64_t i = 0; i < n_groups; ++i) {
+    const uint16_t* g = w + i * group_size;
+    float w_min = INFINITY;
+    float w_max = -w_min;
+    for (int j = 0; j < group_size; ++j) {
+      float v = oracle_bf16_to_f32(g[j]);
+      w_max = std_max(w_max, v);
+      w_min = std_min(w_min, v);
+    }
+    int mask = fabsf(w_min) > fabsf(w_max);
+    float scale, bias;
+    if (bits == 1) {
+      scale = std_max(w_max - w_min, eps);
+      bias = w_min;
+    } else {
+      scale = std_max((w_max - w_min) / n_bins, eps);
+      scale = mask ? scale : -scale;
+      float edge = mask ? w_min : w_max;
+      float q0 = rintf(edge / scale);
+      bias = 0;
+      if (q0 != 0) {
+        scale = edge / q0;
+        bias = edge;
+      }
+    }
+    uint32_t* out = wq + i * int_per_group;
+    for (int64_t j = 0; j < int_per_group; ++j) {
+      uint64_t out_el = 0;
+      for (int k = 0; k < el_per_int; ++k) {
+        float w_el = oracle_bf16_to_f32(g[j * el_per_int + k]);
+        w_el = rintf((w_el - bias) / scale);
+        w_el = std_min(std_max(w_el, 0.0f), n_bins);
+        out_el |= (uint64_t)w_el << (k * bits);
+      }
+      out[j] = (uint32_t)out_el;
+    }
+    scales[i] = oracle_f32_to_bf16(scale);
+    biases[i] = oracle_f32_to_bf16(bias);
+  }
+  return 0;
+}
+
+/* ---- affine dequantize: ROPS:5531-5573 (graph) and QAFF:164 (GPU) -------- */
+
+int oracle_affine_dequantize(const uint32_t* wq, const uint16_t* scales,
+                             const uint16_t* biases, int64_t rows, int64_t K,
+                             int group_size, int bits, int rounding, uint16_t* out) {
+  if (!pow2_bits(bits) || group_size <= 0 || K % group_size) return -1;
+  const int64_t wcols = K * bits / 32;
+  const int64_t G = K / group_size;
+  for (int64_t r = 0; r < rows; r++) {
+    const uint32_t* row = wq + r * wcols;
+    for (int64_t k = 0; k < K; k++) {
+      float q = (float)code_at(row, bits, k);
+      float s = oracle_bf16_to_f32(scales[r * G + k / group_size]);
+      float b = oracle_bf16_to_f32(biases[r * G + k / group_size]);
+      float v;
+      if (rounding == 2) {
+        /* uint32 x bf16 promotes to bf16 (upstream type_rules), so the
+         * product is stored as bf16 before the bf16 add. */
+        v = bf(bf(q * s) + b);
+      } else {
+        v = s * q + b;
+      }
+      out[r * K + k] = oracle_f32_to_bf16(v);
+    }
+  }
+  return 0;
+}
+
+/* ---- mxfp4 -------------------------------------------------------------- */
+
+/* CPUQ:73-90 */
+static const float FP4_LUT[16] = {+0.0f, +0.5f, +1.0f, +1.5f, +2.0f, +3.0f, +4.0f, +6.0f,
+                                  -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
+
+/* CPUQ:91-105 */
+uint16_t oracle_e8m0_to_bf16(uint8_t s) {
+  return (s == 0) ? 0x40 : (s == 0xFF ? 0x7FC0 : (uint16_t)((uint16_t)s << 7));
+}
+
+/* ROPS:5364-5431, e8m0 branch, every op on bf16 arrays rounded as MLX does. */
+int oracle_mxfp4_quantize(const uint16_t* w, int64_t rows, int64_t K, uint32_t* wq,
+                          uint8_t* scales) {
+  if (K % 32) return -1;
+  const int64_t n_groups = rows * (K / 32);
+  for (int64_t i = 0; i < n_groups; i++) {
+    const uint16_t* g = w + i * 32;
+    /* scales = max(abs(wq)) / bf16(6.0) */
+    float amax = 0.0f;
+    for (int j = 0; j < 32; j++) amax = std_max(amax, fabsf(oracle_bf16_to_f32(g[j])));
+    float s = bf(amax / 6.0f);
+    float e_bf; /* `scales` after the where(): bf16 holding the exponent */
+    if (s == 0.0f) {
+      e_bf = 0.0f;
+    } else {
+      /* exponent = int32(round(log2(scales))) in bf16 */
+      int e = (int)rintf(bf(log2f(s)));
+      /* decoded = 2^exponent in float32; round up if it is below the scale */
+      float decoded = ldexpf(1.0f, e);
+      if (decoded < s) e += 1;
+      e_bf = bf((float)e);
+    }
+    /* wq = wq / power(bf16(2), scales) in bf16 */
+    float p = bf(powf(2.0f, e_bf));
+    uint32_t words[4] = {0, 0, 0, 0};
+    for (int j = 0; j < 32; j++) {
+      float v = bf(oracle_bf16_to_f32(g[j]) / p);
+      /* argmin(|bf16(v - lut)|), first minimum wins */
+      int best = 0;
+      float best_d = INFINITY;
+      for (int c = 0; c < 16; c++) {
+        float d = fabsf(bf(v - FP4_LUT[c]));
+        if (d < best_d) {
+          best_d = d;
+          best = c;
+        }
+      }
+      words[j / 8] |= (uint32_t)best << (4 * (j % 8));
+    }
+    memcpy(wq + i * 4, words, sizeof(words));
+    /* scales = uint8(bf16(scales + 127)) */
+    scales[i] = (uint8_t)bf(e_bf + 127.0f);
+  }
+  return 0;
+}
+
+/* ROPS:5646-5695: LUT in the output dtype, scale 2^(s-127) in bf16, 0xFF -> NaN. */
+int oracle_mxfp4_dequantize(const uint32_t* wq, const uint8_t* scales, int64_t rows,
+                            int64_t K, uint16_t* out) {
+  if (K % 32) return -1;
+  const int64_t G = K / 32;
+  for (int64_t r = 0; r < rows; r++) {
+    const uint32_t* row = wq + r * (K / 8);
+    for (int64_t k = 0; k < K; k++) {
+      uint8_t s = scales[r * G + k / 32];
+      float v;
+      if (s == 0xFF) {
+        v = NAN;
+      } else {
+        float sc = bf(powf(2.0f, bf((float)s - 127.0f)));
+        v = bf(FP4_LUT[code_at(row, 4, k)] * sc);
+      }
+      out[r * K + k] = oracle_f32_to_bf16(v);
+    }
+  }
+  return 0;
+}
+
+/* ---- quantized matmul: CPUQ:139-257, 550-597 ---------------------------- */
+
+int oracle_qmm_t_affine(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                        const uint16_t* biases, int64_t M, int64_t N, int64_t K,
+                        int group_size, int bits, uint16_t* out) {
+  if (!pow2_bits(bits) || !valid_gs(group_size) || K % group_size) return -1;
+  const int bitmask = (1 << bits) - 1;
+  const int pack_factor = 8 / bits; /* codes per byte */
+  const int packs_in_group = group_size / pack_factor;
+  for (int64_t m = 0; m < M; m++) {
+    const uint8_t* w_local = (const uint8_t*)wq;
+    const uint16_t* scales_local = scales;
+    const uint16_t* biases_local = biases;
+    for (int64_t n = 0; n < N; n++) {
+      const uint16_t* x_local = x + m * K;
+      float sum = 0;
+      for (int64_t k = 0; k < K; k += group_size) {
+        float scale = oracle_bf16_to_f32(*scales_local++);
+        float bias = oracle_bf16_to_f32(*biases_local++);
+        for (int kw = 0; kw < packs_in_group; kw++) {
+          uint8_t wi = *w_local++;
+          for (int p = 0; p < pack_factor; p++) {
+            /* T(q) is exact; scale*T(q)+bias in float; x (bf16) * float */
+            sum += oracle_bf16_to_f32(*x_local++) * (scale * (float)(wi & bitmask) + bias);
+            if (bits != 8) wi >>= bits;
+          }
+        }
+      }
+      out[m * N + n] = oracle_f32_to_bf16(sum);
+    }
+  }
+  return 0;
+}
+
+int oracle_qmm_affine(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                      const uint16_t* biases, int64_t M, int64_t N, int64_t K,
+                      int group_size, int bits, uint16_t* out) {
+  if (!pow2_bits(bits) || !valid_gs(group_size) || N % group_size) return -1;
+  const int bitmask = (1 << bits) - 1;
+  const int pack_factor = 8 / bits;
+  const int packs_in_group = group_size / pack_factor;
+  float* acc = (float*)malloc(sizeof(float) * (size_t)N);
+  if (!acc) return -1;
+  for (int64_t m = 0; m < M; m++) {
+    const uint8_t* w_local = (const uint8_t*)wq;
+    const uint16_t* scales_local = scales;
+    const uint16_t* biases_local = biases;
+    for (int64_t n = 0; n < N; n++) acc[n] = 0.0f;
+    for (int64_t k = 0; k < K; k++) {
+      float* result_local = acc;
+      float xi = oracle_bf16_to_f32(x[m * K + k]);
+      for (int64_t n = 0; n < N; n += group_size) {
+        float scale = oracle_bf16_to_f32(*scales_local++);
+        float bias = oracle_bf16_to_f32(*biases_local++);
+        for (int ng = 0; ng < packs_in_group; ng++) {
+          uint8_t wi = *w_local++;
+          for (int p = 0; p < pack_factor; p++) {
+            (*result_local++) += xi * (scale * (float)(wi & bitmask) + bias);
+            if (bits != 8) wi >>= bits;
+          }
+        }
+      }
+    }
+    for (int64_t n = 0; n < N; n++) out[m * N + n] = oracle_f32_to_bf16(acc[n]);
+  }
+  free(acc);
+  return 0;
+}
+
+int oracle_fp_qmm_t_mxfp4(const uint16_t* x, const uint32_t* wq, const uint8_t* scales,
+                          int64_t M, int64_t N, int64_t K, uint16_t* out) {
+  if (K % 32) return -1;
+  float* x_row = (float*)malloc(sizeof(float) * (size_t)K);
+  if (!x_row) return -1;
+  for (int64_t m = 0; m < M; m++) {
+    const uint8_t* w_local = (const uint8_t*)wq;
+    const uint8_t* scales_local = scales;
+    for (int64_t k = 0; k < K; k++) x_row[k] = oracle_bf16_to_f32(x[m * K + k]);
+    for (int64_t n = 0; n < N; n++) {
+      const float* x_local = x_row;
+      float sum = 0;
+      for (int64_t k = 0; k < K; k += 32) {
+        float scale = oracle_bf16_to_f32(oracle_e8m0_to_bf16(*scales_local++));
+        float gsum = 0;
+        for (int kw = 0; kw < 16; kw++) {
+          gsum += (*x_local++) * FP4_LUT[w_local[0] & 0xf];
+          gsum += (*x_local++) * FP4_LUT[(w_local[0] >> 4) & 0xf];
+          w_local++;
+        }
+        sum += scale * gsum;
+      }
+      out[m * N + n] = oracle_f32_to_bf16(sum);
+    }
+  }
+  free(x_row);
+  return 0;
+}
+
+int oracle_gather_qmm_t(const uint16_t* x, const uint32_t* wq, const void* scales,
+                        const uint16_t* biases, const uint32_t* lhs,
+                        const uint32_t* rhs, int64_t B, int64_t M, int64_t N,
+                        int64_t K, int group_size, int bits, int mode, uint16_t* out) {
+  const int64_t w_els = N * (K * bits / 32);
+  const int64_t g_els = N * (K / group_size);
+  for (int64_t i = 0; i < B; i++) {
+    int64_t xi = lhs[i], wi = rhs[i];
+    int rc;
+    if (mode == 0) {
+      rc = oracle_qmm_t_affine(x + xi * M * K, wq + wi * w_els,
+                               (const uint16_t*)scales + wi * g_els, biases + wi * g_els,
+                               M, N, K, group_size, bits, out + i * M * N);
+    } else {
+      rc = oracle_fp_qmm_t_mxfp4(x + xi * M * K, wq + wi * w_els,
+                                 (const uint8_t*)scales + wi * g_els, M, N, K,
+                                 out + i * M * N);
+    }
+    if (rc) return rc;
+  }
+  return 0;
+}

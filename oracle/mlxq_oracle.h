@@ -1,0 +1,85 @@
+/*
+ * mlxq_oracle.h — CPU restatement of MLX's quantized-matmul semantics.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker the GPU path is
+ * compared against (and the timed single-core CPU baseline in bench.py).  It
+ * is never linked into, loaded by, or called from the product library
+ * (mlxcel_amd/, include/mlxq.h).
+ *
+ * bf16 values are passed as their raw uint16_t bit patterns.  Every function
+ * names the reference file:line it restates; abbreviations:
+ *   CPUQ = src/lib/mlxcelverse/overlays/cpu/mlx/backend/cpu/quantized.cpp
+ *   ROPS = src/lib/mlxcelverse/overlays/rocm/mlx/ops.cpp
+ *   QAFF = src/lib/mlxcelverse/overlays/rocm/mlx/backend/rocm/quantized/affine_quantize.hip
+ */
+#ifndef MLXQ_ORACLE_H
+#define MLXQ_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* float <-> bf16 with MLX's conversion (round to nearest even, NaN -> 0x7FC0). */
+uint16_t oracle_f32_to_bf16(float f);
+float oracle_bf16_to_f32(uint16_t h);
+void oracle_f32_to_bf16_n(const float* in, uint16_t* out, int64_t n);
+void oracle_bf16_to_f32_n(const uint16_t* in, float* out, int64_t n);
+
+/* Affine quantize, CPUQ:1233-1305 (`quantize<bfloat16_t, uint32_t>`).
+ * w: [rows, K] bf16.  wq: [rows, K*bits/32] u32.  scales/biases: [rows, K/gs] bf16.
+ * bits in {1, 2, 4, 8}; returns 0 on success, -1 on unsupported arguments. */
+int oracle_affine_quantize(const uint16_t* w, int64_t rows, int64_t K, int group_size,
+                           int bits, uint32_t* wq, uint16_t* scales, uint16_t* biases);
+
+/* Affine dequantize.
+ * rounding == 2: MLX CPU graph fallback, ROPS:5531-5573 — `multiply(w, scales)`
+ *                then `add(.., biases)` in bf16: bf16(bf16(q*s) + b).
+ * rounding == 1: ROCm GPU kernel, QAFF:164 — bf16(s*q + b) computed in float. */
+int oracle_affine_dequantize(const uint32_t* wq, const uint16_t* scales,
+                             const uint16_t* biases, int64_t rows, int64_t K,
+                             int group_size, int bits, int rounding, uint16_t* out);
+
+/* mxfp4 scale decode, CPUQ:89-105 `dequantize_scale<T, 32>` (bf16 bits). */
+uint16_t oracle_e8m0_to_bf16(uint8_t s);
+
+/* mxfp4 quantize, the graph fallback of ROPS:5364-5431 evaluated in bf16.
+ * w: [rows, K] bf16, K % 32 == 0.  wq: [rows, K/8] u32.  scales: [rows, K/32] u8. */
+int oracle_mxfp4_quantize(const uint16_t* w, int64_t rows, int64_t K, uint32_t* wq,
+                          uint8_t* scales);
+
+/* mxfp4 dequantize, ROPS:5646-5695 (LUT[nibble] * 2^(s-127); s == 0xFF -> NaN). */
+int oracle_mxfp4_dequantize(const uint32_t* wq, const uint8_t* scales, int64_t rows,
+                            int64_t K, uint16_t* out);
+
+/* `_qmm_t<bfloat16_t, bits, gs>`, CPUQ:199-257: y[m, n] = bf16(sum_k x*(s*q+b)),
+ * float accumulation in MLX's loop order.  x: [M, K], w: [N, K*bits/32]. */
+int oracle_qmm_t_affine(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                        const uint16_t* biases, int64_t M, int64_t N, int64_t K,
+                        int group_size, int bits, uint16_t* out);
+
+/* `_qmm<bfloat16_t, bits, gs>` (transpose=false), CPUQ:139-197:
+ * w: [K, N*bits/32], scales/biases: [K, N/gs]; y[m, n] accumulated over k. */
+int oracle_qmm_affine(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                      const uint16_t* biases, int64_t M, int64_t N, int64_t K,
+                      int group_size, int bits, uint16_t* out);
+
+/* `fp_qmm_t<bfloat16_t, 32, 4>` (mxfp4), CPUQ:550-597. */
+int oracle_fp_qmm_t_mxfp4(const uint16_t* x, const uint32_t* wq, const uint8_t* scales,
+                          int64_t M, int64_t N, int64_t K, uint16_t* out);
+
+/* `_bs_qmm_dispatch_typed` / `fp_bs_qmm_dispatch_mode`, CPUQ:764-813, 875-914:
+ * for each i < B: out[i] = x[lhs[i]] @ dequant(w[rhs[i]])^T.
+ * x: [*, M, K] (lhs indexes its flattened batch), w: [E, N, K*bits/32],
+ * scales/biases: [E, N, K/gs]; mode 0 = affine, 1 = mxfp4 (biases ignored). */
+int oracle_gather_qmm_t(const uint16_t* x, const uint32_t* wq, const void* scales,
+                        const uint16_t* biases, const uint32_t* lhs,
+                        const uint32_t* rhs, int64_t B, int64_t M, int64_t N,
+                        int64_t K, int group_size, int bits, int mode, uint16_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,100 @@
+"""GPU parity for the load-time conversions, bitwise:
+
+* dequantize vs the MLX CPU graph (overlays/rocm/mlx/ops.cpp:5531-5573 affine,
+  5646-5695 mxfp4) as restated by the oracle, plus the closed-form mxfp4 table;
+* quantize vs the MLX CPU quantizer (overlays/cpu/mlx/backend/cpu/
+  quantized.cpp:1233-1305) and the mxfp4 graph quantizer (ops.cpp:5364-5431),
+  plus the hand-derived ramp fixtures;
+* dequantize(slice) == slice(dequantize) (src/lib/mlxcel-core/src/ffi_tests.rs:5108-5170).
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import mlxcel_amd as mq
+import oracle as orc
+from helpers import announce, dev_bf16, dev_u32, dev_u8, host_u16
+
+pytestmark = pytest.mark.gpu
+KAT = np.load(os.path.join(os.path.dirname(__file__), "golden", "kat.npz"))
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_affine_dequantize_bitexact(bits, gs):
+    announce("dequant", bits, gs)
+    w = orc.normal_bf16((96, 1024), 0.02, 500 + bits + gs)
+    wq, s, b = orc.affine_quantize(w, gs, bits)
+    got = host_u16(mq.dequantize(dev_u32(wq), dev_bf16(s), dev_bf16(b), gs, bits))
+    np.testing.assert_array_equal(got, orc.affine_dequantize(wq, s, b, gs, bits, 2))
+
+
+def test_affine_dequantize_halfway_fixture():
+    announce("dequant_halfway")
+    q = (KAT["d2_q"].reshape(-1, 1) * np.array([1, 0, 0, 0, 0, 0, 0, 0], np.uint32)).astype(np.uint32)
+    got = host_u16(mq.dequantize(dev_u32(q), dev_bf16(KAT["d2_s"].reshape(-1, 1)),
+                                 dev_bf16(KAT["d2_b"].reshape(-1, 1)), 32, 8))
+    np.testing.assert_array_equal(got[:, 0], KAT["d2_out"])
+
+
+def test_mxfp4_dequantize_table_and_random():
+    announce("dequant_mxfp4")
+    codes = np.zeros((256, 32), np.uint32)
+    codes[:, :16] = np.arange(16)
+    wq = np.zeros((256, 4), np.uint32)
+    for j in range(32):
+        wq[:, j // 8] |= codes[:, j] << (4 * (j % 8))
+    sc = np.arange(256, dtype=np.uint8).reshape(256, 1)
+    got = host_u16(mq.dequantize(dev_u32(wq), dev_u8(sc), None, 32, 4, "mxfp4"))
+    np.testing.assert_array_equal(got[:, :16].T, KAT["mxfp4_table"])
+    w = orc.normal_bf16((64, 2880), 0.02, 510)
+    wq2, sc2 = orc.mxfp4_quantize(w)
+    got2 = host_u16(mq.dequantize(dev_u32(wq2), dev_u8(sc2), None, 32, 4, "mxfp4"))
+    np.testing.assert_array_equal(got2, orc.mxfp4_dequantize(wq2, sc2))
+
+
+def test_dequantize_commutes_with_row_slice():
+    announce("dequant_slice")
+    w = orc.normal_bf16((64, 512), 0.02, 520)
+    wq, s, b = orc.affine_quantize(w, 64, 4)
+    W, S, B = dev_u32(wq), dev_bf16(s), dev_bf16(b)
+    full = host_u16(mq.dequantize(W, S, B))
+    part = host_u16(mq.dequantize(W[16:40].contiguous(), S[16:40].contiguous(), B[16:40].contiguous()))
+    np.testing.assert_array_equal(full[16:40], part)
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_affine_quantize_bitexact(bits, gs):
+    announce("quant", bits, gs)
+    w = orc.normal_bf16((128, 1024), 0.02, 530 + bits + gs)
+    wq, s, b = mq.quantize(dev_bf16(w), gs, bits)
+    ewq, es, eb = orc.affine_quantize(w, gs, bits)
+    np.testing.assert_array_equal(wq.cpu().numpy(), ewq)
+    np.testing.assert_array_equal(host_u16(s), es)
+    np.testing.assert_array_equal(host_u16(b), eb)
+    kw, ks, kb = mq.quantize(dev_bf16(KAT[f"ramp_w_b{bits}_g{gs}"]), gs, bits)
+    np.testing.assert_array_equal(kw.cpu().numpy(), KAT[f"ramp_wq_b{bits}_g{gs}"])
+    np.testing.assert_array_equal(host_u16(ks), KAT[f"ramp_s_b{bits}_g{gs}"])
+    np.testing.assert_array_equal(host_u16(kb), KAT[f"ramp_b_b{bits}_g{gs}"])
+
+
+def test_mxfp4_quantize_bitexact():
+    announce("quant_mxfp4")
+    w = orc.normal_bf16((256, 2880), 0.02, 540)
+    wq, sc = mq.quantize(dev_bf16(w), mode="mxfp4")
+    ewq, esc = orc.mxfp4_quantize(w)
+    np.testing.assert_array_equal(sc.cpu().numpy(), esc)
+    np.testing.assert_array_equal(wq.cpu().numpy(), ewq)
+
+
+def test_quantize_dequantize_roundtrip_full_size():
+    # Llama-3-8B gate shape: size-independent property at full size
+    announce("roundtrip_full")
+    w = torch.randn(14336, 4096, device="cuda", dtype=torch.float32).mul_(0.02).to(torch.bfloat16)
+    wq, s, b = mq.quantize(w, 64, 4)
+    d = mq.dequantize(wq, s, b, 64, 4).float()
+    err = (d - w.float()).abs().reshape(14336, 64, 64)
+    assert float((err / s.float().abs().unsqueeze(-1)).max()) <= 1.6

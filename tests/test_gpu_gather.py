@@ -1,0 +1,108 @@
+"""GPU parity: gather_qmm (MoE experts) on gfx950 vs the CPU oracle's
+restatement of `_bs_qmm_dispatch_typed` / `fp_bs_qmm_dispatch_mode`
+(overlays/cpu/mlx/backend/cpu/quantized.cpp:764-813, 875-914).
+
+Cases follow the reference's call sites and tests: gpt-oss decode (x
+[T,1,1,K], rhs [T,4], unsorted), the sorted path (x [B,1,K], rhs sorted [B],
+src/models/switch_layers.rs:2180-2203), broadcast index shapes
+(tests/rocm_gather_qmm_expert_batched.rs:30-37), partial tiles (N=516), and
+bitwise repeatability of sorted runs (same file :46).
+"""
+import numpy as np
+import pytest
+import torch
+
+import mlxcel_amd as mq
+import oracle as orc
+from helpers import TOL, announce, dev_bf16, dev_u32, dev_u8, host_u16, max_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def topk_ids(T, E, k, seed):
+    rng = np.random.default_rng(seed)
+    return np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.uint32)
+
+
+def mx_experts(E, N, K, seed):
+    w = orc.normal_bf16((E, N, K), 0.02, seed)
+    return orc.mxfp4_quantize(w)
+
+
+def affine_experts(E, N, K, seed, gs=64, bits=4):
+    w = orc.normal_bf16((E, N, K), 0.02, seed)
+    return orc.affine_quantize(w, gs, bits)
+
+
+@pytest.mark.parametrize("T", [1, 4, 16])
+def test_mxfp4_decode_unsorted(T):
+    announce("gather_mxfp4_unsorted", T)
+    E, N, K = 32, 576, 2880
+    wq, sc = mx_experts(E, N, K, 900)
+    x = orc.normal_bf16((T, 1, 1, K), 1.0, 901 + T)
+    ids = topk_ids(T, E, 4, 902 + T)
+    got = host_u16(mq.gather_qmm(dev_bf16(x), dev_u32(wq), dev_u8(sc), None, None,
+                                 torch.from_numpy(ids.astype(np.int32)).cuda(), True, 32, 4, "mxfp4"))
+    assert got.shape == (T, 4, 1, N)
+    lhs = np.repeat(np.arange(T, dtype=np.uint32), 4)
+    want = orc.gather_qmm_t(x.reshape(T, 1, K), wq, sc, None, lhs, ids.reshape(-1), mode="mxfp4")
+    assert max_rel(got.reshape(T * 4, 1, N), want) <= TOL
+
+
+@pytest.mark.parametrize("T", [16, 64])
+def test_mxfp4_sorted(T):
+    announce("gather_mxfp4_sorted", T)
+    E, N, K = 32, 516, 2880  # N=516: partial column tile
+    wq, sc = mx_experts(E, N, K, 910)
+    ids = topk_ids(T, E, 4, 911 + T).reshape(-1)
+    order = np.argsort(ids, kind="stable")
+    x = orc.normal_bf16((T, 1, K), 1.0, 912 + T)
+    xs = x[order // 4]  # gather_sort: rows in expert order
+    rhs = ids[order]
+    X, W, S, R = dev_bf16(xs), dev_u32(wq), dev_u8(sc), dev_u32(rhs)
+    got = host_u16(mq.gather_qmm(X, W, S, None, None, R, True, 32, 4, "mxfp4", sorted_indices=True))
+    again = host_u16(mq.gather_qmm(X, W, S, None, None, R, True, 32, 4, "mxfp4", sorted_indices=True))
+    np.testing.assert_array_equal(got, again)
+    want = orc.gather_qmm_t(xs, wq, sc, None, np.arange(T * 4, dtype=np.uint32), rhs, mode="mxfp4")
+    assert max_rel(got, want) <= TOL
+    # the unsorted call on the same pairs gives the same rows
+    unsorted = host_u16(mq.gather_qmm(X, W, S, None, None, R, True, 32, 4, "mxfp4", sorted_indices=False))
+    np.testing.assert_array_equal(got, unsorted)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_affine_gather_with_broadcast_indices(bits):
+    announce("gather_affine_broadcast", bits)
+    E, N, K, M = 6, 128, 512, 2
+    wq, s, b = affine_experts(E, N, K, 920 + bits, 64, bits)
+    x = orc.normal_bf16((3, M, K), 1.0, 921)
+    lhs = np.array([[0], [2], [1]], np.int64)          # [3,1]
+    rhs = np.array([5, 0, 3, 3], np.int32)              # [4] -> broadcast [3,4]
+    got = host_u16(mq.gather_qmm(dev_bf16(x), dev_u32(wq), dev_bf16(s), dev_bf16(b),
+                                 torch.from_numpy(lhs).cuda(), torch.from_numpy(rhs).cuda(), True, 64, bits))
+    assert got.shape == (3, 4, M, N)
+    L = np.broadcast_to(lhs, (3, 4)).reshape(-1).astype(np.uint32)
+    Rr = np.broadcast_to(rhs, (3, 4)).reshape(-1).astype(np.uint32)
+    want = orc.gather_qmm_t(x, wq, s, b, L, Rr, 64, bits)
+    assert max_rel(got.reshape(12, M, N), want) <= TOL
+
+
+def test_gather_default_lhs_is_arange():
+    announce("gather_default_lhs")
+    E, N, K = 4, 64, 256
+    wq, s, b = affine_experts(E, N, K, 930)
+    x = orc.normal_bf16((5, 1, K), 1.0, 931)
+    rhs = np.array([3, 1, 1, 0, 2], np.uint32)
+    got = host_u16(mq.gather_qmm(dev_bf16(x), dev_u32(wq), dev_bf16(s), dev_bf16(b), None, dev_u32(rhs)))
+    want = orc.gather_qmm_t(x, wq, s, b, np.arange(5, dtype=np.uint32), rhs, 64, 4)
+    assert max_rel(got, want) <= TOL
+
+
+def test_gather_without_indices_is_quantized_matmul():
+    announce("gather_no_indices")
+    E, N, K = 1, 64, 256
+    wq, s, b = affine_experts(E, N, K, 940)
+    x = orc.normal_bf16((3, K), 1.0, 941)
+    a = host_u16(mq.gather_qmm(dev_bf16(x), dev_u32(wq[0]), dev_bf16(s[0]), dev_bf16(b[0])))
+    c = host_u16(mq.quantized_matmul(dev_bf16(x), dev_u32(wq[0]), dev_bf16(s[0]), dev_bf16(b[0])))
+    np.testing.assert_array_equal(a, c)
