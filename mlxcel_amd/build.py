@@ -35,6 +35,8 @@ COMMON = [
 SOURCES = {
     "api.cpp": [],
     "qmv.hip": [],
+    "qmv_rs.hip": [],
+    "qmv_fr.hip": [],
     "qmm.hip": [],
     "dequant.hip": ["-ffp-contract=off"],
 }

@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstdarg>
 #include <cstring>
 #include <map>
@@ -417,8 +418,6 @@ std::map<int, DevInfo> g_dev;
 struct Workspace {
   void* data = nullptr;
   size_t bytes = 0;
-  unsigned* counters = nullptr;
-  size_t ncounters = 0;
 };
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
@@ -440,9 +439,9 @@ DevInfo device_info(int dev) {
 }
 
 // Scratch that stays allocated for the stream's lifetime; grows (after a
-// stream synchronize) when a call needs more.  Counters are zeroed once at
-// allocation and every kernel that uses them leaves them zero.
-Workspace& workspace(int dev, hipStream_t stream, size_t bytes, size_t ncounters) {
+// stream synchronize, so no queued kernel still uses the old buffer) when a
+// call needs more.
+Workspace& workspace(int dev, hipStream_t stream, size_t bytes) {
   std::lock_guard<std::mutex> lk(g_mu);
   Workspace& w = g_ws[{dev, stream}];
   if (w.bytes < bytes) {
@@ -457,27 +456,24 @@ Workspace& workspace(int dev, hipStream_t stream, size_t bytes, size_t ncounters
     if (hipMalloc(&w.data, sz) != hipSuccess) fail(MLXQ_ENOMEM, "[mlxq] workspace allocation failed");
     w.bytes = sz;
   }
-  if (w.ncounters < ncounters) {
-    if (w.counters) {
-      hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
-      hip_check(hipFree(w.counters), "hipFree");
-      w.counters = nullptr;
-      w.ncounters = 0;
-    }
-    size_t n = 4096;
-    while (n < ncounters) n <<= 1;
-    if (hipMalloc(reinterpret_cast<void**>(&w.counters), n * sizeof(unsigned)) != hipSuccess)
-      fail(MLXQ_ENOMEM, "[mlxq] counter allocation failed");
-    hip_check(hipMemsetAsync(w.counters, 0, n * sizeof(unsigned), stream), "hipMemsetAsync");
-    w.ncounters = n;
-  }
   return w;
 }
 
-}  // namespace
+// A/B overrides for the skinny kernel's shape (waves per workgroup, K-steps
+// per wave); unset or invalid values keep the defaults.
+int env_int(const char* name, int dflt) {
+  const char* v = std::getenv(name);
+  if (!v || !*v) return dflt;
+  return std::atoi(v);
+}
 
-
-namespace {
+// Default (waves per workgroup, loads in flight) by shape.
+void qmv_shape_choice(int64_t N, int64_t K, int& nw, int& p) {
+  (void)N;
+  (void)K;
+  nw = env_int("MLXQ_QMV_NW", 0);
+  p = env_int("MLXQ_QMV_TK", 0);
+}
 
 // Broadcast strides of an index array (or of the default arange over `dshape`)
 // against the broadcast shape `b`.
@@ -532,24 +528,68 @@ void require_dtype(const mlxq_array* a, int dt, const char* name, const char* ta
                 ")");
 }
 
-// Launch the skinny kernel over `nseg` mode-A segments.
+// Skinny-kernel choice for segments of `rows` rows (measured on MI355X at the
+// Llama-3-8B MLP and gpt-oss shapes): the row-streaming kernel (qmv_rs.hip)
+// for 1-2 rows, the MFMA kernel (qmv.hip) for more, or when a shape is not
+// covered.  MLXQ_QMV_KERNEL=fr|rs|mfma forces one (fr: the full-row kernel,
+// qmv_fr.hip, 1-2 rows; rs: up to 4 rows; falling back the same way) and
+// MLXQ_QMV_R sets rows per wave (fr) or per workgroup (rs): A/B switches for
+// tests and measurements.
+enum class Skinny { FR, RS, MFMA };
+
+Skinny skinny_choice(int rows) {
+  const char* k = std::getenv("MLXQ_QMV_KERNEL");
+  if (k && std::strcmp(k, "mfma") == 0) return Skinny::MFMA;
+  if (k && std::strcmp(k, "rs") == 0) return rows <= 4 ? Skinny::RS : Skinny::MFMA;
+  if (k && std::strcmp(k, "fr") == 0) return rows <= 2 ? Skinny::FR : Skinny::MFMA;
+  return rows <= 2 ? Skinny::RS : Skinny::MFMA;
+}
+
+// Launches the full-row or row-streaming kernel when chosen and covered;
+// false: the caller runs the MFMA kernel.
+bool try_fr_rs(const QmmSpec& sp, const mlxq::QmvArgs& a, int nseg, int rows, hipStream_t stream) {
+  const int fmt = fmt_of(sp.mode, sp.bits);
+  Skinny c = skinny_choice(rows);
+  const int r_req = env_int("MLXQ_QMV_R", 0);
+  if (c == Skinny::FR) {
+    const mlxq::QmvFrPlan p = mlxq::qmv_fr_plan(fmt, sp.gs, sp.N, sp.K, rows, r_req);
+    if (p.ok) {
+      if (nseg > 65535) unsupported("too many segments for one launch");
+      hip_check(mlxq::qmv_fr_launch(fmt, sp.gs, a, nseg, p, stream), "qmv launch");
+      return true;
+    }
+    c = Skinny::RS;
+  }
+  if (c == Skinny::RS) {
+    const mlxq::QmvRsPlan p = mlxq::qmv_rs_plan(fmt, sp.gs, sp.N, sp.K, rows, r_req);
+    if (p.ok) {
+      if (nseg > 65535) unsupported("too many segments for one launch");
+      hip_check(mlxq::qmv_rs_launch(fmt, sp.gs, a, nseg, p, stream), "qmv launch");
+      return true;
+    }
+  }
+  return false;
+}
+
+// Launch the skinny kernel over `nseg` segments of at most `max_rows` rows.
 void run_qmv(const QmmSpec& sp, mlxq::QmvArgs a, int nseg, int max_rows, hipStream_t stream) {
+  if (max_rows <= 4 && try_fr_rs(sp, a, nseg, max_rows, stream)) return;
   const int fmt = fmt_of(sp.mode, sp.bits);
   const int dev = current_device();
   const DevInfo di = device_info(dev);
-  const int mt = mlxq::qmv_tile_mt(fmt, sp.gs, max_rows);
+  int nw, pf;
+  qmv_shape_choice(sp.N, sp.K, nw, pf);
   a.rows_lds = max_rows;
-  mlxq::QmvPlan p = mlxq::qmv_plan(fmt, sp.gs, sp.N, sp.K, max_rows, nseg, di.cus);
+  mlxq::QmvPlan p = mlxq::qmv_plan(fmt, sp.gs, sp.N, sp.K, max_rows, nseg, di.cus, nw, pf);
+  if (p.lds > mlxq::kQmvLdsMax) unsupported("activation tile does not fit in LDS");
   a.ks = p.ks;
   a.kst_per_wg = p.kst_per_wg;
   if (p.ks > 1) {
     const size_t ws_bytes = (size_t)p.ks * a.out_rows * sp.N * sizeof(float);
-    Workspace& w = workspace(dev, stream, ws_bytes, (size_t)nseg * p.tiles);
-    a.ws = reinterpret_cast<float*>(w.data);
-    a.counters = w.counters;
+    a.ws = reinterpret_cast<float*>(workspace(dev, stream, ws_bytes).data);
   }
   if (nseg > 65535) unsupported("too many segments for one launch");
-  hip_check(mlxq::qmv_launch(fmt, sp.gs, mt, a, nseg, p, stream), "qmv launch");
+  hip_check(mlxq::qmv_launch(fmt, sp.gs, a, nseg, p, stream), "qmv launch");
 }
 
 }  // namespace
@@ -611,7 +651,14 @@ mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w, cons
       a.X = 1;
       a.w_expert_stride = 0;
       a.s_expert_stride = 0;
-      const int rps = (int)std::min<int64_t>(rows_total, cap);
+      int rps = (int)std::min<int64_t>(rows_total, cap);
+      {
+        int nw, pf;
+        qmv_shape_choice(sp.N, sp.K, nw, pf);
+        const DevInfo di = device_info(current_device());
+        while (rps > 1 && mlxq::qmv_plan(fmt, sp.gs, sp.N, sp.K, rps, 1, di.cus, nw, pf).lds > mlxq::kQmvLdsMax)
+          rps = (rps + 1) / 2;
+      }
       a.rps = rps;
       a.total_rows = (int)rows_total;
       a.X = (int)((rows_total + rps - 1) / rps);
@@ -714,11 +761,24 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq
 
     const int dev = current_device();
     const DevInfo di = device_info(dev);
-    const int mt = mlxq::qmv_tile_mt(fmt, sp.gs, (int)M);
-    mlxq::QmvPlan p = mlxq::qmv_plan(fmt, sp.gs, sp.N, sp.K, (int)M, (int)B, di.cus);
+    const Skinny kind = skinny_choice((int)M);
+    const int r_req = env_int("MLXQ_QMV_R", 0);
+    const mlxq::QmvFrPlan fp =
+        kind == Skinny::FR ? mlxq::qmv_fr_plan(fmt, sp.gs, sp.N, sp.K, (int)M, r_req) : mlxq::QmvFrPlan{};
+    const mlxq::QmvRsPlan rp = (kind == Skinny::RS || (kind == Skinny::FR && !fp.ok))
+                                   ? mlxq::qmv_rs_plan(fmt, sp.gs, sp.N, sp.K, (int)M, r_req)
+                                   : mlxq::QmvRsPlan{};
+    const bool use_rs = fp.ok || rp.ok;
+    int nw, pf;
+    qmv_shape_choice(sp.N, sp.K, nw, pf);
+    mlxq::QmvPlan p;
+    if (!use_rs) {
+      p = mlxq::qmv_plan(fmt, sp.gs, sp.N, sp.K, (int)M, (int)B, di.cus, nw, pf);
+      if (p.lds > mlxq::kQmvLdsMax) unsupported("gather_qmm: activation tile does not fit in LDS");
+    }
     const size_t idx_bytes = ((size_t)B * 2 * sizeof(uint32_t) + 255) & ~(size_t)255;
     const size_t part_bytes = p.ks > 1 ? (size_t)p.ks * B * M * sp.N * sizeof(float) : 0;
-    Workspace& ws = workspace(dev, stream, idx_bytes + part_bytes, (size_t)B * p.tiles);
+    Workspace& ws = workspace(dev, stream, idx_bytes + part_bytes);
     uint32_t* flat = reinterpret_cast<uint32_t*>(ws.data);
     ip.out[0] = flat;
     ip.out[1] = flat + B;
@@ -742,13 +802,18 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq
     a.total_rows = (int)(B * M);
     a.out_rows = (int)(B * M);
     a.rows_lds = (int)M;
+    if (fp.ok) {
+      hip_check(mlxq::qmv_fr_launch(fmt, sp.gs, a, (int)B, fp, stream), "gather qmv launch");
+      return;
+    }
+    if (rp.ok) {
+      hip_check(mlxq::qmv_rs_launch(fmt, sp.gs, a, (int)B, rp, stream), "gather qmv launch");
+      return;
+    }
     a.ks = p.ks;
     a.kst_per_wg = p.kst_per_wg;
-    if (p.ks > 1) {
-      a.ws = reinterpret_cast<float*>(static_cast<char*>(ws.data) + idx_bytes);
-      a.counters = ws.counters;
-    }
-    hip_check(mlxq::qmv_launch(fmt, sp.gs, mt, a, (int)B, p, stream), "gather qmv launch");
+    if (p.ks > 1) a.ws = reinterpret_cast<float*>(static_cast<char*>(ws.data) + idx_bytes);
+    hip_check(mlxq::qmv_launch(fmt, sp.gs, a, (int)B, p, stream), "gather qmv launch");
   });
 }
 

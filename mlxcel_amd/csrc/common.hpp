@@ -55,11 +55,20 @@ __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
 // two per VGPR with a single and-or: VGPR p = (nibble p, nibble p+4).  The
 // matching activation fragment is stored permuted the same way
 // ([x0,x4,x1,x5,x2,x6,x3,x7]); the caller removes the 128*sum(x) offset.
+// v_and_or_b32 is written out because VOP3 cannot encode the two literal
+// masks: the compiler would otherwise emit a separate and + or per pair.
+__device__ __forceinline__ uint32_t and_or_b32(uint32_t a, uint32_t vmask, uint32_t sor) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(vmask), "s"(sor));
+  return r;
+}
+
 __device__ __forceinline__ void unpack_aff4(uint32_t w, uint32_t (&v)[4]) {
-  v[0] = (w & 0x000F000Fu) | 0x43004300u;
-  v[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-  v[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-  v[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+  const uint32_t mask = 0x000F000Fu;  // kept in a VGPR by the constraint above
+  v[0] = and_or_b32(w, mask, 0x43004300u);
+  v[1] = and_or_b32(w >> 4, mask, 0x43004300u);
+  v[2] = and_or_b32(w >> 8, mask, 0x43004300u);
+  v[3] = and_or_b32(w >> 12, mask, 0x43004300u);
 }
 
 // MXFP4: 8 e2m1 codes -> 8 bf16 in natural order using the gfx950 FP4
@@ -75,10 +84,11 @@ __device__ __forceinline__ void unpack_mxfp4(uint32_t w, uint32_t (&v)[4]) {
   v[3] = __builtin_bit_cast(uint32_t, p3);
 }
 
-// AFF8: two words = 8 byte codes -> 8 bf16 (exact: codes are < 256), natural order.
+// AFF8: two words = 8 byte codes -> 8 bf16 (exact: codes are < 256), natural
+// order.  The f32 of a byte has a zero low half, so its bf16 is the high half;
+// v_perm_b32 gathers the two high halves in one instruction.
 __device__ __forceinline__ uint32_t pack_bf16x2_exact(float lo, float hi) {
-  // Both inputs are integers below 256, so truncation is exact.
-  return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
 __device__ __forceinline__ void unpack_aff8(uint32_t w0, uint32_t w1, uint32_t (&v)[4]) {

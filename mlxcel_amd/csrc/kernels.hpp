@@ -10,31 +10,26 @@
 namespace mlxq {
 
 // Skinny (decode) quantized matmul over segments of rows sharing one weight
-// matrix.  Mode A (seg == nullptr): segment s = rows [s*rps, s*rps + rps) of
-// the output, x batch lhs[s] (or s), weight matrix rhs[s] (or s when
-// w_expert_stride != 0, else 0).  Mode B: segment table seg[s] =
-// {expert, row_begin, row_count} over a row map rowmap[r] = {x_row, out_row}.
+// matrix: segment s = output rows [s*rps, s*rps + rps), activations from x
+// batch lhs[s] (or s), weight matrix rhs[s] (or s when w_expert_stride != 0,
+// else 0).
 struct QmvArgs {
   const uint16_t* x;        // bf16 activations, rows of K
   const uint32_t* w;        // packed codes [E][N][K*bits/32]
   const void* scales;       // bf16 (affine) or uint8 e8m0 (mxfp4) [E][N][K/gs]
   const uint16_t* biases;   // bf16 [E][N][K/gs] (affine only)
   uint16_t* out;            // bf16 [out_rows][N]
-  float* ws;                // split-K partials [ks][out_rows][N] (ks > 1)
-  unsigned* counters;       // split-K arrival counters, one per (segment, tile); zero on entry and exit
-  const uint32_t* lhs;      // mode A: x batch index per segment (nullable)
-  const uint32_t* rhs;      // mode A: expert per segment (nullable)
-  const int* seg;           // mode B segment table (nullable)
-  const int* rowmap;        // mode B row map
-  const int* nseg;          // mode B: number of valid segments (device)
+  float* ws;                // split-K partials [ks][out_rows][N] (ks > 1), summed by a second kernel
+  const uint32_t* lhs;      // x batch index per segment (nullable)
+  const uint32_t* rhs;      // expert per segment (nullable)
   int N;
   int K;
   int64_t w_expert_stride;  // uint32 words per weight matrix (0: one matrix)
   int64_t s_expert_stride;  // scale/bias elements per weight matrix
   int E;                    // weight matrices (index clamp)
   int X;                    // x batches (index clamp)
-  int rps;                  // mode A rows per segment
-  int total_rows;           // mode A total rows
+  int rps;                  // rows per segment
+  int total_rows;           // total rows
   int out_rows;             // rows of `out` (split-K workspace stride)
   int rows_lds;             // activation rows staged per workgroup (>= rows of any segment)
   int ks;                   // workgroups splitting K (gridDim.z)
@@ -42,18 +37,54 @@ struct QmvArgs {
 };
 
 struct QmvPlan {
-  int ks = 1;
-  int kst_per_wg = 1;
-  int tiles = 1;
-  size_t lds = 0;
+  int ks = 1;          // workgroups splitting K (gridDim.z)
+  int kst_per_wg = 1;  // K-steps per workgroup
+  int tiles = 1;       // 16-column tiles
+  int nw = 4;          // waves per workgroup
+  int p = 4;           // K-steps per wave, all loaded up front (TK)
+  int mt = 1;          // 16-row MFMA tiles
+  size_t lds = 0;      // dynamic LDS bytes
 };
 
+extern const uint32_t kQmvLdsMax;  // bytes of LDS one workgroup may use
 int qmv_slots(int fmt, int gs);
 int qmv_tile_mt(int fmt, int gs, int rows);
 int qmv_max_rows(int fmt, int gs);
-QmvPlan qmv_plan(int fmt, int gs, int64_t N, int64_t K, int rows_lds, int nseg, int num_cus);
-hipError_t qmv_launch(int fmt, int gs, int mt, const QmvArgs& a, int nseg_slots, const QmvPlan& p,
-                      hipStream_t stream);
+// nw/tk: requested waves per workgroup and K-steps per wave (invalid -> defaults).
+QmvPlan qmv_plan(int fmt, int gs, int64_t N, int64_t K, int rows_lds, int nseg, int num_cus, int nw, int p);
+// Launches the kernel (and, when p.ks > 1, the split-K reduction kernel).
+hipError_t qmv_launch(int fmt, int gs, const QmvArgs& a, int nseg_slots, const QmvPlan& p, hipStream_t stream);
+
+// Row-streaming decode kernel (qmv_rs.hip) for 1 to 4 activation rows per
+// weight matrix: R weight rows per workgroup, one wave per 1 KiB chunk of a
+// row (CPW chunks per wave when a row has more than 8).
+struct QmvRsPlan {
+  bool ok = false;  // false: use qmv_plan / qmv_launch
+  int mr = 1;       // activation rows compiled for (1, 2 or 4)
+  int r = 8;        // weight rows per workgroup
+  int cpw = 1;      // 1 KiB chunks per wave and row
+  int nw = 1;       // waves per workgroup
+  int tiles = 1;    // workgroups along N
+  size_t lds = 0;   // dynamic LDS bytes (staged scales + reduction)
+};
+// r_req: requested rows per workgroup (0 or invalid -> default).
+QmvRsPlan qmv_rs_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int r_req);
+hipError_t qmv_rs_launch(int fmt, int gs, const QmvArgs& a, int nseg, const QmvRsPlan& p, hipStream_t stream);
+
+// Full-row decode kernel (qmv_fr.hip) for 1 or 2 activation rows per weight
+// matrix: 8 waves per workgroup, R whole rows per wave, activations staged in
+// LDS once per workgroup.
+struct QmvFrPlan {
+  bool ok = false;  // false: shape not covered
+  int mr = 1;       // activation rows compiled for
+  int r = 4;        // rows per wave
+  int cmax = 2;     // 1 KiB chunks per row compiled for
+  int chunks = 1;   // 1 KiB chunks per row
+  int tiles = 1;    // workgroups along N
+  size_t lds = 0;   // dynamic LDS bytes
+};
+QmvFrPlan qmv_fr_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int r_req);
+hipError_t qmv_fr_launch(int fmt, int gs, const QmvArgs& a, int nseg, const QmvFrPlan& p, hipStream_t stream);
 
 // Elementwise conversions (dequant.hip).
 hipError_t launch_affine_dequantize(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,

@@ -28,8 +28,8 @@
 //    tile to finish sums the fp32 partials in a fixed order, so results are
 //    bitwise reproducible run to run.
 //  * Segments (gridDim.y) generalise the kernel to batched and gathered
-//    (MoE) products: each segment is a run of rows that share one weight
-//    matrix (expert).
+//    (MoE) products: segment s is the x.shape[-2] rows of batch lhs[s]
+//    multiplied by weight matrix rhs[s] (expert).
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -54,17 +54,59 @@ __device__ __forceinline__ u32x4 lds_read16(const unsigned char* base, uint32_t 
   return *reinterpret_cast<const u32x4*>(base + off);
 }
 
+// LDS layout.  The workgroup shares
+//   [sb]  16 x (GW + 1) x {scale, bias - 128*scale | bias} fp32 (affine) or
+//         16 x (GW + 1) scale fp32 (mxfp4): the scales of the 16 rows over the
+//         workgroup's K range, staged with coalesced loads (one row per
+//         instruction) instead of one scattered load per lane and K-step;
+// and every wave owns a region holding what its K-steps
+// t = kst0 + wave + NW * i (i < TK) need:
+//   [x]   rows_lds x TK x KSTEP bf16 activations (AFF4 fragments pre-permuted
+//         to [x0,x4,x1,x5,x2,x6,x3,x7]); K outside the matrix is zero
+//   [xs]  TK x (KSTEP / XG) x CAP fp32 activation sums ([i][sum][row]; for
+//         S == 4 [i][row][sum]), CAP = 16 * MT / S; absent rows are zero
+//   [zero] 64 zero bytes: the A operand of lanes with no activation row.
+// After the K loop the bytes are reused for the cross-wave reduction.
+struct QmvLds {
+  uint32_t sb, w0, x, xs, zpad, wreg, total;  // x/xs/zpad relative to a wave region
+};
+
+__host__ __device__ inline QmvLds qmv_lds_layout(int fmt, int gs, int rows_lds, int tk, int nw, int mt, int gw) {
+  const int ck = fmt == AFF8 ? 16 : 32;
+  const int kstep = 4 * ck;
+  const int xg = gs < kstep ? gs : kstep;
+  const int s = (kstep + gs - 1) / gs;
+  const int cap = 16 * mt / s;
+  QmvLds l;
+  l.sb = 0;
+  l.w0 = ((uint32_t)16 * (gw + 1) * (fmt != MXFP4 ? 8 : 4) + 15u) & ~15u;  // row pitch gw + 1: no bank conflicts
+  l.x = 0;
+  l.xs = (uint32_t)rows_lds * tk * kstep * 2;
+  l.zpad = (l.xs + (fmt != MXFP4 ? (uint32_t)tk * (kstep / xg) * cap * 4 : 0) + 15u) & ~15u;
+  l.wreg = l.zpad + 64;
+  l.total = l.w0 + (uint32_t)nw * l.wreg;
+  const uint32_t red = (uint32_t)nw * mt * 4 * 64 * 4;
+  if (l.total < red) l.total = red;
+  return l;
+}
+
 template <int FMT, int GS, int MT, int NW, int TK>
 __global__ __launch_bounds__(NW * 64) void qmv_kernel(const QmvArgs a) {
   constexpr int CK = Fmt_traits<FMT>::CK;
-  constexpr int KSTEP = 4 * CK;             // K values per K-step (4 lane groups)
-  constexpr int NJ = CK / 8;                // MFMAs per K-step
-  constexpr int S = (KSTEP + GS - 1) / GS;  // quantization groups per K-step
+  constexpr int KSTEP = 4 * CK;                // K values per K-step (4 lane groups)
+  constexpr int NJ = CK / 8;                   // MFMAs per K-step
+  constexpr int S = (KSTEP + GS - 1) / GS;     // quantization groups per K-step
+  constexpr int XG = GS < KSTEP ? GS : KSTEP;  // K values per activation sum
+  constexpr int XSK = KSTEP / XG;              // activation sums per K-step
+  constexpr int CAP = 16 * MT / S;             // activation rows per segment
   constexpr bool AFF = FMT != MXFP4;
   constexpr int BITS = FMT == AFF8 ? 8 : 4;
+  constexpr int PPK = KSTEP / 8;               // 16-byte activation pieces per K-step
+  constexpr int KPL = 64 / PPK;                // K-steps covered by one wave-wide load
+  constexpr int XL = (TK + KPL - 1) / KPL;     // activation loads per row per lane
+  constexpr int XEARLY = 4;                    // activation loads issued before the weights
 
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ int s_is_last;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -72,166 +114,241 @@ __global__ __launch_bounds__(NW * 64) void qmv_kernel(const QmvArgs a) {
   const int kq = lane >> 4;
   const int tile = blockIdx.x;
   const int sidx = blockIdx.y;
-  const int kz = blockIdx.z;
 
-  // ---- segment: rows sharing one weight matrix ----------------------------
-  int expert, count, row_begin = 0, xbatch = 0;
-  if (a.seg) {
-    if (sidx >= *a.nseg) return;
-    expert = a.seg[3 * sidx + 0];
-    row_begin = a.seg[3 * sidx + 1];
-    count = a.seg[3 * sidx + 2];
-  } else {
-    count = min(a.rps, a.total_rows - sidx * a.rps);
-    expert = a.rhs ? (int)min(a.rhs[sidx], (uint32_t)(a.E - 1)) : (a.w_expert_stride ? sidx : 0);
-    xbatch = a.lhs ? (int)min(a.lhs[sidx], (uint32_t)(a.X - 1)) : sidx;
-  }
+  // ---- segment (wave-uniform) ---------------------------------------------
+  const int count = min(a.rps, a.total_rows - sidx * a.rps);
   if (count <= 0) return;
+  const int expert = a.rhs ? (int)min(a.rhs[sidx], (uint32_t)(a.E - 1)) : (a.w_expert_stride ? sidx : 0);
+  const int xbatch = a.lhs ? (int)min(a.lhs[sidx], (uint32_t)(a.X - 1)) : sidx;
 
   const int N = a.N;
   const int K = a.K;
   const int n0 = tile * 16;
-  const int n = min(n0 + nl, N - 1);
-  const int Kw = K / (32 / BITS);  // uint32 words per weight row
-  const int G = K / GS;            // groups per row
   const int nchunks = K / CK;
-  const uint32_t* wrow = a.w + (int64_t)expert * a.w_expert_stride + (int64_t)n * Kw;
-  const int64_t srow = (int64_t)expert * a.s_expert_stride + (int64_t)n * G;
-
+  const int G = K / GS;
+  const int kst0 = blockIdx.z * a.kst_per_wg;
   const int nkst = (K + KSTEP - 1) / KSTEP;
-  const int kst0 = kz * a.kst_per_wg;
   const int kst1 = min(nkst, kst0 + a.kst_per_wg);
-  const int kb = kst0 * KSTEP;
-  const int KC = a.kst_per_wg * KSTEP;  // LDS row length (K values)
-  const int per = (a.kst_per_wg + NW - 1) / NW;
-  const int wk0 = kst0 + wave * per;
-  const int nst = max(0, min(kst1, wk0 + per) - wk0);
+  const int t0 = kst0 + wave;  // this wave's K-steps: t0 + NW * i
+  const int nst = min(TK, max(0, (kst1 - t0 + NW - 1) / NW));
+  const int rows_lds = a.rows_lds;
+  const int KC = a.kst_per_wg * KSTEP;  // the workgroup's K range
+  const int GW = KC / GS;                // groups of that range per row (>= 1)
+  const int GWP = GW + 1;                // LDS row pitch of the scales
+  const int g0 = (kst0 * KSTEP) / GS;
+  const QmvLds L = qmv_lds_layout(FMT, GS, rows_lds, TK, NW, MT, GW);
+  unsigned char* wr = smem + L.w0 + wave * L.wreg;  // this wave's region
 
-  // ---- 1. issue every weight / scale / bias load of this wave -------------
+  // ---- 1. loads: activations and scales of this wave, then its weights ----
+  // vmcnt retires in order, so the small staged loads can be consumed while
+  // the weight loads (issued last) are still in flight.
+  const uint16_t* xrow0 = a.x + ((int64_t)xbatch * a.rps) * K;
+  auto x_item = [&](int e, int& m, int& i, int& piece) {  // e-th activation load of this lane
+    m = e / XL;
+    i = lane / PPK + KPL * (e - m * XL);
+    piece = lane % PPK;
+  };
+  auto x_load = [&](int e) -> u32x4 {
+    int m, i, piece;
+    x_item(e, m, i, piece);
+    const int t = t0 + NW * i;
+    const int k = t * KSTEP + piece * 8;
+    const bool live = m < count && i < nst && k < K;
+    return live ? *reinterpret_cast<const u32x4*>(xrow0 + (int64_t)m * K + k) : u32x4{0u, 0u, 0u, 0u};
+  };
+  const int nx = rows_lds * XL;
+  u32x4 xv[XEARLY];
+#pragma unroll
+  for (int e = 0; e < XEARLY; e++)
+    if (e < nx) xv[e] = x_load(e);
+
+  // Scales: wave w stages rows w, w + NW, ...; lane j of a load takes group
+  // g0 + j + 64 v, so one instruction reads one row's groups contiguously.
+  constexpr int RPW = 16 / NW;  // rows per wave
+  const int64_t sbase = (int64_t)expert * a.s_expert_stride;
+  const int nsv = (GW + 63) / 64;  // loads per row
+  auto sb_idx = [&](int u, int v, int& r, int& j) -> int64_t {
+    r = wave + NW * u;
+    j = lane + 64 * v;
+    return sbase + (int64_t)min(n0 + r, N - 1) * G + min(g0 + j, G - 1);
+  };
+  constexpr int SBE = 8;  // loads per lane issued before the weights; e -> (u, v) = (e % RPW, e / RPW)
+  uint32_t s_raw[SBE], b_raw[SBE];
+#pragma unroll
+  for (int e = 0; e < SBE; e++) {
+    s_raw[e] = b_raw[e] = 0u;
+    if (e < RPW * nsv) {
+      int r, j;
+      const int64_t o = sb_idx(e % RPW, e / RPW, r, j);
+      if constexpr (AFF) {
+        s_raw[e] = reinterpret_cast<const uint16_t*>(a.scales)[o];
+        b_raw[e] = a.biases[o];
+      } else {
+        s_raw[e] = reinterpret_cast<const uint8_t*>(a.scales)[o];
+      }
+    }
+  }
+
+  // Weight loads: unconditional (clamped indices; a clamped chunk meets zero
+  // activations) so they go out back to back.
+  const u32x4* wrow = reinterpret_cast<const u32x4*>(a.w + (int64_t)expert * a.w_expert_stride +
+                                                     (int64_t)min(n0 + nl, N - 1) * (K / (32 / BITS)));
   u32x4 wv[TK];
-  uint32_t sraw[TK][S];
-  uint32_t braw[TK][S];
 #pragma unroll
   for (int i = 0; i < TK; i++) {
-    if (i < nst) {
-      const int t = wk0 + i;
-      const int c = t * 4 + kq;
-      wv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow) + (c < nchunks ? c : 0));
-      const int gt = (t * KSTEP) / GS;
+    const int c = min((t0 + NW * min(i, max(nst - 1, 0))) * 4 + kq, nchunks - 1);
+    wv[i] = __builtin_nontemporal_load(wrow + c);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep uses of staged data below the weight loads
+
+  // ---- 2. stage this wave's operands in its LDS region ---------------------
+  float* xsw = reinterpret_cast<float*>(wr + L.xs);
+  auto x_put = [&](int e, u32x4 v) {
+    int m, i, piece;
+    x_item(e, m, i, piece);
+    if constexpr (AFF) {
+      float s = sum_bf16x8(v);
 #pragma unroll
-      for (int sl = 0; sl < S; sl++) {
-        const int g = min(gt + sl, G - 1);
-        if constexpr (AFF) {
-          sraw[i][sl] = reinterpret_cast<const uint16_t*>(a.scales)[srow + g];
-          braw[i][sl] = a.biases[srow + g];
-        } else {
-          sraw[i][sl] = reinterpret_cast<const uint8_t*>(a.scales)[srow + g];
-        }
+      for (int off = 1; off < XG / 8; off <<= 1) s += __shfl_xor(s, off);
+      if (i < TK && (piece % (XG / 8)) == 0) {
+        const int sl = piece / (XG / 8);
+        xsw[S == 4 ? (i * CAP + m) * XSK + sl : (i * XSK + sl) * CAP + m] = s;
       }
     }
-  }
-
-  // ---- 2. stage this workgroup's activations (and group sums) in LDS ------
-  // Layout: x[m][KC] bf16 (AFF4 fragments pre-permuted), 16 zero bytes,
-  // then xsum[m][KC/GS] fp32.
-  const int rows_lds = a.rows_lds;
-  const uint32_t zpad = (uint32_t)rows_lds * KC * 2;
-  float* xsum = reinterpret_cast<float*>(smem + zpad + 16);
-  const int GPW = KC / GS;  // groups per workgroup K range
-  {
-    const int per_row8 = KC / 8;
-    const int total8 = rows_lds * per_row8;
-    for (int idx = threadIdx.x; idx < total8; idx += NW * 64) {
-      const int m = idx / per_row8;
-      const int k8 = idx - m * per_row8;
-      const int k = kb + k8 * 8;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (m < count && k < K) {
-        int64_t xr;
-        if (a.seg) {
-          xr = a.rowmap[2 * (row_begin + m)];
-        } else {
-          xr = (int64_t)xbatch * a.rps + m;
-        }
-        v = *reinterpret_cast<const u32x4*>(a.x + xr * K + k);
-      }
-      if constexpr (AFF) {
-        float s = sum_bf16x8(v);
-#pragma unroll
-        for (int off = 1; off < GS / 8; off <<= 1) s += __shfl_xor(s, off);
-        if ((k8 % (GS / 8)) == 0) xsum[m * GPW + (k8 * 8) / GS] = s;
-      }
+    if (i < TK) {
       if constexpr (FMT == AFF4) v = perm_aff4(v);
-      *reinterpret_cast<u32x4*>(smem + ((uint32_t)m * KC + k8 * 8) * 2) = v;
+      *reinterpret_cast<u32x4*>(wr + L.x + (uint32_t)((m * TK + i) * KSTEP + piece * 8) * 2) = v;
     }
-    if (threadIdx.x == 0) *reinterpret_cast<u32x4*>(smem + zpad) = u32x4{0u, 0u, 0u, 0u};
+  };
+#pragma unroll
+  for (int e = 0; e < XEARLY; e++)
+    if (e < nx) x_put(e, xv[e]);
+  for (int e = XEARLY; e < nx; e++) x_put(e, x_load(e));
+  if constexpr (AFF) {  // sums of rows this segment does not have
+    for (int e = lane; e < TK * XSK * (CAP - rows_lds); e += 64) {
+      const int m = rows_lds + e % (CAP - rows_lds);
+      const int r = e / (CAP - rows_lds);  // (i, sl) pair
+      const int i = r / XSK, sl = r % XSK;
+      xsw[S == 4 ? (i * CAP + m) * XSK + sl : (i * XSK + sl) * CAP + m] = 0.f;
+    }
   }
-  __syncthreads();
+  auto sb_put = [&](int r, int j, uint32_t sr, uint32_t br) {
+    if (j >= GW) return;
+    if constexpr (AFF) {
+      const float sc = bf16_bits_to_f32(sr);
+      const float bi = bf16_bits_to_f32(br);
+      reinterpret_cast<float2*>(smem + L.sb)[r * GWP + j] =
+          float2{sc, (FMT == AFF4) ? __builtin_fmaf(-128.0f, sc, bi) : bi};
+    } else {
+      reinterpret_cast<float*>(smem + L.sb)[r * GWP + j] = e8m0_to_f32(sr);
+    }
+  };
+#pragma unroll
+  for (int e = 0; e < SBE; e++) {
+    if (e < RPW * nsv) {
+      int r, j;
+      sb_idx(e % RPW, e / RPW, r, j);
+      sb_put(r, j, s_raw[e], b_raw[e]);
+    }
+  }
+  for (int e = SBE; e < RPW * nsv; e++) {  // wide K ranges: the rest
+    int r, j;
+    const int64_t o = sb_idx(e % RPW, e / RPW, r, j);
+    if constexpr (AFF) {
+      sb_put(r, j, reinterpret_cast<const uint16_t*>(a.scales)[o], a.biases[o]);
+    } else {
+      sb_put(r, j, reinterpret_cast<const uint8_t*>(a.scales)[o], 0u);
+    }
+  }
+  if (lane < 4) reinterpret_cast<u32x4*>(wr + L.zpad)[lane] = u32x4{0u, 0u, 0u, 0u};
+  __syncthreads();  // the shared scales (and every wave's own region)
 
-  // ---- 3. MFMA over the K-steps, fold per group ----------------------------
+  // ---- 3. MFMA over this wave's K-steps, fold per group --------------------
   const int slot_kq = (kq * CK) / GS < S ? (kq * CK) / GS : 0;
-  uint32_t xoff[MT];
+  uint32_t abase[MT];
   bool aact[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; mt++) {
     const int R = 16 * mt + nl;
-    const int mA = R / S;
-    aact[mt] = (mA < count) && ((R % S) == slot_kq);
-    xoff[mt] = ((uint32_t)mA * KC + kq * CK) * 2;
+    aact[mt] = R / S < count && (R % S) == slot_kq;
+    abase[mt] = (uint32_t)(wr - smem) + L.x + (uint32_t)((R / S) * TK * KSTEP + kq * CK) * 2;
   }
+  // scales of K-step i: group (wave + NW i) * S + sl of row nl (GS <= KSTEP),
+  // or (wave + NW i) / 2 when a group spans two K-steps (NW is even)
+  const uint32_t sbb = L.sb + (uint32_t)(nl * GWP + (GS <= KSTEP ? wave * S : wave / 2)) * (AFF ? 8 : 4);
+  constexpr uint32_t SB_STEP = (uint32_t)(GS <= KSTEP ? NW * S : NW / 2) * (AFF ? 8 : 4);
+  const uint32_t zp = (uint32_t)(wr - smem) + L.zpad;
+  uint32_t xsb[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++) {
+    const int m0 = (16 * mt + 4 * kq) / S;
+    xsb[mt] = (uint32_t)(wr - smem) + L.xs + (uint32_t)(S == 4 ? m0 * XSK : m0) * 4;
+  }
+
   f32x4 acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; mt++) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
   for (int i = 0; i < TK; i++) {
-    if (i < nst) {
-      const int t = wk0 + i;
-      const bool cvalid = (t * 4 + kq) < nchunks;
-      const uint32_t kloc2 = (uint32_t)(t - kst0) * KSTEP * 2;
+    if (i < nst) {  // wave-uniform
+      const u32x4 w = wv[i];
+      uint32_t ab[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++) ab[mt] = aact[mt] ? abase[mt] + (uint32_t)(i * KSTEP) * 2 : zp;
       f32x4 d[MT];
 #pragma unroll
-      for (int j = 0; j < NJ; j++) {
+      for (int jj = 0; jj < NJ; jj++) {
         uint32_t bv[4];
-        if constexpr (FMT == AFF4) unpack_aff4(wv[i][j], bv);
-        if constexpr (FMT == MXFP4) unpack_mxfp4(wv[i][j], bv);
-        if constexpr (FMT == AFF8) unpack_aff8(wv[i][2 * j], wv[i][2 * j + 1], bv);
+        if constexpr (FMT == AFF4) unpack_aff4(w[jj], bv);
+        if constexpr (FMT == MXFP4) unpack_mxfp4(w[jj], bv);
+        if constexpr (FMT == AFF8) unpack_aff8(w[2 * jj], w[2 * jj + 1], bv);
         const bf16x8 b = as_bf16x8(bv);
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
-          const uint32_t off = (aact[mt] && cvalid) ? xoff[mt] + kloc2 + 16u * j : zpad;
-          const bf16x8 av = __builtin_bit_cast(bf16x8, lds_read16(smem, off));
-          d[mt] = mfma16x16x32(av, b, j == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : d[mt]);
+          const bf16x8 av = __builtin_bit_cast(bf16x8, lds_read16(smem, ab[mt] + 16u * jj));
+          d[mt] = mfma16x16x32(av, b, jj == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : d[mt]);
         }
       }
-      // fold: acc += s * D (+ b' * xsum)
-      const int gl0 = (t - kst0) * KSTEP / GS;
+      // fold: acc += s * D (+ b' * sum(x)) per output row
+      float sc[S], bp[S];
+#pragma unroll
+      for (int sl = 0; sl < S; sl++) {
+        if constexpr (AFF) {
+          const float2 v2 = *reinterpret_cast<const float2*>(smem + sbb + i * SB_STEP + sl * 8);
+          sc[sl] = v2.x;
+          bp[sl] = v2.y;
+        } else {
+          sc[sl] = *reinterpret_cast<const float*>(smem + sbb + i * SB_STEP + sl * 4);
+          bp[sl] = 0.f;
+        }
+      }
 #pragma unroll
       for (int mt = 0; mt < MT; mt++) {
+        float xs[4];
+        if constexpr (AFF) {
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            // D row (16mt + 4kq + q) is activation row m0 + q / S, sum slot q % S
+            const int dm = q / S, sl = q % S;
+            const uint32_t off = S == 4 ? (uint32_t)((i * CAP) * XSK + sl) * 4
+                                        : (uint32_t)((i * XSK + sl) * CAP + dm) * 4;
+            xs[q] = *reinterpret_cast<const float*>(smem + xsb[mt] + off);
+          }
+        }
 #pragma unroll
         for (int q = 0; q < 4; q++) {
           const int sl = q % S;
-          float sc;
-          if constexpr (AFF) {
-            sc = bf16_bits_to_f32(sraw[i][sl]);
-          } else {
-            sc = e8m0_to_f32(sraw[i][sl]);
-          }
           float v = acc[mt][q];
-          if constexpr (AFF) {
-            const float bi = bf16_bits_to_f32(braw[i][sl]);
-            const float bp = (FMT == AFF4) ? __builtin_fmaf(-128.0f, sc, bi) : bi;
-            const int mD = min((16 * mt + 4 * kq + q) / S, rows_lds - 1);
-            v = __builtin_fmaf(bp, xsum[mD * GPW + gl0 + sl], v);
-          }
-          acc[mt][q] = __builtin_fmaf(sc, d[mt][q], v);
+          if constexpr (AFF) v = __builtin_fmaf(bp[sl], xs[q], v);
+          acc[mt][q] = __builtin_fmaf(sc[sl], d[mt][q], v);
         }
       }
     }
   }
 
   // ---- 4. reduce the waves of this workgroup through LDS -------------------
-  __syncthreads();  // every wave is done reading the activations
+  __syncthreads();  // every wave is done reading LDS
   float* red = reinterpret_cast<float*>(smem);
 #pragma unroll
   for (int mt = 0; mt < MT; mt++)
@@ -240,64 +357,45 @@ __global__ __launch_bounds__(NW * 64) void qmv_kernel(const QmvArgs a) {
   __syncthreads();
 
   const bool split = a.ks > 1;
-  if (wave == 0) {
+  for (int e = threadIdx.x; e < MT * 64; e += NW * 64) {
+    const int mt = e >> 6;
+    const int ln = e & 63;
+    const int lq = ln >> 4;
+    const int lnl = ln & 15;
+    float tot[4];
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
-      float tot[4];
+    for (int q = 0; q < 4; q++) {
+      float s = 0.f;
+      for (int w = 0; w < NW; w++) s += red[((w * MT + mt) * 4 + q) * 64 + ln];
+      tot[q] = s;
+    }
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        float s = 0.f;
-        for (int w = 0; w < NW; w++) s += red[((w * MT + mt) * 4 + q) * 64 + lane];
-        tot[q] = s;
-      }
-      // rows 16mt+4kq+q hold (m = R / S, slot = R % S): sum the S slots of each m
+    for (int u = 0; u < 4 / S; u++) {
+      float y = 0.f;
 #pragma unroll
-      for (int u = 0; u < 4 / S; u++) {
-        float y = 0.f;
-#pragma unroll
-        for (int sl = 0; sl < S; sl++) y += tot[u * S + sl];
-        const int m = (16 * mt + 4 * kq) / S + u;
-        if (m < count && n0 + nl < N) {
-          const int64_t orow = a.seg ? (int64_t)a.rowmap[2 * (row_begin + m) + 1]
-                                     : (int64_t)sidx * a.rps + m;
-          if (split) {
-            a.ws[((int64_t)kz * a.out_rows + orow) * N + n0 + nl] = y;
-          } else {
-            a.out[orow * N + n0 + nl] = (uint16_t)f32_to_bf16_bits(y);
-          }
+      for (int sl = 0; sl < S; sl++) y += tot[u * S + sl];
+      const int m = (16 * mt + 4 * lq) / S + u;
+      if (m < count && n0 + lnl < N) {
+        const int64_t orow = (int64_t)sidx * a.rps + m;
+        if (split) {
+          a.ws[((int64_t)blockIdx.z * a.out_rows + orow) * N + n0 + lnl] = y;
+        } else {
+          a.out[orow * N + n0 + lnl] = (uint16_t)f32_to_bf16_bits(y);
         }
       }
     }
   }
-  if (!split) return;
+}
 
-  // ---- 5. split-K: the last workgroup of this tile sums the partials --------
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned prev = atomicAdd(&a.counters[sidx * gridDim.x + tile], 1u);
-    s_is_last = (prev == (unsigned)(a.ks - 1));
-  }
-  __syncthreads();
-  if (!s_is_last) return;
-  __threadfence();
-  if (wave == 0) {
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
-#pragma unroll
-      for (int u = 0; u < 4 / S; u++) {
-        const int m = (16 * mt + 4 * kq) / S + u;
-        if (m < count && n0 + nl < N) {
-          const int64_t orow = a.seg ? (int64_t)a.rowmap[2 * (row_begin + m) + 1]
-                                     : (int64_t)sidx * a.rps + m;
-          float y = 0.f;
-          for (int z = 0; z < a.ks; z++) y += a.ws[((int64_t)z * a.out_rows + orow) * N + n0 + nl];
-          a.out[orow * N + n0 + nl] = (uint16_t)f32_to_bf16_bits(y);
-        }
-      }
-    }
-  }
-  if (threadIdx.x == 0) a.counters[sidx * gridDim.x + tile] = 0u;
+// Second pass of a K split: out = bf16(sum over z of the fp32 partials), in a
+// fixed order (bitwise reproducible; no cross-workgroup fences needed).
+__global__ __launch_bounds__(256) void qmv_splitk_reduce(const float* __restrict__ ws, uint16_t* __restrict__ out,
+                                                         int64_t n, int ks) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float y = 0.f;
+  for (int z = 0; z < ks; z++) y += ws[(int64_t)z * n + i];
+  out[i] = (uint16_t)f32_to_bf16_bits(y);
 }
 
 // ---- gather index preparation ----------------------------------------------
@@ -341,26 +439,41 @@ hipError_t launch_index_prep(const IdxPrepArgs& a, hipStream_t stream) {
 // ---- host launch -----------------------------------------------------------
 
 namespace {
-constexpr int kNW = 4;
-constexpr int kTK = 8;
 
+// (NW, TK) instantiated for every format: waves per workgroup and K-steps
+// per wave.  One workgroup covers NW * TK K-steps.
 template <int FMT, int GS, int MT>
-hipError_t launch_t(const QmvArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((qmv_kernel<FMT, GS, MT, kNW, kTK>), grid, dim3(kNW * 64), lds, stream, a);
-  return hipGetLastError();
+hipError_t launch_nwt(int nw, int tk, const QmvArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
+#define QMV_CASE(NW_, TK_)                                                                             \
+  if (nw == NW_ && tk == TK_) {                                                                        \
+    hipLaunchKernelGGL((qmv_kernel<FMT, GS, MT, NW_, TK_>), grid, dim3(NW_ * 64), lds, stream, a);    \
+    return hipGetLastError();                                                                          \
+  }
+  QMV_CASE(4, 4)
+  QMV_CASE(4, 8)
+  QMV_CASE(8, 4)
+  QMV_CASE(8, 8)
+  QMV_CASE(16, 4)
+  QMV_CASE(16, 8)
+#undef QMV_CASE
+  return hipErrorInvalidValue;
 }
 
 template <int FMT, int GS>
-hipError_t launch_mt(int mt, const QmvArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
+hipError_t launch_mt(int mt, int nw, int tk, const QmvArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
   switch (mt) {
-    case 1: return launch_t<FMT, GS, 1>(a, grid, lds, stream);
-    case 2: return launch_t<FMT, GS, 2>(a, grid, lds, stream);
-    default: return launch_t<FMT, GS, 4>(a, grid, lds, stream);
+    case 1: return launch_nwt<FMT, GS, 1>(nw, tk, a, grid, lds, stream);
+    case 2: return launch_nwt<FMT, GS, 2>(nw, tk, a, grid, lds, stream);
+    default: return launch_nwt<FMT, GS, 4>(nw, tk, a, grid, lds, stream);
   }
 }
+
+bool valid_nwt(int nw, int tk) { return (nw == 4 || nw == 8 || nw == 16) && (tk == 4 || tk == 8); }
 }  // namespace
 
 int qmv_ck(int fmt) { return fmt == AFF8 ? 16 : 32; }
+
+const uint32_t kQmvLdsMax = 160 * 1024;  // LDS per workgroup on gfx950
 
 int qmv_slots(int fmt, int gs) {
   const int kstep = 4 * qmv_ck(fmt);
@@ -375,56 +488,83 @@ int qmv_tile_mt(int fmt, int gs, int rows) {
 
 int qmv_max_rows(int fmt, int gs) { return 16 * 4 / qmv_slots(fmt, gs); }
 
-QmvPlan qmv_plan(int fmt, int gs, int64_t N, int64_t K, int rows_lds, int nseg, int num_cus) {
-  QmvPlan p;
+QmvPlan qmv_plan(int fmt, int gs, int64_t N, int64_t K, int rows_lds, int nseg, int num_cus, int nw_req,
+                 int tk_req) {
+  QmvPlan pl;
   const int kstep = 4 * qmv_ck(fmt);
   const int nkst = (int)((K + kstep - 1) / kstep);
   const int tiles = (int)((N + 15) / 16);
-  // K-steps per workgroup: at most kNW * kTK (every wave holds <= kTK loads in
-  // registers), rounded so that the workgroup K range is a multiple of 128.
-  const int step_align = 128 / kstep;  // K-steps per 128 K values
-  int max_kst = kNW * kTK;
-  // Split K across workgroups until there are enough workgroups to cover the
-  // chip twice or the per-workgroup range gets short.
-  int ks = (nkst + max_kst - 1) / max_kst;
-  while ((int64_t)tiles * nseg * ks < 2LL * num_cus && (nkst + ks) / (ks + 1) >= 4 * step_align * 2) ks++;
-  int kst_per = (nkst + ks - 1) / ks;
-  kst_per = ((kst_per + step_align - 1) / step_align) * step_align;
-  ks = (nkst + kst_per - 1) / kst_per;
-  // Dynamic LDS: activations rows x KC bf16, a 16-byte zero pad, group sums
-  // rows x KC/gs fp32; the same bytes later hold the cross-wave reduction.
-  auto lds_bytes = [&](int kp) {
-    const int KC = kp * kstep;
-    const size_t x = (size_t)rows_lds * KC * 2 + 16 + (size_t)rows_lds * (KC / gs) * 4;
-    const size_t red = (size_t)kNW * 4 * 4 * 64 * 4;  // NW x MT(<=4) x 4 x 64 floats
-    return x > red ? x : red;
-  };
-  while (lds_bytes(kst_per) > 64 * 1024 && kst_per > step_align) {
-    kst_per = ((kst_per / 2 + step_align - 1) / step_align) * step_align;
-    ks = (nkst + kst_per - 1) / kst_per;
+  const int mt = qmv_tile_mt(fmt, gs, rows_lds);
+  // Workgroup K ranges are whole multiples of 128 K values (the largest
+  // group), so activation sums never straddle two workgroups.
+  const int step_align = 128 / kstep;
+  // Default shape: the first (NW, TK) whose NW * TK covers K, so one
+  // workgroup streams whole rows and no second pass is needed.
+  int nw = 16 / mt, tk = 8;
+  const int opts[5][2] = {{8, 4}, {16, 4}, {16, 8}, {8, 8}, {4, 8}};
+  for (auto& o : opts) {
+    if (o[0] * mt > 16) continue;
+    if (o[0] * o[1] >= nkst) {
+      nw = o[0];
+      tk = o[1];
+      break;
+    }
   }
-  p.ks = ks;
-  p.kst_per_wg = kst_per;
-  p.tiles = tiles;
-  p.lds = lds_bytes(kst_per);
-  return p;
+  if (valid_nwt(nw_req, tk_req) && nw_req * mt <= 16) {
+    nw = nw_req;
+    tk = tk_req;
+  }
+  auto per_of = [&](int k) {
+    int per = (nkst + k - 1) / k;
+    per = ((per + step_align - 1) / step_align) * step_align;
+    return per;
+  };
+  // the per-wave regions must fit the LDS of one workgroup (160 KiB on gfx950)
+  auto lds_of = [&](int nw_, int tk_) {
+    int k = 1;
+    while (per_of(k) > nw_ * tk_) k++;
+    return qmv_lds_layout(fmt, gs, rows_lds, tk_, nw_, mt, per_of(k) * kstep / gs).total;
+  };
+  while (lds_of(nw, tk) > kQmvLdsMax && nw > 4) nw /= 2;
+  while (lds_of(nw, tk) > kQmvLdsMax && tk > 4) tk = 4;
+  int ks = 1;
+  while (per_of(ks) > nw * tk) ks++;  // a workgroup holds at most NW * TK K-steps
+  const int per = per_of(ks);
+  pl.ks = (nkst + per - 1) / per;
+  pl.kst_per_wg = per;
+  pl.tiles = tiles;
+  pl.nw = nw;
+  pl.p = tk;
+  pl.mt = mt;
+  pl.lds = qmv_lds_layout(fmt, gs, rows_lds, tk, nw, mt, per * kstep / gs).total;
+  (void)num_cus;
+  (void)nseg;
+  return pl;
 }
 
-hipError_t qmv_launch(int fmt, int gs, int mt, const QmvArgs& a, int nseg_slots, const QmvPlan& p,
-                      hipStream_t stream) {
+hipError_t qmv_launch(int fmt, int gs, const QmvArgs& a, int nseg_slots, const QmvPlan& p, hipStream_t stream) {
   dim3 grid((unsigned)p.tiles, (unsigned)nseg_slots, (unsigned)p.ks);
+  hipError_t e;
   switch (fmt) {
     case AFF4:
-      if (gs == 32) return launch_mt<AFF4, 32>(mt, a, grid, p.lds, stream);
-      if (gs == 64) return launch_mt<AFF4, 64>(mt, a, grid, p.lds, stream);
-      return launch_mt<AFF4, 128>(mt, a, grid, p.lds, stream);
+      e = gs == 32 ? launch_mt<AFF4, 32>(p.mt, p.nw, p.p, a, grid, p.lds, stream)
+        : gs == 64 ? launch_mt<AFF4, 64>(p.mt, p.nw, p.p, a, grid, p.lds, stream)
+                   : launch_mt<AFF4, 128>(p.mt, p.nw, p.p, a, grid, p.lds, stream);
+      break;
     case AFF8:
-      if (gs == 32) return launch_mt<AFF8, 32>(mt, a, grid, p.lds, stream);
-      if (gs == 64) return launch_mt<AFF8, 64>(mt, a, grid, p.lds, stream);
-      return launch_mt<AFF8, 128>(mt, a, grid, p.lds, stream);
+      e = gs == 32 ? launch_mt<AFF8, 32>(p.mt, p.nw, p.p, a, grid, p.lds, stream)
+        : gs == 64 ? launch_mt<AFF8, 64>(p.mt, p.nw, p.p, a, grid, p.lds, stream)
+                   : launch_mt<AFF8, 128>(p.mt, p.nw, p.p, a, grid, p.lds, stream);
+      break;
     default:
-      return launch_mt<MXFP4, 32>(mt, a, grid, p.lds, stream);
+      e = launch_mt<MXFP4, 32>(p.mt, p.nw, p.p, a, grid, p.lds, stream);
+      break;
   }
+  if (e != hipSuccess || p.ks == 1) return e;
+  const int64_t n = (int64_t)a.out_rows * a.N;
+  hipLaunchKernelGGL(qmv_splitk_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a.ws, a.out, n,
+                     p.ks);
+  return hipGetLastError();
 }
 
 }  // namespace mlxq

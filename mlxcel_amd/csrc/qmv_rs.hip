@@ -1,0 +1,411 @@
+// qmv_rs.hip — row-streaming decode kernel (1 to 4 activation rows per
+// weight matrix) for gfx950.
+//
+// Same product as qmv.hip (reference decode route: overlays/rocm/mlx/backend/
+// rocm/quantized/qmv_tiled_kernel.hip:29-128 and the MoE decode kernels of
+// qmm.hip:5578-6054; CPU math overlays/cpu/mlx/backend/cpu/quantized.cpp:
+// 199-257 affine, 550-597 mxfp4), shaped for how HBM3E wants to be read.
+//
+// Access pattern.  A packed weight row is cut into 1 KiB chunks; chunk c of
+// every row of a workgroup's R-row tile is read by wave c, one 16-byte lane
+// per 1/64 of the chunk.  Every load instruction therefore moves 1 KiB of
+// consecutive bytes and a workgroup reads R whole rows, so the bytes in
+// flight form a few dense address ranges.  (Reading the same bytes as 16 rows
+// x 64 B per instruction, the fragment layout an MFMA wants, costs about 25%
+// more time on MI355X at these sizes.)
+//
+// Arithmetic.  A lane always covers the same 32 (4-bit) or 16 (8-bit) K
+// positions of its rows, so its activations for those positions are loaded
+// once into registers.  The codes are widened to bf16 pairs (AFF4 "128 + q"
+// with one and-or per pair, MXFP4 with the gfx950 fp4 conversion, AFF8 via
+// byte -> f32 -> bf16) and multiplied with v_dot2_f32_bf16 in fp32.  A lane's
+// 16 bytes lie inside one quantization group, so the scale and bias apply
+// once per lane and row:  y += s * sum((128+q) x) + (b - 128 s) * sum(x).
+// Partial sums of all (row, activation-row) pairs are reduced across the 64
+// lanes with a halving butterfly and across waves through LDS in a fixed
+// order, so results are bitwise reproducible.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace mlxq {
+
+namespace {
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum CNT values per lane over each row of 16 lanes with DPP exchanges (no
+// LDS round trips).  Step s pairs every lane with one whose bit (3 - s)
+// differs: row_mirror (i <-> 15-i), row_half_mirror (i <-> 7-i in each half),
+// then quad_perm swaps of bit 1 and bit 0; the pairs of successive steps
+// never repeat a lane, so after four steps each value has been summed over
+// all 16 lanes.  While more than one value is left, a step halves them: the
+// lane with the bit set keeps the upper half and sends the lower.  Afterwards
+// lane i (of its row) holds values [(i / Q) * C, (i / Q) * C + C) where
+// C = max(CNT / 16, 1) and Q = max(16 / CNT, 1).
+template <int CNT, int STEP>
+__device__ __forceinline__ void row_butterfly(float* v, int lane) {
+  if constexpr (STEP < 4) {
+    constexpr int BIT = 8 >> STEP;
+    constexpr int CTRL = STEP == 0 ? 0x140 : (STEP == 1 ? 0x141 : (STEP == 2 ? 0x4E : 0xB1));
+    if constexpr (CNT > 1) {
+      constexpr int H = CNT / 2;
+      const bool up = (lane & BIT) != 0;
+#pragma unroll
+      for (int i = 0; i < H; i++) {
+        const float keep = up ? v[i + H] : v[i];
+        const float send = up ? v[i] : v[i + H];
+        v[i] = keep + dpp<CTRL>(send);
+      }
+      row_butterfly<H, STEP + 1>(v, lane);
+    } else {
+      v[0] += dpp<CTRL>(v[0]);
+      row_butterfly<1, STEP + 1>(v, lane);
+    }
+  }
+}
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+}
+
+constexpr int log2i(int v) { return v <= 1 ? 0 : 1 + log2i(v / 2); }
+
+}  // namespace
+
+// LDS bytes of one workgroup: the tile's scales (G groups x R rows, row
+// fastest; (scale, bias - 128 scale | bias) fp32 pairs for affine, scale fp32
+// for mxfp4) and the reduction buffer (NW waves x 4 lane rows x R*MR partials).
+__host__ __device__ inline uint32_t qmv_rs_lds(int fmt, int r, int mr, int nw, int64_t G) {
+  const uint32_t sb = (uint32_t)(r * G * (fmt != MXFP4 ? 8 : 4));
+  return ((sb + 15u) & ~15u) + (uint32_t)(nw * 4 * r * mr * 4);
+}
+
+namespace {
+
+constexpr uint32_t kDeadLane = 0x80000000u;  // a buffer offset past every operand: loads return 0
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// [x0,x1,x2,x3,x4,x5,x6,x7] (bf16, 4 words) -> [x0,x4,x1,x5,x2,x6,x3,x7]
+__device__ __forceinline__ u32x4 perm_aff4_v(u32x4 x) {
+  return u32x4{__builtin_amdgcn_perm(x[2], x[0], 0x05040100u), __builtin_amdgcn_perm(x[2], x[0], 0x07060302u),
+               __builtin_amdgcn_perm(x[3], x[1], 0x05040100u), __builtin_amdgcn_perm(x[3], x[1], 0x07060302u)};
+}
+
+}  // namespace
+
+// FMT: weight format; MR: activation rows (>= rows of any segment);
+// R: weight rows per workgroup (power of two); CPW: 1 KiB chunks per wave and row.
+template <int FMT, int MR, int R, int CPW>
+__global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shift) {
+  constexpr bool AFF = FMT != MXFP4;
+  constexpr int BITS = FMT == AFF8 ? 8 : 4;
+  constexpr int KL = 128 / BITS;  // K positions per lane chunk (16 bytes)
+  constexpr int XV = KL / 8;      // 16-byte activation pieces per lane chunk
+  constexpr int NP = KL / 2;      // bf16 pairs per lane chunk
+  constexpr int V = R * MR;       // partial sums per lane
+  static_assert(V <= 64 && (V & (V - 1)) == 0, "partials per lane must be a power of two <= 64");
+  static_assert((R & (R - 1)) == 0 && R <= 16, "R must be a power of two <= 16");
+  constexpr int LR = log2i(R);
+  constexpr int VC = V >= 16 ? V / 16 : 1;  // partials per lane after the row butterfly
+  constexpr int VQ = V >= 16 ? 1 : 16 / V;  // lanes per partial after it
+  constexpr int SBE = 4;                    // scale loads per thread issued before the weights
+  constexpr int ESZ = AFF ? 2 : 1;          // bytes per stored scale
+
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int NW = blockDim.x >> 6;
+  const int NT = blockDim.x;
+  const int sidx = blockIdx.y;
+
+  // ---- segment (workgroup-uniform) ----------------------------------------
+  const int count = min(a.rps, a.total_rows - sidx * a.rps);
+  if (count <= 0) return;
+  const int expert = a.rhs ? (int)min(a.rhs[sidx], (uint32_t)(a.E - 1)) : (a.w_expert_stride ? sidx : 0);
+  const int xbatch = a.lhs ? (int)min(a.lhs[sidx], (uint32_t)(a.X - 1)) : sidx;
+
+  const int N = a.N;
+  const int K = a.K;
+  const int row0 = blockIdx.x * R;
+  const int nlc = K / KL;  // lane chunks per row
+  const uint32_t RB = (uint32_t)nlc * 16u;  // bytes per weight row
+  const int G = K >> gs_shift;
+  float* sbl = reinterpret_cast<float*>(smem);
+  float* red = reinterpret_cast<float*>(smem + ((R * G * (AFF ? 8 : 4) + 15) & ~15));
+
+  // Buffer resources: bounds-checked loads return 0 past the end, which
+  // covers rows past N, activation rows past `count` and dead lanes.
+  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.w + (int64_t)expert * a.w_expert_stride, (uint32_t)N * RB);
+  const __amdgpu_buffer_rsrc_t xr =
+      buffer_rsrc(a.x + (int64_t)xbatch * a.rps * K, (uint32_t)count * (uint32_t)K * 2u);
+  const int64_t sb0 = (int64_t)expert * a.s_expert_stride;
+  const __amdgpu_buffer_rsrc_t sr =
+      buffer_rsrc(reinterpret_cast<const uint8_t*>(a.scales) + sb0 * ESZ, (uint32_t)(N * G * ESZ));
+  const __amdgpu_buffer_rsrc_t br = buffer_rsrc(AFF ? (const void*)(a.biases + sb0) : a.scales,
+                                                (uint32_t)(AFF ? N * G * 2 : 0));
+
+  int kc[CPW];
+  bool live[CPW];
+  uint32_t wo[CPW], xo[CPW];
+#pragma unroll
+  for (int j = 0; j < CPW; j++) {
+    kc[j] = (wave + NW * j) * 64 + lane;
+    live[j] = kc[j] < nlc;
+    wo[j] = live[j] ? (uint32_t)kc[j] * 16u : kDeadLane;
+    xo[j] = live[j] ? (uint32_t)kc[j] * (KL * 2) : kDeadLane;
+  }
+
+  // ---- 1. loads: activations, the tile's scales, then weights -------------
+  u32x4 xv[MR][CPW][XV];
+#pragma unroll
+  for (int m = 0; m < MR; m++)
+#pragma unroll
+    for (int j = 0; j < CPW; j++)
+#pragma unroll
+      for (int v = 0; v < XV; v++)
+        xv[m][j][v] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo[j] + (uint32_t)(m * K * 2 + v * 16), 0, 0));
+
+  // Scales of the G x R tile: thread t stages row t % R, units (of `upw`
+  // groups: one word, or one byte/short for odd rows) t / R, t / R + NT / R, ...
+  const int upw = AFF ? ((G & 1) ? 1 : 2) : ((G & 3) ? ((G & 1) ? 1 : 2) : 4);
+  const int gu = G / upw;
+  const int sr_row = threadIdx.x & (R - 1);
+  const int sj0 = threadIdx.x >> LR;
+  const int sjs = NT >> LR;
+  const uint32_t srow_off = (uint32_t)((row0 + sr_row) * G);  // in groups
+  auto load_unit = [&](int jn, uint32_t& s_, uint32_t& b_) {
+    const uint32_t og = srow_off + (uint32_t)(jn * upw);
+    if constexpr (AFF) {
+      if (upw == 2) {
+        s_ = __builtin_amdgcn_raw_buffer_load_b32(sr, og * 2u, 0, 0);
+        b_ = __builtin_amdgcn_raw_buffer_load_b32(br, og * 2u, 0, 0);
+      } else {
+        s_ = __builtin_amdgcn_raw_buffer_load_b16(sr, og * 2u, 0, 0);
+        b_ = __builtin_amdgcn_raw_buffer_load_b16(br, og * 2u, 0, 0);
+      }
+    } else {
+      s_ = upw == 4 ? __builtin_amdgcn_raw_buffer_load_b32(sr, og, 0, 0)
+                    : (upw == 2 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(sr, og, 0, 0)
+                                : (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(sr, og, 0, 0));
+      b_ = 0u;
+    }
+  };
+  uint32_t sraw[SBE], braw[SBE];
+#pragma unroll
+  for (int i = 0; i < SBE; i++) load_unit(sj0 + sjs * i, sraw[i], braw[i]);
+
+  u32x4 wv[R][CPW];
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int j = 0; j < CPW; j++)
+      wv[r][j] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo[j] + (uint32_t)(row0 + r) * RB, 0, 2 /* nt */));
+  __builtin_amdgcn_sched_barrier(0);  // keep the arithmetic below the loads
+
+  // ---- 2. stage the scales; activation sums and operand order -------------
+  auto put_unit = [&](int jn, uint32_t s_, uint32_t b_) {
+    if (jn >= gu) return;
+    for (int h = 0; h < upw; h++) {
+      const int idx = (jn * upw + h) * R + sr_row;
+      if constexpr (AFF) {
+        const float sc = bf16_bits_to_f32((s_ >> (16 * h)) & 0xFFFFu);
+        const float bi = bf16_bits_to_f32((b_ >> (16 * h)) & 0xFFFFu);
+        reinterpret_cast<float2*>(sbl)[idx] = float2{sc, FMT == AFF4 ? __builtin_fmaf(-128.0f, sc, bi) : bi};
+      } else {
+        sbl[idx] = e8m0_to_f32((s_ >> (8 * h)) & 0xFFu);
+      }
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < SBE; i++) put_unit(sj0 + sjs * i, sraw[i], braw[i]);
+  for (int jn = sj0 + sjs * SBE; jn < gu; jn += sjs) {  // long rows: the rest
+    uint32_t s_, b_;
+    load_unit(jn, s_, b_);
+    put_unit(jn, s_, b_);
+  }
+
+  float xs[MR][CPW];
+#pragma unroll
+  for (int m = 0; m < MR; m++)
+#pragma unroll
+    for (int j = 0; j < CPW; j++) {
+      float s = 0.f;
+      if constexpr (AFF) {
+#pragma unroll
+        for (int v = 0; v < XV; v++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) s = dot2(xv[m][j][v][e], 0x3F803F80u, s);  // pairs times (1, 1)
+      }
+      xs[m][j] = s;
+      if constexpr (FMT == AFF4) {
+#pragma unroll
+        for (int v = 0; v < XV; v++) xv[m][j][v] = perm_aff4_v(xv[m][j][v]);
+      }
+    }
+  __syncthreads();  // the staged scales
+
+  // ---- 3. dot products, one scale/bias fold per lane chunk -----------------
+  uint32_t sbase[CPW];  // LDS byte offset of this lane's group, row 0
+#pragma unroll
+  for (int j = 0; j < CPW; j++)
+    sbase[j] = (uint32_t)(min((kc[j] * KL) >> gs_shift, G - 1) * R) * (AFF ? 8u : 4u);
+
+  float y[R][MR];
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int m = 0; m < MR; m++) y[r][m] = 0.f;
+
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int j = 0; j < CPW; j++) {
+      float sc, bp = 0.f;
+      if constexpr (AFF) {
+        const float2 t = *reinterpret_cast<const float2*>(smem + sbase[j] + r * 8);
+        sc = t.x;
+        bp = t.y;
+      } else {
+        sc = *reinterpret_cast<const float*>(smem + sbase[j] + r * 4);
+      }
+      if (!live[j]) sc = bp = 0.f;  // lanes past the end of the row add exactly 0
+      uint32_t pr[NP];
+      const u32x4 w = wv[r][j];
+      if constexpr (FMT == AFF8) {
+        uint32_t t[4];
+        unpack_aff8(w[0], w[1], t);
+#pragma unroll
+        for (int e = 0; e < 4; e++) pr[e] = t[e];
+        unpack_aff8(w[2], w[3], t);
+#pragma unroll
+        for (int e = 0; e < 4; e++) pr[4 + e] = t[e];
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          uint32_t t[4];
+          if constexpr (FMT == AFF4) unpack_aff4(w[q], t);
+          else unpack_mxfp4(w[q], t);
+#pragma unroll
+          for (int e = 0; e < 4; e++) pr[4 * q + e] = t[e];
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < MR; m++) {
+        float d = 0.f;
+#pragma unroll
+        for (int p = 0; p < NP; p++) {
+          // pair p covers lane-chunk K positions 2p, 2p+1 (AFF4: the permuted pair of word p/4)
+          d = dot2(pr[p], xv[m][j][p / 4][p % 4], d);
+        }
+        float acc = y[r][m];
+        if constexpr (AFF) acc = __builtin_fmaf(bp, xs[m][j], acc);
+        y[r][m] = __builtin_fmaf(sc, d, acc);
+      }
+    }
+
+  // ---- 4. reduce: 16-lane rows (DPP), then rows and waves (LDS) ------------
+  float v[V];
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int m = 0; m < MR; m++) v[r * MR + m] = y[r][m];
+  row_butterfly<V, 0>(v, lane);
+  const int li = lane & 15;
+  if (li % VQ == 0) {
+#pragma unroll
+    for (int c = 0; c < VC; c++) red[(wave * 4 + (lane >> 4)) * V + (li / VQ) * VC + c] = v[c];
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < V) {
+    const int idx = threadIdx.x;
+    float tot = 0.f;
+    for (int q = 0; q < NW * 4; q++) tot += red[q * V + idx];
+    const int r = idx / MR, m = idx % MR;
+    const int row = row0 + r;
+    if (row < N && m < count) a.out[((int64_t)sidx * a.rps + m) * N + row] = (uint16_t)f32_to_bf16_bits(tot);
+  }
+}
+
+// ---- host ------------------------------------------------------------------
+
+namespace {
+
+template <int FMT>
+hipError_t rs_launch_fmt(const QmvRsPlan& p, const QmvArgs& a, int gs_shift, dim3 grid, hipStream_t stream) {
+  const dim3 block((unsigned)(p.nw * 64));
+#define RS_CASE(MR_, R_, CPW_)                                                                        \
+  if (p.mr == MR_ && p.r == R_ && p.cpw == CPW_) {                                                    \
+    hipLaunchKernelGGL((qmv_rs_kernel<FMT, MR_, R_, CPW_>), grid, block, p.lds, stream, a, gs_shift); \
+    return hipGetLastError();                                                                         \
+  }
+  RS_CASE(1, 4, 1)
+  RS_CASE(1, 8, 1)
+  RS_CASE(1, 16, 1)
+  RS_CASE(2, 4, 1)
+  RS_CASE(2, 8, 1)
+  RS_CASE(4, 4, 1)
+  RS_CASE(4, 8, 1)
+  RS_CASE(1, 4, 2)
+  RS_CASE(1, 8, 2)
+  RS_CASE(2, 4, 2)
+  RS_CASE(2, 8, 2)
+  RS_CASE(4, 4, 2)
+#undef RS_CASE
+  return hipErrorInvalidValue;
+}
+
+bool rs_valid(int mr, int r, int cpw) {
+  if (cpw == 1) return (mr == 1 && (r == 4 || r == 8 || r == 16)) || ((mr == 2 || mr == 4) && (r == 4 || r == 8));
+  if (cpw == 2) return ((mr == 1 || mr == 2) && (r == 4 || r == 8)) || (mr == 4 && r == 4);
+  return false;
+}
+
+}  // namespace
+
+QmvRsPlan qmv_rs_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int r_req) {
+  QmvRsPlan p;
+  const int kl = fmt == AFF8 ? 16 : 32;
+  const int64_t nlc = K / kl;
+  const int64_t chunks = (nlc + 63) / 64;
+  p.mr = rows <= 1 ? 1 : (rows <= 2 ? 2 : 4);
+  if (rows > 4 || rows < 1) return p;
+  // at most 8 waves of up to 256 registers (two per SIMD)
+  p.cpw = chunks <= 8 ? 1 : 2;
+  if (chunks > 16) return p;
+  p.nw = (int)((chunks + p.cpw - 1) / p.cpw);
+  p.r = 8;
+  if (p.cpw == 2 && p.mr == 4) p.r = 4;
+  if (r_req > 0 && rs_valid(p.mr, r_req, p.cpw)) p.r = r_req;
+  p.tiles = (int)((N + p.r - 1) / p.r);
+  const int64_t G = K / gs;
+  p.lds = qmv_rs_lds(fmt, p.r, p.mr, p.nw, G);
+  // buffer offsets are 32-bit and 0x80000000 marks a dead lane: every operand
+  // of one launch must stay below 2 GiB
+  const int64_t wbytes = N * (K / kl) * 16, sbytes = N * G * 2;
+  p.ok = rs_valid(p.mr, p.r, p.cpw) && K % kl == 0 && K % gs == 0 && p.lds <= kQmvLdsMax &&
+         wbytes + (int64_t)p.r * (K / kl) * 16 < ((int64_t)1 << 31) && sbytes < ((int64_t)1 << 31) &&
+         (int64_t)4 * K * 2 < ((int64_t)1 << 31);
+  return p;
+}
+
+hipError_t qmv_rs_launch(int fmt, int gs, const QmvArgs& a, int nseg, const QmvRsPlan& p, hipStream_t stream) {
+  if (!p.ok) return hipErrorInvalidValue;
+  const int gs_shift = log2i(gs);
+  const dim3 grid((unsigned)p.tiles, (unsigned)nseg, 1);
+  switch (fmt) {
+    case AFF4: return rs_launch_fmt<AFF4>(p, a, gs_shift, grid, stream);
+    case AFF8: return rs_launch_fmt<AFF8>(p, a, gs_shift, grid, stream);
+    default: return rs_launch_fmt<MXFP4>(p, a, gs_shift, grid, stream);
+  }
+}
+
+}  // namespace mlxq
