@@ -5,15 +5,19 @@ the Llama-3-8B MLP decode projections at M=1, 4-bit affine, group 64:
 gate (N=14336, K=4096), up (same) and down (N=4096, K=14336), three qmv
 launches of 33,067,008 algorithmic bytes each (packed W + bf16 scales +
 bf16 biases + x + y).  Weights rotate across 8 distinct layers (~793 MB) so
-every launch streams from HBM, not the 256 MB MALL.  `value` = algorithmic
-bytes / time over K timed steps (HIP events on the launch stream).
+every launch streams from HBM, not the 256 MB MALL.  Each layer's step is one
+HIP graph, so the timed region holds GPU work only; `value` = algorithmic
+bytes / time over K timed steps (HIP events on the replay stream).
+`roofline` is the gate kernel alone: bytes per launch / its average launch
+duration, timed the same way.
 
 Also reported (extra): the M in {1,2,4,8} x {4,8}-bit decode sweep, mxfp4
 gather_qmm (gpt-oss-20b MoE shapes), the measured device copy ceiling, and
 the single-core CPU baseline (the oracle's restatement of MLX's CPU
 `_qmm_t`, overlays/cpu/mlx/backend/cpu/quantized.cpp:199-257).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+       python bench.py --traffic-probe   (under rocprofv3 --pmc: copy calibration + gate launches)
 """
 from __future__ import annotations
 
@@ -35,6 +39,12 @@ import mlxcel_amd as mq  # noqa: E402
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0  # dense
 MALL_BYTES = 256 << 20
+# HBM bytes per gate launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on
+# `bench.py --traffic-probe`, each counter scaled by what it reads for a
+# device copy of exactly 256 MiB (FETCH_SIZE x 1.9998, WRITE_SIZE x 1.0):
+# 16433.6 KiB fetched + 56 KiB written per launch (profiles/
+# qmv_rs_gate_m1_traffic.txt).  Re-measure when the kernel changes.
+TRAFFIC_GATE = 33_709_700
 
 
 def qmv_bytes(M, N, K, bits, gs):
@@ -59,6 +69,7 @@ def randn_bf16(shape, seed):
 
 
 def timed(fn, iters, warmup):
+    """ms per call of fn(i), HIP events on the current stream around `iters` calls."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
@@ -70,12 +81,38 @@ def timed(fn, iters, warmup):
         fn(i)
     t1.record(stream)
     torch.cuda.synchronize()
-    return t0.elapsed_time(t1) / iters  # ms per call of fn
+    return t0.elapsed_time(t1) / iters
+
+
+def capture(fn):
+    """HIP graph of fn() (launches only).  The library keeps scratch per
+    (device, stream), so the warm-up runs on the stream that is captured."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def timed_graphs(graphs, iters, warmup):
+    """ms per replay, replaying graphs[i % len(graphs)] for i < iters."""
+    return timed(lambda i: graphs[i % len(graphs)].replay(), iters, warmup)
 
 
 # ---- headline: MLP decode step ----------------------------------------------
 
 def headline(steps, warmup, layers=8):
+    """One step = gate, up and down of one layer; steps rotate over `layers`
+    layers so every launch streams its weights from HBM.  Each layer's step is
+    one HIP graph (three kernel launches), so the timed region holds only GPU
+    work.  Returns (GB/s, ms per step, avg us per launch, bytes per launch,
+    gate us per launch, one gate matrix)."""
     K1, N1 = 4096, 14336
     mlp = []
     for l in range(layers):
@@ -89,18 +126,27 @@ def headline(steps, warmup, layers=8):
     out_u = torch.empty_like(out_g)
     out_d = torch.empty(1, K1, dtype=torch.bfloat16, device="cuda")
 
-    def step(i):
-        gate, up, down = mlp[i % layers]
-        mq.quantized_matmul(x, *gate, True, 64, 4, out=out_g)
-        mq.quantized_matmul(x, *up, True, 64, 4, out=out_u)
-        mq.quantized_matmul(h, *down, True, 64, 4, out=out_d)
+    def step_fn(l):
+        gate, up, down = mlp[l]
 
-    ms = timed(step, steps, warmup)
+        def f():
+            mq.quantized_matmul(x, *gate, True, 64, 4, out=out_g)
+            mq.quantized_matmul(x, *up, True, 64, 4, out=out_u)
+            mq.quantized_matmul(h, *down, True, 64, 4, out=out_d)
+        return f
+
+    graphs = [capture(step_fn(l)) for l in range(layers)]
+    ms = timed_graphs(graphs, steps, warmup)
     per_launch = qmv_bytes(1, N1, K1, 4, 64)
     assert per_launch == qmv_bytes(1, K1, N1, 4, 64) == 33_067_008
     value = 3 * per_launch / (ms * 1e-3) / 1e9
-    launch_us = ms * 1e3 / 3
-    return value, ms, launch_us, per_launch, mlp[0][0]
+    # the dominant kernel alone: the gate projection (row-streaming qmv), one
+    # graph of `layers` back-to-back launches over distinct weights, timed on
+    # the replay stream (kernel-trace shows no gap between these launches)
+    gate_graph = capture(lambda: [mq.quantized_matmul(x, *mlp[l][0], True, 64, 4, out=out_g) for l in range(layers)])
+    reps = max(1, steps // layers)
+    gate_us = timed_graphs([gate_graph], reps, max(1, warmup // layers)) * 1e3 / layers
+    return value, ms, ms * 1e3 / 3, per_launch, gate_us, mlp[0][0]
 
 
 # ---- extras -------------------------------------------------------------------
@@ -114,6 +160,8 @@ def copy_ceiling():
 
 
 def qmv_sweep(iters=200):
+    """Decode sweep: M in {1,2,4,8} x {4,8}-bit at the
+    Llama-3-8B MLP shapes; one graph launches every weight copy once."""
     res = []
     for bits in (4, 8):
         for (N, K, name) in ((14336, 4096, "gate_up"), (4096, 14336, "down")):
@@ -123,11 +171,33 @@ def qmv_sweep(iters=200):
             for M in (1, 2, 4, 8):
                 x = randn_bf16((M, K), 9)
                 out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
-                ms = timed(lambda i: mq.quantized_matmul(x, *ws[i % copies], True, 64, bits, out=out), iters, 20)
+                g = capture(lambda: [mq.quantized_matmul(x, *w, True, 64, bits, out=out) for w in ws])
+                ms = timed_graphs([g], max(1, iters // copies), 2) / copies
                 b = qmv_bytes(M, N, K, bits, 64)
                 res.append({"bits": bits, "shape": name, "N": N, "K": K, "M": M, "us": round(ms * 1e3, 2),
                             "GBps": round(b / (ms * 1e-3) / 1e9, 1),
                             "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)})
+                del g
+            del ws
+    return res
+
+
+def qmm_prefill(iters=20):
+    """Prefill GEMM: M in {512, 2048}, 4/8-bit, the
+    Llama-3-8B gate/up and down shapes; TFLOPS = 2 M N K / time."""
+    res = []
+    for bits in (4, 8):
+        for (N, K, name) in ((14336, 4096, "gate_up"), (4096, 14336, "down")):
+            ws = [make_affine(N, K, bits, 64, 80 + c) for c in range(3)]
+            for M in (512, 2048):
+                x = randn_bf16((M, K), 13)
+                out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+                g = capture(lambda: [mq.quantized_matmul(x, *w, True, 64, bits, out=out) for w in ws])
+                ms = timed_graphs([g], max(1, iters // len(ws)), 1) / len(ws)
+                tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+                res.append({"bits": bits, "shape": name, "M": M, "N": N, "K": K, "us": round(ms * 1e3, 1),
+                            "TFLOPS": round(tf, 1), "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 3)})
+                del g
             del ws
     return res
 
@@ -167,7 +237,8 @@ def gather_moe(iters=100):
                 mq.gather_qmm(x, *gu[c], None, None, rhs[s], True, 32, 4, "mxfp4")
                 mq.gather_qmm(hidden, *dn[c], None, None, rhs[s], True, 32, 4, "mxfp4")
 
-        ms = timed(step, iters, 5)
+        graphs = [capture(lambda j=j: step(j)) for j in range(nsets)]
+        ms = timed_graphs(graphs, iters, 5)
         avg_touched = float(np.mean(touched))
         b = avg_touched * per_expert + T * H * 2 + T * 4 * I2 * 2 + T * 4 * H * 2 * 2
         res.append({"T": T, "sorted": sorted_mode, "experts_touched": round(avg_touched, 2), "us": round(ms * 1e3, 2),
@@ -199,6 +270,26 @@ def cpu_baseline(gate, budget_s=10.0):
                       f"{per * 1e3:.1f} ms/call, oracle restatement of MLX CPU _qmm_t (scalar, 1 thread)"}
 
 
+def traffic_probe():
+    """Dispatches whose HBM counters calibrate and measure traffic: a device
+    copy of exactly 256 MiB (reads 256 MiB, writes 256 MiB), then the gate
+    projection over 5 distinct weight sets (33,067,008 algorithmic bytes each)."""
+    n = 256 << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    gates = [make_affine(14336, 4096, 4, 64, 2000 + c) for c in range(5)]
+    x = randn_bf16((1, 4096), 7)
+    out = torch.empty(1, 14336, dtype=torch.bfloat16, device="cuda")
+    torch.cuda.synchronize()
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    for g in gates:
+        mq.quantized_matmul(x, *g, True, 64, 4, out=out)
+    torch.cuda.synchronize()
+    print(json.dumps({"traffic_probe": {"copy_bytes": n, "gate_algorithmic_bytes": qmv_bytes(1, 14336, 4096, 4, 64)}}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -206,6 +297,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run 5 copies of 256 MiB and 5 gate launches, eager, for rocprofv3 --pmc")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build runs the quantized-matmul kernels on a single "
@@ -214,9 +307,12 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
     mq.load_library()
+    if args.traffic_probe:
+        traffic_probe()
+        return
 
-    value, ms, launch_us, per_launch, gate = headline(args.steps, args.warmup)
-    achieved = per_launch / (launch_us * 1e-6) / 1e9
+    value, ms, launch_us, per_launch, gate_us, gate = headline(args.steps, args.warmup)
+    achieved = per_launch / (gate_us * 1e-6) / 1e9
     line = {
         "metric": "qmv HBM GB/s at M=1 (4-bit affine g64, Llama-3-8B MLP decode projections)",
         "value": round(value, 1),
@@ -232,15 +328,16 @@ def main():
         "data": "synthetic: x ~ N(0,1) bf16, W ~ N(0,0.02) bf16 quantized MLX-style (affine 4-bit, g64)",
         "config": {"workload": "llama3-8b MLP decode qmv: gate+up (N=14336,K=4096) + down (N=4096,K=14336), M=1",
                    "bits": 4, "group_size": 64, "M": 1, "layers_rotated": 8,
-                   "bytes_per_step": 3 * per_launch},
+                   "bytes_per_step": 3 * per_launch, "avg_us_per_launch": round(launch_us, 3)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "qmv_kernel<AFF4,64,1,4,8>", "bytes_per_launch": per_launch,
-                     "avg_launch_us": round(launch_us, 3)},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_GATE,
+                     "kernel": "qmv_rs_kernel<AFF4,1,8,1> (gate, N=14336 K=4096 M=1)",
+                     "bytes_per_launch": per_launch, "avg_launch_us": round(gate_us, 3)},
     }
     if not args.no_extra:
         extra = {"copy_ceiling_GBps": round(copy_ceiling(), 1)}
         extra["qmv_sweep"] = qmv_sweep()
+        extra["qmm_prefill"] = qmm_prefill()
         extra["gather_mxfp4_moe"] = gather_moe()
         line["extra"] = extra
     if not args.no_cpu:

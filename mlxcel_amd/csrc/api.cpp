@@ -645,6 +645,32 @@ mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w, cons
     const int fmt = fmt_of(sp.mode, sp.bits);
     const int cap = mlxq::qmv_max_rows(fmt, sp.gs);
     View wv{w}, xv{x};
+    if (wv.ndim() == 2 && rows_total >= env_int("MLXQ_QMM_MIN_ROWS", 65)) {
+      // prefill: one GEMM over all rows (every leading dim of x folds into rows)
+      const int dev = current_device();
+      const mlxq::QmmPlan qp = mlxq::qmm_plan(fmt, sp.gs, rows_total, sp.N, sp.K, device_info(dev).cus);
+      if (qp.ok) {
+        mlxq::QmmArgs q{};
+        q.x = a.x;
+        q.w = a.w;
+        q.scales = a.scales;
+        q.biases = a.biases;
+        q.out = a.out;
+        q.M = (int)rows_total;
+        q.N = (int)sp.N;
+        q.K = (int)sp.K;
+        int shift = 0;
+        while ((1 << shift) < sp.gs) shift++;
+        q.gs_shift = shift;
+        q.ksplit = qp.ksplit;
+        q.ksteps_per_split = qp.ksteps_per_split;
+        if (qp.ksplit > 1)
+          q.ws = reinterpret_cast<float*>(
+              workspace(dev, stream, (size_t)qp.ksplit * rows_total * sp.N * sizeof(float)).data);
+        hip_check(mlxq::qmm_launch(fmt, q, qp, stream), "qmm launch");
+        return;
+      }
+    }
     if (wv.ndim() == 2) {
       // every leading dim of x folds into rows (qmm.hip:3606-3620 does the same fold)
       a.E = 1;

@@ -86,6 +86,29 @@ struct QmvFrPlan {
 QmvFrPlan qmv_fr_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int r_req);
 hipError_t qmv_fr_launch(int fmt, int gs, const QmvArgs& a, int nseg, const QmvFrPlan& p, hipStream_t stream);
 
+// Prefill GEMM (qmm.hip): y[M, N] = x[M, K] @ dequant(w)[N, K]^T, 256 x 128
+// output tiles, K split across workgroups when the grid is short.
+struct QmmArgs {
+  const uint16_t* x;       // bf16 [M, K]
+  const uint32_t* w;       // packed codes [N, K*bits/32]
+  const void* scales;      // bf16 or e8m0 [N, K/gs]
+  const uint16_t* biases;  // bf16 [N, K/gs] (affine)
+  uint16_t* out;           // bf16 [M, N]
+  float* ws;               // fp32 partials [ksplit, M, N] when ksplit > 1
+  int M, N, K;
+  int gs_shift;            // log2(group size)
+  int ksplit;              // workgroups along K
+  int ksteps_per_split;    // 64-wide K-steps per workgroup
+};
+struct QmmPlan {
+  bool ok = false;
+  int tiles_n = 1, tiles_m = 1, ksplit = 1, ksteps_per_split = 1;
+};
+QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus);
+hipError_t qmm_launch(int fmt, const QmmArgs& a, const QmmPlan& p, hipStream_t stream);
+// out[i] = bf16(sum over z < ks of ws[z * n + i]) (qmv.hip)
+hipError_t launch_splitk_reduce(const float* ws, uint16_t* out, int64_t n, int ks, hipStream_t stream);
+
 // Elementwise conversions (dequant.hip).
 hipError_t launch_affine_dequantize(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                                     uint16_t* out, int64_t rows, int64_t K, int gs, int bits,

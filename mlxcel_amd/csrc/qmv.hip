@@ -398,6 +398,11 @@ __global__ __launch_bounds__(256) void qmv_splitk_reduce(const float* __restrict
   out[i] = (uint16_t)f32_to_bf16_bits(y);
 }
 
+hipError_t launch_splitk_reduce(const float* ws, uint16_t* out, int64_t n, int ks, hipStream_t stream) {
+  hipLaunchKernelGGL(qmv_splitk_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, ws, out, n, ks);
+  return hipGetLastError();
+}
+
 // ---- gather index preparation ----------------------------------------------
 
 __device__ __forceinline__ int64_t load_index(const void* p, int dtype, int64_t loc) {

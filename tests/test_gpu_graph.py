@@ -1,0 +1,101 @@
+"""HIP-graph capture of the hot path: the C-ABI entry points launch only
+kernels on the caller's stream (no allocation, synchronisation or memset once
+the workspace exists), so a captured quantized_matmul / gather_qmm replays
+the same bits.  Each graph is replayed several times with eager work and
+synchronisations in between, and every replay is compared with the eager
+result bitwise.
+"""
+import numpy as np
+import pytest
+import torch
+
+import mlxcel_amd as mq
+import oracle as orc
+from helpers import TOL, affine_case, announce, dev_bf16, dev_u32, dev_u8, host_u16, max_rel, mxfp4_case
+
+pytestmark = pytest.mark.gpu
+
+
+def capture(fn):
+    # The library keeps its scratch per (device, stream): warm up on the
+    # stream that is then captured, so the capture itself allocates nothing.
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        fn()
+    return g
+
+
+def replay_and_check(g, out, want_u16, other_work):
+    for rep in range(3):
+        out.zero_()
+        other_work()  # eager work on the same device between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(host_u16(out), want_u16, err_msg=f"replay {rep}")
+
+
+@pytest.mark.parametrize("kernel,M", [("rs", 1), ("rs", 2), ("fr", 1), ("mfma", 1), ("mfma", 8)])
+def test_quantized_matmul_graph(monkeypatch, kernel, M):
+    monkeypatch.setenv("MLXQ_QMV_KERNEL", kernel)
+    announce("graph_qmm", kernel, M)
+    N, K = 1024, 4096
+    x, wq, s, b = affine_case(M, N, K, 64, 4, 1200 + M)
+    X, W, S, B = dev_bf16(x), dev_u32(wq), dev_bf16(s), dev_bf16(b)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    eager = host_u16(mq.quantized_matmul(X, W, S, B, True, 64, 4))
+    assert max_rel(eager, orc.qmm_t_affine(x, wq, s, b, 64, 4)) <= TOL
+    g = capture(lambda: mq.quantized_matmul(X, W, S, B, True, 64, 4, out=out))
+    junk = torch.randn(1 << 20, device="cuda")
+    replay_and_check(g, out, eager, lambda: junk.mul_(1.0001))
+
+
+def test_prefill_qmm_graph_with_split_k():
+    # the prefill GEMM with K split across workgroups uses the stream's scratch
+    announce("graph_qmm_prefill")
+    M, N, K = 256, 256, 8192
+    x, wq, s, b = affine_case(M, N, K, 64, 4, 1250)
+    X, W, S, B = dev_bf16(x), dev_u32(wq), dev_bf16(s), dev_bf16(b)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    eager = host_u16(mq.quantized_matmul(X, W, S, B, True, 64, 4))
+    g = capture(lambda: mq.quantized_matmul(X, W, S, B, True, 64, 4, out=out))
+    junk = torch.randn(1 << 20, device="cuda")
+    replay_and_check(g, out, eager, lambda: junk.mul_(0.999))
+
+
+def test_gather_qmm_graph():
+    announce("graph_gather")
+    E, N, K, T = 8, 576, 2880, 2
+    x = orc.normal_bf16((T, 1, 1, K), 1.0, 1300)
+    w = orc.normal_bf16((E, N, K), 0.02, 1301)
+    wq, sc = orc.mxfp4_quantize(w)
+    ids = np.array([[3, 0, 7, 5], [1, 3, 6, 2]], np.int32)
+    X, W, S, I = dev_bf16(x), dev_u32(wq), dev_u8(sc), torch.from_numpy(ids).cuda()
+    out = torch.empty(T, 4, 1, N, dtype=torch.bfloat16, device="cuda")
+    eager = host_u16(mq.gather_qmm(X, W, S, None, None, I, True, 32, 4, "mxfp4"))
+    g = capture(lambda: mq.gather_qmm(X, W, S, None, None, I, True, 32, 4, "mxfp4", out=out))
+    junk = torch.randn(1 << 20, device="cuda")
+    replay_and_check(g, out, eager, lambda: junk.add_(1.0))
+
+
+def test_graph_sees_new_inputs_in_place():
+    # a replay reads the captured buffers' current contents
+    announce("graph_inplace")
+    N, K = 512, 2048
+    x1, wq, s, b = affine_case(1, N, K, 64, 4, 1400)
+    x2 = orc.normal_bf16((1, K), 1.0, 1401)
+    X, W, S, B = dev_bf16(x1), dev_u32(wq), dev_bf16(s), dev_bf16(b)
+    out = torch.empty(1, N, dtype=torch.bfloat16, device="cuda")
+    g = capture(lambda: mq.quantized_matmul(X, W, S, B, True, 64, 4, out=out))
+    X.copy_(dev_bf16(x2))
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    want = host_u16(mq.quantized_matmul(dev_bf16(x2), W, S, B, True, 64, 4))
+    np.testing.assert_array_equal(host_u16(out), want)

@@ -1,0 +1,77 @@
+"""GPU parity of the prefill GEMM (qmm.hip): quantized_matmul with more than
+64 activation rows, against the oracle's restatement of MLX's `_qmm_t` /
+`fp_qmm_t` (overlays/cpu/mlx/backend/cpu/quantized.cpp:199-257, 550-597) at
+sizes the oracle finishes in seconds, and at the full Llama-3-8B prefill
+shapes against a float32 torch product of the
+bit-exact dequantized weights.  max|y - y_ref| / max|y_ref| <= 1e-2.
+"""
+import numpy as np
+import pytest
+import torch
+
+import mlxcel_amd as mq
+import oracle as orc
+from helpers import TOL, affine_case, announce, dev_bf16, dev_u32, dev_u8, host_u16, max_rel, mxfp4_case
+
+pytestmark = pytest.mark.gpu
+
+
+def run(x, wq, s, b, gs, bits):
+    y = mq.quantized_matmul(dev_bf16(x), dev_u32(wq), dev_bf16(s), dev_bf16(b), True, gs, bits)
+    torch.cuda.synchronize()
+    return host_u16(y)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("M,N,K", [(65, 200, 1024), (300, 136, 2048), (512, 384, 512)])
+def test_affine_qmm_vs_oracle(bits, gs, M, N, K):
+    announce("qmm_affine", bits, gs, M, N, K)
+    x, wq, s, b = affine_case(M, N, K, gs, bits, 2100 + M + N + bits + gs)
+    assert max_rel(run(x, wq, s, b, gs, bits), orc.qmm_t_affine(x, wq, s, b, gs, bits)) <= TOL
+
+
+def test_affine_qmm_split_k_and_batch_fold():
+    # few output tiles and a long K: the K range is split across workgroups;
+    # x given as [2, 128, K] folds into 256 rows
+    announce("qmm_splitk")
+    M, N, K = 256, 256, 8192
+    x, wq, s, b = affine_case(M, N, K, 64, 4, 2201)
+    y = mq.quantized_matmul(dev_bf16(x).reshape(2, 128, K), dev_u32(wq), dev_bf16(s), dev_bf16(b))
+    got = host_u16(y).reshape(M, N)
+    assert max_rel(got, orc.qmm_t_affine(x, wq, s, b, 64, 4)) <= TOL
+    again = host_u16(mq.quantized_matmul(dev_bf16(x).reshape(2, 128, K), dev_u32(wq), dev_bf16(s),
+                                         dev_bf16(b))).reshape(M, N)
+    np.testing.assert_array_equal(got, again)
+
+
+def test_mxfp4_qmm_vs_oracle():
+    announce("qmm_mxfp4")
+    M, N, K = 192, 576, 2880
+    x, wq, sc = mxfp4_case(M, N, K, 2301)
+    got = host_u16(mq.quantized_matmul(dev_bf16(x), dev_u32(wq), dev_u8(sc), None, True, 32, 4, "mxfp4"))
+    assert max_rel(got, orc.fp_qmm_t_mxfp4(x, wq, sc)) <= TOL
+
+
+def test_k_not_multiple_of_64_uses_row_segments():
+    announce("qmm_fallback_k")
+    M, N, K = 96, 128, 2592
+    x, wq, s, b = affine_case(M, N, K, 32, 4, 2401)
+    assert max_rel(run(x, wq, s, b, 32, 4), orc.qmm_t_affine(x, wq, s, b, 32, 4)) <= TOL
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M", [512, 2048])
+@pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336)])
+def test_llama_prefill_shapes_vs_dequant_fp32(bits, M, N, K):
+    # full size: reference = float32 product of the bit-exact dequantized weights
+    announce("qmm_llama", bits, M, N, K)
+    g = torch.Generator(device="cuda").manual_seed(2500 + M + N + bits)
+    w = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    wq, s, b = mq.quantize(w, 64, bits)
+    wd = mq.dequantize(wq, s, b, 64, bits).float()
+    y = mq.quantized_matmul(x, wq, s, b, True, 64, bits).float()
+    ref = x.float() @ wd.t()
+    err = float((y - ref).abs().max() / ref.abs().max())
+    assert err <= TOL, err
