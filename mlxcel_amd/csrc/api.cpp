@@ -648,7 +648,9 @@ mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w, cons
     if (wv.ndim() == 2 && rows_total >= env_int("MLXQ_QMM_MIN_ROWS", 65)) {
       // prefill: one GEMM over all rows (every leading dim of x folds into rows)
       const int dev = current_device();
-      const mlxq::QmmPlan qp = mlxq::qmm_plan(fmt, sp.gs, rows_total, sp.N, sp.K, device_info(dev).cus);
+      // MLXQ_QMM_TILE / MLXQ_QMM_KSPLIT: A/B overrides of the tile shape and K split
+      const mlxq::QmmPlan qp = mlxq::qmm_plan(fmt, sp.gs, rows_total, sp.N, sp.K, device_info(dev).cus,
+                                              env_int("MLXQ_QMM_TILE", -1), env_int("MLXQ_QMM_KSPLIT", 0));
       if (qp.ok) {
         mlxq::QmmArgs q{};
         q.x = a.x;
@@ -657,6 +659,7 @@ mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w, cons
         q.biases = a.biases;
         q.out = a.out;
         q.M = (int)rows_total;
+        q.x_rows = (int)rows_total;
         q.N = (int)sp.N;
         q.K = (int)sp.K;
         int shift = 0;
@@ -787,6 +790,110 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq
 
     const int dev = current_device();
     const DevInfo di = device_info(dev);
+
+    // Many rows per expert (MoE prefill, large batches): group rows by expert
+    // on the device, then one GEMM tile reads each expert's weights once per
+    // tile of rows (qmm.hip), instead of once per index entry.  Auto when the
+    // entries average >= 8 rows per touched expert; MLXQ_GATHER_GROUP=0|1
+    // forces the choice (A/B switch for tests).
+    const int grp_env = env_int("MLXQ_GATHER_GROUP", -1);
+    const int64_t rows = B * M;
+    const bool want_group = grp_env == 1 || (grp_env != 0 && rows >= 8 * std::min<int64_t>(E, B));
+    if (E <= mlxq::kGroupMaxExperts && want_group) {
+      const int64_t per_expert = rows / std::max<int64_t>(1, std::min<int64_t>(E, B));
+      const mlxq::QmmPlan qp =
+          mlxq::qmm_plan_grouped(fmt, sp.gs, sp.N, sp.K, per_expert <= 64 ? 3 : (per_expert <= 128 ? 2 : 0));
+      const bool use_qmm = qp.ok && X * M * sp.K * 2 < ((int64_t)1 << 31);
+      // K not a multiple of 64: the MFMA skinny kernel over the same grouping
+      const int cap_rows = use_qmm ? qp.rows_per_tile : (int)std::min<int64_t>(cap, rows);
+      const int64_t maxseg = rows / cap_rows + std::min<int64_t>(E, B) + 1;
+      if (maxseg > 65535) unsupported("gather_qmm: too many expert segments for one launch");
+      mlxq::QmvPlan p;
+      if (!use_qmm) {
+        int nw, pf;
+        qmv_shape_choice(sp.N, sp.K, nw, pf);
+        p = mlxq::qmv_plan(fmt, sp.gs, sp.N, sp.K, cap_rows, (int)maxseg, di.cus, nw, pf);
+        if (p.lds > mlxq::kQmvLdsMax) unsupported("gather_qmm: activation tile does not fit in LDS");
+      }
+      auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+      const size_t o_x = al((size_t)B * 2 * sizeof(uint32_t));
+      const size_t o_o = o_x + al((size_t)rows * sizeof(uint32_t));
+      const size_t o_seg = o_o + al((size_t)rows * sizeof(uint32_t));
+      const size_t o_n = o_seg + al((size_t)maxseg * 3 * sizeof(uint32_t));
+      const size_t o_part = o_n + 256;
+      const size_t part = (!use_qmm && p.ks > 1) ? (size_t)p.ks * rows * sp.N * sizeof(float) : 0;
+      Workspace& ws = workspace(dev, stream, o_part + part);
+      char* base = static_cast<char*>(ws.data);
+      uint32_t* flat = reinterpret_cast<uint32_t*>(base);
+      ip.out[0] = flat;
+      ip.out[1] = flat + B;
+      hip_check(mlxq::launch_index_prep(ip, stream), "index_prep launch");
+      mlxq::GroupArgs ga{};
+      ga.lhs = flat;
+      ga.rhs = flat + B;
+      ga.B = (int)B;
+      ga.M = (int)M;
+      ga.E = (int)E;
+      ga.cap = cap_rows;
+      ga.xrows = reinterpret_cast<uint32_t*>(base + o_x);
+      ga.orows = reinterpret_cast<uint32_t*>(base + o_o);
+      ga.seg = reinterpret_cast<uint32_t*>(base + o_seg);
+      ga.nseg = reinterpret_cast<uint32_t*>(base + o_n);
+      hip_check(mlxq::launch_group_by_expert(ga, stream), "group launch");
+      if (use_qmm) {
+        mlxq::QmmArgs q{};
+        q.x = static_cast<const uint16_t*>(x->data);
+        q.w = static_cast<const uint32_t*>(w->data);
+        q.scales = scales->data;
+        q.biases = biases ? static_cast<const uint16_t*>(biases->data) : nullptr;
+        q.out = static_cast<uint16_t*>(out->data);
+        q.M = (int)rows;
+        q.x_rows = (int)(X * M);
+        q.N = (int)sp.N;
+        q.K = (int)sp.K;
+        int shift = 0;
+        while ((1 << shift) < sp.gs) shift++;
+        q.gs_shift = shift;
+        q.ksplit = 1;
+        q.ksteps_per_split = qp.ksteps_per_split;
+        q.seg = ga.seg;
+        q.nseg_dev = ga.nseg;
+        q.xrows = ga.xrows;
+        q.orows = ga.orows;
+        q.w_expert_stride = wv.dim(-2) * wv.dim(-1);
+        q.s_expert_stride = sv.dim(-2) * sv.dim(-1);
+        mlxq::QmmPlan gp = qp;
+        gp.tiles_m = (int)maxseg;
+        hip_check(mlxq::qmm_launch(fmt, q, gp, stream), "gather qmm launch");
+        return;
+      }
+      mlxq::QmvArgs a{};
+      a.x = static_cast<const uint16_t*>(x->data);
+      a.w = static_cast<const uint32_t*>(w->data);
+      a.scales = scales->data;
+      a.biases = biases ? static_cast<const uint16_t*>(biases->data) : nullptr;
+      a.out = static_cast<uint16_t*>(out->data);
+      a.N = (int)sp.N;
+      a.K = (int)sp.K;
+      a.E = (int)E;
+      a.X = (int)X;
+      a.w_expert_stride = wv.dim(-2) * wv.dim(-1);
+      a.s_expert_stride = sv.dim(-2) * sv.dim(-1);
+      a.rps = cap_rows;
+      a.total_rows = (int)rows;
+      a.out_rows = (int)rows;
+      a.rows_lds = cap_rows;
+      a.ks = p.ks;
+      a.kst_per_wg = p.kst_per_wg;
+      if (p.ks > 1) a.ws = reinterpret_cast<float*>(base + o_part);
+      a.seg = ga.seg;
+      a.nseg_dev = ga.nseg;
+      a.xrows = ga.xrows;
+      a.orows = ga.orows;
+      hip_check(mlxq::qmv_launch(fmt, sp.gs, a, (int)maxseg, p, stream), "gather qmv launch");
+      return;
+    }
+
     const Skinny kind = skinny_choice((int)M);
     const int r_req = env_int("MLXQ_QMV_R", 0);
     const mlxq::QmvFrPlan fp =

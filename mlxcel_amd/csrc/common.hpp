@@ -84,6 +84,16 @@ __device__ __forceinline__ void unpack_mxfp4(uint32_t w, uint32_t (&v)[4]) {
   v[3] = __builtin_bit_cast(uint32_t, p3);
 }
 
+// MXFP4 with its e8m0 scale folded in: v[h] = (code 2h, code 2h+1) * scale as
+// bf16, for a normal power-of-two scale (exact: the products are fp4 code
+// points times 2^k).
+__device__ __forceinline__ void unpack_mxfp4_scaled(uint32_t w, float scale, uint32_t* v) {
+  v[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0));
+  v[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1));
+  v[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2));
+  v[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3));
+}
+
 // AFF8: two words = 8 byte codes -> 8 bf16 (exact: codes are < 256), natural
 // order.  The f32 of a byte has a zero low half, so its bf16 is the high half;
 // v_perm_b32 gathers the two high halves in one instruction.

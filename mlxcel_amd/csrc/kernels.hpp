@@ -34,6 +34,12 @@ struct QmvArgs {
   int rows_lds;             // activation rows staged per workgroup (>= rows of any segment)
   int ks;                   // workgroups splitting K (gridDim.z)
   int kst_per_wg;           // K-steps per workgroup
+  // Gathers grouped by expert (qmv.hip MFMA kernel only): segment table and
+  // per-row indirection built by launch_group_by_expert; null otherwise.
+  const uint32_t* seg;      // [max segments][3] = {expert, first grouped row, rows}
+  const uint32_t* nseg_dev; // segments in the table
+  const uint32_t* xrows;    // grouped row -> x row (flattened over x's batch)
+  const uint32_t* orows;    // grouped row -> output row
 };
 
 struct QmvPlan {
@@ -99,12 +105,27 @@ struct QmmArgs {
   int gs_shift;            // log2(group size)
   int ksplit;              // workgroups along K
   int ksteps_per_split;    // 64-wide K-steps per workgroup
+  int x_rows;              // rows of x addressable (bounds of the x buffer)
+  // Gathers grouped by expert: segment table / row indirection from
+  // launch_group_by_expert (segments of at most the tile's rows) and the
+  // per-expert strides of w (uint32 words) and scales/biases (elements).
+  const uint32_t* seg;
+  const uint32_t* nseg_dev;
+  const uint32_t* xrows;
+  const uint32_t* orows;
+  int64_t w_expert_stride;
+  int64_t s_expert_stride;
 };
 struct QmmPlan {
   bool ok = false;
+  int tile = 0;  // 0: 256 x 128, 1: 256 x 256, 2: 128 x 128, 3: 64 x 128 output tiles
+  int rows_per_tile = 256;
   int tiles_n = 1, tiles_m = 1, ksplit = 1, ksteps_per_split = 1;
 };
-QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus);
+// Grouped gather: tiles along N for `tile`; tiles_m = segments is set by the caller.
+QmmPlan qmm_plan_grouped(int fmt, int gs, int64_t N, int64_t K, int tile);
+// tile_req / ksplit_req < 0 (or 0 for ksplit) choose by shape.
+QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus, int tile_req, int ksplit_req);
 hipError_t qmm_launch(int fmt, const QmmArgs& a, const QmmPlan& p, hipStream_t stream);
 // out[i] = bf16(sum over z < ks of ws[z * n + i]) (qmv.hip)
 hipError_t launch_splitk_reduce(const float* ws, uint16_t* out, int64_t n, int ks, hipStream_t stream);
@@ -135,5 +156,18 @@ struct IdxPrepArgs {
   uint32_t* out[2];
 };
 hipError_t launch_index_prep(const IdxPrepArgs& a, hipStream_t stream);
+
+// Groups B gather entries (flat uint32 lhs/rhs, rhs < E) by expert; see qmv.hip.
+struct GroupArgs {
+  const uint32_t* lhs;
+  const uint32_t* rhs;
+  int B, M, E, cap;
+  uint32_t* xrows;  // [B*M]
+  uint32_t* orows;  // [B*M]
+  uint32_t* seg;    // [B*M/cap + min(E, B) + 1][3]
+  uint32_t* nseg;   // [1]
+};
+constexpr int kGroupMaxExperts = 8192;  // LDS: (3 E + 1024) words
+hipError_t launch_group_by_expert(const GroupArgs& a, hipStream_t stream);
 
 }  // namespace mlxq

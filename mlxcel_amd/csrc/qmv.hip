@@ -116,10 +116,22 @@ __global__ __launch_bounds__(NW * 64) void qmv_kernel(const QmvArgs a) {
   const int sidx = blockIdx.y;
 
   // ---- segment (wave-uniform) ---------------------------------------------
-  const int count = min(a.rps, a.total_rows - sidx * a.rps);
-  if (count <= 0) return;
-  const int expert = a.rhs ? (int)min(a.rhs[sidx], (uint32_t)(a.E - 1)) : (a.w_expert_stride ? sidx : 0);
-  const int xbatch = a.lhs ? (int)min(a.lhs[sidx], (uint32_t)(a.X - 1)) : sidx;
+  // Either segment sidx of `rps` consecutive rows (batch lhs[sidx], expert
+  // rhs[sidx]), or, for gathers grouped by expert, table entry sidx: rows
+  // r0 .. r0+count-1 of the grouped order, read and written through
+  // xrows / orows.
+  int count, expert, r0 = 0, xbatch = 0;
+  if (a.seg) {
+    if (sidx >= (int)a.nseg_dev[0]) return;
+    expert = (int)a.seg[3 * sidx];
+    r0 = (int)a.seg[3 * sidx + 1];
+    count = (int)a.seg[3 * sidx + 2];
+  } else {
+    count = min(a.rps, a.total_rows - sidx * a.rps);
+    if (count <= 0) return;
+    expert = a.rhs ? (int)min(a.rhs[sidx], (uint32_t)(a.E - 1)) : (a.w_expert_stride ? sidx : 0);
+    xbatch = a.lhs ? (int)min(a.lhs[sidx], (uint32_t)(a.X - 1)) : sidx;
+  }
 
   const int N = a.N;
   const int K = a.K;
@@ -154,7 +166,8 @@ __global__ __launch_bounds__(NW * 64) void qmv_kernel(const QmvArgs a) {
     const int t = t0 + NW * i;
     const int k = t * KSTEP + piece * 8;
     const bool live = m < count && i < nst && k < K;
-    return live ? *reinterpret_cast<const u32x4*>(xrow0 + (int64_t)m * K + k) : u32x4{0u, 0u, 0u, 0u};
+    const uint16_t* xr = a.seg ? a.x + (int64_t)a.xrows[r0 + min(m, count - 1)] * K : xrow0 + (int64_t)m * K;
+    return live ? *reinterpret_cast<const u32x4*>(xr + k) : u32x4{0u, 0u, 0u, 0u};
   };
   const int nx = rows_lds * XL;
   u32x4 xv[XEARLY];
@@ -376,7 +389,7 @@ __global__ __launch_bounds__(NW * 64) void qmv_kernel(const QmvArgs a) {
       for (int sl = 0; sl < S; sl++) y += tot[u * S + sl];
       const int m = (16 * mt + 4 * lq) / S + u;
       if (m < count && n0 + lnl < N) {
-        const int64_t orow = (int64_t)sidx * a.rps + m;
+        const int64_t orow = a.seg ? (int64_t)a.orows[r0 + m] : (int64_t)sidx * a.rps + m;
         if (split) {
           a.ws[((int64_t)blockIdx.z * a.out_rows + orow) * N + n0 + lnl] = y;
         } else {
@@ -438,6 +451,93 @@ __global__ __launch_bounds__(256) void index_prep_kernel(const IdxPrepArgs a) {
 
 hipError_t launch_index_prep(const IdxPrepArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL(index_prep_kernel, dim3((unsigned)((a.B + 255) / 256)), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+// ---- gather grouping by expert (one workgroup) ------------------------------
+// Counting sort of the B index entries by expert (rhs), then segments of at
+// most `cap` rows of one expert.  Entry b contributes output rows b*M + m
+// (m < M) computed from x rows lhs[b]*M + m.  Rows of one expert are
+// contiguous in xrows/orows; their order inside the expert follows LDS
+// atomics and does not affect any result (each output row is computed on its
+// own).  seg[s] = {expert, first grouped row, rows}; nseg[0] = segment count.
+
+namespace {
+constexpr int kGroupThreads = 1024;
+
+// exclusive scan of one value per thread over the workgroup (Hillis-Steele in LDS)
+__device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* tmp) {
+  const int t = threadIdx.x;
+  tmp[t] = v;
+  __syncthreads();
+  for (int off = 1; off < kGroupThreads; off <<= 1) {
+    const uint32_t add = t >= off ? tmp[t - off] : 0u;
+    __syncthreads();
+    tmp[t] += add;
+    __syncthreads();
+  }
+  const uint32_t incl = tmp[t];
+  __syncthreads();
+  return incl - v;
+}
+}  // namespace
+
+__global__ __launch_bounds__(kGroupThreads) void group_by_expert_kernel(GroupArgs a) {
+  extern __shared__ uint32_t gsh[];
+  uint32_t* cnt = gsh;                 // [E] entries per expert
+  uint32_t* start = gsh + a.E;         // [E] first grouped entry
+  uint32_t* sstart = gsh + 2 * a.E;    // [E] first segment
+  uint32_t* tmp = gsh + 3 * a.E;       // [kGroupThreads] scan scratch
+  const int t = threadIdx.x;
+  for (int e = t; e < a.E; e += kGroupThreads) cnt[e] = 0u;
+  __syncthreads();
+  for (int b = t; b < a.B; b += kGroupThreads) atomicAdd(&cnt[a.rhs[b]], 1u);
+  __syncthreads();
+  // each thread owns a contiguous run of experts; scan the run totals
+  const int per = (a.E + kGroupThreads - 1) / kGroupThreads;
+  const int e0 = min(t * per, a.E), e1 = min(e0 + per, a.E);
+  uint32_t ent = 0, segs = 0;
+  for (int e = e0; e < e1; e++) {
+    ent += cnt[e];
+    segs += (cnt[e] * (uint32_t)a.M + (uint32_t)a.cap - 1) / (uint32_t)a.cap;
+  }
+  uint32_t ent0 = block_exclusive_scan(ent, tmp);
+  uint32_t seg0 = block_exclusive_scan(segs, tmp);
+  for (int e = e0; e < e1; e++) {
+    start[e] = ent0;
+    sstart[e] = seg0;
+    ent0 += cnt[e];
+    seg0 += (cnt[e] * (uint32_t)a.M + (uint32_t)a.cap - 1) / (uint32_t)a.cap;
+  }
+  if (t == kGroupThreads - 1) a.nseg[0] = seg0;
+  __syncthreads();
+  // segment table: expert e's rows [start*M, (start+cnt)*M) in pieces of cap
+  for (int e = t; e < a.E; e += kGroupThreads) {
+    const uint32_t rows = cnt[e] * (uint32_t)a.M;
+    const uint32_t row0 = start[e] * (uint32_t)a.M;
+    for (uint32_t j = 0, s = sstart[e]; j * (uint32_t)a.cap < rows; j++, s++) {
+      a.seg[3 * s] = (uint32_t)e;
+      a.seg[3 * s + 1] = row0 + j * (uint32_t)a.cap;
+      a.seg[3 * s + 2] = min((uint32_t)a.cap, rows - j * (uint32_t)a.cap);
+    }
+  }
+  __syncthreads();
+  // scatter rows (cnt is reused as the fill counter)
+  for (int e = t; e < a.E; e += kGroupThreads) cnt[e] = 0u;
+  __syncthreads();
+  for (int b = t; b < a.B; b += kGroupThreads) {
+    const uint32_t e = a.rhs[b];
+    const uint32_t p = start[e] + atomicAdd(&cnt[e], 1u);
+    for (int m = 0; m < a.M; m++) {
+      a.xrows[p * a.M + m] = a.lhs[b] * (uint32_t)a.M + (uint32_t)m;
+      a.orows[p * a.M + m] = (uint32_t)b * (uint32_t)a.M + (uint32_t)m;
+    }
+  }
+}
+
+hipError_t launch_group_by_expert(const GroupArgs& a, hipStream_t stream) {
+  const size_t lds = (size_t)(3 * a.E + kGroupThreads) * sizeof(uint32_t);
+  hipLaunchKernelGGL(group_by_expert_kernel, dim3(1), dim3(kGroupThreads), lds, stream, a);
   return hipGetLastError();
 }
 

@@ -106,3 +106,59 @@ def test_gather_without_indices_is_quantized_matmul():
     a = host_u16(mq.gather_qmm(dev_bf16(x), dev_u32(wq[0]), dev_bf16(s[0]), dev_bf16(b[0])))
     c = host_u16(mq.quantized_matmul(dev_bf16(x), dev_u32(wq[0]), dev_bf16(s[0]), dev_bf16(b[0])))
     np.testing.assert_array_equal(a, c)
+
+
+@pytest.mark.parametrize("K", [1024, 1056])
+@pytest.mark.parametrize("group", [0, 1])
+@pytest.mark.parametrize("E,T,M,mode", [(32, 64, 1, "mxfp4"), (8, 40, 2, "affine"), (300, 50, 1, "affine"),
+                                        (4, 16, 3, "mxfp4"), (2, 160, 1, "affine")])
+def test_grouped_by_expert_matches_stack(monkeypatch, K, group, E, T, M, mode):
+    # rows regrouped by expert on the device (MLXQ_GATHER_GROUP=1: the grouped
+    # GEMM, or the MFMA skinny kernel when K is not a multiple of 64) and
+    # per-entry segments (=0) both equal the stack of per-index matmuls
+    # (CPUQ:792-812); E=2, T=160 gives segments of more than 64 rows
+    if mode == "mxfp4" and K % 32:
+        pytest.skip("mxfp4 needs K % 32 == 0")
+    monkeypatch.setenv("MLXQ_GATHER_GROUP", str(group))
+    announce("gather_grouped", K, group, E, T, M, mode)
+    N = 264
+    rng = np.random.default_rng(1700 + E + T + M)
+    x = orc.normal_bf16((T, M, K), 1.0, 1701 + T)
+    rhs = rng.integers(0, E, size=(T, 2)).astype(np.int64)  # two experts per token, repeats likely
+    lhs = np.repeat(np.arange(T)[:, None], 2, axis=1).astype(np.int32)
+    if mode == "mxfp4":
+        wq, sc = mx_experts(E, N, K, 1702 + E)
+        got = host_u16(mq.gather_qmm(dev_bf16(x), dev_u32(wq), dev_u8(sc), None, torch.from_numpy(lhs).cuda(),
+                                     torch.from_numpy(rhs).cuda(), True, 32, 4, "mxfp4"))
+        want = orc.gather_qmm_t(x, wq, sc, None, lhs.reshape(-1).astype(np.uint32),
+                                rhs.reshape(-1).astype(np.uint32), mode="mxfp4")
+    else:
+        gs = 64 if K % 64 == 0 else 32
+        wq, s, b = affine_experts(E, N, K, 1703 + E, gs=gs)
+        got = host_u16(mq.gather_qmm(dev_bf16(x), dev_u32(wq), dev_bf16(s), dev_bf16(b),
+                                     torch.from_numpy(lhs).cuda(), torch.from_numpy(rhs).cuda(), True, gs, 4))
+        want = orc.gather_qmm_t(x, wq, s, b, lhs.reshape(-1).astype(np.uint32), rhs.reshape(-1).astype(np.uint32),
+                                group_size=gs)
+    assert got.shape == (T, 2, M, N)
+    assert max_rel(got.reshape(T * 2, M, N), want) <= TOL
+
+
+def test_grouped_gather_is_deterministic_and_matches_per_entry(monkeypatch):
+    announce("gather_grouped_det")
+    E, N, K, T = 32, 576, 2880, 256
+    wq, sc = mx_experts(E, N, K, 1800)
+    ids = topk_ids(T, E, 4, 1801).reshape(-1)
+    x = orc.normal_bf16((T, 1, K), 1.0, 1802)
+    lhs = torch.from_numpy(np.repeat(np.arange(T), 4).astype(np.int32)).cuda()
+    rhs = torch.from_numpy(ids.astype(np.int32)).cuda()
+    args = (dev_bf16(x), dev_u32(wq), dev_u8(sc), None, lhs, rhs, True, 32, 4, "mxfp4")
+    monkeypatch.setenv("MLXQ_GATHER_GROUP", "1")
+    g1 = host_u16(mq.gather_qmm(*args))
+    g2 = host_u16(mq.gather_qmm(*args))
+    np.testing.assert_array_equal(g1, g2)
+    monkeypatch.setenv("MLXQ_GATHER_GROUP", "0")
+    per_entry = host_u16(mq.gather_qmm(*args))
+    assert max_rel(g1, per_entry) <= TOL
+    want = orc.gather_qmm_t(x, wq, sc, None, np.repeat(np.arange(T), 4).astype(np.uint32), ids.astype(np.uint32),
+                            mode="mxfp4")
+    assert max_rel(g1.reshape(T * 4, 1, N), want) <= TOL

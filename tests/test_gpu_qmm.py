@@ -22,19 +22,25 @@ def run(x, wq, s, b, gs, bits):
     return host_u16(y)
 
 
+@pytest.mark.parametrize("tile", [-1, 0, 1, 2])
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("gs", [32, 64, 128])
 @pytest.mark.parametrize("M,N,K", [(65, 200, 1024), (300, 136, 2048), (512, 384, 512)])
-def test_affine_qmm_vs_oracle(bits, gs, M, N, K):
-    announce("qmm_affine", bits, gs, M, N, K)
+def test_affine_qmm_vs_oracle(monkeypatch, tile, bits, gs, M, N, K):
+    # every output-tile shape (MLXQ_QMM_TILE: 256x128, 256x256, 128x128; -1 = by shape)
+    monkeypatch.setenv("MLXQ_QMM_TILE", str(tile))
+    announce("qmm_affine", tile, bits, gs, M, N, K)
     x, wq, s, b = affine_case(M, N, K, gs, bits, 2100 + M + N + bits + gs)
     assert max_rel(run(x, wq, s, b, gs, bits), orc.qmm_t_affine(x, wq, s, b, gs, bits)) <= TOL
 
 
-def test_affine_qmm_split_k_and_batch_fold():
-    # few output tiles and a long K: the K range is split across workgroups;
-    # x given as [2, 128, K] folds into 256 rows
-    announce("qmm_splitk")
+@pytest.mark.parametrize("tile,ksplit", [(-1, 0), (1, 3), (2, 5)])
+def test_affine_qmm_split_k_and_batch_fold(monkeypatch, tile, ksplit):
+    # few output tiles and a long K: the K range is split across workgroups
+    # (uneven splits included); x given as [2, 128, K] folds into 256 rows
+    monkeypatch.setenv("MLXQ_QMM_TILE", str(tile))
+    monkeypatch.setenv("MLXQ_QMM_KSPLIT", str(ksplit))
+    announce("qmm_splitk", tile, ksplit)
     M, N, K = 256, 256, 8192
     x, wq, s, b = affine_case(M, N, K, 64, 4, 2201)
     y = mq.quantized_matmul(dev_bf16(x).reshape(2, 128, K), dev_u32(wq), dev_bf16(s), dev_bf16(b))
@@ -45,8 +51,10 @@ def test_affine_qmm_split_k_and_batch_fold():
     np.testing.assert_array_equal(got, again)
 
 
-def test_mxfp4_qmm_vs_oracle():
-    announce("qmm_mxfp4")
+@pytest.mark.parametrize("tile", [0, 1, 2])
+def test_mxfp4_qmm_vs_oracle(monkeypatch, tile):
+    monkeypatch.setenv("MLXQ_QMM_TILE", str(tile))
+    announce("qmm_mxfp4", tile)
     M, N, K = 192, 576, 2880
     x, wq, sc = mxfp4_case(M, N, K, 2301)
     got = host_u16(mq.quantized_matmul(dev_bf16(x), dev_u32(wq), dev_u8(sc), None, True, 32, 4, "mxfp4"))
