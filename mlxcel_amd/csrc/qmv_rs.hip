@@ -75,12 +75,16 @@ constexpr int log2i(int v) { return v <= 1 ? 0 : 1 + log2i(v / 2); }
 
 }  // namespace
 
-// LDS bytes of one workgroup: the tile's scales (G groups x R rows, row
-// fastest; (scale, bias - 128 scale | bias) fp32 pairs for affine, scale fp32
-// for mxfp4) and the reduction buffer (NW waves x 4 lane rows x R*MR partials).
-__host__ __device__ inline uint32_t qmv_rs_lds(int fmt, int r, int mr, int nw, int64_t G) {
-  const uint32_t sb = (uint32_t)(r * G * (fmt != MXFP4 ? 8 : 4));
-  return ((sb + 15u) & ~15u) + (uint32_t)(nw * 4 * r * mr * 4);
+// LDS bytes of one workgroup: per wave, the scales of its chunks
+// (CPW x groups-per-chunk x R rows, row fastest; (scale, bias - 128 scale |
+// bias) fp32 pairs for affine, scale fp32 for mxfp4), then the reduction
+// buffer (NW waves x 4 lane rows x R*MR partials).
+__host__ __device__ inline uint32_t qmv_rs_wave_lds(int fmt, int r, int cpw, int gs) {
+  const int kl = fmt == AFF8 ? 16 : 32;
+  return (uint32_t)(cpw * (64 * kl / gs) * r * (fmt != MXFP4 ? 8 : 4));
+}
+__host__ __device__ inline uint32_t qmv_rs_lds(int fmt, int r, int mr, int nw, int cpw, int gs) {
+  return (uint32_t)nw * qmv_rs_wave_lds(fmt, r, cpw, gs) + (uint32_t)(nw * 4 * r * mr * 4);
 }
 
 namespace {
@@ -114,7 +118,7 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
   constexpr int LR = log2i(R);
   constexpr int VC = V >= 16 ? V / 16 : 1;  // partials per lane after the row butterfly
   constexpr int VQ = V >= 16 ? 1 : 16 / V;  // lanes per partial after it
-  constexpr int SBE = 4;                    // scale loads per thread issued before the weights
+  constexpr int SBE = 4;                    // scale loads per lane issued before the weights (at most)
   constexpr int ESZ = AFF ? 2 : 1;          // bytes per stored scale
 
   extern __shared__ __align__(16) unsigned char smem[];
@@ -137,8 +141,9 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
   const int nlc = K / KL;  // lane chunks per row
   const uint32_t RB = (uint32_t)nlc * 16u;  // bytes per weight row
   const int G = K >> gs_shift;
-  float* sbl = reinterpret_cast<float*>(smem);
-  float* red = reinterpret_cast<float*>(smem + ((R * G * (AFF ? 8 : 4) + 15) & ~15));
+  const int gs = 1 << gs_shift;
+  unsigned char* wsl = smem + wave * qmv_rs_wave_lds(FMT, R, CPW, gs);  // this wave's scales
+  float* red = reinterpret_cast<float*>(smem + NW * qmv_rs_wave_lds(FMT, R, CPW, gs));
 
   // Buffer resources: bounds-checked loads return 0 past the end, which
   // covers rows past N, activation rows past `count` and dead lanes.
@@ -173,34 +178,49 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
         xv[m][j][v] = __builtin_bit_cast(
             u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo[j] + (uint32_t)(m * K * 2 + v * 16), 0, 0));
 
-  // Scales of the G x R tile: thread t stages row t % R, units (of `upw`
-  // groups: one word, or one byte/short for odd rows) t / R, t / R + NT / R, ...
-  const int upw = AFF ? ((G & 1) ? 1 : 2) : ((G & 3) ? ((G & 1) ? 1 : 2) : 4);
-  const int gu = G / upw;
-  const int sr_row = threadIdx.x & (R - 1);
-  const int sj0 = threadIdx.x >> LR;
-  const int sjs = NT >> LR;
-  const uint32_t srow_off = (uint32_t)((row0 + sr_row) * G);  // in groups
-  auto load_unit = [&](int jn, uint32_t& s_, uint32_t& b_) {
-    const uint32_t og = srow_off + (uint32_t)(jn * upw);
-    if constexpr (AFF) {
-      if (upw == 2) {
-        s_ = __builtin_amdgcn_raw_buffer_load_b32(sr, og * 2u, 0, 0);
-        b_ = __builtin_amdgcn_raw_buffer_load_b32(br, og * 2u, 0, 0);
-      } else {
-        s_ = __builtin_amdgcn_raw_buffer_load_b16(sr, og * 2u, 0, 0);
-        b_ = __builtin_amdgcn_raw_buffer_load_b16(br, og * 2u, 0, 0);
-      }
-    } else {
-      s_ = upw == 4 ? __builtin_amdgcn_raw_buffer_load_b32(sr, og, 0, 0)
-                    : (upw == 2 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(sr, og, 0, 0)
-                                : (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(sr, og, 0, 0));
-      b_ = 0u;
-    }
+  // Scales of this wave's chunks: for each chunk j (groups gbase[j] ..
+  // gbase[j] + gc - 1) and row r, gc / upw units of upw groups (a word when
+  // every row starts word-aligned, else a short or byte); lane L loads units
+  // L, L + 64, ...  A wave reads only what it wrote itself, so no workgroup
+  // barrier stands between the loads and the arithmetic.
+  const int upw = AFF ? ((G & 1) ? 1 : 2) : ((G & 3) ? ((G & 1) ? 1 : 2) : 4);  // groups per unit
+  const int gc = (64 * KL) >> gs_shift;               // groups per chunk (>= 8)
+  const int upc = gc / upw;                           // units per chunk and row
+  const int lupc = __builtin_ctz((unsigned)upc);
+  const int nunits = CPW * R * upc;
+  const int nld = (nunits + 63) / 64;                 // loads per lane (uniform)
+  int gbase[CPW];
+#pragma unroll
+  for (int j = 0; j < CPW; j++) gbase[j] = ((wave + NW * j) * 64 * KL) >> gs_shift;
+  auto unit_of = [&](int u, int& j, int& r, int& gl) {
+    r = u & (R - 1);
+    const int rest = u >> LR;
+    gl = rest & (upc - 1);
+    j = min(rest >> lupc, CPW - 1);
   };
   uint32_t sraw[SBE], braw[SBE];
 #pragma unroll
-  for (int i = 0; i < SBE; i++) load_unit(sj0 + sjs * i, sraw[i], braw[i]);
+  for (int i = 0; i < SBE; i++) {
+    sraw[i] = braw[i] = 0u;
+    if (i < nld) {  // wave-uniform
+      int j, r, gl;
+      unit_of(lane + 64 * i, j, r, gl);
+      const uint32_t og = (uint32_t)((row0 + r) * G + gbase[j] + gl * upw);  // in groups
+      if constexpr (AFF) {
+        if (upw == 2) {
+          sraw[i] = __builtin_amdgcn_raw_buffer_load_b32(sr, og * 2u, 0, 0);
+          braw[i] = __builtin_amdgcn_raw_buffer_load_b32(br, og * 2u, 0, 0);
+        } else {
+          sraw[i] = __builtin_amdgcn_raw_buffer_load_b16(sr, og * 2u, 0, 0);
+          braw[i] = __builtin_amdgcn_raw_buffer_load_b16(br, og * 2u, 0, 0);
+        }
+      } else {
+        sraw[i] = upw == 4 ? __builtin_amdgcn_raw_buffer_load_b32(sr, og, 0, 0)
+                           : (upw == 2 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(sr, og, 0, 0)
+                                       : (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(sr, og, 0, 0));
+      }
+    }
+  }
 
   u32x4 wv[R][CPW];
 #pragma unroll
@@ -212,25 +232,22 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
   __builtin_amdgcn_sched_barrier(0);  // keep the arithmetic below the loads
 
   // ---- 2. stage the scales; activation sums and operand order -------------
-  auto put_unit = [&](int jn, uint32_t s_, uint32_t b_) {
-    if (jn >= gu) return;
-    for (int h = 0; h < upw; h++) {
-      const int idx = (jn * upw + h) * R + sr_row;
-      if constexpr (AFF) {
-        const float sc = bf16_bits_to_f32((s_ >> (16 * h)) & 0xFFFFu);
-        const float bi = bf16_bits_to_f32((b_ >> (16 * h)) & 0xFFFFu);
-        reinterpret_cast<float2*>(sbl)[idx] = float2{sc, FMT == AFF4 ? __builtin_fmaf(-128.0f, sc, bi) : bi};
-      } else {
-        sbl[idx] = e8m0_to_f32((s_ >> (8 * h)) & 0xFFu);
+#pragma unroll
+  for (int i = 0; i < SBE; i++) {
+    if (i < nld && lane + 64 * i < nunits) {
+      int j, r, gl;
+      unit_of(lane + 64 * i, j, r, gl);
+      for (int h = 0; h < upw; h++) {
+        const int idx = (j * gc + gl * upw + h) * R + r;
+        if constexpr (AFF) {
+          const float sc = bf16_bits_to_f32((sraw[i] >> (16 * h)) & 0xFFFFu);
+          const float bi = bf16_bits_to_f32((braw[i] >> (16 * h)) & 0xFFFFu);
+          reinterpret_cast<float2*>(wsl)[idx] = float2{sc, FMT == AFF4 ? __builtin_fmaf(-128.0f, sc, bi) : bi};
+        } else {
+          reinterpret_cast<float*>(wsl)[idx] = e8m0_to_f32((sraw[i] >> (8 * h)) & 0xFFu);
+        }
       }
     }
-  };
-#pragma unroll
-  for (int i = 0; i < SBE; i++) put_unit(sj0 + sjs * i, sraw[i], braw[i]);
-  for (int jn = sj0 + sjs * SBE; jn < gu; jn += sjs) {  // long rows: the rest
-    uint32_t s_, b_;
-    load_unit(jn, s_, b_);
-    put_unit(jn, s_, b_);
   }
 
   float xs[MR][CPW];
@@ -251,13 +268,15 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
         for (int v = 0; v < XV; v++) xv[m][j][v] = perm_aff4_v(xv[m][j][v]);
       }
     }
-  __syncthreads();  // the staged scales
+  // the wave's own LDS writes complete in order before its reads (this also
+  // fences the compiler)
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
   // ---- 3. dot products, one scale/bias fold per lane chunk -----------------
   uint32_t sbase[CPW];  // LDS byte offset of this lane's group, row 0
 #pragma unroll
   for (int j = 0; j < CPW; j++)
-    sbase[j] = (uint32_t)(min((kc[j] * KL) >> gs_shift, G - 1) * R) * (AFF ? 8u : 4u);
+    sbase[j] = (uint32_t)(wsl - smem) + (uint32_t)((j * gc + ((lane * KL) >> gs_shift)) * R) * (AFF ? 8u : 4u);
 
   float y[R][MR];
 #pragma unroll
@@ -386,12 +405,16 @@ QmvRsPlan qmv_rs_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int r_req
   if (p.cpw == 2 && p.mr == 4) p.r = 4;
   if (r_req > 0 && rs_valid(p.mr, r_req, p.cpw)) p.r = r_req;
   p.tiles = (int)((N + p.r - 1) / p.r);
+  p.lds = qmv_rs_lds(fmt, p.r, p.mr, p.nw, p.cpw, gs);
+  // every scale load of a wave is issued before its weights: at most 4 per lane
   const int64_t G = K / gs;
-  p.lds = qmv_rs_lds(fmt, p.r, p.mr, p.nw, G);
+  const int upw = fmt != MXFP4 ? ((G & 1) ? 1 : 2) : ((G & 3) ? ((G & 1) ? 1 : 2) : 4);
+  const int gc = 64 * kl / gs;
+  const int units = p.cpw * p.r * gc / upw;
   // buffer offsets are 32-bit and 0x80000000 marks a dead lane: every operand
   // of one launch must stay below 2 GiB
   const int64_t wbytes = N * (K / kl) * 16, sbytes = N * G * 2;
-  p.ok = rs_valid(p.mr, p.r, p.cpw) && K % kl == 0 && K % gs == 0 && p.lds <= kQmvLdsMax &&
+  p.ok = rs_valid(p.mr, p.r, p.cpw) && K % kl == 0 && K % gs == 0 && p.lds <= kQmvLdsMax && units <= 4 * 64 &&
          wbytes + (int64_t)p.r * (K / kl) * 16 < ((int64_t)1 << 31) && sbytes < ((int64_t)1 << 31) &&
          (int64_t)4 * K * 2 < ((int64_t)1 << 31);
   return p;
