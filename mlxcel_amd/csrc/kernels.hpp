@@ -115,13 +115,22 @@ struct QmmArgs {
   const uint32_t* orows;
   int64_t w_expert_stride;
   int64_t s_expert_stride;
+  // Tile walk of the 32x32-MFMA kernel (qmm_tile_kernel): output tiles per
+  // dimension and whether consecutive tiles advance along M (1) or N (0).
+  int tiles_m, tiles_n, m_fast;
 };
 struct QmmPlan {
   bool ok = false;
-  int tile = 0;  // 0: 256 x 128, 1: 256 x 256, 2: 128 x 128, 3: 64 x 128 output tiles
+  // output tile: 0 = 256 x 128, 1 = 256 x 256, 2 = 128 x 128, 3 = 64 x 128
+  // (16x16-MFMA kernel); 4 = 256 x 256, 5 = 256 x 128, 6 = 128 x 128
+  // (32x32-MFMA tile kernel)
+  int tile = 0;
   int rows_per_tile = 256;
   int tiles_n = 1, tiles_m = 1, ksplit = 1, ksteps_per_split = 1;
+  int m_fast = 0;  // tile kernel: consecutive workgroups walk along M
 };
+// rows of x per output tile of a tile code (0 if unknown)
+int qmm_tile_rows(int tile);
 // Grouped gather: tiles along N for `tile`; tiles_m = segments is set by the caller.
 QmmPlan qmm_plan_grouped(int fmt, int gs, int64_t N, int64_t K, int tile);
 // tile_req / ksplit_req < 0 (or 0 for ksplit) choose by shape.

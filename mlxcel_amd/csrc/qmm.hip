@@ -47,6 +47,18 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // Byte j of w as a float (v_cvt_f32_ubyte<j>).
 __device__ __forceinline__ float ubyte(uint32_t w, int j) { return (float)((w >> (8 * j)) & 0xFFu); }
 
+// Byte J of w as a float, one v_cvt_f32_ubyte<J> (written out: from a masked
+// word the compiler otherwise emits a bit-field extract plus a conversion).
+template <int J>
+__device__ __forceinline__ float cvt_ubyte(uint32_t w) {
+  float r;
+  if constexpr (J == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(w));
+  else if constexpr (J == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(w));
+  else if constexpr (J == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(w));
+  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(w));
+  return r;
+}
+
 }  // namespace
 
 // BM x BN output tile per workgroup; each wave owns (BM/2) x (BN/2).
@@ -246,25 +258,419 @@ __global__ __launch_bounds__(NT) void qmm_kernel(const QmmArgs a) {
       }
 }
 
+// ---- 32x32-MFMA tile kernel -------------------------------------------------
+//
+// y[BM x BN tile] with 4 waves in a 2 x 2 grid; a wave owns (BM/2) x (BN/2)
+// output elements as (BM/64) x (BN/64) v_mfma_f32_32x32x16_bf16 tiles (the
+// 256 x 256 tile keeps 256 fp32 accumulators per lane, in AGPRs).
+//
+// Per 64-wide K-step, activations [BM][64] and dequantized weights [BN][64]
+// (bf16) sit in double-buffered LDS.  Rows are 128 bytes with the 16-byte
+// chunk c of row r stored at c ^ (r & 7), so the 8 lanes of one LDS cycle
+// (8 rows, same chunk) hit distinct banks for both the staging writes and the
+// fragment reads.  One K-step, one barrier: while the MFMAs of step ks run
+// from buffer ks&1, the wave dequantizes step ks+1 from registers into the
+// other buffer and then issues the global loads of step ks+2, a whole K-step
+// ahead of their first use.
+//
+// Memory requests are what the L1/TA sees per instruction, so every load is
+// shaped to touch few lines: activations as 8 lanes x 16 B per 128-byte row
+// piece; weights as WT lanes x 16 B per row piece (a row's 64 codes of one
+// K-step are contiguous); scales and biases as one 16-byte chunk per row
+// (8 bf16 groups or 16 e8m0 groups) every few K-steps, staged in a small
+// double-buffered LDS table [group][row].
+//
+// Workgroups are numbered so that each XCD (workgroup id mod 8) walks a
+// contiguous run of tiles, keeping the tiles its CUs share in its own L2.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+#ifndef QMM_VALU_PER_MFMA
+#define QMM_VALU_PER_MFMA 6
+#endif
+#ifndef QMM_DS_BURST
+#define QMM_DS_BURST 1
+#endif
+
+template <int FMT, int BM, int BN, int NWM, int NWN>
+__global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs a) {
+  constexpr int NT = 64 * NWM * NWN;         // threads
+  constexpr int TM = BM / NWM, TN = BN / NWN;  // wave tile
+  constexpr int FM = TM / 32, FN = TN / 32;  // 32 x 32 MFMA tiles per wave
+  constexpr bool AFF = FMT != MXFP4;
+  constexpr int BITS = FMT == AFF8 ? 8 : 4;
+  constexpr int RS = BK;                     // LDS row stride (bf16): 128 bytes, swizzled
+  constexpr int XL = BM * BK * 2 / 16 / NT;  // 16-byte activation loads per thread and K-step
+  constexpr int WT = BK * BITS / 8 / 16;     // threads per weight row and K-step (16 bytes each)
+  constexpr int WROWS = NT / WT;             // weight rows per pass
+  constexpr int WP = BN / WROWS;             // weight loads per thread and K-step
+  constexpr int VPL = 128 / BITS;            // values per 16-byte weight load
+  constexpr int CHG = AFF ? 8 : 16;          // groups in a 16-byte scale chunk
+  static_assert(WP >= 1 && WROWS * WP == BN && BN <= NT && XL >= 1, "tile shape");
+
+  __shared__ __align__(16) uint16_t xs[2][BM * RS];
+  __shared__ __align__(16) uint16_t wsm[2][BN * RS];
+  // per-chunk (scale, bias) table: affine u32 (bf16 scale | bf16 bias << 16)
+  // [slot][group][row]; mxfp4 e8m0 bytes [slot][group][row]
+  __shared__ __align__(16) uint32_t tbl[2 * 8 * BN];
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const int wm = wave / NWN, wn = wave % NWN;
+  const int M = a.M, N = a.N, K = a.K;
+
+  // ---- workgroup -> (split, tile): XCD-contiguous runs --------------------
+  const int T = a.tiles_m * a.tiles_n;
+  const int G = T * a.ksplit;
+  int b = blockIdx.x;
+  {
+    const int q = G >> 3, r = G & 7, x = b & 7, j = b >> 3;
+    b = x < r ? x * (q + 1) + j : r * (q + 1) + (x - r) * q + j;
+  }
+  const int z = b / T, tt = b - z * T;
+  const int tm = a.m_fast ? tt % a.tiles_m : tt / a.tiles_n;
+  const int tn = a.m_fast ? tt / a.tiles_m : tt % a.tiles_n;
+  const int n0 = tn * BN;
+  const int nks = a.ksteps_per_split;
+  const int ks0 = z * nks;
+  const int ks1 = min(ks0 + nks, K / BK);
+
+  int m0 = tm * BM, rows = min(BM, M - m0), r0 = 0;
+  int64_t wbase = 0, sbase = 0;
+  if (a.seg) {
+    if (tm >= (int)a.nseg_dev[0]) return;
+    const int expert = (int)a.seg[3 * tm];
+    r0 = (int)a.seg[3 * tm + 1];
+    rows = (int)a.seg[3 * tm + 2];
+    m0 = 0;
+    wbase = (int64_t)expert * a.w_expert_stride;
+    sbase = (int64_t)expert * a.s_expert_stride;
+  }
+
+  const __amdgpu_buffer_rsrc_t xr = qrsrc(a.x, (uint32_t)((int64_t)a.x_rows * K * 2));
+  const uint32_t RB = (uint32_t)(K * BITS / 8);
+  const __amdgpu_buffer_rsrc_t wr = qrsrc(a.w + wbase, (uint32_t)((int64_t)N * RB));
+  const int GR = K >> a.gs_shift;  // groups per row
+  const __amdgpu_buffer_rsrc_t sr = qrsrc(reinterpret_cast<const uint8_t*>(a.scales) + sbase * (AFF ? 2 : 1),
+                                          (uint32_t)((int64_t)N * GR * (AFF ? 2 : 1)));
+  const __amdgpu_buffer_rsrc_t br =
+      qrsrc(AFF ? (const void*)(a.biases + sbase) : a.scales, (uint32_t)(AFF ? (int64_t)N * GR * 2 : 0));
+  const int gs_shift = a.gs_shift;
+  const int SPC = (CHG << gs_shift) / BK;  // K-steps per scale chunk (4, 8 or 16)
+
+  // activations: thread t stages rows (t / 8) + (NT / 8) i, 16-byte chunk t % 8
+  constexpr int XROWS = NT / 8;
+  const int xrow = t >> 3, xch = t & 7;
+  uint32_t xoff[XL];
+#pragma unroll
+  for (int i = 0; i < XL; i++) {
+    const int tr = xrow + XROWS * i;
+    const uint32_t xrw = a.seg ? (tr < rows ? a.xrows[r0 + tr] : 0u) : (uint32_t)(m0 + tr);
+    xoff[i] = tr < rows ? xrw * (uint32_t)K * 2u + (uint32_t)xch * 16u : kDeadQ;
+  }
+  const int xdst = xrow * RS + ((xch ^ (xrow & 7)) << 3);  // + XROWS i rows (same swizzle)
+
+  // weights: thread t dequantizes rows wrow + WROWS p, 16-byte piece wpc
+  const int wrow = t / WT, wpc = t % WT;
+  uint32_t woff[WP];
+#pragma unroll
+  for (int p = 0; p < WP; p++) {
+    const int n = n0 + wrow + WROWS * p;
+    woff[p] = n < N ? (uint32_t)n * RB + (uint32_t)(wpc * 16) : kDeadQ;
+  }
+
+  // scale chunks: thread t < BN loads the 16-byte chunk of row n0 + t
+  const bool sload = t < BN;
+  const uint32_t srow_off = (n0 + t < N && sload) ? (uint32_t)(n0 + t) * (uint32_t)GR * (AFF ? 2u : 1u) : kDeadQ;
+  // Scale rows need not be 16-byte aligned (K / gs groups per row, e.g. 90
+  // e8m0 bytes): a chunk is read as 5 dwords from the dword boundary below
+  // and realigned by the byte offset in registers.
+  const uint32_t sal = srow_off & 3u;
+  u32x4 sc_r = {0u, 0u, 0u, 0u}, bi_r = {0u, 0u, 0u, 0u};
+  uint32_t sc_x = 0u, bi_x = 0u;
+  auto chunk_load = [&](int c) {
+    if (sload) {
+      const uint32_t o = (srow_off & ~3u) + (uint32_t)c * 16u;
+      sc_r = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, o, 0, 0));
+      sc_x = __builtin_amdgcn_raw_buffer_load_b32(sr, o + 16u, 0, 0);
+      if constexpr (AFF) {
+        bi_r = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(br, o, 0, 0));
+        bi_x = __builtin_amdgcn_raw_buffer_load_b32(br, o + 16u, 0, 0);
+      }
+    }
+  };
+  auto realign = [&](u32x4& v, uint32_t x) {
+    if (sal != 0u) {
+      v = u32x4{__builtin_amdgcn_alignbyte(v[1], v[0], sal), __builtin_amdgcn_alignbyte(v[2], v[1], sal),
+                __builtin_amdgcn_alignbyte(v[3], v[2], sal), __builtin_amdgcn_alignbyte(x, v[3], sal)};
+    }
+  };
+  auto chunk_write = [&](int c) {
+    if (sload) {
+      realign(sc_r, sc_x);
+      if constexpr (AFF) realign(bi_r, bi_x);
+      const int slot = c & 1;
+      if constexpr (AFF) {
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+          tbl[(slot * 8 + j) * BN + t] =
+              __builtin_amdgcn_perm(bi_r[j >> 1], sc_r[j >> 1], (j & 1) ? 0x07060302u : 0x05040100u);
+      } else {
+        uint8_t* tb = reinterpret_cast<uint8_t*>(tbl);
+#pragma unroll
+        for (int j = 0; j < 16; j++) tb[(slot * 16 + j) * BN + t] = (uint8_t)(sc_r[j >> 2] >> (8 * (j & 3)));
+      }
+    }
+  };
+
+  u32x4 xreg[XL], wreg[WP];
+  auto load_step = [&](int ks) {
+    const int k0 = ks * BK;
+#pragma unroll
+    for (int p = 0; p < WP; p++)
+      wreg[p] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, woff[p] + (uint32_t)(k0 * BITS / 8), 0, 0));
+#pragma unroll
+    for (int i = 0; i < XL; i++)
+      xreg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff[i] + (uint32_t)k0 * 2u, 0, 0));
+  };
+
+  // Register -> LDS for step ks in NPART parts so each can sit between the
+  // MFMAs of one slice: part p stores the activation loads and dequantizes
+  // the weight words that fall in the p-th share.
+  constexpr int NPART = BK / 16;
+  constexpr int NWORD = WP * 4;  // weight words per thread and K-step
+  auto store_part = [&](int buf, int p, int ks) {
+#pragma unroll
+    for (int i = 0; i < XL; i++)
+      if (i * NPART / XL == p) *reinterpret_cast<u32x4*>(&xs[buf][xdst + XROWS * i * RS]) = xreg[i];
+    // this thread's group of step ks (one per 16-byte piece: VPL <= group size)
+    const int g = ((ks * BK + wpc * VPL) >> gs_shift);
+    const int gslot = ((g / CHG) & 1) * CHG + g % CHG;
+#pragma unroll
+    for (int e = 0; e < NWORD; e++) {
+      if (e * NPART / NWORD != p) continue;
+      const int pp = e / 4;  // which weight load
+      const int r = wrow + WROWS * pp;
+      const uint32_t w = wreg[pp][e % 4];
+      uint16_t* rowp = &wsm[buf][r * RS];
+      const int r7 = r & 7;
+      if constexpr (AFF) {
+        const uint32_t sb = tbl[gslot * BN + r];
+        const float sc = __uint_as_float(sb << 16);
+        const float bi = __uint_as_float(sb & 0xFFFF0000u);
+        if constexpr (BITS == 4) {
+          // 8 codes: natural pair h = (nibble 2h, nibble 2h + 1) = (byte h of lo, byte h of hi)
+          const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+          const u32x4 o = {pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<0>(lo), bi), __builtin_fmaf(sc, cvt_ubyte<0>(hi), bi)),
+                           pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<1>(lo), bi), __builtin_fmaf(sc, cvt_ubyte<1>(hi), bi)),
+                           pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<2>(lo), bi), __builtin_fmaf(sc, cvt_ubyte<2>(hi), bi)),
+                           pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<3>(lo), bi), __builtin_fmaf(sc, cvt_ubyte<3>(hi), bi))};
+          const int ch = wpc * 4 + (e % 4);  // logical 16-byte chunk (8 values)
+          *reinterpret_cast<u32x4*>(rowp + ((ch ^ r7) << 3)) = o;
+        } else {
+          const u32x2 o = {pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<0>(w), bi), __builtin_fmaf(sc, cvt_ubyte<1>(w), bi)),
+                           pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<2>(w), bi), __builtin_fmaf(sc, cvt_ubyte<3>(w), bi))};
+          const int v = wpc * 16 + (e % 4) * 4;  // first of the 4 values
+          *reinterpret_cast<u32x2*>(rowp + ((((v >> 3) ^ r7) << 3) | (v & 7))) = o;
+        }
+      } else {
+        // fp4 code points times a normal power of two are exact in bf16 (one
+        // scaled conversion per pair); 2^-127 and NaN take the explicit product
+        const uint32_t sb = reinterpret_cast<const uint8_t*>(tbl)[gslot * BN + r];
+        const float sc = e8m0_to_f32(sb);
+        uint32_t o[4];
+        if (sb - 1u < 254u) {
+          unpack_mxfp4_scaled(w, sc, o);
+        } else {
+          uint32_t v[4];
+          unpack_mxfp4(w, v);
+#pragma unroll
+          for (int h = 0; h < 4; h++)
+            o[h] = pack_bf16x2(bf16_bits_to_f32(v[h] & 0xFFFFu) * sc, bf16_bits_to_f32(v[h] >> 16) * sc);
+        }
+        const int ch = wpc * 4 + (e % 4);
+        *reinterpret_cast<u32x4*>(rowp + ((ch ^ r7) << 3)) = u32x4{o[0], o[1], o[2], o[3]};
+      }
+    }
+  };
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int j = 0; j < FN; j++)
+#pragma unroll
+      for (int q = 0; q < 16; q++) acc[i][j][q] = 0.f;
+
+  // fragment of 32 x 32 x 16: lane holds row/column (lane % 32), k 8 * (lane / 32) .. + 8;
+  // slice s reads logical chunk 2 s + lane / 32 of its row, stored at that ^ (row & 7)
+  const int fr = lane & 31;
+  const int c0 = (lane >> 5) ^ (fr & 7);
+  const int arow = (wm * TM + fr) * RS, brow = (wn * TN + fr) * RS;
+  int soff[NPART];
+#pragma unroll
+  for (int s = 0; s < NPART; s++) soff[s] = ((2 * s) ^ c0) << 3;
+
+  // Steady state: step ks computes from buffer ks&1 while step ks+1 goes to
+  // the other buffer (first two slices) and step ks+2 is loaded.  A barrier
+  // after those stores publishes the other buffer, so the last slice can
+  // already fetch the first fragments of step ks+1; the barrier at the end of
+  // the step keeps the next step's stores off the buffer still being read.
+  // Steps past ks1 load (bounds-checked) and store into a buffer nobody
+  // reads, which keeps the slice code free of branches so the scheduler can
+  // interleave it.
+  if (ks0 < ks1) {
+    {
+      const int c = ks0 / SPC;
+      chunk_load(c);
+      chunk_write(c);
+      if ((ks0 + 1) % SPC == 0 && ks0 + 1 < ks1) {
+        chunk_load(c + 1);
+        chunk_write(c + 1);
+      }
+      if ((ks0 + 2) % SPC == 0 && ks0 + 2 < ks1) chunk_load((ks0 + 2) / SPC);
+    }
+    load_step(ks0);
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < NPART; p++) store_part(0, p, ks0);
+    load_step(ks0 + 1);
+    __syncthreads();
+    bf16x8 af[2][FM], bv[2][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++) af[0][i] = *reinterpret_cast<const bf16x8*>(xs[0] + arow + i * 32 * RS + soff[0]);
+#pragma unroll
+    for (int j = 0; j < FN; j++) bv[0][j] = *reinterpret_cast<const bf16x8*>(wsm[0] + brow + j * 32 * RS + soff[0]);
+    for (int ks = ks0; ks < ks1; ks++) {
+      // scale chunks: table of step ks+2 written now (published by this
+      // step's barriers), loads for step ks+3 issued a step ahead
+      if ((ks + 2) % SPC == 0 && ks + 2 < ks1) chunk_write((ks + 2) / SPC);
+      if ((ks + 3) % SPC == 0 && ks + 3 < ks1) chunk_load((ks + 3) / SPC);
+      const int buf = (ks - ks0) & 1;
+      const uint16_t* xb = xs[buf];
+      const uint16_t* wb = wsm[buf];
+#pragma unroll
+      for (int s = 0; s < NPART; s++) {
+        const int cur = s & 1;
+        if (s + 1 < NPART) {
+#pragma unroll
+          for (int i = 0; i < FM; i++)
+            af[cur ^ 1][i] = *reinterpret_cast<const bf16x8*>(xb + arow + i * 32 * RS + soff[s + 1]);
+#pragma unroll
+          for (int j = 0; j < FN; j++)
+            bv[cur ^ 1][j] = *reinterpret_cast<const bf16x8*>(wb + brow + j * 32 * RS + soff[s + 1]);
+        } else {
+          // first fragments of step ks+1 (published by the barrier after slice 1)
+          const uint16_t* xn = xs[buf ^ 1];
+          const uint16_t* wnx = wsm[buf ^ 1];
+#pragma unroll
+          for (int i = 0; i < FM; i++)
+            af[cur ^ 1][i] = *reinterpret_cast<const bf16x8*>(xn + arow + i * 32 * RS + soff[0]);
+#pragma unroll
+          for (int j = 0; j < FN; j++)
+            bv[cur ^ 1][j] = *reinterpret_cast<const bf16x8*>(wnx + brow + j * 32 * RS + soff[0]);
+        }
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+          for (int j = 0; j < FN; j++) acc[i][j] = mfma32x32x16(af[cur][i], bv[cur][j], acc[i][j]);
+        // step ks+1 goes to the other buffer in the first two slices, then
+        // the registers take the loads of step ks+2
+        if (s == 0) {
+          store_part(buf ^ 1, 0, ks + 1);
+          store_part(buf ^ 1, 1, ks + 1);
+        } else if (s == 1) {
+          store_part(buf ^ 1, 2, ks + 1);
+          store_part(buf ^ 1, 3, ks + 1);
+          load_step(ks + 2);
+        }
+        // interleave within the slice: one MFMA, then a share of the VALU,
+        // LDS and global-load work; slices are scheduled one by one
+        constexpr int NMF = FM * FN;
+#if QMM_DS_BURST
+        // the next slice's fragment reads go out first, a whole slice of
+        // MFMAs ahead of their use
+        __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);  // DS read
+#endif
+#pragma unroll
+        for (int q = 0; q < NMF; q++) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, QMM_VALU_PER_MFMA, 0);  // VALU
+#if !QMM_DS_BURST
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                  // DS read
+#endif
+          __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                  // DS write
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                  // VMEM read
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (s == 1) __syncthreads();  // step ks+1's buffer complete
+      }
+      __syncthreads();  // step ks's buffer no longer read
+    }
+  }
+
+  // ---- epilogue: lane holds column (lane % 32) and rows 8 (q / 4) + 4 (lane / 32) + q % 4
+  const bool split = a.ksplit > 1;
+  auto put = [&](int tr, int c, float v) {
+    if (tr < rows && c < N) {
+      const int64_t r = a.seg ? (int64_t)a.orows[r0 + tr] : (int64_t)(m0 + tr);
+      if (split) a.ws[((int64_t)z * M + r) * N + c] = v;
+      else a.out[r * N + c] = (uint16_t)f32_to_bf16_bits(v);
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+      const int tr0 = wm * TM + i * 32 + 4 * (lane >> 5);
+      const int c = n0 + wn * TN + j * 32 + fr;
+      const f32x16 v = acc[i][j];
+      // element indices spelled out: a loop index here can leave the array in scratch
+#define QMM_PUT4(Q) put(tr0 + 2 * (Q), c, v[Q]); put(tr0 + 2 * (Q) + 1, c, v[(Q) + 1]); \
+                    put(tr0 + 2 * (Q) + 2, c, v[(Q) + 2]); put(tr0 + 2 * (Q) + 3, c, v[(Q) + 3]);
+      QMM_PUT4(0) QMM_PUT4(4) QMM_PUT4(8) QMM_PUT4(12)
+#undef QMM_PUT4
+    }
+}
+
 // ---- host ------------------------------------------------------------------
 
-// Tile shapes (BM x BN): 0 = 256 x 128, 1 = 256 x 256, 2 = 128 x 128, 3 = 64 x 128.
+namespace {
+// Tile codes: 0 = 256 x 128, 1 = 256 x 256, 2 = 128 x 128, 3 = 64 x 128
+// (16x16-MFMA kernel, grid (n, m, split)); 4 = 256 x 256 (8 waves), 5 = 256 x 128,
+// 6 = 128 x 128, 7 = 256 x 256 (4 waves) (32x32-MFMA tile kernel, 1-D
+// XCD-ordered grid).
+constexpr int kTiles = 8;
+const int kBM[kTiles] = {256, 256, 128, 64, 256, 256, 128, 256};
+const int kBN[kTiles] = {128, 256, 128, 128, 256, 128, 128, 256};
+bool is_tile_kernel(int tile) { return tile >= 4; }
+}  // namespace
+
+int qmm_tile_rows(int tile) { return tile >= 0 && tile < kTiles ? kBM[tile] : 0; }
+
 QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus, int tile_req, int ksplit_req) {
   QmmPlan p;
   const int bits = fmt == AFF8 ? 8 : 4;
   if (K % BK != 0 || K % gs != 0 || M <= 0 || N <= 0) return p;
   if (M * K * 2 >= ((int64_t)1 << 31) || N * K * bits / 8 >= ((int64_t)1 << 31)) return p;
-  static const int kBM[4] = {256, 256, 128, 64}, kBN[4] = {128, 256, 128, 128};
   const int nks = (int)(K / BK);
   auto tiles_of = [&](int t) { return ((M + kBM[t] - 1) / kBM[t]) * ((N + kBN[t] - 1) / kBN[t]); };
-  int tile = 0;
-  if (tile_req >= 0 && tile_req <= 3) {
+  int tile;
+  if (tile_req >= 0 && tile_req < kTiles) {
     tile = tile_req;
   } else {
-    // the largest tile that still gives every CU a workgroup without a K split
-    tile = tiles_of(1) >= num_cus ? 1 : (tiles_of(0) >= (num_cus * 3) / 4 ? 0 : 2);
+    // 256 x 256 (8 waves) when there are enough tiles or K is long enough
+    // for a K split to fill the CUs; else 128 x 128, two workgroups per CU
+    // (measured on MI355X at the Llama-3-8B prefill shapes)
+    tile = (tiles_of(4) >= num_cus / 2 || K >= 8192) ? 4 : 6;
   }
   p.tile = tile;
+  p.rows_per_tile = kBM[tile];
   p.tiles_n = (int)((N + kBN[tile] - 1) / kBN[tile]);
   p.tiles_m = (int)((M + kBM[tile] - 1) / kBM[tile]);
   const int64_t tiles = (int64_t)p.tiles_n * p.tiles_m;
@@ -277,13 +683,27 @@ QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus, 
   }
   p.ksteps_per_split = (nks + ks - 1) / ks;
   p.ksplit = (nks + p.ksteps_per_split - 1) / p.ksteps_per_split;
-  p.ok = true;
+  // consecutive tiles along M share weights, along N share activations: walk
+  // along the dimension whose operand is the smaller of the two to re-read
+  p.m_fast = M * K * 2 <= N * K * bits / 8 ? 1 : 0;
+  p.ok = tiles * p.ksplit < ((int64_t)1 << 31);
   return p;
 }
 
 namespace {
 template <int FMT>
-void qmm_launch_fmt(const QmmArgs& a, const QmmPlan& p, dim3 grid, hipStream_t stream) {
+void qmm_launch_fmt(const QmmArgs& a, const QmmPlan& p, hipStream_t stream) {
+  if (is_tile_kernel(p.tile)) {
+    const dim3 grid((unsigned)((int64_t)p.tiles_m * p.tiles_n * p.ksplit));
+    switch (p.tile) {
+      case 4: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 256, 256, 2, 4>), grid, dim3(512), 0, stream, a); break;
+      case 5: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 256, 128, 2, 2>), grid, dim3(256), 0, stream, a); break;
+      case 7: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 256, 256, 2, 2>), grid, dim3(256), 0, stream, a); break;
+      default: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 128, 128, 2, 2>), grid, dim3(256), 0, stream, a); break;
+    }
+    return;
+  }
+  const dim3 grid((unsigned)p.tiles_n, (unsigned)p.tiles_m, (unsigned)p.ksplit);
   switch (p.tile) {
     case 1: hipLaunchKernelGGL((qmm_kernel<FMT, 256, 256>), grid, dim3(NT), 0, stream, a); break;
     case 2: hipLaunchKernelGGL((qmm_kernel<FMT, 128, 128>), grid, dim3(NT), 0, stream, a); break;
@@ -296,26 +716,29 @@ void qmm_launch_fmt(const QmmArgs& a, const QmmPlan& p, dim3 grid, hipStream_t s
 QmmPlan qmm_plan_grouped(int fmt, int gs, int64_t N, int64_t K, int tile) {
   QmmPlan p;
   const int bits = fmt == AFF8 ? 8 : 4;
-  if (K % BK != 0 || K % gs != 0 || N <= 0 || tile < 0 || tile > 3) return p;
+  if (K % BK != 0 || K % gs != 0 || N <= 0 || tile < 0 || tile >= kTiles) return p;
   if (N * K * bits / 8 >= ((int64_t)1 << 31)) return p;
-  static const int kBM[4] = {256, 256, 128, 64}, kBN[4] = {128, 256, 128, 128};
   p.tile = tile;
   p.rows_per_tile = kBM[tile];
   p.tiles_n = (int)((N + kBN[tile] - 1) / kBN[tile]);
   p.tiles_m = 0;  // the caller sets the segment count
   p.ksplit = 1;
   p.ksteps_per_split = (int)(K / BK);
+  p.m_fast = 0;
   p.ok = true;
   return p;
 }
 
-hipError_t qmm_launch(int fmt, const QmmArgs& a, const QmmPlan& p, hipStream_t stream) {
+hipError_t qmm_launch(int fmt, const QmmArgs& a_in, const QmmPlan& p, hipStream_t stream) {
   if (!p.ok) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)p.tiles_n, (unsigned)p.tiles_m, (unsigned)p.ksplit);
+  QmmArgs a = a_in;
+  a.tiles_m = p.tiles_m;
+  a.tiles_n = p.tiles_n;
+  a.m_fast = p.m_fast;
   switch (fmt) {
-    case AFF4: qmm_launch_fmt<AFF4>(a, p, grid, stream); break;
-    case AFF8: qmm_launch_fmt<AFF8>(a, p, grid, stream); break;
-    default: qmm_launch_fmt<MXFP4>(a, p, grid, stream); break;
+    case AFF4: qmm_launch_fmt<AFF4>(a, p, stream); break;
+    case AFF8: qmm_launch_fmt<AFF8>(a, p, stream); break;
+    default: qmm_launch_fmt<MXFP4>(a, p, stream); break;
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.ksplit == 1) return e;
