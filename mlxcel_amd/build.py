@@ -37,6 +37,7 @@ SOURCES = {
     "qmv.hip": [],
     "qmv_rs.hip": [],
     "qmv_fr.hip": [],
+    "qmv_b4.hip": [],
     "qmm.hip": [],
     "dequant.hip": ["-ffp-contract=off"],
 }

@@ -535,21 +535,34 @@ void require_dtype(const mlxq_array* a, int dt, const char* name, const char* ta
 // qmv_fr.hip, 1-2 rows; rs: up to 4 rows; falling back the same way) and
 // MLXQ_QMV_R sets rows per wave (fr) or per workgroup (rs): A/B switches for
 // tests and measurements.
-enum class Skinny { FR, RS, MFMA };
+enum class Skinny { FR, RS, B4, MFMA };
 
-Skinny skinny_choice(int rows) {
+// Rows from which a dense quantized_matmul runs the prefill GEMM (qmm.hip):
+// at 9-16 rows its 128 x 128 tiles already beat the skinny kernels on
+// MI355X (MLXQ_QMM_MIN_ROWS overrides, for tests and measurements).
+constexpr int kQmmMinRows = 9;
+
+// Defaults measured at the Llama-3-8B MLP shapes (gate K=4096, down
+// K=14336): row-streaming up to 4 rows; block-MFMA for 5-8 rows of 8-bit
+// and mxfp4 codes, and of 4-bit codes with K <= 8192; the MFMA kernel
+// otherwise.  (Above 8 rows a dense quantized_matmul goes to the prefill
+// GEMM instead, see kQmmMinRows.)
+Skinny skinny_choice(int rows, int fmt = mlxq::AFF4, int64_t K = 0) {
   const char* k = std::getenv("MLXQ_QMV_KERNEL");
   if (k && std::strcmp(k, "mfma") == 0) return Skinny::MFMA;
   if (k && std::strcmp(k, "rs") == 0) return rows <= 4 ? Skinny::RS : Skinny::MFMA;
   if (k && std::strcmp(k, "fr") == 0) return rows <= 2 ? Skinny::FR : Skinny::MFMA;
-  return rows <= 2 ? Skinny::RS : Skinny::MFMA;
+  if (k && std::strcmp(k, "b4") == 0) return rows <= 16 ? Skinny::B4 : Skinny::MFMA;
+  if (rows <= 4) return Skinny::RS;
+  if (rows <= 8 && (fmt != mlxq::AFF4 || K <= 8192)) return Skinny::B4;
+  return Skinny::MFMA;
 }
 
 // Launches the full-row or row-streaming kernel when chosen and covered;
 // false: the caller runs the MFMA kernel.
 bool try_fr_rs(const QmmSpec& sp, const mlxq::QmvArgs& a, int nseg, int rows, hipStream_t stream) {
   const int fmt = fmt_of(sp.mode, sp.bits);
-  Skinny c = skinny_choice(rows);
+  Skinny c = skinny_choice(rows, fmt, sp.K);
   const int r_req = env_int("MLXQ_QMV_R", 0);
   if (c == Skinny::FR) {
     const mlxq::QmvFrPlan p = mlxq::qmv_fr_plan(fmt, sp.gs, sp.N, sp.K, rows, r_req);
@@ -559,6 +572,16 @@ bool try_fr_rs(const QmmSpec& sp, const mlxq::QmvArgs& a, int nseg, int rows, hi
       return true;
     }
     c = Skinny::RS;
+  }
+  if (c == Skinny::B4) {
+    const mlxq::QmvB4Plan p = mlxq::qmv_b4_plan(fmt, sp.gs, sp.N, sp.K, rows, env_int("MLXQ_QMV_B4_RG", 0),
+                                                env_int("MLXQ_QMV_B4_CPW", 0));
+    if (p.ok) {
+      if (nseg > 65535) unsupported("too many segments for one launch");
+      hip_check(mlxq::qmv_b4_launch(fmt, sp.gs, a, nseg, p, stream), "qmv launch");
+      return true;
+    }
+    c = rows <= 4 ? Skinny::RS : Skinny::MFMA;
   }
   if (c == Skinny::RS) {
     const mlxq::QmvRsPlan p = mlxq::qmv_rs_plan(fmt, sp.gs, sp.N, sp.K, rows, r_req);
@@ -573,7 +596,7 @@ bool try_fr_rs(const QmmSpec& sp, const mlxq::QmvArgs& a, int nseg, int rows, hi
 
 // Launch the skinny kernel over `nseg` segments of at most `max_rows` rows.
 void run_qmv(const QmmSpec& sp, mlxq::QmvArgs a, int nseg, int max_rows, hipStream_t stream) {
-  if (max_rows <= 4 && try_fr_rs(sp, a, nseg, max_rows, stream)) return;
+  if (max_rows <= 16 && try_fr_rs(sp, a, nseg, max_rows, stream)) return;
   const int fmt = fmt_of(sp.mode, sp.bits);
   const int dev = current_device();
   const DevInfo di = device_info(dev);
@@ -645,7 +668,7 @@ mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w, cons
     const int fmt = fmt_of(sp.mode, sp.bits);
     const int cap = mlxq::qmv_max_rows(fmt, sp.gs);
     View wv{w}, xv{x};
-    if (wv.ndim() == 2 && rows_total >= env_int("MLXQ_QMM_MIN_ROWS", 65)) {
+    if (wv.ndim() == 2 && rows_total >= env_int("MLXQ_QMM_MIN_ROWS", kQmmMinRows)) {
       // prefill: one GEMM over all rows (every leading dim of x folds into rows)
       const int dev = current_device();
       // MLXQ_QMM_TILE / MLXQ_QMM_KSPLIT: A/B overrides of the tile shape and K split
@@ -894,14 +917,19 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq
       return;
     }
 
-    const Skinny kind = skinny_choice((int)M);
+    const Skinny kind = skinny_choice((int)M, fmt, sp.K);
     const int r_req = env_int("MLXQ_QMV_R", 0);
     const mlxq::QmvFrPlan fp =
         kind == Skinny::FR ? mlxq::qmv_fr_plan(fmt, sp.gs, sp.N, sp.K, (int)M, r_req) : mlxq::QmvFrPlan{};
-    const mlxq::QmvRsPlan rp = (kind == Skinny::RS || (kind == Skinny::FR && !fp.ok))
-                                   ? mlxq::qmv_rs_plan(fmt, sp.gs, sp.N, sp.K, (int)M, r_req)
-                                   : mlxq::QmvRsPlan{};
-    const bool use_rs = fp.ok || rp.ok;
+    const mlxq::QmvB4Plan bp =
+        kind == Skinny::B4 ? mlxq::qmv_b4_plan(fmt, sp.gs, sp.N, sp.K, (int)M, env_int("MLXQ_QMV_B4_RG", 0),
+                                               env_int("MLXQ_QMV_B4_CPW", 0))
+                           : mlxq::QmvB4Plan{};
+    const mlxq::QmvRsPlan rp =
+        (kind == Skinny::RS || (kind == Skinny::FR && !fp.ok) || (kind == Skinny::B4 && !bp.ok && M <= 4))
+            ? mlxq::qmv_rs_plan(fmt, sp.gs, sp.N, sp.K, (int)M, r_req)
+            : mlxq::QmvRsPlan{};
+    const bool use_rs = fp.ok || rp.ok || bp.ok;
     int nw, pf;
     qmv_shape_choice(sp.N, sp.K, nw, pf);
     mlxq::QmvPlan p;
@@ -937,6 +965,10 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq
     a.rows_lds = (int)M;
     if (fp.ok) {
       hip_check(mlxq::qmv_fr_launch(fmt, sp.gs, a, (int)B, fp, stream), "gather qmv launch");
+      return;
+    }
+    if (bp.ok) {
+      hip_check(mlxq::qmv_b4_launch(fmt, sp.gs, a, (int)B, bp, stream), "gather qmv launch");
       return;
     }
     if (rp.ok) {

@@ -77,6 +77,23 @@ struct QmvRsPlan {
 QmvRsPlan qmv_rs_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int r_req);
 hipError_t qmv_rs_launch(int fmt, int gs, const QmvArgs& a, int nseg, const QmvRsPlan& p, hipStream_t stream);
 
+// Block-MFMA decode kernel (qmv_b4.hip) for 1 to 16 activation rows per
+// weight matrix: v_mfma_f32_4x4x4bf16_1k over 4 weight rows x 256-byte pieces
+// per wave-load, RG groups of 4 rows per workgroup, waves split K in chunks
+// of 16 pieces (CPW chunks per wave).
+struct QmvB4Plan {
+  bool ok = false;  // false: shape not covered
+  int ms = 1;       // sets of 4 activation rows compiled for (1, 2 or 4)
+  int rg = 4;       // groups of 4 weight rows per workgroup
+  int cpw = 1;      // chunks per wave
+  int nw = 1;       // waves per workgroup
+  int tiles = 1;    // workgroups along N
+  size_t lds = 0;   // dynamic LDS bytes (cross-wave reduction)
+};
+// rg_req / cpw_req: requested shape (0 -> default)
+QmvB4Plan qmv_b4_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int rg_req, int cpw_req);
+hipError_t qmv_b4_launch(int fmt, int gs, const QmvArgs& a, int nseg, const QmvB4Plan& p, hipStream_t stream);
+
 // Full-row decode kernel (qmv_fr.hip) for 1 or 2 activation rows per weight
 // matrix: 8 waves per workgroup, R whole rows per wave, activations staged in
 // LDS once per workgroup.

@@ -667,7 +667,7 @@ QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus, 
     // 256 x 256 (8 waves) when there are enough tiles or K is long enough
     // for a K split to fill the CUs; else 128 x 128, two workgroups per CU
     // (measured on MI355X at the Llama-3-8B prefill shapes)
-    tile = (tiles_of(4) >= num_cus / 2 || K >= 8192) ? 4 : 6;
+    tile = (M > 128 && (tiles_of(4) >= num_cus / 2 || K >= 8192)) ? 4 : 6;
   }
   p.tile = tile;
   p.rows_per_tile = kBM[tile];
@@ -678,8 +678,13 @@ QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus, 
   if (ksplit_req > 0) {
     ks = ksplit_req;
   } else {
-    // split K while the grid covers less than the CUs and each split keeps >= 8 K-steps
-    while (tiles * ks * 2 <= num_cus && nks / (ks * 2) >= 8) ks *= 2;
+    // split K while the grid covers less than the CUs (two workgroups per CU
+    // for few rows, where each tile is cheap) and each split keeps >= 8 K-steps
+    if (M <= 128) {
+      while (tiles * ks < 2 * num_cus && nks / (ks * 2) >= 8) ks *= 2;
+    } else {
+      while (tiles * ks * 2 <= num_cus && nks / (ks * 2) >= 8) ks *= 2;
+    }
   }
   p.ksteps_per_split = (nks + ks - 1) / ks;
   p.ksplit = (nks + p.ksteps_per_split - 1) / p.ksteps_per_split;
