@@ -246,6 +246,201 @@ def gather_moe(iters=100):
     return res
 
 
+# ---- end-to-end decode --------------------------------
+#
+# A Qwen3-8B-shaped decoder (36 layers, hidden 4096, 32 query / 8 key-value
+# heads of 128, SwiGLU intermediate 12288, vocabulary 151936) with random
+# weights ~N(0, 0.02), every linear layer (q/k/v/o, gate/up/down, lm_head)
+# 4-bit affine g64 and run through this library's quantized_matmul; the
+# glue (RMSNorm, per-head q/k RMSNorm, rotary embedding, grouped-query
+# attention over a bf16 KV cache, SwiGLU, residuals, greedy argmax) is
+# torch.  The reference measures the same through `mlxcel generate`; MLX is
+# not available here, so this driver stands in for mlxcel's model code.
+# Attention products keep every right-hand operand contiguous.
+
+
+class QwenShape:
+    def __init__(self, layers=36, hidden=4096, nq=32, nkv=8, hd=128, inter=12288, vocab=151936,
+                 eps=1e-6, theta=1.0e6):
+        self.layers, self.hidden, self.nq, self.nkv, self.hd = layers, hidden, nq, nkv, hd
+        self.inter, self.vocab, self.eps, self.theta = inter, vocab, eps, theta
+
+
+class QuantDecoder:
+    """Random-weight quantized decoder; decode steps capture into HIP graphs."""
+
+    def __init__(self, shape: QwenShape, batch: int, max_ctx: int, seed: int = 0, gs: int = 64, bits: int = 4):
+        self.c, self.B, self.T, self.gs, self.bits = shape, batch, max_ctx, gs, bits
+        c = shape
+        dev = "cuda"
+        gen = torch.Generator(device=dev).manual_seed(seed)
+
+        def lin(out_f, in_f):
+            w = (torch.randn(out_f, in_f, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+            q = mq.quantize(w, gs, bits)
+            del w
+            return q
+
+        def norm(n):
+            return (1.0 + 0.02 * torch.randn(n, device=dev, generator=gen)).to(torch.bfloat16)
+
+        self.layers = []
+        for _ in range(c.layers):
+            self.layers.append(dict(
+                q=lin(c.nq * c.hd, c.hidden), k=lin(c.nkv * c.hd, c.hidden), v=lin(c.nkv * c.hd, c.hidden),
+                o=lin(c.hidden, c.nq * c.hd), g=lin(c.inter, c.hidden), u=lin(c.inter, c.hidden),
+                d=lin(c.hidden, c.inter), n1=norm(c.hidden), n2=norm(c.hidden), qn=norm(c.hd), kn=norm(c.hd)))
+        self.embed = (torch.randn(c.vocab, c.hidden, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+        self.lm = lin(c.vocab, c.hidden)
+        self.nf = norm(c.hidden)
+        self.kc = [torch.zeros(batch, c.nkv, max_ctx, c.hd, dtype=torch.bfloat16, device=dev) for _ in self.layers]
+        self.vc = [torch.zeros_like(k) for k in self.kc]
+        inv = 1.0 / (c.theta ** (torch.arange(0, c.hd, 2, device=dev, dtype=torch.float32) / c.hd))
+        ang = torch.arange(max_ctx, device=dev, dtype=torch.float32)[:, None] * inv[None, :]
+        self.cos = torch.cat([ang.cos(), ang.cos()], -1)  # [T, hd]
+        self.sin = torch.cat([ang.sin(), ang.sin()], -1)
+        self.weight_bytes = sum(t.numel() * t.element_size() for L in self.layers for k in "qkvogud" for t in L[k])
+        self.weight_bytes += sum(t.numel() * t.element_size() for t in self.lm)
+
+    def qmm(self, x, w):
+        return mq.quantized_matmul(x, *w, True, self.gs, self.bits)
+
+    def rms(self, x, w):
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.c.eps) * w.float()).to(torch.bfloat16)
+
+    def rope(self, x, cos, sin):
+        # x [..., S, heads, hd] (bf16); cos/sin [S, hd]
+        xf = x.float()
+        h = xf.shape[-1] // 2
+        rot = torch.cat([-xf[..., h:], xf[..., :h]], -1)
+        return (xf * cos[:, None, :] + rot * sin[:, None, :]).to(torch.bfloat16)
+
+    def attend(self, q, kc, vc, mask):
+        # q [B, nkv, G*S, hd]; kc/vc [B, nkv, T, hd] (rows contiguous); mask [G*S, T]
+        # additive.  Scores are formed as kc @ q^T so the cache is never a
+        # transposed right-hand operand; only small tensors are transposed.
+        qt = q.transpose(-1, -2).contiguous()
+        st = torch.matmul(kc, qt).float() * (1.0 / math.sqrt(self.c.hd)) + mask.transpose(0, 1)
+        p = torch.softmax(st, -2).to(torch.bfloat16).transpose(-1, -2).contiguous()
+        return torch.matmul(p, vc)
+
+    def layer(self, L, i, h, pos0, S, T, mask):
+        """h [B*S, hidden] at positions pos0 .. pos0+S-1 (pos0: device scalar)."""
+        c, B = self.c, self.B
+        x = self.rms(h, L["n1"])
+        q = self.qmm(x, L["q"]).view(B, S, c.nq, c.hd)
+        k = self.qmm(x, L["k"]).view(B, S, c.nkv, c.hd)
+        v = self.qmm(x, L["v"]).view(B, S, c.nkv, c.hd)
+        q, k = self.rms(q, L["qn"]), self.rms(k, L["kn"])
+        idx = pos0 + torch.arange(S, device=h.device)
+        cos, sin = self.cos.index_select(0, idx), self.sin.index_select(0, idx)
+        q, k = self.rope(q, cos, sin), self.rope(k, cos, sin)
+        self.kc[i].index_copy_(2, idx, k.transpose(1, 2))
+        self.vc[i].index_copy_(2, idx, v.transpose(1, 2))
+        G = c.nq // c.nkv
+        qg = q.view(B, S, c.nkv, G, c.hd).permute(0, 2, 3, 1, 4).reshape(B, c.nkv, G * S, c.hd)
+        o = self.attend(qg, self.kc[i][:, :, :T], self.vc[i][:, :, :T], mask)
+        o = o.view(B, c.nkv, G, S, c.hd).permute(0, 3, 1, 2, 4).reshape(B * S, c.nq * c.hd)
+        h = h + self.qmm(o, L["o"])
+        x = self.rms(h, L["n2"])
+        a = torch.nn.functional.silu(self.qmm(x, L["g"]).float()) * self.qmm(x, L["u"]).float()
+        return h + self.qmm(a.to(torch.bfloat16), L["d"])
+
+    def forward(self, tokens, pos0, S, T, mask):
+        h = self.embed.index_select(0, tokens.reshape(-1))
+        for i, L in enumerate(self.layers):
+            h = self.layer(L, i, h, pos0, S, T, mask)
+        return self.qmm(self.rms(h.view(self.B, S, -1)[:, -1], self.nf), self.lm)  # logits of the last position
+
+    def prefill(self, prompt):
+        """prompt [B, S] int64 -> logits [B, vocab] of the last position (causal attention)."""
+        S = prompt.shape[1]
+        G = self.c.nq // self.c.nkv
+        causal = torch.full((S, S), float("-inf"), device=prompt.device).triu(1)
+        mask = causal.repeat(G, 1)  # rows (g, s)
+        return self.forward(prompt, torch.zeros((), dtype=torch.int64, device=prompt.device), S, S, mask)
+
+    def decode_graph(self, T):
+        """Graph of one greedy decode step attending to cache positions < T:
+        reads self.tok [B] and self.pos (device), writes the next token into
+        self.tok and advances self.pos."""
+        dev = self.embed.device
+        G = self.c.nq // self.c.nkv
+
+        if getattr(self, "logits", None) is None:
+            self.logits = torch.empty(self.B, self.c.vocab, dtype=torch.bfloat16, device=dev)
+
+        def step():
+            ar = torch.arange(T, device=dev)
+            mask = torch.where(ar[None, :] <= self.pos, 0.0, float("-inf")).expand(G, T)
+            logits = self.forward(self.tok, self.pos, 1, T, mask)
+            self.logits.copy_(logits)
+            self.tok.copy_(torch.argmax(logits, -1))
+            self.pos.add_(1)
+
+        saved = (self.tok.clone(), self.pos.clone())
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step()  # warm-up on the capture stream (library workspace, allocator pools)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            step()
+        torch.cuda.synchronize()
+        self.tok.copy_(saved[0])
+        self.pos.copy_(saved[1])
+        return g
+
+    def generate(self, prompt, steps, bucket=64):
+        """Greedy decode `steps` tokens after `prompt`; returns (tokens [B, steps],
+        prefill seconds, decode seconds).  Each step replays the graph of the
+        smallest cache bucket covering its position."""
+        B, S = prompt.shape
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        logits = self.prefill(prompt)
+        torch.cuda.synchronize()
+        t_pre = time.perf_counter() - t0
+        self.tok = torch.argmax(logits, -1)
+        self.pos = torch.full((), S, dtype=torch.int64, device=prompt.device)
+        graphs = {}
+        for p in range(S, S + steps):
+            T = min(self.T, ((p + 1 + bucket - 1) // bucket) * bucket)
+            if T not in graphs:
+                graphs[T] = self.decode_graph(T)
+        out = torch.empty(B, steps, dtype=torch.int64, device=prompt.device)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i, p in enumerate(range(S, S + steps)):
+            out[:, i] = self.tok
+            T = min(self.T, ((p + 1 + bucket - 1) // bucket) * bucket)
+            graphs[T].replay()
+        torch.cuda.synchronize()
+        return out, t_pre, time.perf_counter() - t0
+
+
+def e2e_decode(batches=(1, 16), prompt_len=512, steps=256, layers=36):
+    """Decode tokens/s of the Qwen3-8B-shaped 4-bit model at each batch."""
+    res = []
+    for B in batches:
+        model = QuantDecoder(QwenShape(layers=layers), B, prompt_len + steps, seed=11)
+        g = torch.Generator(device="cuda").manual_seed(12)
+        prompt = torch.randint(0, model.c.vocab, (B, prompt_len), device="cuda", generator=g)
+        model.generate(prompt[:, :64], 8)  # warm-up (kernels, allocator)
+        toks, t_pre, t_dec = model.generate(prompt, steps)
+        res.append({"batch": B, "prompt": prompt_len, "decode_tokens": steps,
+                    "decode_tok_s": round(B * steps / t_dec, 1), "ms_per_step": round(t_dec / steps * 1e3, 3),
+                    "prefill_tok_s": round(B * prompt_len / t_pre, 1),
+                    "weight_GB": round(model.weight_bytes / 1e9, 3),
+                    "weight_stream_GBps": round(model.weight_bytes / (t_dec / steps) / 1e9, 1)})
+        del model
+        torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(gate, budget_s=10.0):
     """Single-core oracle `_qmm_t` on the gate projection (same bytes as the GPU launch)."""
     import oracle as orc
@@ -339,6 +534,7 @@ def main():
         extra["qmv_sweep"] = qmv_sweep()
         extra["qmm_prefill"] = qmm_prefill()
         extra["gather_mxfp4_moe"] = gather_moe()
+        extra["e2e_decode_qwen3_8b_shape"] = e2e_decode()
         line["extra"] = extra
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(gate)
