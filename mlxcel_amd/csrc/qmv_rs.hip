@@ -104,8 +104,13 @@ __device__ __forceinline__ u32x4 perm_aff4_v(u32x4 x) {
 }  // namespace
 
 // FMT: weight format; MR: activation rows (>= rows of any segment);
-// R: weight rows per workgroup (power of two); CPW: 1 KiB chunks per wave and row.
-template <int FMT, int MR, int R, int CPW>
+// R: weight rows per workgroup (power of two); CPW: 1 KiB chunks per wave and
+// row; UPW: quantization groups per scale load (1, 2 or 4: the widest load
+// every row's scales stay aligned for, chosen on the host from K / gs).  The
+// load width is a template parameter so the scale loads carry no branches:
+// a branch join there makes the compiler wait for the loads before it issues
+// the weight stream.
+template <int FMT, int MR, int R, int CPW, int UPW>
 __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shift) {
   constexpr bool AFF = FMT != MXFP4;
   constexpr int BITS = FMT == AFF8 ? 8 : 4;
@@ -183,7 +188,7 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
   // every row starts word-aligned, else a short or byte); lane L loads units
   // L, L + 64, ...  A wave reads only what it wrote itself, so no workgroup
   // barrier stands between the loads and the arithmetic.
-  const int upw = AFF ? ((G & 1) ? 1 : 2) : ((G & 3) ? ((G & 1) ? 1 : 2) : 4);  // groups per unit
+  constexpr int upw = UPW;  // groups per unit
   const int gc = (64 * KL) >> gs_shift;               // groups per chunk (>= 8)
   const int upc = gc / upw;                           // units per chunk and row
   const int lupc = __builtin_ctz((unsigned)upc);
@@ -207,7 +212,7 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
       unit_of(lane + 64 * i, j, r, gl);
       const uint32_t og = (uint32_t)((row0 + r) * G + gbase[j] + gl * upw);  // in groups
       if constexpr (AFF) {
-        if (upw == 2) {
+        if constexpr (UPW == 2) {
           sraw[i] = __builtin_amdgcn_raw_buffer_load_b32(sr, og * 2u, 0, 0);
           braw[i] = __builtin_amdgcn_raw_buffer_load_b32(br, og * 2u, 0, 0);
         } else {
@@ -215,9 +220,9 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
           braw[i] = __builtin_amdgcn_raw_buffer_load_b16(br, og * 2u, 0, 0);
         }
       } else {
-        sraw[i] = upw == 4 ? __builtin_amdgcn_raw_buffer_load_b32(sr, og, 0, 0)
-                           : (upw == 2 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(sr, og, 0, 0)
-                                       : (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(sr, og, 0, 0));
+        if constexpr (UPW == 4) sraw[i] = __builtin_amdgcn_raw_buffer_load_b32(sr, og, 0, 0);
+        else if constexpr (UPW == 2) sraw[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(sr, og, 0, 0);
+        else sraw[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(sr, og, 0, 0);
       }
     }
   }
@@ -358,13 +363,13 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
 
 namespace {
 
-template <int FMT>
-hipError_t rs_launch_fmt(const QmvRsPlan& p, const QmvArgs& a, int gs_shift, dim3 grid, hipStream_t stream) {
+template <int FMT, int UPW>
+hipError_t rs_launch_upw(const QmvRsPlan& p, const QmvArgs& a, int gs_shift, dim3 grid, hipStream_t stream) {
   const dim3 block((unsigned)(p.nw * 64));
-#define RS_CASE(MR_, R_, CPW_)                                                                        \
-  if (p.mr == MR_ && p.r == R_ && p.cpw == CPW_) {                                                    \
-    hipLaunchKernelGGL((qmv_rs_kernel<FMT, MR_, R_, CPW_>), grid, block, p.lds, stream, a, gs_shift); \
-    return hipGetLastError();                                                                         \
+#define RS_CASE(MR_, R_, CPW_)                                                                             \
+  if (p.mr == MR_ && p.r == R_ && p.cpw == CPW_) {                                                         \
+    hipLaunchKernelGGL((qmv_rs_kernel<FMT, MR_, R_, CPW_, UPW>), grid, block, p.lds, stream, a, gs_shift); \
+    return hipGetLastError();                                                                              \
   }
   RS_CASE(1, 4, 1)
   RS_CASE(1, 8, 1)
@@ -380,6 +385,20 @@ hipError_t rs_launch_fmt(const QmvRsPlan& p, const QmvArgs& a, int gs_shift, dim
   RS_CASE(4, 4, 2)
 #undef RS_CASE
   return hipErrorInvalidValue;
+}
+
+// scale groups per load: the widest load every row's scales stay aligned for
+int rs_upw(int fmt, int64_t G) {
+  if (fmt != MXFP4) return (G & 1) ? 1 : 2;
+  return (G & 3) ? ((G & 1) ? 1 : 2) : 4;
+}
+
+template <int FMT>
+hipError_t rs_launch_fmt(const QmvRsPlan& p, const QmvArgs& a, int gs_shift, dim3 grid, hipStream_t stream) {
+  const int upw = rs_upw(FMT, (int64_t)a.K >> gs_shift);
+  if (upw == 1) return rs_launch_upw<FMT, 1>(p, a, gs_shift, grid, stream);
+  if (FMT == MXFP4 && upw == 4) return rs_launch_upw<FMT, 4>(p, a, gs_shift, grid, stream);
+  return rs_launch_upw<FMT, 2>(p, a, gs_shift, grid, stream);
 }
 
 bool rs_valid(int mr, int r, int cpw) {
@@ -408,7 +427,7 @@ QmvRsPlan qmv_rs_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int r_req
   p.lds = qmv_rs_lds(fmt, p.r, p.mr, p.nw, p.cpw, gs);
   // every scale load of a wave is issued before its weights: at most 4 per lane
   const int64_t G = K / gs;
-  const int upw = fmt != MXFP4 ? ((G & 1) ? 1 : 2) : ((G & 3) ? ((G & 1) ? 1 : 2) : 4);
+  const int upw = rs_upw(fmt, G);
   const int gc = 64 * kl / gs;
   const int units = p.cpw * p.r * gc / upw;
   // buffer offsets are 32-bit and 0x80000000 marks a dead lane: every operand
