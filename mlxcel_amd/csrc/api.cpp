@@ -500,6 +500,47 @@ void bstrides_for(const mlxq_array* idx, const Shape& dshape, const Shape& b, in
   }
 }
 
+// An index array the decode kernels can read in place (no index_prep
+// launch): contiguous 32- or 64-bit integers already in the broadcast shape;
+// or, with no array, the default arange over `dflt` when it equals the
+// leading broadcast dims followed by ones, so entry b maps to b / div (x rows
+// repeated over trailing index dims, as for MoE top-k routing).
+struct DirectIdx {
+  bool ok = false;
+  const uint32_t* p = nullptr;
+  int stride = 1;
+  int div = 1;
+};
+
+DirectIdx direct_index(const mlxq_array* idx, const Shape& dflt, const Shape& b) {
+  DirectIdx d;
+  if (idx) {
+    if (View{idx}.shape() != b) return d;
+    const int dt = idx->dtype;
+    if (dt != MLXQ_INT32 && dt != MLXQ_UINT32 && dt != MLXQ_INT64 && dt != MLXQ_UINT64) return d;
+    int64_t acc = 1;
+    for (int i = idx->ndim - 1; i >= 0; i--) {
+      if (idx->shape[i] != 1 && idx->strides[i] != acc) return d;
+      acc *= idx->shape[i];
+    }
+    d.ok = true;
+    d.p = static_cast<const uint32_t*>(idx->data);
+    d.stride = (dt == MLXQ_INT64 || dt == MLXQ_UINT64) ? 2 : 1;
+    return d;
+  }
+  if (dflt.size() != b.size()) return d;
+  size_t k = b.size();
+  while (k > 0 && dflt[k - 1] == 1 && b[k - 1] != 1) k--;
+  for (size_t i = 0; i < k; i++)
+    if (dflt[i] != b[i]) return d;
+  int64_t div = 1;
+  for (size_t i = k; i < b.size(); i++) div *= b[i];
+  if (div > (1 << 30)) return d;
+  d.ok = true;
+  d.div = (int)div;
+  return d;
+}
+
 int fmt_of(Mode m, int bits) {
   if (m == MXFP4_M) return mlxq::MXFP4;
   return bits == 8 ? mlxq::AFF8 : mlxq::AFF4;
@@ -937,13 +978,26 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq
       p = mlxq::qmv_plan(fmt, sp.gs, sp.N, sp.K, (int)M, (int)B, di.cus, nw, pf);
       if (p.lds > mlxq::kQmvLdsMax) unsupported("gather_qmm: activation tile does not fit in LDS");
     }
-    const size_t idx_bytes = ((size_t)B * 2 * sizeof(uint32_t) + 255) & ~(size_t)255;
+    // indices the kernels can read in place skip the index_prep launch
+    const DirectIdx dl = direct_index(lhs_indices, dsh[0], g.idx_shape);
+    const DirectIdx dr = direct_index(rhs_indices, dsh[1], g.idx_shape);
+    const bool direct = dl.ok && dr.ok && dr.div == 1 && env_int("MLXQ_GATHER_DIRECT", 1) != 0;
+    const size_t idx_bytes = direct ? 0 : ((size_t)B * 2 * sizeof(uint32_t) + 255) & ~(size_t)255;
     const size_t part_bytes = p.ks > 1 ? (size_t)p.ks * B * M * sp.N * sizeof(float) : 0;
-    Workspace& ws = workspace(dev, stream, idx_bytes + part_bytes);
-    uint32_t* flat = reinterpret_cast<uint32_t*>(ws.data);
-    ip.out[0] = flat;
-    ip.out[1] = flat + B;
-    hip_check(mlxq::launch_index_prep(ip, stream), "index_prep launch");
+    char* wsb = nullptr;
+    if (idx_bytes + part_bytes > 0) wsb = static_cast<char*>(workspace(dev, stream, idx_bytes + part_bytes).data);
+    const uint32_t* lhs_p = dl.p;
+    const uint32_t* rhs_p = dr.p;
+    int lhs_stride = dl.stride, rhs_stride = dr.stride, lhs_div = dl.div;
+    if (!direct) {
+      uint32_t* flat = reinterpret_cast<uint32_t*>(wsb);
+      ip.out[0] = flat;
+      ip.out[1] = flat + B;
+      hip_check(mlxq::launch_index_prep(ip, stream), "index_prep launch");
+      lhs_p = flat;
+      rhs_p = flat + B;
+      lhs_stride = rhs_stride = lhs_div = 1;
+    }
 
     mlxq::QmvArgs a{};
     a.x = static_cast<const uint16_t*>(x->data);
@@ -951,8 +1005,11 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq
     a.scales = scales->data;
     a.biases = biases ? static_cast<const uint16_t*>(biases->data) : nullptr;
     a.out = static_cast<uint16_t*>(out->data);
-    a.lhs = flat;
-    a.rhs = flat + B;
+    a.lhs = lhs_p;
+    a.rhs = rhs_p;
+    a.lhs_stride = lhs_stride;
+    a.rhs_stride = rhs_stride;
+    a.lhs_div = lhs_div;
     a.N = (int)sp.N;
     a.K = (int)sp.K;
     a.E = (int)E;
@@ -977,7 +1034,7 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq
     }
     a.ks = p.ks;
     a.kst_per_wg = p.kst_per_wg;
-    if (p.ks > 1) a.ws = reinterpret_cast<float*>(static_cast<char*>(ws.data) + idx_bytes);
+    if (p.ks > 1) a.ws = reinterpret_cast<float*>(wsb + idx_bytes);
     hip_check(mlxq::qmv_launch(fmt, sp.gs, a, (int)B, p, stream), "gather qmv launch");
   });
 }

@@ -41,6 +41,17 @@ __device__ __forceinline__ float e8m0_to_f32(uint32_t s) {
   return __uint_as_float(bits);
 }
 
+// ---- gather indices ----------------------------------------------------------
+// Segment sidx of a gather reads its expert / x batch from an index array of
+// 32- or 64-bit integers (64-bit: the low word, which is the value cast to
+// uint32 as the reference casts indices), clamped to the valid range; with no
+// index array the expert is sidx (batched weights) or 0, the x batch
+// sidx / div.
+__device__ __forceinline__ int seg_index(const uint32_t* idx, int stride, int sidx, int clamp, int dflt) {
+  if (!idx) return dflt;
+  return (int)min(idx[(int64_t)sidx * (stride > 1 ? stride : 1)], (uint32_t)(clamp - 1));
+}
+
 // ---- MFMA ------------------------------------------------------------------
 // v_mfma_f32_16x16x32_bf16: D[16x16] += A[16x32] * B[32x16], fp32 accumulate.
 // Lane i holds A row (i % 16), B column (i % 16), both over the 8 k-slots

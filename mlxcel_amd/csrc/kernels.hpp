@@ -22,6 +22,10 @@ struct QmvArgs {
   float* ws;                // split-K partials [ks][out_rows][N] (ks > 1), summed by a second kernel
   const uint32_t* lhs;      // x batch index per segment (nullable)
   const uint32_t* rhs;      // expert per segment (nullable)
+  // Index element strides in 32-bit words (1: 32-bit indices, 2: 64-bit,
+  // low word read; 0 counts as 1) and, with no lhs, the divisor that maps a
+  // segment to its x batch (x batch = segment / lhs_div; 0 counts as 1).
+  int lhs_stride, rhs_stride, lhs_div;
   int N;
   int K;
   int64_t w_expert_stride;  // uint32 words per weight matrix (0: one matrix)

@@ -137,8 +137,8 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
   // ---- segment (workgroup-uniform) ----------------------------------------
   const int count = min(a.rps, a.total_rows - sidx * a.rps);
   if (count <= 0) return;
-  const int expert = a.rhs ? (int)min(a.rhs[sidx], (uint32_t)(a.E - 1)) : (a.w_expert_stride ? sidx : 0);
-  const int xbatch = a.lhs ? (int)min(a.lhs[sidx], (uint32_t)(a.X - 1)) : sidx;
+  const int expert = seg_index(a.rhs, a.rhs_stride, sidx, a.E, a.w_expert_stride ? sidx : 0);
+  const int xbatch = seg_index(a.lhs, a.lhs_stride, sidx, a.X, a.lhs_div > 1 ? sidx / a.lhs_div : sidx);
 
   const int N = a.N;
   const int K = a.K;

@@ -162,3 +162,46 @@ def test_grouped_gather_is_deterministic_and_matches_per_entry(monkeypatch):
     want = orc.gather_qmm_t(x, wq, sc, None, np.repeat(np.arange(T), 4).astype(np.uint32), ids.astype(np.uint32),
                             mode="mxfp4")
     assert max_rel(g1.reshape(T * 4, 1, N), want) <= TOL
+
+
+@pytest.mark.parametrize("dtype", [torch.int32, torch.int64])
+@pytest.mark.parametrize("case", ["topk_default_lhs", "explicit_lhs", "broadcast_rhs", "strided_rhs", "out_of_range"])
+def test_direct_indices_match_index_prep(monkeypatch, dtype, case):
+    # The decode kernels read contiguous 32/64-bit index arrays (and the
+    # default lhs of the top-k pattern) in place; every other index layout
+    # goes through index_prep.  Both routes must give the same bits.
+    announce("gather_direct_indices", dtype, case)
+    E, N, K, T = 8, 200, 1024, 5
+    wq, s, b = affine_experts(E, N, K, 960)
+    W, S, Bi = dev_u32(wq), dev_bf16(s), dev_bf16(b)
+    ids = topk_ids(T, E, 3, 961)
+    if case == "topk_default_lhs":
+        x = dev_bf16(orc.normal_bf16((T, 1, 1, K), 1.0, 962))
+        lhs, rhs = None, torch.from_numpy(ids.astype(np.int64)).to(dtype).cuda()
+    elif case == "explicit_lhs":
+        x = dev_bf16(orc.normal_bf16((T, 1, K), 1.0, 963))
+        lhs = torch.from_numpy(np.repeat(np.arange(T), 3).reshape(T, 3)[:, ::-1].copy()).to(dtype).cuda()
+        rhs = torch.from_numpy(ids.astype(np.int64)).to(dtype).cuda()
+    elif case == "broadcast_rhs":
+        x = dev_bf16(orc.normal_bf16((T, 3, 1, K), 1.0, 964))
+        lhs, rhs = None, torch.from_numpy(ids[0].astype(np.int64)).to(dtype).cuda()  # [3] broadcast over T
+    elif case == "strided_rhs":
+        x = dev_bf16(orc.normal_bf16((T, 1, 1, K), 1.0, 965))
+        full = torch.from_numpy(np.concatenate([ids, ids], 1).astype(np.int64)).to(dtype).cuda()
+        lhs, rhs = None, full[:, ::2]  # non-contiguous view
+    else:
+        x = dev_bf16(orc.normal_bf16((T, 1, 1, K), 1.0, 966))
+        bad = ids.astype(np.int64).copy()
+        bad[0, 0], bad[2, 1] = 50, -1  # clamped to the last expert, like index_prep
+        lhs, rhs = None, torch.from_numpy(bad).to(dtype).cuda()
+    outs = []
+    for direct in ("1", "0"):
+        monkeypatch.setenv("MLXQ_GATHER_DIRECT", direct)
+        y = mq.gather_qmm(x, W, S, Bi, lhs, rhs, True, 64, 4)
+        torch.cuda.synchronize()
+        outs.append(host_u16(y))
+    np.testing.assert_array_equal(outs[0], outs[1])
+    if case == "topk_default_lhs":
+        want = orc.gather_qmm_t(orc.normal_bf16((T, 1, K), 1.0, 962), wq, s, b,
+                                np.repeat(np.arange(T, dtype=np.uint32), 3), ids.reshape(-1))
+        assert max_rel(outs[0].reshape(T * 3, 1, N), want) <= TOL
