@@ -321,6 +321,7 @@ hipError_t b4_launch_ms(const QmvB4Plan& p, const QmvArgs& a, int gs_shift, dim3
   B4_CASE(1, 1)
   B4_CASE(2, 1)
   B4_CASE(4, 1)
+  B4_CASE(8, 1)
   B4_CASE(1, 2)
   B4_CASE(2, 2)
   B4_CASE(4, 2)
@@ -343,6 +344,7 @@ hipError_t b4_launch_fmt(const QmvB4Plan& p, const QmvArgs& a, int gs_shift, dim
 bool b4_valid(int ms, int rg, int cpw) {
   if (ms != 1 && ms != 2 && ms != 4) return false;
   if (ms == 4 && rg == 4 && cpw == 2) return false;  // spills
+  if (cpw == 1 && rg == 8) return ms <= 2;
   if (cpw == 1 || cpw == 2) return rg == 1 || rg == 2 || rg == 4;
   if (cpw == 4) return rg == 1 || rg == 2;
   if (cpw == 8) return rg == 1;
@@ -364,8 +366,10 @@ QmvB4Plan qmv_b4_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int rg_re
   if (chunks > 64) return p;
   const int xregs = p.ms * p.cpw * (kl / 8) * 4;
   if (xregs > 128) return p;
-  p.rg = p.ms == 4 ? 1 : (p.ms == 2 ? (p.cpw >= 4 ? 1 : 2) : (p.cpw >= 4 ? 8 / p.cpw : 4));
-  if (p.rg > 4) p.rg = 4;
+  // weight rows per workgroup: each lane's activations are reused across its
+  // RG weight pieces, so more rows cut the activation re-reads (L2 -> CU
+  // traffic of 64 MS bytes per lane and piece against 16 RG of weights)
+  p.rg = p.ms == 4 ? 1 : (p.ms == 2 ? (p.cpw >= 4 ? 1 : 4) : (p.cpw >= 4 ? 8 / p.cpw : (p.cpw == 1 ? 8 : 4)));
   if (cpw_req > 0) p.cpw = cpw_req;
   if (rg_req > 0) p.rg = rg_req;
   p.nw = (int)((chunks + p.cpw - 1) / p.cpw);

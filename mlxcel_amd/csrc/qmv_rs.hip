@@ -184,8 +184,9 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
             u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo[j] + (uint32_t)(m * K * 2 + v * 16), 0, 0));
 
   // Scales of this wave's chunks: for each chunk j (groups gbase[j] ..
-  // gbase[j] + gc - 1) and row r, gc / upw units of upw groups (a word when
-  // every row starts word-aligned, else a short or byte); lane L loads units
+  // gbase[j] + gc - 1) and row r, gc / upw units of upw groups (up to four
+  // groups per load when every row's scales start at a multiple of four
+  // groups, else two or one); lane L loads units
   // L, L + 64, ...  A wave reads only what it wrote itself, so no workgroup
   // barrier stands between the loads and the arithmetic.
   constexpr int upw = UPW;  // groups per unit
@@ -203,26 +204,37 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
     gl = rest & (upc - 1);
     j = min(rest >> lupc, CPW - 1);
   };
-  uint32_t sraw[SBE], braw[SBE];
+  // affine units of 4 groups are 8 bytes: words [i][0] hold groups 0-1,
+  // [i][1] groups 2-3
+  constexpr int SW = AFF && UPW == 4 ? 2 : 1;
+  uint32_t sraw[SBE][SW], braw[SBE][SW];
 #pragma unroll
   for (int i = 0; i < SBE; i++) {
-    sraw[i] = braw[i] = 0u;
+#pragma unroll
+    for (int h = 0; h < SW; h++) sraw[i][h] = braw[i][h] = 0u;
     if (i < nld) {  // wave-uniform
       int j, r, gl;
       unit_of(lane + 64 * i, j, r, gl);
       const uint32_t og = (uint32_t)((row0 + r) * G + gbase[j] + gl * upw);  // in groups
       if constexpr (AFF) {
-        if constexpr (UPW == 2) {
-          sraw[i] = __builtin_amdgcn_raw_buffer_load_b32(sr, og * 2u, 0, 0);
-          braw[i] = __builtin_amdgcn_raw_buffer_load_b32(br, og * 2u, 0, 0);
+        if constexpr (UPW == 4) {
+          const u32x2 s2 = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(sr, og * 2u, 0, 0));
+          const u32x2 b2 = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(br, og * 2u, 0, 0));
+          sraw[i][0] = s2[0];
+          sraw[i][SW - 1] = s2[1];
+          braw[i][0] = b2[0];
+          braw[i][SW - 1] = b2[1];
+        } else if constexpr (UPW == 2) {
+          sraw[i][0] = __builtin_amdgcn_raw_buffer_load_b32(sr, og * 2u, 0, 0);
+          braw[i][0] = __builtin_amdgcn_raw_buffer_load_b32(br, og * 2u, 0, 0);
         } else {
-          sraw[i] = __builtin_amdgcn_raw_buffer_load_b16(sr, og * 2u, 0, 0);
-          braw[i] = __builtin_amdgcn_raw_buffer_load_b16(br, og * 2u, 0, 0);
+          sraw[i][0] = __builtin_amdgcn_raw_buffer_load_b16(sr, og * 2u, 0, 0);
+          braw[i][0] = __builtin_amdgcn_raw_buffer_load_b16(br, og * 2u, 0, 0);
         }
       } else {
-        if constexpr (UPW == 4) sraw[i] = __builtin_amdgcn_raw_buffer_load_b32(sr, og, 0, 0);
-        else if constexpr (UPW == 2) sraw[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(sr, og, 0, 0);
-        else sraw[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(sr, og, 0, 0);
+        if constexpr (UPW == 4) sraw[i][0] = __builtin_amdgcn_raw_buffer_load_b32(sr, og, 0, 0);
+        else if constexpr (UPW == 2) sraw[i][0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(sr, og, 0, 0);
+        else sraw[i][0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(sr, og, 0, 0);
       }
     }
   }
@@ -242,14 +254,15 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
     if (i < nld && lane + 64 * i < nunits) {
       int j, r, gl;
       unit_of(lane + 64 * i, j, r, gl);
-      for (int h = 0; h < upw; h++) {
-        const int idx = (j * gc + gl * upw + h) * R + r;
+#pragma unroll
+      for (int h = 0; h < UPW; h++) {
+        const int idx = (j * gc + gl * UPW + h) * R + r;
         if constexpr (AFF) {
-          const float sc = bf16_bits_to_f32((sraw[i] >> (16 * h)) & 0xFFFFu);
-          const float bi = bf16_bits_to_f32((braw[i] >> (16 * h)) & 0xFFFFu);
+          const float sc = bf16_bits_to_f32((sraw[i][h >> 1] >> (16 * (h & 1))) & 0xFFFFu);
+          const float bi = bf16_bits_to_f32((braw[i][h >> 1] >> (16 * (h & 1))) & 0xFFFFu);
           reinterpret_cast<float2*>(wsl)[idx] = float2{sc, FMT == AFF4 ? __builtin_fmaf(-128.0f, sc, bi) : bi};
         } else {
-          reinterpret_cast<float*>(wsl)[idx] = e8m0_to_f32((sraw[i] >> (8 * h)) & 0xFFu);
+          reinterpret_cast<float*>(wsl)[idx] = e8m0_to_f32((sraw[i][0] >> (8 * h)) & 0xFFu);
         }
       }
     }
@@ -389,7 +402,7 @@ hipError_t rs_launch_upw(const QmvRsPlan& p, const QmvArgs& a, int gs_shift, dim
 
 // scale groups per load: the widest load every row's scales stay aligned for
 int rs_upw(int fmt, int64_t G) {
-  if (fmt != MXFP4) return (G & 1) ? 1 : 2;
+  (void)fmt;
   return (G & 3) ? ((G & 1) ? 1 : 2) : 4;
 }
 
@@ -397,7 +410,7 @@ template <int FMT>
 hipError_t rs_launch_fmt(const QmvRsPlan& p, const QmvArgs& a, int gs_shift, dim3 grid, hipStream_t stream) {
   const int upw = rs_upw(FMT, (int64_t)a.K >> gs_shift);
   if (upw == 1) return rs_launch_upw<FMT, 1>(p, a, gs_shift, grid, stream);
-  if (FMT == MXFP4 && upw == 4) return rs_launch_upw<FMT, 4>(p, a, gs_shift, grid, stream);
+  if (upw == 4) return rs_launch_upw<FMT, 4>(p, a, gs_shift, grid, stream);
   return rs_launch_upw<FMT, 2>(p, a, gs_shift, grid, stream);
 }
 

@@ -19,7 +19,7 @@ from helpers import TOL, affine_case, announce, dev_bf16, dev_u32, dev_u8, host_
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(1, 1), (2, 1), (4, 1), (1, 2), (2, 2), (4, 2), (1, 4), (2, 4), (1, 8)]  # (row groups, chunks/wave)
+SHAPES = [(1, 1), (2, 1), (4, 1), (8, 1), (1, 2), (2, 2), (4, 2), (1, 4), (2, 4), (1, 8)]  # (row groups, chunks/wave)
 
 
 def affine(x, wq, s, b, gs, bits):
