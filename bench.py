@@ -5,23 +5,29 @@ the Llama-3-8B MLP decode projections at M=1, 4-bit affine, group 64:
 gate (N=14336, K=4096), up (same) and down (N=4096, K=14336), three qmv
 launches of 33,067,008 algorithmic bytes each (packed W + bf16 scales +
 bf16 biases + x + y).  Weights rotate across 8 distinct layers (~793 MB) so
-every launch streams from HBM, not the 256 MB MALL.  Each layer's step is one
-HIP graph, so the timed region holds GPU work only; `value` = algorithmic
-bytes / time over K timed steps (HIP events on the replay stream).
+every launch streams from HBM, not the 256 MB MALL.  The steps of the 8
+layers are one HIP graph (as a decode step's graph holds every layer), so the
+timed region holds GPU work only; `value` = algorithmic bytes / time over
+exactly K timed steps (HIP events on the replay stream).
 `roofline` is the gate kernel alone: bytes per launch / its average launch
-duration, timed the same way.
+duration, timed the same way; `roofline.read_ceiling` is the fastest plain
+streaming read of the same bytes per launch on this device, timed the same
+way (the practical bound at this size).
 
-Also reported (extra): the M in {1,2,4,8} x {4,8}-bit decode sweep, mxfp4
-gather_qmm (gpt-oss-20b MoE shapes), the measured device copy ceiling, and
-the single-core CPU baseline (the oracle's restatement of MLX's CPU
-`_qmm_t`, overlays/cpu/mlx/backend/cpu/quantized.cpp:199-257).
+Also reported (extra): the M in {1,2,4,8,16} x {4,8}-bit decode sweep, the
+qmm prefill configs, mxfp4 gather_qmm (gpt-oss-20b MoE shapes), end-to-end
+decode of a Qwen3-8B-shaped model, the measured device copy ceiling, and the
+single-core CPU baseline (the oracle's restatement of MLX's CPU `_qmm_t`,
+overlays/cpu/mlx/backend/cpu/quantized.cpp:199-257).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+                       [--extras copy,sweep,qmm,gather,e2e]
        python bench.py --traffic-probe   (under rocprofv3 --pmc: copy calibration + gate launches)
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -41,10 +47,11 @@ BF16_PEAK_TFLOPS = 2500.0  # dense
 MALL_BYTES = 256 << 20
 # HBM bytes per gate launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on
 # `bench.py --traffic-probe`, each counter scaled by what it reads for a
-# device copy of exactly 256 MiB (FETCH_SIZE x 1.9998, WRITE_SIZE x 1.0):
-# 16433.6 KiB fetched + 56 KiB written per launch (profiles/
-# qmv_rs_gate_m1_traffic.txt).  Re-measure when the kernel changes.
-TRAFFIC_GATE = 33_709_700
+# device copy of exactly 256 MiB (FETCH_SIZE x 1.999798, WRITE_SIZE x 1.0):
+# 16209.3 KiB fetched + 56 KiB written per launch (profiles/
+# qmv_rs_gate_m1_traffic.txt), 1.0056 x the algorithmic bytes.  Re-measure
+# when the kernel changes.
+TRAFFIC_GATE = 33_250_656
 
 
 def qmv_bytes(M, N, K, bits, gs):
@@ -109,10 +116,9 @@ def timed_graphs(graphs, iters, warmup):
 
 def headline(steps, warmup, layers=8):
     """One step = gate, up and down of one layer; steps rotate over `layers`
-    layers so every launch streams its weights from HBM.  Each layer's step is
-    one HIP graph (three kernel launches), so the timed region holds only GPU
-    work.  Returns (GB/s, ms per step, avg us per launch, bytes per launch,
-    gate us per launch, one gate matrix)."""
+    layers so every launch streams its weights from HBM.  The timed region
+    replays HIP graphs only (GPU work only).  Returns (GB/s, ms per step, avg
+    us per launch, bytes per launch, gate us per launch, one gate matrix)."""
     K1, N1 = 4096, 14336
     mlp = []
     for l in range(layers):
@@ -135,14 +141,39 @@ def headline(steps, warmup, layers=8):
             mq.quantized_matmul(h, *down, True, 64, 4, out=out_d)
         return f
 
-    graphs = [capture(step_fn(l)) for l in range(layers)]
-    ms = timed_graphs(graphs, steps, warmup)
+    # one graph runs the steps of all `layers` layers back to back, as a decode
+    # step's graph runs every layer; a second graph holds the first
+    # steps % layers of them, so exactly `steps` steps are timed
+    def run(n):
+        def f():
+            for l in range(n):
+                step_fn(l)()
+        return f
+
+    full = capture(run(layers))
+    rem = steps % layers
+    part = capture(run(rem)) if rem else None
+    for _ in range(max(1, warmup // layers)):
+        full.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(steps // layers):
+        full.replay()
+    if part is not None:
+        part.replay()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
     per_launch = qmv_bytes(1, N1, K1, 4, 64)
     assert per_launch == qmv_bytes(1, K1, N1, 4, 64) == 33_067_008
     value = 3 * per_launch / (ms * 1e-3) / 1e9
     # the dominant kernel alone: the gate projection (row-streaming qmv), one
     # graph of `layers` back-to-back launches over distinct weights, timed on
-    # the replay stream (kernel-trace shows no gap between these launches)
+    # the replay stream (rocprofv3's kernel trace of the same command gives the
+    # kernel bodies alone; the two agree within ~2%)
     gate_graph = capture(lambda: [mq.quantized_matmul(x, *mlp[l][0], True, 64, 4, out=out_g) for l in range(layers)])
     reps = max(1, steps // layers)
     gate_us = timed_graphs([gate_graph], reps, max(1, warmup // layers)) * 1e3 / layers
@@ -150,6 +181,40 @@ def headline(steps, warmup, layers=8):
 
 
 # ---- extras -------------------------------------------------------------------
+
+def read_ceiling(nbytes=33_067_008, reps=40):
+    """Fastest streaming read of `nbytes` per launch on this device: a plain
+    16-byte-load kernel (mlxcel_amd/csrc/bench_read.hip) that folds what it
+    reads with xor and writes nothing, timed like the gate kernel (one graph
+    of back-to-back launches over distinct buffers that together overflow the
+    MALL).  The best of a few launch shapes is the practical HBM bound for a
+    decode projection of that size; it sits well below the 8 TB/s spec."""
+    lib = ctypes.CDLL(os.path.join(ROOT, "mlxcel_amd", "libmlxq_bench.so"))
+    lib.mlxq_bench_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_void_p]
+    lib.mlxq_bench_read.restype = ctypes.c_int
+    copies = max(2, math.ceil(2.4 * MALL_BYTES / nbytes))
+    bufs = [torch.full((nbytes,), c + 1, dtype=torch.uint8, device="cuda") for c in range(copies)]
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    best = None
+    for wgs, thr in ((1024, 256), (2048, 256), (1024, 512), (4096, 512)):
+        def launch_all(wgs=wgs, thr=thr):
+            st = torch.cuda.current_stream().cuda_stream
+            for b in bufs:
+                rc = lib.mlxq_bench_read(b.data_ptr(), nbytes, sink.data_ptr(), wgs, thr, st)
+                if rc != 0:
+                    raise RuntimeError(f"mlxq_bench_read failed: {rc}")
+        g = capture(launch_all)
+        us = timed_graphs([g], reps, 3) * 1e3 / copies
+        if best is None or us < best[0]:
+            best = (us, wgs, thr)
+        del g
+    del bufs
+    us, wgs, thr = best
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"bytes": nbytes, "us": round(us, 3), "GBps": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3),
+            "workgroups": wgs, "threads": thr}
+
 
 def copy_ceiling():
     n = 1 << 30
@@ -161,14 +226,15 @@ def copy_ceiling():
 
 def qmv_sweep(iters=200):
     """Decode sweep: M in {1,2,4,8} x {4,8}-bit at the
-    Llama-3-8B MLP shapes; one graph launches every weight copy once."""
+    Llama-3-8B MLP shapes, plus M=16 (the batch-16 decode of configs[4]); one
+    graph launches every weight copy once."""
     res = []
     for bits in (4, 8):
         for (N, K, name) in ((14336, 4096, "gate_up"), (4096, 14336, "down")):
             wbytes = qmv_bytes(0, N, K, bits, 64)
             copies = max(2, math.ceil(2.4 * MALL_BYTES / wbytes))
             ws = [make_affine(N, K, bits, 64, 50 + c) for c in range(copies)]
-            for M in (1, 2, 4, 8):
+            for M in (1, 2, 4, 8, 16):
                 x = randn_bf16((M, K), 9)
                 out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
                 g = capture(lambda: [mq.quantized_matmul(x, *w, True, 64, bits, out=out) for w in ws])
@@ -491,6 +557,8 @@ def main():
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--extras", default="copy,sweep,qmm,gather,e2e",
+                    help="comma-separated extra sections: copy, sweep, qmm, gather, e2e")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run 5 copies of 256 MiB and 5 gate launches, eager, for rocprofv3 --pmc")
@@ -508,6 +576,7 @@ def main():
 
     value, ms, launch_us, per_launch, gate_us, gate = headline(args.steps, args.warmup)
     achieved = per_launch / (gate_us * 1e-6) / 1e9
+    ceiling = read_ceiling(per_launch)
     line = {
         "metric": "qmv HBM GB/s at M=1 (4-bit affine g64, Llama-3-8B MLP decode projections)",
         "value": round(value, 1),
@@ -526,15 +595,23 @@ def main():
                    "bytes_per_step": 3 * per_launch, "avg_us_per_launch": round(launch_us, 3)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_GATE,
-                     "kernel": "qmv_rs_kernel<AFF4,1,8,1> (gate, N=14336 K=4096 M=1)",
-                     "bytes_per_launch": per_launch, "avg_launch_us": round(gate_us, 3)},
+                     "kernel": "qmv_rs_kernel<AFF4, MR=1, R=8, CPW=1, UPW=4> (gate, N=14336 K=4096 M=1)",
+                     "bytes_per_launch": per_launch, "avg_launch_us": round(gate_us, 3),
+                     "read_ceiling": ceiling, "frac_of_read_ceiling": round(achieved / ceiling["GBps"], 3)},
     }
     if not args.no_extra:
-        extra = {"copy_ceiling_GBps": round(copy_ceiling(), 1)}
-        extra["qmv_sweep"] = qmv_sweep()
-        extra["qmm_prefill"] = qmm_prefill()
-        extra["gather_mxfp4_moe"] = gather_moe()
-        extra["e2e_decode_qwen3_8b_shape"] = e2e_decode()
+        want = set(args.extras.split(","))
+        extra = {}
+        if "copy" in want:
+            extra["copy_ceiling_GBps"] = round(copy_ceiling(), 1)
+        if "sweep" in want:
+            extra["qmv_sweep"] = qmv_sweep()
+        if "qmm" in want:
+            extra["qmm_prefill"] = qmm_prefill()
+        if "gather" in want:
+            extra["gather_mxfp4_moe"] = gather_moe()
+        if "e2e" in want:
+            extra["e2e_decode_qwen3_8b_shape"] = e2e_decode()
         line["extra"] = extra
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(gate)
