@@ -41,6 +41,7 @@ SOURCES = {
     "qmv_rs.hip": [],
     "qmv_fr.hip": [],
     "qmv_b4.hip": [],
+    "qmv_mid.hip": [],
     "qmm.hip": [],
     "dequant.hip": ["-ffp-contract=off"],
 }

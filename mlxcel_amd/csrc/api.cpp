@@ -582,6 +582,11 @@ enum class Skinny { FR, RS, B4, MFMA };
 // at 9-16 rows its 128 x 128 tiles already beat the skinny kernels on
 // MI355X (MLXQ_QMM_MIN_ROWS overrides, for tests and measurements).
 constexpr int kQmmMinRows = 9;
+// The mid-size decode kernel takes 9-16 rows, and 5-8 rows over long rows
+// (K > 8192), where it beats the block-MFMA and skinny-MFMA kernels (MI355X,
+// Llama-3-8B MLP shapes: 4-bit gate M=16 22 us vs 40, down M=8 20 us vs 34).
+constexpr int kMidMinRows = 9;
+constexpr int kMidMinRowsLongK = 5;
 
 // Defaults measured at the Llama-3-8B MLP shapes (gate K=4096, down
 // K=14336): row-streaming up to 4 rows; block-MFMA for 5-8 rows of 8-bit
@@ -600,6 +605,18 @@ Skinny skinny_choice(int rows, int fmt = mlxq::AFF4, int64_t K = 0) {
   if (rows <= 4) return Skinny::RS;
   if (rows <= 8 && (fmt != mlxq::AFF4 || K <= 8192)) return Skinny::B4;
   return Skinny::MFMA;
+}
+
+// Dense (2-D weight) calls of `rows` activation rows that the mid-size decode
+// kernel takes (affine only): MLXQ_QMV_KERNEL=mid forces it (up to 16 rows),
+// another MLXQ_QMV_KERNEL value or MLXQ_QMV_MID=0 keeps it off.
+bool use_mid(int rows, int fmt, int64_t K) {
+  if (fmt == mlxq::MXFP4 || rows > 16) return false;
+  const char* k = std::getenv("MLXQ_QMV_KERNEL");
+  if (k && std::strcmp(k, "mid") == 0) return true;
+  if (k && *k) return false;
+  if (env_int("MLXQ_QMV_MID", 1) == 0) return false;
+  return rows >= kMidMinRows || (rows >= kMidMinRowsLongK && K > 8192);
 }
 
 // Launches the full-row or row-streaming kernel when chosen and covered;
@@ -712,6 +729,31 @@ mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w, cons
     const int fmt = fmt_of(sp.mode, sp.bits);
     const int cap = mlxq::qmv_max_rows(fmt, sp.gs);
     View wv{w}, xv{x};
+    if (wv.ndim() == 2 && rows_total <= 16 && use_mid((int)rows_total, fmt, sp.K)) {
+      // 5-16 rows: activations staged once per 128 weight rows (qmv_mid.hip)
+      const int dev = current_device();
+      const mlxq::QmvMidPlan mp = mlxq::qmv_mid_plan(fmt, sp.gs, sp.N, sp.K, (int)rows_total);
+      if (mp.ok) {
+        mlxq::QmvMidArgs m{};
+        m.x = a.x;
+        m.w = a.w;
+        m.scales = static_cast<const uint16_t*>(a.scales);
+        m.biases = a.biases;
+        m.out = a.out;
+        m.M = (int)rows_total;
+        m.N = (int)sp.N;
+        m.K = (int)sp.K;
+        int shift = 0;
+        while ((1 << shift) < sp.gs) shift++;
+        m.gs_shift = shift;
+        m.ks = mp.ks;
+        if (mp.ks > 1)
+          m.ws = reinterpret_cast<float*>(
+              workspace(dev, stream, (size_t)mp.ks * rows_total * sp.N * sizeof(float)).data);
+        hip_check(mlxq::qmv_mid_launch(fmt, m, mp, stream), "qmv_mid launch");
+        return;
+      }
+    }
     if (wv.ndim() == 2 && rows_total >= env_int("MLXQ_QMM_MIN_ROWS", kQmmMinRows)) {
       // prefill: one GEMM over all rows (every leading dim of x folds into rows)
       const int dev = current_device();

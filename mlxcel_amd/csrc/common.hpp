@@ -63,23 +63,24 @@ __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
 // ---- unpack one 32-bit word of codes into an MFMA bf16 operand fragment ----
 //
 // AFF4: 8 nibbles -> 8 bf16 "128 + q" (0x4300 | q is exactly 128+q in bf16),
-// two per VGPR with a single and-or: VGPR p = (nibble p, nibble p+4).  The
-// matching activation fragment is stored permuted the same way
-// ([x0,x4,x1,x5,x2,x6,x3,x7]); the caller removes the 128*sum(x) offset.
-// v_and_or_b32 is written out because VOP3 cannot encode the two literal
-// masks: the compiler would otherwise emit a separate and + or per pair.
-__device__ __forceinline__ uint32_t and_or_b32(uint32_t a, uint32_t vmask, uint32_t sor) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(vmask), "s"(sor));
-  return r;
-}
-
+// two per VGPR: VGPR p = (nibble p, nibble p+4).  The matching activation
+// fragment is stored permuted the same way ([x0,x4,x1,x5,x2,x6,x3,x7]); the
+// caller removes the 128*sum(x) offset.  The nibbles are split into bytes
+// (lo: nibbles 0,2,4,6; hi: 1,3,5,7) and each pair is one v_perm_b32 that
+// interleaves two of those bytes with 0x43 bytes: 7 instructions per word,
+// all of them ordinary VALU operations the compiler schedules and sees.  (A
+// hand-written v_and_or_b32 does the same in 7 too, but inline assembly is
+// invisible to the compiler's hazard checks: it inserted no wait states
+// between such a write and an MFMA reading the result, and the MFMA then read
+// stale operands.)
 __device__ __forceinline__ void unpack_aff4(uint32_t w, uint32_t (&v)[4]) {
-  const uint32_t mask = 0x000F000Fu;  // kept in a VGPR by the constraint above
-  v[0] = and_or_b32(w, mask, 0x43004300u);
-  v[1] = and_or_b32(w >> 4, mask, 0x43004300u);
-  v[2] = and_or_b32(w >> 8, mask, 0x43004300u);
-  v[3] = and_or_b32(w >> 12, mask, 0x43004300u);
+  const uint32_t lo = w & 0x0F0F0F0Fu;
+  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
+  const uint32_t c = 0x43434343u;
+  v[0] = __builtin_amdgcn_perm(c, lo, 0x04020400u);  // (n0, n4): bytes lo.0, 0x43, lo.2, 0x43
+  v[1] = __builtin_amdgcn_perm(c, hi, 0x04020400u);  // (n1, n5)
+  v[2] = __builtin_amdgcn_perm(c, lo, 0x04030401u);  // (n2, n6)
+  v[3] = __builtin_amdgcn_perm(c, hi, 0x04030401u);  // (n3, n7)
 }
 
 // MXFP4: 8 e2m1 codes -> 8 bf16 in natural order using the gfx950 FP4

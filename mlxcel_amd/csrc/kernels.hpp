@@ -98,6 +98,37 @@ struct QmvB4Plan {
 QmvB4Plan qmv_b4_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int rg_req, int cpw_req);
 hipError_t qmv_b4_launch(int fmt, int gs, const QmvArgs& a, int nseg, const QmvB4Plan& p, hipStream_t stream);
 
+// Mid-size decode (qmv_mid.hip): 1-16 activation rows against one affine
+// 4/8-bit weight matrix; workgroups of 128 weight rows x one K range of 8
+// windows; fp32 partials of several K ranges are added by launch_splitk_reduce.
+struct QmvMidArgs {
+  const uint16_t* x;       // bf16 [M][K]
+  const uint32_t* w;       // packed codes [N][K*bits/32]
+  const uint16_t* scales;  // bf16 [N][K/gs]
+  const uint16_t* biases;  // bf16 [N][K/gs]
+  uint16_t* out;           // bf16 [M][N]
+  float* ws;               // fp32 partials [ks][M][N] (ks > 1)
+  int M, N, K, gs_shift;
+  int ks;                  // K ranges (gridDim.y)
+};
+struct QmvMidLds {
+  int xpitch = 0;  // bf16 per staged activation row
+  uint32_t xl = 0, xs = 0, sc = 0, zero = 0, total = 0;  // byte offsets / size
+};
+struct QmvMidPlan {
+  bool ok = false;
+  int s = 1;           // quantization groups per 4-chunk window
+  int na = 1;          // 16-row MFMA A tiles (activation row x group slot)
+  int row_blocks = 0;  // workgroups along N (128 weight rows each)
+  int kr = 0;          // K per workgroup
+  int ks = 1;          // workgroups along K
+  int sw = 8;          // scale groups per staging load
+  size_t lds = 0;
+};
+QmvMidPlan qmv_mid_plan(int fmt, int gs, int64_t N, int64_t K, int rows);
+// Launches the kernel and, with several K ranges, the fixed-order reduction.
+hipError_t qmv_mid_launch(int fmt, const QmvMidArgs& a, const QmvMidPlan& p, hipStream_t stream);
+
 // Full-row decode kernel (qmv_fr.hip) for 1 or 2 activation rows per weight
 // matrix: 8 waves per workgroup, R whole rows per wave, activations staged in
 // LDS once per workgroup.

@@ -1,0 +1,388 @@
+// qmv_mid.hip — decode kernel for 5 to 16 activation rows per weight matrix
+// (affine 4/8-bit) on gfx950.
+//
+// Same product as the other decode kernels (reference decode route: overlays/
+// rocm/mlx/backend/rocm/quantized/qmv_tiled_kernel.hip:29-128; CPU math
+// overlays/cpu/mlx/backend/cpu/quantized.cpp:199-257): y[m,n] = sum_g s[n,g] *
+// sum_{k in g} x[m,k] q[n,k] + b[n,g] * sum_{k in g} x[m,k], fp32
+// accumulation, one bf16 rounding on store.
+//
+// Why a kernel of its own: at 16 activation rows the activations weigh 32
+// bytes per k against 8 bytes per k for 16 rows of 4-bit codes, so a kernel
+// that reloads them for every 16 weight rows moves several times more
+// activation bytes (L2 -> CU) than weight bytes (HBM -> CU).  Here a
+// workgroup owns 128 weight rows and one K range: it stages that range of the
+// activations, their group sums and the rows' scales in LDS once, and its
+// four waves (two 16-row tiles each) stream the weights past them.
+//
+// Products: v_mfma_f32_16x16x32_bf16 with the weights as the B operand (lane i
+// holds weight row i % 16, 16-byte code chunk i / 16 of a 4-chunk window) and
+// the activations as A.  A window holds S quantization groups (S = window /
+// group size, at least 1); A row r carries activation row r / S restricted to
+// the chunks of group r % S and zeros elsewhere, so an MFMA never mixes groups
+// and the fold y += s * D + (b - 128 s) * sum(x) (AFF4 "128 + q" codes; AFF8
+// codes are the bytes themselves, so b) runs once per output, window and
+// group.  The activations are staged permuted to the AFF4 pair order
+// ([x0,x4,x1,x5,x2,x6,x3,x7] per 8) so the codes widen with one and-or per
+// pair.
+//
+// Each workgroup covers a K range of 8 windows (1024 k for 4-bit, 512 for
+// 8-bit); every wave keeps 4 windows of weight loads in flight per tile.  K ranges
+// of one row block write fp32 partials that a second kernel adds in a fixed
+// order (bitwise reproducible).  (A last-workgroup-adds-them variant needs a
+// device-scope release/acquire per workgroup, which on MI355X writes back and
+// invalidates the XCD's L2: it measured ~50 us per launch.)
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace mlxq {
+
+namespace {
+
+constexpr int MID_NW = 4;                      // waves per workgroup
+constexpr int MID_T = 2;                       // 16-row tiles per wave
+constexpr int MID_ROWS = MID_NW * MID_T * 16;  // weight rows per workgroup
+constexpr int MID_WIN = 8;                     // windows per workgroup
+constexpr int MID_P = 4;                       // windows of weight loads in flight per tile
+constexpr int MID_NT = 64 * MID_NW;            // threads per workgroup
+constexpr uint32_t kDeadMid = 0x80000000u;     // a buffer offset past every operand: loads return 0
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t mid_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ float dot2m(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+}
+
+// [x0..x7] (bf16, 4 words) -> [x0,x4,x1,x5,x2,x6,x3,x7]
+__device__ __forceinline__ u32x4 perm_aff4_mid(u32x4 x) {
+  return u32x4{__builtin_amdgcn_perm(x[2], x[0], 0x05040100u), __builtin_amdgcn_perm(x[2], x[0], 0x07060302u),
+               __builtin_amdgcn_perm(x[3], x[1], 0x05040100u), __builtin_amdgcn_perm(x[3], x[1], 0x07060302u)};
+}
+
+}  // namespace
+
+__host__ __device__ inline QmvMidLds qmv_mid_lds(int fmt, int gs, int kr, int na) {
+  const int kw = fmt == AFF8 ? 64 : 128;
+  QmvMidLds l;
+  l.xpitch = kr + 8;  // bf16 per staged activation row (16 bytes of padding shift rows across banks)
+  l.xl = 0;
+  l.xs = l.xl + 16u * (uint32_t)l.xpitch * 2u;
+  l.sc = l.xs + (uint32_t)(kr / kw) * 16u * (uint32_t)na * 4u;
+  l.zero = l.sc + (uint32_t)MID_ROWS * (uint32_t)(kr / gs) * 8u;
+  l.total = l.zero + 16u;
+  return l;
+}
+
+// FMT: AFF4 or AFF8; S: quantization groups per window; NA: 16-row A tiles
+// (16 NA >= rows * S); SW: scale groups per staging load (8 or 2).
+template <int FMT, int S, int NA, int SW>
+__global__ __launch_bounds__(MID_NT) void qmv_mid_kernel(const QmvMidArgs a) {
+  constexpr int CK = FMT == AFF8 ? 16 : 32;  // k per 16-byte code chunk
+  constexpr int KW = 4 * CK;                 // k per window (4 chunks)
+  constexpr int NQ = CK / 8;                 // MFMAs per window, tile and A tile
+  constexpr int XG = KW / S;                 // k per group slot of a window
+  constexpr int YV = 4 / S;                  // activation rows per lane and A tile after the fold
+  constexpr int KR = MID_WIN * KW;           // k per workgroup
+  constexpr int XPMAX = 16 * KR / 8 / MID_NT;  // activation pieces per thread, upper bound
+  constexpr int SPMAX = SW == 8 ? 2 : 4;     // scale loads per thread and operand, upper bound (checked on the host)
+
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int M = a.M;
+  const int N = a.N;
+  const int K = a.K;
+  constexpr int kr = KR;
+  const int rb = blockIdx.x;
+  const int sp = blockIdx.y;
+  const int k0 = sp * kr;
+  constexpr int nwin = MID_WIN;  // every split is a full K range (K % KR == 0)
+  const int G = K >> a.gs_shift;
+  const int ngr = kr >> a.gs_shift;  // groups per K range
+  const int row_wg = rb * MID_ROWS;
+  const QmvMidLds L = qmv_mid_lds(FMT, 1 << a.gs_shift, kr, NA);
+
+  const uint32_t RB = (uint32_t)(K / CK) * 16u;  // bytes per weight row
+  const __amdgpu_buffer_rsrc_t wr = mid_rsrc(a.w, (uint32_t)N * RB);
+  const __amdgpu_buffer_rsrc_t xr = mid_rsrc(a.x, (uint32_t)M * (uint32_t)K * 2u);
+  const __amdgpu_buffer_rsrc_t sr = mid_rsrc(a.scales, (uint32_t)N * (uint32_t)G * 2u);
+  const __amdgpu_buffer_rsrc_t br = mid_rsrc(a.biases, (uint32_t)N * (uint32_t)G * 2u);
+
+  // ---- 1. loads: activation range, the block's scales, then the first
+  // windows of weights (the staged data is consumed first; loads retire in
+  // order) ---------------------------------------------------------------------
+  const int xpieces = M * (kr / 8);
+  u32x4 xpre[XPMAX];
+#pragma unroll
+  for (int i = 0; i < XPMAX; i++) {
+    const int p = tid + i * MID_NT;
+    const int m = p / (kr / 8), c = p % (kr / 8);
+    const uint32_t o = p < xpieces ? (uint32_t)(m * K + k0 + 8 * c) * 2u : kDeadMid;
+    xpre[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, o, 0, 0));
+  }
+  const int sunits = MID_ROWS * ngr / SW;  // per operand
+  u32x4 spre[SPMAX], bpre[SPMAX];
+#pragma unroll
+  for (int i = 0; i < SPMAX; i++) {
+    const int u = tid + i * MID_NT;
+    const int r = u / (ngr / SW), gl = (u % (ngr / SW)) * SW;
+    const int n = row_wg + r;
+    const uint32_t o = (u < sunits && n < N) ? (uint32_t)(n * G + (k0 >> a.gs_shift) + gl) * 2u : kDeadMid;
+    if constexpr (SW == 8) {
+      spre[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, o, 0, 0));
+      bpre[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(br, o, 0, 0));
+    } else {
+      spre[i] = u32x4{__builtin_amdgcn_raw_buffer_load_b32(sr, o, 0, 0), 0u, 0u, 0u};
+      bpre[i] = u32x4{__builtin_amdgcn_raw_buffer_load_b32(br, o, 0, 0), 0u, 0u, 0u};
+    }
+  }
+
+  // weight tiles of this wave: rows row_wg + wave*32 + t*16 + (lane & 15);
+  // lane's chunk in a window: lane >> 4
+  const int nl = lane & 15;
+  const int g = lane >> 4;
+  uint32_t woff[MID_T];
+#pragma unroll
+  for (int t = 0; t < MID_T; t++) {
+    const int n = row_wg + wave * (MID_T * 16) + t * 16 + nl;
+    woff[t] = n < N ? (uint32_t)n * RB + (uint32_t)(k0 / CK + g) * 16u : kDeadMid;
+  }
+  u32x4 wbuf[MID_P][MID_T];
+#pragma unroll
+  for (int p = 0; p < MID_P; p++)
+#pragma unroll
+    for (int t = 0; t < MID_T; t++)
+      wbuf[p][t] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, woff[t] == kDeadMid ? kDeadMid : woff[t] + p * 64u, 0,
+                                                       2 /* nt */));
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- 2. stage activations (AFF4 pair order), scales, a zero piece ---------
+  uint16_t* xl = reinterpret_cast<uint16_t*>(smem + L.xl);
+#pragma unroll
+  for (int i = 0; i < XPMAX; i++) {
+    const int p = tid + i * MID_NT;
+    if (p < xpieces) {
+      const int m = p / (kr / 8), c = p % (kr / 8);
+      const u32x4 v = FMT == AFF4 ? perm_aff4_mid(xpre[i]) : xpre[i];
+      *reinterpret_cast<u32x4*>(xl + m * L.xpitch + 8 * c) = v;
+    }
+  }
+  float2* sl = reinterpret_cast<float2*>(smem + L.sc);
+#pragma unroll
+  for (int i = 0; i < SPMAX; i++) {
+    const int u = tid + i * MID_NT;
+    if (u < sunits) {
+      const int r = u / (ngr / SW), gl = (u % (ngr / SW)) * SW;
+#pragma unroll
+      for (int h = 0; h < SW; h++) {
+        const uint32_t sb = (spre[i][h >> 1] >> (16 * (h & 1))) & 0xFFFFu;
+        const uint32_t bb = (bpre[i][h >> 1] >> (16 * (h & 1))) & 0xFFFFu;
+        const float s = bf16_bits_to_f32(sb), b = bf16_bits_to_f32(bb);
+        sl[r * ngr + gl + h] = float2{s, FMT == AFF4 ? __builtin_fmaf(-128.0f, s, b) : b};
+      }
+    }
+  }
+  if (tid == 0) *reinterpret_cast<u32x4*>(smem + L.zero) = u32x4{0u, 0u, 0u, 0u};
+  __syncthreads();
+
+  // group sums of the activations: xs[w][r] = sum of row r / S over slot r % S
+  // of window w (zero for rows past M)
+  float* xsl = reinterpret_cast<float*>(smem + L.xs);
+  for (int e = tid; e < nwin * 16 * NA; e += MID_NT) {
+    const int w = e / (16 * NA), r = e % (16 * NA);
+    const int m = r / S, slot = r % S;
+    float s = 0.f;
+    if (m < M) {
+      const uint16_t* src = xl + m * L.xpitch + w * KW + slot * XG;
+      for (int c = 0; c < XG; c += 8) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(src + c);
+        s = dot2m(v[0], 0x3F803F80u, s);
+        s = dot2m(v[1], 0x3F803F80u, s);
+        s = dot2m(v[2], 0x3F803F80u, s);
+        s = dot2m(v[3], 0x3F803F80u, s);
+      }
+    }
+    xsl[e] = s;
+  }
+  __syncthreads();
+
+  // ---- 3. windows: A from LDS, B from the weight ring, fold per group -------
+  // A operand of lane (row r = lane & 15, chunk g) for A tile a: activation
+  // row (16a + r) / S if chunk g belongs to slot (16a + r) % S, else the zero
+  // piece.  Addresses advance by wstep per window and qstep per MFMA.
+  const int slot_g = (g * CK) / XG;  // slot of this lane's chunk
+  uint32_t abase[NA], wstep[NA], qstep[NA];
+#pragma unroll
+  for (int t = 0; t < NA; t++) {
+    const int r = 16 * t + nl;
+    const int m = r / S, slot = r % S;
+    const bool live = m < M && slot == slot_g;
+    abase[t] = live ? L.xl + (uint32_t)(m * L.xpitch + g * CK) * 2u : L.zero;
+    wstep[t] = live ? KW * 2u : 0u;
+    qstep[t] = live ? 16u : 0u;
+  }
+  // fold rows of this lane: D row 4 * g + i of A tile a is activation row
+  // (16a + 4g + i) / S, slot (16a + 4g + i) % S
+  float y[MID_T][NA][YV];
+#pragma unroll
+  for (int t = 0; t < MID_T; t++)
+#pragma unroll
+    for (int u = 0; u < NA; u++)
+#pragma unroll
+      for (int j = 0; j < YV; j++) y[t][u][j] = 0.f;
+
+  const uint32_t srow0 = L.sc + (uint32_t)((wave * MID_T * 16 + nl) * ngr) * 8u;  // this lane's row, tile 0
+  const int gsh = a.gs_shift;
+
+  {
+#pragma unroll
+    for (int w = 0; w < MID_WIN; w++) {
+      bf16x8 A[NA][NQ];
+#pragma unroll
+      for (int t = 0; t < NA; t++)
+#pragma unroll
+        for (int q = 0; q < NQ; q++)
+          A[t][q] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(smem + abase[t] + (uint32_t)w * wstep[t] +
+                                                                                (uint32_t)q * qstep[t]));
+      f32x4 xsv[NA];
+#pragma unroll
+      for (int t = 0; t < NA; t++) xsv[t] = *reinterpret_cast<const f32x4*>(xsl + w * 16 * NA + 16 * t + 4 * g);
+      // first group of this window (groups of one window are consecutive)
+      const int grp0 = (w * KW) >> gsh;
+#pragma unroll
+      for (int t = 0; t < MID_T; t++) {
+        // ring slot w % MID_P: take window w, refill it with window w + MID_P
+        const u32x4 wv = wbuf[w % MID_P][t];
+        if (w + MID_P < MID_WIN)
+          wbuf[w % MID_P][t] = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         wr, woff[t] == kDeadMid ? kDeadMid : woff[t] + (uint32_t)(w + MID_P) * 64u, 0, 2 /* nt */));
+        bf16x8 B[NQ];
+        if constexpr (FMT == AFF4) {
+#pragma unroll
+          for (int q = 0; q < NQ; q++) {
+            uint32_t pr[4];
+            unpack_aff4(wv[q], pr);
+            B[q] = as_bf16x8(pr);
+          }
+        } else {
+          uint32_t pr[4];
+          unpack_aff8(wv[0], wv[1], pr);
+          B[0] = as_bf16x8(pr);
+          unpack_aff8(wv[2], wv[3], pr);
+          B[1] = as_bf16x8(pr);
+        }
+        // scale pairs (s, b') of this lane's weight row for the window's slots
+        float2 sc[S];
+        const unsigned char* sp0 = smem + srow0 + (uint32_t)((t * 16 * ngr + grp0) * 8);
+#pragma unroll
+        for (int h = 0; h < S; h++) sc[h] = reinterpret_cast<const float2*>(sp0)[h];
+#pragma unroll
+        for (int u = 0; u < NA; u++) {
+          f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int q = 0; q < NQ; q++) d = mfma16x16x32(A[u][q], B[q], d);
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const int slot = (4 * g + i) % S;  // 16u is a multiple of S
+            y[t][u][i / S] = __builtin_fmaf(sc[slot].x, d[i], __builtin_fmaf(sc[slot].y, xsv[u][i], y[t][u][i / S]));
+          }
+        }
+      }
+      // one window at a time: hoisting the operand reads of later windows
+      // costs more registers than the overlap gains
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // ---- 4. store: bf16 (one K range) or this range's fp32 partials ----------
+#pragma unroll
+  for (int t = 0; t < MID_T; t++) {
+    const int n = row_wg + wave * (MID_T * 16) + t * 16 + nl;
+#pragma unroll
+    for (int u = 0; u < NA; u++)
+#pragma unroll
+      for (int j = 0; j < YV; j++) {
+        const int m = (16 * u + 4 * g) / S + j;
+        if (m < M && n < N) {
+          if (a.ks == 1) a.out[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_bits(y[t][u][j]);
+          else a.ws[((int64_t)sp * M + m) * N + n] = y[t][u][j];
+        }
+      }
+  }
+}
+
+// ---- host ------------------------------------------------------------------
+
+namespace {
+
+template <int FMT, int S, int NA>
+hipError_t mid_launch_sna(const QmvMidPlan& p, const QmvMidArgs& a, hipStream_t stream) {
+  const dim3 grid((unsigned)p.row_blocks, (unsigned)p.ks, 1);
+  if (p.sw == 8) hipLaunchKernelGGL((qmv_mid_kernel<FMT, S, NA, 8>), grid, dim3(MID_NT), p.lds, stream, a);
+  else hipLaunchKernelGGL((qmv_mid_kernel<FMT, S, NA, 2>), grid, dim3(MID_NT), p.lds, stream, a);
+  return hipGetLastError();
+}
+
+template <int FMT, int S>
+hipError_t mid_launch_s(const QmvMidPlan& p, const QmvMidArgs& a, hipStream_t stream) {
+  switch (p.na) {
+    case 1: return mid_launch_sna<FMT, S, 1>(p, a, stream);
+    case 2: return mid_launch_sna<FMT, S, 2>(p, a, stream);
+    default:
+      if constexpr (S == 4) return mid_launch_sna<FMT, S, 4>(p, a, stream);
+      return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+QmvMidPlan qmv_mid_plan(int fmt, int gs, int64_t N, int64_t K, int rows) {
+  QmvMidPlan p;
+  if (fmt != AFF4 && fmt != AFF8) return p;
+  if (rows < 1 || rows > 16 || (gs != 32 && gs != 64 && gs != 128) || N < 1 || K < 1) return p;
+  const int kw = fmt == AFF8 ? 64 : 128;
+  p.s = kw / gs > 1 ? kw / gs : 1;
+  const int ar = rows * p.s;
+  p.na = ar <= 16 ? 1 : (ar <= 32 ? 2 : 4);
+  if (p.na == 4 && p.s != 4) return p;
+  p.row_blocks = (int)((N + MID_ROWS - 1) / MID_ROWS);
+  p.kr = MID_WIN * kw;  // K per workgroup (a multiple of every group size)
+  if (K % p.kr != 0) return p;
+  p.ks = (int)(K / p.kr);
+  const int64_t G = K / gs;
+  const int ngr = p.kr / gs;
+  p.sw = (G % 8 == 0 && ngr % 8 == 0) ? 8 : ((G % 2 == 0 && ngr % 2 == 0) ? 2 : 0);
+  if (!p.sw) return p;
+  // staging loads per thread stay within the kernel's register arrays
+  if ((MID_ROWS * ngr / p.sw + MID_NT - 1) / MID_NT > (p.sw == 8 ? 2 : 4)) return p;
+  p.lds = qmv_mid_lds(fmt, gs, p.kr, p.na).total;
+  // buffer offsets are 32-bit and 0x80000000 marks a dead lane
+  const int64_t wbytes = N * K * (fmt == AFF8 ? 8 : 4) / 8;
+  p.ok = p.lds <= 80 * 1024 && wbytes < ((int64_t)1 << 31) && N * G * 2 < ((int64_t)1 << 31) &&
+         (int64_t)rows * K * 2 < ((int64_t)1 << 31) && p.ks <= 65535 && p.row_blocks <= 65535;
+  return p;
+}
+
+hipError_t qmv_mid_launch(int fmt, const QmvMidArgs& a, const QmvMidPlan& p, hipStream_t stream) {
+  if (!p.ok || (p.ks > 1 && !a.ws)) return hipErrorInvalidValue;
+  hipError_t e;
+  if (fmt == AFF4) {
+    switch (p.s) {
+      case 1: e = mid_launch_s<AFF4, 1>(p, a, stream); break;
+      case 2: e = mid_launch_s<AFF4, 2>(p, a, stream); break;
+      default: e = mid_launch_s<AFF4, 4>(p, a, stream); break;
+    }
+  } else {
+    e = p.s == 2 ? mid_launch_s<AFF8, 2>(p, a, stream) : mid_launch_s<AFF8, 1>(p, a, stream);
+  }
+  if (e != hipSuccess || p.ks == 1) return e;
+  return launch_splitk_reduce(a.ws, a.out, (int64_t)a.M * a.N, p.ks, stream);
+}
+
+}  // namespace mlxq
