@@ -582,11 +582,11 @@ enum class Skinny { FR, RS, B4, MFMA };
 // at 9-16 rows its 128 x 128 tiles already beat the skinny kernels on
 // MI355X (MLXQ_QMM_MIN_ROWS overrides, for tests and measurements).
 constexpr int kQmmMinRows = 9;
-// The mid-size decode kernel takes 9-16 rows, and 5-8 rows over long rows
-// (K > 8192), where it beats the block-MFMA and skinny-MFMA kernels (MI355X,
-// Llama-3-8B MLP shapes: 4-bit gate M=16 22 us vs 40, down M=8 20 us vs 34).
-constexpr int kMidMinRows = 9;
-constexpr int kMidMinRowsLongK = 5;
+// The mid-size decode kernel takes 5-16 rows (affine), where it beats the
+// block-MFMA, skinny-MFMA and prefill kernels (MI355X, Llama-3-8B MLP shapes:
+// 4-bit gate M=8 13.4 us vs 17.7, down M=8 16.5 us vs 33.6, gate M=16 22 us
+// vs 40).
+constexpr int kMidMinRows = 5;
 
 // Defaults measured at the Llama-3-8B MLP shapes (gate K=4096, down
 // K=14336): row-streaming up to 4 rows; block-MFMA for 5-8 rows of 8-bit
@@ -616,7 +616,8 @@ bool use_mid(int rows, int fmt, int64_t K) {
   if (k && std::strcmp(k, "mid") == 0) return true;
   if (k && *k) return false;
   if (env_int("MLXQ_QMV_MID", 1) == 0) return false;
-  return rows >= kMidMinRows || (rows >= kMidMinRowsLongK && K > 8192);
+  (void)K;
+  return rows >= kMidMinRows;
 }
 
 // Launches the full-row or row-streaming kernel when chosen and covered;

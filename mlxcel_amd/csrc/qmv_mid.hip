@@ -55,6 +55,22 @@ __device__ __forceinline__ float dot2m(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dppm(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of PG (4, 8 or 16) lanes: quad swaps, then the
+// half-row and row mirrors, which pair the partial sums of adjacent groups.
+template <int PG>
+__device__ __forceinline__ float group_sum(float v) {
+  v += dppm<0xB1>(v);  // quad_perm [1,0,3,2]
+  v += dppm<0x4E>(v);  // quad_perm [2,3,0,1]
+  if constexpr (PG >= 8) v += dppm<0x141>(v);   // row_half_mirror
+  if constexpr (PG >= 16) v += dppm<0x140>(v);  // row_mirror
+  return v;
+}
+
 // [x0..x7] (bf16, 4 words) -> [x0,x4,x1,x5,x2,x6,x3,x7]
 __device__ __forceinline__ u32x4 perm_aff4_mid(u32x4 x) {
   return u32x4{__builtin_amdgcn_perm(x[2], x[0], 0x05040100u), __builtin_amdgcn_perm(x[2], x[0], 0x07060302u),
@@ -70,15 +86,20 @@ __host__ __device__ inline QmvMidLds qmv_mid_lds(int fmt, int gs, int kr, int na
   l.xl = 0;
   l.xs = l.xl + 16u * (uint32_t)l.xpitch * 2u;
   l.sc = l.xs + (uint32_t)(kr / kw) * 16u * (uint32_t)na * 4u;
-  l.zero = l.sc + (uint32_t)MID_ROWS * (uint32_t)(kr / gs) * 8u;
+  // scale rows are (kr / gs + 2) pairs apart: the 16 rows a tile's lanes read
+  // at once then fall on distinct LDS banks
+  l.zero = l.sc + (uint32_t)MID_ROWS * (uint32_t)(kr / gs + 2) * 8u;
   l.total = l.zero + 16u;
   return l;
 }
 
 // FMT: AFF4 or AFF8; S: quantization groups per window; NA: 16-row A tiles
-// (16 NA >= rows * S); SW: scale groups per staging load (8 or 2).
+// (1 or 2, 16 NA >= rows * S); SW: scale groups per staging load (8 or 2).
+// One A tile fits two waves per SIMD without spilling (the register bound
+// below makes the allocator pack the accumulators); more A tiles keep their
+// own allocation.
 template <int FMT, int S, int NA, int SW>
-__global__ __launch_bounds__(MID_NT) void qmv_mid_kernel(const QmvMidArgs a) {
+__global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const QmvMidArgs a) {
   constexpr int CK = FMT == AFF8 ? 16 : 32;  // k per 16-byte code chunk
   constexpr int KW = 4 * CK;                 // k per window (4 chunks)
   constexpr int NQ = CK / 8;                 // MFMAs per window, tile and A tile
@@ -103,6 +124,7 @@ __global__ __launch_bounds__(MID_NT) void qmv_mid_kernel(const QmvMidArgs a) {
   constexpr int nwin = MID_WIN;  // every split is a full K range (K % KR == 0)
   const int G = K >> a.gs_shift;
   const int ngr = kr >> a.gs_shift;  // groups per K range
+  const int spitch = ngr + 2;        // scale pairs per staged row
   const int row_wg = rb * MID_ROWS;
   const QmvMidLds L = qmv_mid_lds(FMT, 1 << a.gs_shift, kr, NA);
 
@@ -162,15 +184,27 @@ __global__ __launch_bounds__(MID_NT) void qmv_mid_kernel(const QmvMidArgs a) {
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- 2. stage activations (AFF4 pair order), scales, a zero piece ---------
+  // Group sums come from the staging registers: a wave's 64 lanes hold 64
+  // consecutive 8-value pieces of one activation row, and the XG / 8 pieces
+  // of one (window, slot) are adjacent lanes.
   uint16_t* xl = reinterpret_cast<uint16_t*>(smem + L.xl);
+  float* xsl = reinterpret_cast<float*>(smem + L.xs);
+  constexpr int PG = XG / 8;  // pieces per group slot (4, 8 or 16)
 #pragma unroll
   for (int i = 0; i < XPMAX; i++) {
     const int p = tid + i * MID_NT;
+    const int m = p / (kr / 8), c = p % (kr / 8);
     if (p < xpieces) {
-      const int m = p / (kr / 8), c = p % (kr / 8);
       const u32x4 v = FMT == AFF4 ? perm_aff4_mid(xpre[i]) : xpre[i];
       *reinterpret_cast<u32x4*>(xl + m * L.xpitch + 8 * c) = v;
     }
+    float sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) sum = dot2m(xpre[i][e], 0x3F803F80u, sum);  // pairs times (1, 1); dead pieces are 0
+    sum = group_sum<PG>(sum);
+    const int w = (8 * c) / KW, slot = ((8 * c) % KW) / XG;
+    const int r = m * S + slot;
+    if ((lane & (PG - 1)) == 0 && r < 16 * NA) xsl[w * 16 * NA + r] = sum;
   }
   float2* sl = reinterpret_cast<float2*>(smem + L.sc);
 #pragma unroll
@@ -183,32 +217,11 @@ __global__ __launch_bounds__(MID_NT) void qmv_mid_kernel(const QmvMidArgs a) {
         const uint32_t sb = (spre[i][h >> 1] >> (16 * (h & 1))) & 0xFFFFu;
         const uint32_t bb = (bpre[i][h >> 1] >> (16 * (h & 1))) & 0xFFFFu;
         const float s = bf16_bits_to_f32(sb), b = bf16_bits_to_f32(bb);
-        sl[r * ngr + gl + h] = float2{s, FMT == AFF4 ? __builtin_fmaf(-128.0f, s, b) : b};
+        sl[r * spitch + gl + h] = float2{s, FMT == AFF4 ? __builtin_fmaf(-128.0f, s, b) : b};
       }
     }
   }
   if (tid == 0) *reinterpret_cast<u32x4*>(smem + L.zero) = u32x4{0u, 0u, 0u, 0u};
-  __syncthreads();
-
-  // group sums of the activations: xs[w][r] = sum of row r / S over slot r % S
-  // of window w (zero for rows past M)
-  float* xsl = reinterpret_cast<float*>(smem + L.xs);
-  for (int e = tid; e < nwin * 16 * NA; e += MID_NT) {
-    const int w = e / (16 * NA), r = e % (16 * NA);
-    const int m = r / S, slot = r % S;
-    float s = 0.f;
-    if (m < M) {
-      const uint16_t* src = xl + m * L.xpitch + w * KW + slot * XG;
-      for (int c = 0; c < XG; c += 8) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(src + c);
-        s = dot2m(v[0], 0x3F803F80u, s);
-        s = dot2m(v[1], 0x3F803F80u, s);
-        s = dot2m(v[2], 0x3F803F80u, s);
-        s = dot2m(v[3], 0x3F803F80u, s);
-      }
-    }
-    xsl[e] = s;
-  }
   __syncthreads();
 
   // ---- 3. windows: A from LDS, B from the weight ring, fold per group -------
@@ -236,7 +249,7 @@ __global__ __launch_bounds__(MID_NT) void qmv_mid_kernel(const QmvMidArgs a) {
 #pragma unroll
       for (int j = 0; j < YV; j++) y[t][u][j] = 0.f;
 
-  const uint32_t srow0 = L.sc + (uint32_t)((wave * MID_T * 16 + nl) * ngr) * 8u;  // this lane's row, tile 0
+  const uint32_t srow0 = L.sc + (uint32_t)((wave * MID_T * 16 + nl) * spitch) * 8u;  // this lane's row, tile 0
   const int gsh = a.gs_shift;
 
   {
@@ -279,7 +292,7 @@ __global__ __launch_bounds__(MID_NT) void qmv_mid_kernel(const QmvMidArgs a) {
         }
         // scale pairs (s, b') of this lane's weight row for the window's slots
         float2 sc[S];
-        const unsigned char* sp0 = smem + srow0 + (uint32_t)((t * 16 * ngr + grp0) * 8);
+        const unsigned char* sp0 = smem + srow0 + (uint32_t)((t * 16 * spitch + grp0) * 8);
 #pragma unroll
         for (int h = 0; h < S; h++) sc[h] = reinterpret_cast<const float2*>(sp0)[h];
 #pragma unroll
@@ -334,9 +347,7 @@ hipError_t mid_launch_s(const QmvMidPlan& p, const QmvMidArgs& a, hipStream_t st
   switch (p.na) {
     case 1: return mid_launch_sna<FMT, S, 1>(p, a, stream);
     case 2: return mid_launch_sna<FMT, S, 2>(p, a, stream);
-    default:
-      if constexpr (S == 4) return mid_launch_sna<FMT, S, 4>(p, a, stream);
-      return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
   }
 }
 
@@ -349,8 +360,9 @@ QmvMidPlan qmv_mid_plan(int fmt, int gs, int64_t N, int64_t K, int rows) {
   const int kw = fmt == AFF8 ? 64 : 128;
   p.s = kw / gs > 1 ? kw / gs : 1;
   const int ar = rows * p.s;
-  p.na = ar <= 16 ? 1 : (ar <= 32 ? 2 : 4);
-  if (p.na == 4 && p.s != 4) return p;
+  // more than two A tiles (4-bit g32 above 8 rows) would spill: other kernels
+  p.na = ar <= 16 ? 1 : 2;
+  if (ar > 32) return p;
   p.row_blocks = (int)((N + MID_ROWS - 1) / MID_ROWS);
   p.kr = MID_WIN * kw;  // K per workgroup (a multiple of every group size)
   if (K % p.kr != 0) return p;

@@ -5,8 +5,9 @@ cpu/quantized.cpp:199-257), max|y - y_ref| / max|y_ref| <= 1e-2.
 
 Shapes reach every compiled variant: group slots per window S in {1, 2, 4}
 (4-bit g128/g64/g32, 8-bit g64/g32, and 8-bit g128, where one group spans two
-windows and the scales stage two groups per load), 1, 2 and 4 activation A
-tiles, a partial last row block (N not a multiple of 128), a single K range
+windows and the scales stage two groups per load), 1 and 2 activation A
+tiles (4-bit g32 above 8 rows would need 4 and runs another kernel), a
+partial last row block (N not a multiple of 128), a single K range
 (direct bf16 store) and several (fp32 partials added by the reduction
 kernel), back-to-back calls and graph replays.
 """
