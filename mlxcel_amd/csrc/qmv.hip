@@ -14,7 +14,7 @@
 //    load instruction moves 1 KiB of HBM.  Every load of the wave's K range is
 //    issued before any arithmetic.
 //  * The codes are widened in registers into bf16 MFMA fragments
-//    (AFF4: one and-or per pair, "128+q" trick; MXFP4: the gfx950 fp4
+//    (AFF4: one byte permute per pair, "128+q" trick; MXFP4: the gfx950 fp4
 //    conversion; AFF8: byte -> f32 -> bf16) and multiplied on
 //    v_mfma_f32_16x16x32_bf16 against the activations held in LDS.
 //  * Quantization groups never mix inside an MFMA row: A-operand row

@@ -15,7 +15,7 @@
 // 256 contiguous bytes (lane 4b+j reads piece b of row j), each lane keeps its
 // own row, and the matrix core does the multiply-adds the row-streaming
 // kernel spends v_dot2 instructions on.  Per 16-byte piece a lane does:
-//   * unpack: AFF4 "128 + q" bf16 pairs (one and-or per pair, the activations
+//   * unpack: AFF4 "128 + q" bf16 pairs (one byte permute per pair, the activations
 //     permuted to match), AFF8 byte -> f32 -> bf16, MXFP4 the gfx950 scaled
 //     fp4 conversion with the e8m0 scale folded in (exact);
 //   * KL/4 MFMAs per set of 4 activation rows, C starting at 0;
@@ -100,9 +100,22 @@ __global__ __launch_bounds__(512) void qmv_b4_kernel(const QmvArgs a, int gs_shi
   const int j = lane & 3;   // weight row within a group / activation row within a set
   const int sidx = blockIdx.y;
 
-  const int count = min(a.rps, a.total_rows - sidx * a.rps);
+  int count = min(a.rps, a.total_rows - sidx * a.rps);
   if (count <= 0) return;
   const int expert = seg_index(a.rhs, a.rhs_stride, sidx, a.E, a.w_expert_stride ? sidx : 0);
+  if (a.runs) {
+    // Expert runs of a sorted gather (one activation row per entry, 4 MS >=
+    // a.runs rows compiled): entry sidx starts a segment where the expert
+    // changes or at a multiple of a.runs, and the segment takes the following
+    // entries of the same expert up to the next multiple; other workgroups
+    // exit.
+    const int cap = a.runs;
+    if (sidx % cap != 0 && seg_index(a.rhs, a.rhs_stride, sidx - 1, a.E, 0) == expert) return;
+    count = 1;
+    while (count < cap && (sidx + count) % cap != 0 && sidx + count < a.total_rows &&
+           seg_index(a.rhs, a.rhs_stride, sidx + count, a.E, 0) == expert)
+      count++;
+  }
   const int xbatch = seg_index(a.lhs, a.lhs_stride, sidx, a.X, a.lhs_div > 1 ? sidx / a.lhs_div : sidx);
 
   const int N = a.N;

@@ -23,8 +23,8 @@
 // and the fold y += s * D + (b - 128 s) * sum(x) (AFF4 "128 + q" codes; AFF8
 // codes are the bytes themselves, so b) runs once per output, window and
 // group.  The activations are staged permuted to the AFF4 pair order
-// ([x0,x4,x1,x5,x2,x6,x3,x7] per 8) so the codes widen with one and-or per
-// pair.
+// ([x0,x4,x1,x5,x2,x6,x3,x7] per 8) so the codes widen with one byte permute
+// per pair.
 //
 // Each workgroup covers a K range of 8 windows (1024 k for 4-bit, 512 for
 // 8-bit); every wave keeps 4 windows of weight loads in flight per tile.  K ranges

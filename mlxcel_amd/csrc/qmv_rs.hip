@@ -17,7 +17,7 @@
 // Arithmetic.  A lane always covers the same 32 (4-bit) or 16 (8-bit) K
 // positions of its rows, so its activations for those positions are loaded
 // once into registers.  The codes are widened to bf16 pairs (AFF4 "128 + q"
-// with one and-or per pair, MXFP4 with the gfx950 fp4 conversion, AFF8 via
+// with one byte permute per pair, MXFP4 with the gfx950 fp4 conversion, AFF8 via
 // byte -> f32 -> bf16) and multiplied with v_dot2_f32_bf16 in fp32.  A lane's
 // 16 bytes lie inside one quantization group, so the scale and bias apply
 // once per lane and row:  y += s * sum((128+q) x) + (b - 128 s) * sum(x).
@@ -135,9 +135,22 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
   const int sidx = blockIdx.y;
 
   // ---- segment (workgroup-uniform) ----------------------------------------
-  const int count = min(a.rps, a.total_rows - sidx * a.rps);
+  int count = min(a.rps, a.total_rows - sidx * a.rps);
   if (count <= 0) return;
   const int expert = seg_index(a.rhs, a.rhs_stride, sidx, a.E, a.w_expert_stride ? sidx : 0);
+  if (a.runs) {
+    // Expert runs of a sorted gather (one activation row per entry, MR >= 4):
+    // entry sidx starts a segment where the expert changes or at a multiple
+    // of 4, and the segment takes the following entries of the same expert
+    // up to the next multiple of 4; every other entry's workgroup exits.  So
+    // each entry is computed once and each run of an expert streams its
+    // weights once per 4 entries instead of once per entry.
+    if ((sidx & 3) != 0 && seg_index(a.rhs, a.rhs_stride, sidx - 1, a.E, 0) == expert) return;
+    count = 1;
+    while (count < 4 && ((sidx + count) & 3) != 0 && sidx + count < a.total_rows &&
+           seg_index(a.rhs, a.rhs_stride, sidx + count, a.E, 0) == expert)
+      count++;
+  }
   const int xbatch = seg_index(a.lhs, a.lhs_stride, sidx, a.X, a.lhs_div > 1 ? sidx / a.lhs_div : sidx);
 
   const int N = a.N;

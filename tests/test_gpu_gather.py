@@ -65,9 +65,12 @@ def test_mxfp4_sorted(T):
     np.testing.assert_array_equal(got, again)
     want = orc.gather_qmm_t(xs, wq, sc, None, np.arange(T * 4, dtype=np.uint32), rhs, mode="mxfp4")
     assert max_rel(got, want) <= TOL
-    # the unsorted call on the same pairs gives the same rows
+    # the unsorted call on the same pairs gives the same rows within tolerance
+    # (tests/rocm_gather_qmm_expert_batched.rs:26-35 holds them to a tolerance
+    # too; the sorted call runs equal experts together, which changes the
+    # order of the fp32 sums)
     unsorted = host_u16(mq.gather_qmm(X, W, S, None, None, R, True, 32, 4, "mxfp4", sorted_indices=False))
-    np.testing.assert_array_equal(got, unsorted)
+    assert max_rel(unsorted, got) <= TOL
 
 
 @pytest.mark.parametrize("bits", [4, 8])
@@ -205,3 +208,49 @@ def test_direct_indices_match_index_prep(monkeypatch, dtype, case):
         want = orc.gather_qmm_t(orc.normal_bf16((T, 1, K), 1.0, 962), wq, s, b,
                                 np.repeat(np.arange(T, dtype=np.uint32), 3), ids.reshape(-1))
         assert max_rel(outs[0].reshape(T * 3, 1, N), want) <= TOL
+
+
+@pytest.mark.parametrize("pattern", ["random_sorted", "one_expert", "pairs", "alternating", "unsorted"])
+@pytest.mark.parametrize("dtype", [torch.int32, torch.int64])
+def test_sorted_runs(monkeypatch, pattern, dtype):
+    # sorted gathers run equal consecutive experts as one segment of up to 4
+    # entries; every pattern must give the per-entry result (oracle), with
+    # runs longer than 4, runs across multiples of 4, a ragged tail (B = 37),
+    # and input that is not actually sorted
+    announce("gather_sorted_runs", pattern, dtype)
+    E, N, K, B = 8, 264, 2048, 37
+    rng = np.random.default_rng(970)
+    if pattern == "random_sorted":
+        rhs = np.sort(rng.integers(0, E, B))
+    elif pattern == "one_expert":
+        rhs = np.full(B, 5)
+    elif pattern == "pairs":
+        rhs = np.repeat(np.arange(B) // 2 % E, 1)
+    elif pattern == "alternating":
+        rhs = np.arange(B) % 2 * 3
+    else:
+        rhs = rng.integers(0, E, B)
+    wq, sc = mx_experts(E, N, K, 971)
+    x = orc.normal_bf16((B, 1, K), 1.0, 972)
+    R = torch.from_numpy(rhs.astype(np.int64)).to(dtype).cuda()
+    X, W, S = dev_bf16(x), dev_u32(wq), dev_u8(sc)
+    got = host_u16(mq.gather_qmm(X, W, S, None, None, R, True, 32, 4, "mxfp4", sorted_indices=True))
+    want = orc.gather_qmm_t(x, wq, sc, None, np.arange(B, dtype=np.uint32), rhs.astype(np.uint32), mode="mxfp4")
+    assert max_rel(got, want) <= TOL
+    again = host_u16(mq.gather_qmm(X, W, S, None, None, R, True, 32, 4, "mxfp4", sorted_indices=True))
+    np.testing.assert_array_equal(got, again)
+    monkeypatch.setenv("MLXQ_GATHER_RUNS", "0")
+    per_entry = host_u16(mq.gather_qmm(X, W, S, None, None, R, True, 32, 4, "mxfp4", sorted_indices=True))
+    assert max_rel(per_entry, got) <= TOL
+
+
+def test_sorted_runs_affine():
+    announce("gather_sorted_runs_affine")
+    E, N, K, B = 6, 200, 4096, 24
+    rhs = np.sort(np.random.default_rng(973).integers(0, E, B)).astype(np.int32)
+    wq, s, b = affine_experts(E, N, K, 974)
+    x = orc.normal_bf16((B, 1, K), 1.0, 975)
+    got = host_u16(mq.gather_qmm(dev_bf16(x), dev_u32(wq), dev_bf16(s), dev_bf16(b), None,
+                                 torch.from_numpy(rhs).cuda(), True, 64, 4, sorted_indices=True))
+    want = orc.gather_qmm_t(x, wq, s, b, np.arange(B, dtype=np.uint32), rhs.astype(np.uint32))
+    assert max_rel(got, want) <= TOL
