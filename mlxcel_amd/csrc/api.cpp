@@ -901,6 +901,34 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq
     const int dev = current_device();
     const DevInfo di = device_info(dev);
 
+    // Expert-sorted mxfp4 gathers with one row per entry and >= 4 rows per
+    // expert on average (mlxcel's sorted MoE path, gpt_oss.rs:317-345): one
+    // kernel streams each expert's weights once per 64 of its rows, finding
+    // the rows by binary search in the sorted indices (qmm_group.hip); fewer
+    // rows per expert run as segments of up to 4 entries (below).  Like the reference's sorted route, it
+    // relies on sorted_indices being true.  MLXQ_GATHER_SORTED=0 turns it off.
+    if (sorted_indices && M == 1 && fmt == mlxq::MXFP4 && B >= 32 && B >= 4 * E &&
+        env_int("MLXQ_GATHER_SORTED", 1) != 0) {
+      const DirectIdx dl = direct_index(lhs_indices, dsh[0], g.idx_shape);
+      const DirectIdx dr = direct_index(rhs_indices, dsh[1], g.idx_shape);
+      const mlxq::QmmGroupPlan gp = mlxq::qmm_group_plan(fmt, sp.N, sp.K, E, B);
+      if (gp.ok && dr.ok && dr.p && dl.ok && !dl.p && dl.div == 1) {
+        mlxq::QmmGroupArgs q{};
+        q.x = static_cast<const uint16_t*>(x->data);
+        q.w = static_cast<const uint32_t*>(w->data);
+        q.scales = static_cast<const uint8_t*>(scales->data);
+        q.out = static_cast<uint16_t*>(out->data);
+        q.rhs = dr.p;
+        q.rhs_stride = dr.stride;
+        q.N = (int)sp.N;
+        q.K = (int)sp.K;
+        q.E = (int)E;
+        q.B = (int)B;
+        hip_check(mlxq::qmm_group_launch(q, gp, stream), "gather group launch");
+        return;
+      }
+    }
+
     // Many rows per expert (MoE prefill, large batches): group rows by expert
     // on the device, then one GEMM tile reads each expert's weights once per
     // tile of rows (qmm.hip), instead of once per index entry.  Auto when the

@@ -133,6 +133,25 @@ QmvMidPlan qmv_mid_plan(int fmt, int gs, int64_t N, int64_t K, int rows);
 // Launches the kernel and, with several K ranges, the fixed-order reduction.
 hipError_t qmv_mid_launch(int fmt, const QmvMidArgs& a, const QmvMidPlan& p, hipStream_t stream);
 
+// Expert-sorted gather (qmm_group.hip), mxfp4, one activation row per index
+// entry: a workgroup per (128 weight rows, expert) finds the expert's rows in
+// the sorted indices and streams its weights once per 64 rows.
+struct QmmGroupArgs {
+  const uint16_t* x;       // bf16 [B][K], row b = entry b
+  const uint32_t* w;       // packed codes [E][N][K/8]
+  const uint8_t* scales;   // e8m0 [E][N][K/32]
+  uint16_t* out;           // bf16 [B][N]
+  const uint32_t* rhs;     // sorted expert per entry (32- or 64-bit, low word)
+  int rhs_stride;          // 32-bit words per index (1 or 2)
+  int N, K, E, B;
+};
+struct QmmGroupPlan {
+  bool ok = false;
+  int row_blocks = 0;  // workgroups along N (128 weight rows each)
+};
+QmmGroupPlan qmm_group_plan(int fmt, int64_t N, int64_t K, int64_t E, int64_t B);
+hipError_t qmm_group_launch(const QmmGroupArgs& a, const QmmGroupPlan& p, hipStream_t stream);
+
 // Full-row decode kernel (qmv_fr.hip) for 1 or 2 activation rows per weight
 // matrix: 8 waves per workgroup, R whole rows per wave, activations staged in
 // LDS once per workgroup.

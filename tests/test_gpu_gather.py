@@ -213,13 +213,18 @@ def test_direct_indices_match_index_prep(monkeypatch, dtype, case):
 @pytest.mark.parametrize("pattern", ["random_sorted", "one_expert", "pairs", "alternating", "unsorted"])
 @pytest.mark.parametrize("dtype", [torch.int32, torch.int64])
 def test_sorted_runs(monkeypatch, pattern, dtype):
-    # sorted gathers run equal consecutive experts as one segment of up to 4
-    # entries; every pattern must give the per-entry result (oracle), with
-    # runs longer than 4, runs across multiples of 4, a ragged tail (B = 37),
-    # and input that is not actually sorted
+    # the run path of sorted gathers: equal consecutive experts form segments
+    # of up to 4 entries; every pattern must give the per-entry result
+    # (oracle), with runs longer than 4, runs across multiples of 4, a ragged
+    # tail (B = 37), and input that is not actually sorted
     announce("gather_sorted_runs", pattern, dtype)
     E, N, K, B = 8, 264, 2048, 37
     rng = np.random.default_rng(970)
+    # the run path; the expert-grouped path (the default for sorted mxfp4
+    # gathers, test_sorted_grouped_mxfp4) relies on sorted_indices the way
+    # the reference's sorted route does, and "pairs" (wrapping at E),
+    # "alternating" and "unsorted" are not sorted
+    monkeypatch.setenv("MLXQ_GATHER_SORTED", "0")
     if pattern == "random_sorted":
         rhs = np.sort(rng.integers(0, E, B))
     elif pattern == "one_expert":
@@ -254,3 +259,36 @@ def test_sorted_runs_affine():
                                  torch.from_numpy(rhs).cuda(), True, 64, 4, sorted_indices=True))
     want = orc.gather_qmm_t(x, wq, s, b, np.arange(B, dtype=np.uint32), rhs.astype(np.uint32))
     assert max_rel(got, want) <= TOL
+
+
+@pytest.mark.parametrize("pattern", ["uniform", "one_expert", "skewed", "clamped_tail"])
+@pytest.mark.parametrize("dtype", [torch.int32, torch.int64])
+def test_sorted_grouped_mxfp4(pattern, dtype):
+    # the expert-grouped kernel (qmm_group.hip): 1024 sorted entries; experts
+    # with no rows, with more than 64 rows (chunks of 64), all rows on one
+    # expert, and out-of-range indices at the end (clamped to the last expert,
+    # which keeps the order); N = 516 ends inside a 128-row block and
+    # K = 2880 inside a 128-k window
+    announce("gather_sorted_grouped", pattern, dtype)
+    E, N, K, B = 32, 516, 2880, 1024
+    rng = np.random.default_rng(980)
+    if pattern == "uniform":
+        rhs = np.sort(rng.integers(0, E, B))
+    elif pattern == "one_expert":
+        rhs = np.full(B, 7)
+    elif pattern == "skewed":
+        rhs = np.sort(np.minimum(rng.geometric(0.15, B) - 1, E - 1))
+    else:
+        rhs = np.sort(rng.integers(0, E, B))
+        rhs[-20:] = 1000
+    wq, sc = mx_experts(E, N, K, 981)
+    x = orc.normal_bf16((B, 1, K), 1.0, 982)
+    R = torch.from_numpy(rhs.astype(np.int64)).to(dtype).cuda()
+    X, W, S = dev_bf16(x), dev_u32(wq), dev_u8(sc)
+    got = host_u16(mq.gather_qmm(X, W, S, None, None, R, True, 32, 4, "mxfp4", sorted_indices=True))
+    assert got.shape == (B, 1, N)
+    want = orc.gather_qmm_t(x, wq, sc, None, np.arange(B, dtype=np.uint32),
+                            np.minimum(rhs, E - 1).astype(np.uint32), mode="mxfp4")
+    assert max_rel(got, want) <= TOL
+    again = host_u16(mq.gather_qmm(X, W, S, None, None, R, True, 32, 4, "mxfp4", sorted_indices=True))
+    np.testing.assert_array_equal(got, again)
