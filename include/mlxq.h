@@ -107,8 +107,11 @@ mlxq_status mlxq_quantized_matmul_shape(const mlxq_array* x, const mlxq_array* w
  * shape, as mlx::core::gather_qmm (ops.cpp:5841-5948): out.shape =
  * broadcast(lhs, rhs).shape + [x.shape[-2], N].  NULL lhs/rhs default to
  * arange over the batch dims of x/w; both NULL is quantized_matmul.
- * `sorted_indices` is the reference's hint that rhs is sorted; results do
- * not depend on it.  `global_scale` (nvfp4 only in the reference) must be
+ * `sorted_indices` is the reference's promise that rhs is non-decreasing in
+ * the flat order of the broadcast batch; as in the reference's expert-run
+ * kernels (rocm/quantized/qmm.hip:4705-4740, found by binary search) the
+ * result is unspecified when the promise is false.  Sorted and unsorted
+ * routes differ only in summation order (same tolerance).  `global_scale` (nvfp4 only in the reference) must be
  * NULL.  Index arrays may be any integer dtype and any strides
  * (broadcasting included). */
 mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w,
