@@ -143,4 +143,65 @@ __device__ __forceinline__ float sum_bf16x8(u32x4 x) {
   return s;
 }
 
+// ---- buffer loads, dot products, cross-lane sums -------------------------------
+
+constexpr int log2i(int v) { return v <= 1 ? 0 : 1 + log2i(v / 2); }
+
+// A buffer offset past every operand (all operands of a launch stay below
+// 2 GiB): bounds-checked buffer loads at it return 0.
+constexpr uint32_t kDeadOfs = 0x80000000u;
+
+// Raw buffer resource over [base, base + bytes): loads past the end return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// c + a.lo * b.lo + a.hi * b.hi over bf16 pairs, fp32 accumulate
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum CNT values per lane over each row of 16 lanes with DPP exchanges (no
+// LDS round trips).  Step s pairs every lane with one whose bit (3 - s)
+// differs: row_mirror (i <-> 15-i), row_half_mirror (i <-> 7-i in each half),
+// then quad_perm swaps of bit 1 and bit 0; the pairs of successive steps
+// never repeat a lane, so after four steps each value has been summed over
+// all 16 lanes.  While more than one value is left, a step halves them: the
+// lane with the bit set keeps the upper half and sends the lower.  Afterwards
+// lane i (of its row) holds values [(i / Q) * C, (i / Q) * C + C) where
+// C = max(CNT / 16, 1) and Q = max(16 / CNT, 1).
+template <int CNT, int STEP>
+__device__ __forceinline__ void row_butterfly(float* v, int lane) {
+  if constexpr (STEP < 4) {
+    constexpr int BIT = 8 >> STEP;
+    constexpr int CTRL = STEP == 0 ? 0x140 : (STEP == 1 ? 0x141 : (STEP == 2 ? 0x4E : 0xB1));
+    if constexpr (CNT > 1) {
+      constexpr int H = CNT / 2;
+      const bool up = (lane & BIT) != 0;
+#pragma unroll
+      for (int i = 0; i < H; i++) {
+        const float keep = up ? v[i + H] : v[i];
+        const float send = up ? v[i] : v[i + H];
+        v[i] = keep + dpp<CTRL>(send);
+      }
+      row_butterfly<H, STEP + 1>(v, lane);
+    } else {
+      v[0] += dpp<CTRL>(v[0]);
+      row_butterfly<1, STEP + 1>(v, lane);
+    }
+  }
+}
+
+// [x0,x1,x2,x3,x4,x5,x6,x7] (bf16, 4 words) -> [x0,x4,x1,x5,x2,x6,x3,x7]: the
+// pair order of unpack_aff4
+__device__ __forceinline__ u32x4 perm_aff4_v(u32x4 x) {
+  return u32x4{__builtin_amdgcn_perm(x[2], x[0], 0x05040100u), __builtin_amdgcn_perm(x[2], x[0], 0x07060302u),
+               __builtin_amdgcn_perm(x[3], x[1], 0x05040100u), __builtin_amdgcn_perm(x[3], x[1], 0x07060302u)};
+}
+
 }  // namespace mlxq

@@ -31,11 +31,6 @@ namespace {
 constexpr int BK = 64;
 constexpr int LDSK = BK + 8;  // padded row length (bf16)
 constexpr int NT = 256;       // threads per workgroup (4 waves, 2 x 2)
-constexpr uint32_t kDeadQ = 0x80000000u;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t qrsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
@@ -103,14 +98,14 @@ __global__ __launch_bounds__(NT) void qmm_kernel(const QmmArgs a) {
     sbase = (int64_t)expert * a.s_expert_stride;
   }
 
-  const __amdgpu_buffer_rsrc_t xr = qrsrc(a.x, (uint32_t)((int64_t)a.x_rows * K * 2));
+  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.x, (uint32_t)((int64_t)a.x_rows * K * 2));
   const uint32_t RB = (uint32_t)(K * BITS / 8);  // bytes per weight row
-  const __amdgpu_buffer_rsrc_t wr = qrsrc(a.w + wbase, (uint32_t)((int64_t)N * RB));
+  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.w + wbase, (uint32_t)((int64_t)N * RB));
   const int G = K >> a.gs_shift;
   const __amdgpu_buffer_rsrc_t sr =
-      qrsrc(reinterpret_cast<const uint8_t*>(a.scales) + sbase * (AFF ? 2 : 1), (uint32_t)((int64_t)N * G * (AFF ? 2 : 1)));
+      buffer_rsrc(reinterpret_cast<const uint8_t*>(a.scales) + sbase * (AFF ? 2 : 1), (uint32_t)((int64_t)N * G * (AFF ? 2 : 1)));
   const __amdgpu_buffer_rsrc_t br =
-      qrsrc(AFF ? (const void*)(a.biases + sbase) : a.scales, (uint32_t)(AFF ? (int64_t)N * G * 2 : 0));
+      buffer_rsrc(AFF ? (const void*)(a.biases + sbase) : a.scales, (uint32_t)(AFF ? (int64_t)N * G * 2 : 0));
 
   // ---- global -> register staging of one K-step ----------------------------
   // activations: thread t loads row (t / 8) + 32 i, 16-byte chunk t % 8
@@ -122,7 +117,7 @@ __global__ __launch_bounds__(NT) void qmm_kernel(const QmmArgs a) {
   for (int i = 0; i < XPASS; i++) {
     const int tr = xrow + 32 * i;
     const uint32_t xrw = a.seg ? (tr < rows ? a.xrows[r0 + tr] : 0u) : (uint32_t)(m0 + tr);
-    xbase[i] = tr < rows ? xrw * (uint32_t)K * 2u + (uint32_t)xch * 16u : kDeadQ;
+    xbase[i] = tr < rows ? xrw * (uint32_t)K * 2u + (uint32_t)xch * 16u : kDeadOfs;
   }
   u32x4 xreg[XPASS];
   u32x4 wreg[WPASS];
@@ -136,10 +131,10 @@ __global__ __launch_bounds__(NT) void qmm_kernel(const QmmArgs a) {
     for (int p = 0; p < WPASS; p++) {
       const int n = n0 + wrow + WROWS * p;
       const bool live = n < N;
-      const uint32_t off = live ? (uint32_t)n * RB + (uint32_t)(k0 * BITS / 8 + wpc * 16) : kDeadQ;
+      const uint32_t off = live ? (uint32_t)n * RB + (uint32_t)(k0 * BITS / 8 + wpc * 16) : kDeadOfs;
       wreg[p] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 2 /* nt */));
       const int g = (k0 + wpc * VPL) >> a.gs_shift;
-      const uint32_t so = live ? (uint32_t)(n * G + g) : kDeadQ;
+      const uint32_t so = live ? (uint32_t)(n * G + g) : kDeadOfs;
       if constexpr (AFF) {
         sreg[p] = __builtin_amdgcn_raw_buffer_load_b16(sr, so * 2u, 0, 0);
         breg[p] = __builtin_amdgcn_raw_buffer_load_b16(br, so * 2u, 0, 0);
@@ -351,14 +346,14 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
     sbase = (int64_t)expert * a.s_expert_stride;
   }
 
-  const __amdgpu_buffer_rsrc_t xr = qrsrc(a.x, (uint32_t)((int64_t)a.x_rows * K * 2));
+  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.x, (uint32_t)((int64_t)a.x_rows * K * 2));
   const uint32_t RB = (uint32_t)(K * BITS / 8);
-  const __amdgpu_buffer_rsrc_t wr = qrsrc(a.w + wbase, (uint32_t)((int64_t)N * RB));
+  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.w + wbase, (uint32_t)((int64_t)N * RB));
   const int GR = K >> a.gs_shift;  // groups per row
-  const __amdgpu_buffer_rsrc_t sr = qrsrc(reinterpret_cast<const uint8_t*>(a.scales) + sbase * (AFF ? 2 : 1),
+  const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(reinterpret_cast<const uint8_t*>(a.scales) + sbase * (AFF ? 2 : 1),
                                           (uint32_t)((int64_t)N * GR * (AFF ? 2 : 1)));
   const __amdgpu_buffer_rsrc_t br =
-      qrsrc(AFF ? (const void*)(a.biases + sbase) : a.scales, (uint32_t)(AFF ? (int64_t)N * GR * 2 : 0));
+      buffer_rsrc(AFF ? (const void*)(a.biases + sbase) : a.scales, (uint32_t)(AFF ? (int64_t)N * GR * 2 : 0));
   const int gs_shift = a.gs_shift;
   const int SPC = (CHG << gs_shift) / BK;  // K-steps per scale chunk (4, 8 or 16)
 
@@ -370,7 +365,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
   for (int i = 0; i < XL; i++) {
     const int tr = xrow + XROWS * i;
     const uint32_t xrw = a.seg ? (tr < rows ? a.xrows[r0 + tr] : 0u) : (uint32_t)(m0 + tr);
-    xoff[i] = tr < rows ? xrw * (uint32_t)K * 2u + (uint32_t)xch * 16u : kDeadQ;
+    xoff[i] = tr < rows ? xrw * (uint32_t)K * 2u + (uint32_t)xch * 16u : kDeadOfs;
   }
   const int xdst = xrow * RS + ((xch ^ (xrow & 7)) << 3);  // + XROWS i rows (same swizzle)
 
@@ -380,12 +375,12 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
 #pragma unroll
   for (int p = 0; p < WP; p++) {
     const int n = n0 + wrow + WROWS * p;
-    woff[p] = n < N ? (uint32_t)n * RB + (uint32_t)(wpc * 16) : kDeadQ;
+    woff[p] = n < N ? (uint32_t)n * RB + (uint32_t)(wpc * 16) : kDeadOfs;
   }
 
   // scale chunks: thread t < BN loads the 16-byte chunk of row n0 + t
   const bool sload = t < BN;
-  const uint32_t srow_off = (n0 + t < N && sload) ? (uint32_t)(n0 + t) * (uint32_t)GR * (AFF ? 2u : 1u) : kDeadQ;
+  const uint32_t srow_off = (n0 + t < N && sload) ? (uint32_t)(n0 + t) * (uint32_t)GR * (AFF ? 2u : 1u) : kDeadOfs;
   // Scale rows need not be 16-byte aligned (K / gs groups per row, e.g. 90
   // e8m0 bytes): a chunk is read as 5 dwords from the dword boundary below
   // and realigned by the byte offset in registers.

@@ -37,11 +37,6 @@ constexpr int GQ_KB = 256;                   // k per staged block (2 windows)
 constexpr int GQ_NT = 64 * GQ_NW;
 constexpr int GQ_XPITCH = GQ_KB + 8;         // bf16 per staged row (16 bytes of padding)
 constexpr int GQ_XP = GQ_MC * GQ_KB / 8 / GQ_NT;  // 16-byte activation pieces per thread and block (8)
-constexpr uint32_t kDeadG = 0x80000000u;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t g_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
 
 // First entry whose (clamped) expert is >= v in the sorted index array;
 // wave-uniform.  Each step samples 64 evenly spaced entries of [lo, hi).
@@ -89,8 +84,8 @@ __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGrou
   const uint32_t RB = (uint32_t)nchunk * 16u;    // bytes per weight row
   const int nwin = (nchunk + 3) / 4;             // 128-k windows
   const int nblk = (nwin + 1) / 2;               // 256-k blocks
-  const __amdgpu_buffer_rsrc_t wr = g_rsrc(a.w + (int64_t)e * N * (nchunk * 4), (uint32_t)N * RB);
-  const __amdgpu_buffer_rsrc_t sr = g_rsrc(a.scales + (int64_t)e * N * nchunk, (uint32_t)(N * nchunk));
+  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.w + (int64_t)e * N * (nchunk * 4), (uint32_t)N * RB);
+  const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(a.scales + (int64_t)e * N * nchunk, (uint32_t)(N * nchunk));
 
   const int nl = lane & 15;
   const int g = lane >> 4;
@@ -98,8 +93,8 @@ __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGrou
 #pragma unroll
   for (int t = 0; t < GQ_T; t++) {
     const int n = nb0 + wave * (GQ_T * 16) + t * 16 + nl;
-    wrow[t] = n < N ? (uint32_t)n * RB : kDeadG;
-    srow[t] = n < N ? (uint32_t)(n * nchunk) : kDeadG;
+    wrow[t] = n < N ? (uint32_t)n * RB : kDeadOfs;
+    srow[t] = n < N ? (uint32_t)(n * nchunk) : kDeadOfs;
   }
 
   // weights + scales of block b for tile t, window v (0/1) of the block
@@ -113,19 +108,19 @@ __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGrou
   };
   auto sload = [&](int b, int t, int v) -> uint32_t {
     const int c = (2 * b + v) * 4 + g;
-    const uint32_t o = (srow[t] != kDeadG && c < nchunk) ? srow[t] + (uint32_t)c : kDeadG;
+    const uint32_t o = (srow[t] != kDeadOfs && c < nchunk) ? srow[t] + (uint32_t)c : kDeadOfs;
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(sr, o, 0, 0);
   };
 
   for (int r0 = lo; r0 < hi; r0 += GQ_MC) {
     const int cnt = min(GQ_MC, hi - r0);
     const int nat = (cnt + 15) / 16;  // live A tiles (uniform)
-    const __amdgpu_buffer_rsrc_t xr = g_rsrc(a.x + (int64_t)r0 * K, (uint32_t)cnt * (uint32_t)K * 2u);
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.x + (int64_t)r0 * K, (uint32_t)cnt * (uint32_t)K * 2u);
     auto xload = [&](int b, int i) -> u32x4 {
       const int p = tid + i * GQ_NT;
       const int m = p / (GQ_KB / 8), c = p % (GQ_KB / 8);
       const int k = b * GQ_KB + 8 * c;
-      const uint32_t o = (m < cnt && k < K) ? (uint32_t)(m * K + k) * 2u : kDeadG;
+      const uint32_t o = (m < cnt && k < K) ? (uint32_t)(m * K + k) * 2u : kDeadOfs;
       return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, o, 0, 0));
     };
 

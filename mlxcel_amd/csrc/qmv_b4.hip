@@ -56,28 +56,6 @@ __device__ __forceinline__ void mfma4_acc(f32x4& d, uint32_t a0, uint32_t a1, ui
 }
 __device__ __forceinline__ void mfma4_done(f32x4& d) { asm volatile("s_nop 7\n\ts_nop 7" : "+v"(d)); }
 
-template <int CTRL>
-__device__ __forceinline__ float dppf(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-
-__device__ __forceinline__ float dot2b(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
-}
-
-constexpr uint32_t kDead = 0x80000000u;  // a buffer offset past every operand: loads return 0
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-
-// [x0..x7] (bf16, 4 words) -> [x0,x4,x1,x5,x2,x6,x3,x7]: the order of the
-// AFF4 "128 + q" pairs (nibble p with nibble p + 4 of a word)
-__device__ __forceinline__ u32x4 perm_aff4_x(u32x4 x) {
-  return u32x4{__builtin_amdgcn_perm(x[2], x[0], 0x05040100u), __builtin_amdgcn_perm(x[2], x[0], 0x07060302u),
-               __builtin_amdgcn_perm(x[3], x[1], 0x05040100u), __builtin_amdgcn_perm(x[3], x[1], 0x07060302u)};
-}
-
 }  // namespace
 
 // FMT: weight format; MS: sets of 4 activation rows (1, 2 or 4); RG: groups
@@ -126,13 +104,13 @@ __global__ __launch_bounds__(512) void qmv_b4_kernel(const QmvArgs a, int gs_shi
   const int G = K >> gs_shift;
   constexpr int ESZ = AFF ? 2 : 1;
 
-  const __amdgpu_buffer_rsrc_t wr = rsrc(a.w + (int64_t)expert * a.w_expert_stride, (uint32_t)N * RB);
-  const __amdgpu_buffer_rsrc_t xr = rsrc(a.x + (int64_t)xbatch * a.rps * K, (uint32_t)count * (uint32_t)K * 2u);
+  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.w + (int64_t)expert * a.w_expert_stride, (uint32_t)N * RB);
+  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.x + (int64_t)xbatch * a.rps * K, (uint32_t)count * (uint32_t)K * 2u);
   const int64_t sb0 = (int64_t)expert * a.s_expert_stride;
   const __amdgpu_buffer_rsrc_t sr =
-      rsrc(reinterpret_cast<const uint8_t*>(a.scales) + sb0 * ESZ, (uint32_t)(N * G * ESZ));
+      buffer_rsrc(reinterpret_cast<const uint8_t*>(a.scales) + sb0 * ESZ, (uint32_t)(N * G * ESZ));
   const __amdgpu_buffer_rsrc_t br =
-      rsrc(AFF ? (const void*)(a.biases + sb0) : a.scales, (uint32_t)(AFF ? N * G * 2 : 0));
+      buffer_rsrc(AFF ? (const void*)(a.biases + sb0) : a.scales, (uint32_t)(AFF ? N * G * 2 : 0));
 
   // pieces of this lane: chunk (wave + NW c), piece b
   int pc[CPW];
@@ -151,7 +129,7 @@ __global__ __launch_bounds__(512) void qmv_b4_kernel(const QmvArgs a, int gs_shi
     for (int s = 0; s < MS; s++)
 #pragma unroll
       for (int v = 0; v < XV; v++) {
-        const uint32_t o = live[c] ? (uint32_t)((4 * s + j) * K + pc[c] * KL) * 2u + (uint32_t)v * 16u : kDead;
+        const uint32_t o = live[c] ? (uint32_t)((4 * s + j) * K + pc[c] * KL) * 2u + (uint32_t)v * 16u : kDeadOfs;
         xv[c][s][v] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, o, 0, 0));
       }
   uint32_t sraw[CPW][RG], braw[CPW][RG];
@@ -161,7 +139,7 @@ __global__ __launch_bounds__(512) void qmv_b4_kernel(const QmvArgs a, int gs_shi
     for (int g = 0; g < RG; g++) {
       const int n = row0 + 4 * g + j;
       const uint32_t og = (uint32_t)(n * G + ((pc[c] * KL) >> gs_shift));  // in groups
-      const uint32_t ob = (live[c] && n < N) ? og * (uint32_t)ESZ : kDead;
+      const uint32_t ob = (live[c] && n < N) ? og * (uint32_t)ESZ : kDeadOfs;
       if constexpr (AFF) {
         sraw[c][g] = __builtin_amdgcn_raw_buffer_load_b16(sr, ob, 0, 0);
         braw[c][g] = __builtin_amdgcn_raw_buffer_load_b16(br, ob, 0, 0);
@@ -176,7 +154,7 @@ __global__ __launch_bounds__(512) void qmv_b4_kernel(const QmvArgs a, int gs_shi
 #pragma unroll
     for (int g = 0; g < RG; g++) {
       const int n = row0 + 4 * g + j;
-      const uint32_t o = (live[c] && n < N) ? (uint32_t)n * RB + (uint32_t)pc[c] * 16u : kDead;
+      const uint32_t o = (live[c] && n < N) ? (uint32_t)n * RB + (uint32_t)pc[c] * 16u : kDeadOfs;
       wv[c][g] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, o, 0, 2 /* nt */));
     }
   __builtin_amdgcn_sched_barrier(0);  // keep the arithmetic below the loads
@@ -194,13 +172,13 @@ __global__ __launch_bounds__(512) void qmv_b4_kernel(const QmvArgs a, int gs_shi
 #pragma unroll
         for (int v = 0; v < XV; v++)
 #pragma unroll
-          for (int e = 0; e < 4; e++) own = dot2b(xv[c][s][v][e], 0x3F803F80u, own);  // pairs times (1, 1)
+          for (int e = 0; e < 4; e++) own = dot2(xv[c][s][v][e], 0x3F803F80u, own);  // pairs times (1, 1)
         // the quad's four rows, broadcast from lanes 4b + 0..3
-        xs[c][s] = f32x4{dppf<0x00>(own), dppf<0x55>(own), dppf<0xAA>(own), dppf<0xFF>(own)};
+        xs[c][s] = f32x4{dpp<0x00>(own), dpp<0x55>(own), dpp<0xAA>(own), dpp<0xFF>(own)};
       }
       if constexpr (FMT == AFF4) {
 #pragma unroll
-        for (int v = 0; v < XV; v++) xv[c][s][v] = perm_aff4_x(xv[c][s][v]);
+        for (int v = 0; v < XV; v++) xv[c][s][v] = perm_aff4_v(xv[c][s][v]);
       }
     }
 
@@ -292,8 +270,8 @@ __global__ __launch_bounds__(512) void qmv_b4_kernel(const QmvArgs a, int gs_shi
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         float v = y[s][g][r];
-        v += dppf<0x124>(v);  // row_ror:4
-        v += dppf<0x128>(v);  // row_ror:8
+        v += dpp<0x124>(v);  // row_ror:4
+        v += dpp<0x128>(v);  // row_ror:8
         y[s][g][r] = v;
       }
   if ((lane & 15) < 4) {
@@ -321,7 +299,6 @@ __global__ __launch_bounds__(512) void qmv_b4_kernel(const QmvArgs a, int gs_shi
 
 namespace {
 
-constexpr int log2c(int v) { return v <= 1 ? 0 : 1 + log2c(v / 2); }
 
 template <int FMT, int MS>
 hipError_t b4_launch_ms(const QmvB4Plan& p, const QmvArgs& a, int gs_shift, dim3 grid, hipStream_t stream) {
@@ -403,7 +380,7 @@ QmvB4Plan qmv_b4_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int rg_re
 
 hipError_t qmv_b4_launch(int fmt, int gs, const QmvArgs& a, int nseg, const QmvB4Plan& p, hipStream_t stream) {
   if (!p.ok) return hipErrorInvalidValue;
-  const int gs_shift = log2c(gs);
+  const int gs_shift = log2i(gs);
   const dim3 grid((unsigned)p.tiles, (unsigned)nseg, 1);
   switch (fmt) {
     case AFF4: return b4_launch_fmt<AFF4>(p, a, gs_shift, grid, stream);

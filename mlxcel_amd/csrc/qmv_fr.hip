@@ -35,56 +35,8 @@ namespace mlxq {
 
 namespace {
 
-constexpr uint32_t kDead = 0x80000000u;  // a buffer offset past every operand: loads return 0
-constexpr int kWaves = 8;                // waves per workgroup
-constexpr int kSPre = 4;                 // scale units per thread issued before the weights
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
-}
-
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-
-// Sum CNT (<= 16) values per lane over each row of 16 lanes: step s pairs
-// lanes whose bit 3-s differs (row_mirror, row_half_mirror, quad swaps); the
-// lane with the bit set keeps the upper half of the values while more than
-// one is left.  Afterwards lane i of a row holds value i / (16 / CNT).
-template <int CNT, int STEP>
-__device__ __forceinline__ void row_butterfly(float* v, int lane) {
-  if constexpr (STEP < 4) {
-    constexpr int BIT = 8 >> STEP;
-    constexpr int CTRL = STEP == 0 ? 0x140 : (STEP == 1 ? 0x141 : (STEP == 2 ? 0x4E : 0xB1));
-    if constexpr (CNT > 1) {
-      constexpr int H = CNT / 2;
-      const bool up = (lane & BIT) != 0;
-#pragma unroll
-      for (int i = 0; i < H; i++) {
-        const float keep = up ? v[i + H] : v[i];
-        const float send = up ? v[i] : v[i + H];
-        v[i] = keep + dpp<CTRL>(send);
-      }
-      row_butterfly<H, STEP + 1>(v, lane);
-    } else {
-      v[0] += dpp<CTRL>(v[0]);
-      row_butterfly<1, STEP + 1>(v, lane);
-    }
-  }
-}
-
-constexpr int log2c(int v) { return v <= 1 ? 0 : 1 + log2c(v / 2); }
-
-// [x0..x7] (bf16) -> [x0,x4,x1,x5,x2,x6,x3,x7], the AFF4 operand order
-__device__ __forceinline__ u32x4 perm_aff4_x(u32x4 x) {
-  return u32x4{__builtin_amdgcn_perm(x[2], x[0], 0x05040100u), __builtin_amdgcn_perm(x[2], x[0], 0x07060302u),
-               __builtin_amdgcn_perm(x[3], x[1], 0x05040100u), __builtin_amdgcn_perm(x[3], x[1], 0x07060302u)};
-}
+constexpr int kWaves = 8;  // waves per workgroup
+constexpr int kSPre = 4;   // scale units per thread issued before the weights
 
 }  // namespace
 
@@ -113,13 +65,13 @@ __global__ __launch_bounds__(kWaves * 64) void qmv_fr_kernel(const QmvArgs a, in
   constexpr int XV = KL / 8;      // 16-byte activation pieces per lane and chunk
   constexpr int NP = KL / 2;      // bf16 pairs per lane and chunk
   constexpr int RW = kWaves * R;  // rows per workgroup
-  constexpr int LRW = log2c(RW);
+  constexpr int LRW = log2i(RW);
   constexpr int V = R * MR;       // partial sums per lane
   static_assert(V <= 16 && (V & (V - 1)) == 0, "partials per lane must be a power of two <= 16");
   constexpr int VQ = 16 / V;      // lanes holding one partial after the row butterfly
   constexpr int SB = AFF ? 8 : 4; // LDS bytes per staged scale
   constexpr int NT = kWaves * 64;
-  constexpr int LXV = log2c(XV);
+  constexpr int LXV = log2i(XV);
   constexpr int XPRE = (MR * CMAX * 64 * XV + NT - 1) / NT;  // activation loads per thread
 
   extern __shared__ __align__(16) unsigned char smem[];
@@ -143,13 +95,13 @@ __global__ __launch_bounds__(kWaves * 64) void qmv_fr_kernel(const QmvArgs a, in
   const int wrow0 = row0 + wave * R;       // this wave's first row
   const QmvFrLds L = qmv_fr_lds(FMT, MR, R, chunks, G);
 
-  const __amdgpu_buffer_rsrc_t wr = rsrc(a.w + (int64_t)expert * a.w_expert_stride, (uint32_t)N * RB);
-  const __amdgpu_buffer_rsrc_t xr = rsrc(a.x + (int64_t)xbatch * a.rps * K, (uint32_t)count * (uint32_t)K * 2u);
+  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.w + (int64_t)expert * a.w_expert_stride, (uint32_t)N * RB);
+  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.x + (int64_t)xbatch * a.rps * K, (uint32_t)count * (uint32_t)K * 2u);
   const int64_t sb0 = (int64_t)expert * a.s_expert_stride;
   const __amdgpu_buffer_rsrc_t sr =
-      rsrc(reinterpret_cast<const uint8_t*>(a.scales) + sb0 * (AFF ? 2 : 1), (uint32_t)(N * G * (AFF ? 2 : 1)));
+      buffer_rsrc(reinterpret_cast<const uint8_t*>(a.scales) + sb0 * (AFF ? 2 : 1), (uint32_t)(N * G * (AFF ? 2 : 1)));
   const __amdgpu_buffer_rsrc_t br =
-      rsrc(AFF ? (const void*)(a.biases + sb0) : a.scales, (uint32_t)(AFF ? N * G * 2 : 0));
+      buffer_rsrc(AFF ? (const void*)(a.biases + sb0) : a.scales, (uint32_t)(AFF ? N * G * 2 : 0));
 
   // ---- 1. loads: activations, scales, then this wave's rows ----------------
   // activation piece i of row m: 8 bf16 at K = 8 i (pieces past K read 0);
@@ -162,7 +114,7 @@ __global__ __launch_bounds__(kWaves * 64) void qmv_fr_kernel(const QmvArgs a, in
 #pragma unroll
     for (int u = 0; u < XPRE; u++) {
       const int i = (int)threadIdx.x + NT * u;
-      const uint32_t off = i < kp ? (uint32_t)(m * K + 8 * i) * 2u : kDead;
+      const uint32_t off = i < kp ? (uint32_t)(m * K + 8 * i) * 2u : kDeadOfs;
       xpre[m][u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
     }
 
@@ -198,7 +150,7 @@ __global__ __launch_bounds__(kWaves * 64) void qmv_fr_kernel(const QmvArgs a, in
   // this lane's byte offset in chunk j of a row (padded lanes read 0)
   uint32_t wo[CMAX];
 #pragma unroll
-  for (int j = 0; j < CMAX; j++) wo[j] = (j < chunks && j * 64 + lane < nlc) ? (uint32_t)(j * 1024 + lane * 16) : kDead;
+  for (int j = 0; j < CMAX; j++) wo[j] = (j < chunks && j * 64 + lane < nlc) ? (uint32_t)(j * 1024 + lane * 16) : kDeadOfs;
   u32x4 wv[R][CMAX];
 #pragma unroll
   for (int r = 0; r < R; r++) {
@@ -220,7 +172,7 @@ __global__ __launch_bounds__(kWaves * 64) void qmv_fr_kernel(const QmvArgs a, in
       s += dpp<0xB1>(s);                                           // + the piece on lane ^ 1
       if constexpr (XV == 4) s += dpp<0x4E>(s);                    // + the pieces on lanes ^ 2
     }
-    if constexpr (FMT == AFF4) v = perm_aff4_x(v);
+    if constexpr (FMT == AFF4) v = perm_aff4_v(v);
     if (i < xpieces) {
       const int j = i >> (6 + LXV), ln = (i >> LXV) & 63, pv = i & (XV - 1);
       *reinterpret_cast<u32x4*>(smem + L.x + (uint32_t)(((m * chunks + j) * XV + pv) * 1024 + ln * 16)) = v;
@@ -395,7 +347,7 @@ QmvFrPlan qmv_fr_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int r_req
 
 hipError_t qmv_fr_launch(int fmt, int gs, const QmvArgs& a, int nseg, const QmvFrPlan& p, hipStream_t stream) {
   if (!p.ok) return hipErrorInvalidValue;
-  const int gs_shift = log2c(gs);
+  const int gs_shift = log2i(gs);
   const dim3 grid((unsigned)p.tiles, (unsigned)nseg, 1);
   switch (fmt) {
     case AFF4: return p.mr == 1 ? fr_launch<AFF4, 1>(p, a, gs_shift, grid, stream)

@@ -45,29 +45,15 @@ constexpr int MID_ROWS = MID_NW * MID_T * 16;  // weight rows per workgroup
 constexpr int MID_WIN = 8;                     // windows per workgroup
 constexpr int MID_P = 4;                       // windows of weight loads in flight per tile
 constexpr int MID_NT = 64 * MID_NW;            // threads per workgroup
-constexpr uint32_t kDeadMid = 0x80000000u;     // a buffer offset past every operand: loads return 0
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t mid_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-
-__device__ __forceinline__ float dot2m(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
-}
-
-template <int CTRL>
-__device__ __forceinline__ float dppm(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
 
 // Sum over aligned groups of PG (4, 8 or 16) lanes: quad swaps, then the
 // half-row and row mirrors, which pair the partial sums of adjacent groups.
 template <int PG>
 __device__ __forceinline__ float group_sum(float v) {
-  v += dppm<0xB1>(v);  // quad_perm [1,0,3,2]
-  v += dppm<0x4E>(v);  // quad_perm [2,3,0,1]
-  if constexpr (PG >= 8) v += dppm<0x141>(v);   // row_half_mirror
-  if constexpr (PG >= 16) v += dppm<0x140>(v);  // row_mirror
+  v += dpp<0xB1>(v);  // quad_perm [1,0,3,2]
+  v += dpp<0x4E>(v);  // quad_perm [2,3,0,1]
+  if constexpr (PG >= 8) v += dpp<0x141>(v);   // row_half_mirror
+  if constexpr (PG >= 16) v += dpp<0x140>(v);  // row_mirror
   return v;
 }
 
@@ -129,10 +115,10 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
   const QmvMidLds L = qmv_mid_lds(FMT, 1 << a.gs_shift, kr, NA);
 
   const uint32_t RB = (uint32_t)(K / CK) * 16u;  // bytes per weight row
-  const __amdgpu_buffer_rsrc_t wr = mid_rsrc(a.w, (uint32_t)N * RB);
-  const __amdgpu_buffer_rsrc_t xr = mid_rsrc(a.x, (uint32_t)M * (uint32_t)K * 2u);
-  const __amdgpu_buffer_rsrc_t sr = mid_rsrc(a.scales, (uint32_t)N * (uint32_t)G * 2u);
-  const __amdgpu_buffer_rsrc_t br = mid_rsrc(a.biases, (uint32_t)N * (uint32_t)G * 2u);
+  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.w, (uint32_t)N * RB);
+  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.x, (uint32_t)M * (uint32_t)K * 2u);
+  const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(a.scales, (uint32_t)N * (uint32_t)G * 2u);
+  const __amdgpu_buffer_rsrc_t br = buffer_rsrc(a.biases, (uint32_t)N * (uint32_t)G * 2u);
 
   // ---- 1. loads: activation range, the block's scales, then the first
   // windows of weights (the staged data is consumed first; loads retire in
@@ -143,7 +129,7 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
   for (int i = 0; i < XPMAX; i++) {
     const int p = tid + i * MID_NT;
     const int m = p / (kr / 8), c = p % (kr / 8);
-    const uint32_t o = p < xpieces ? (uint32_t)(m * K + k0 + 8 * c) * 2u : kDeadMid;
+    const uint32_t o = p < xpieces ? (uint32_t)(m * K + k0 + 8 * c) * 2u : kDeadOfs;
     xpre[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, o, 0, 0));
   }
   const int sunits = MID_ROWS * ngr / SW;  // per operand
@@ -153,7 +139,7 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
     const int u = tid + i * MID_NT;
     const int r = u / (ngr / SW), gl = (u % (ngr / SW)) * SW;
     const int n = row_wg + r;
-    const uint32_t o = (u < sunits && n < N) ? (uint32_t)(n * G + (k0 >> a.gs_shift) + gl) * 2u : kDeadMid;
+    const uint32_t o = (u < sunits && n < N) ? (uint32_t)(n * G + (k0 >> a.gs_shift) + gl) * 2u : kDeadOfs;
     if constexpr (SW == 8) {
       spre[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, o, 0, 0));
       bpre[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(br, o, 0, 0));
@@ -171,7 +157,7 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
 #pragma unroll
   for (int t = 0; t < MID_T; t++) {
     const int n = row_wg + wave * (MID_T * 16) + t * 16 + nl;
-    woff[t] = n < N ? (uint32_t)n * RB + (uint32_t)(k0 / CK + g) * 16u : kDeadMid;
+    woff[t] = n < N ? (uint32_t)n * RB + (uint32_t)(k0 / CK + g) * 16u : kDeadOfs;
   }
   u32x4 wbuf[MID_P][MID_T];
 #pragma unroll
@@ -179,7 +165,7 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
 #pragma unroll
     for (int t = 0; t < MID_T; t++)
       wbuf[p][t] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, woff[t] == kDeadMid ? kDeadMid : woff[t] + p * 64u, 0,
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, woff[t] == kDeadOfs ? kDeadOfs : woff[t] + p * 64u, 0,
                                                        2 /* nt */));
   __builtin_amdgcn_sched_barrier(0);
 
@@ -200,7 +186,7 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
     }
     float sum = 0.f;
 #pragma unroll
-    for (int e = 0; e < 4; e++) sum = dot2m(xpre[i][e], 0x3F803F80u, sum);  // pairs times (1, 1); dead pieces are 0
+    for (int e = 0; e < 4; e++) sum = dot2(xpre[i][e], 0x3F803F80u, sum);  // pairs times (1, 1); dead pieces are 0
     sum = group_sum<PG>(sum);
     const int w = (8 * c) / KW, slot = ((8 * c) % KW) / XG;
     const int r = m * S + slot;
@@ -274,7 +260,7 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
         if (w + MID_P < MID_WIN)
           wbuf[w % MID_P][t] = __builtin_bit_cast(
               u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                         wr, woff[t] == kDeadMid ? kDeadMid : woff[t] + (uint32_t)(w + MID_P) * 64u, 0, 2 /* nt */));
+                         wr, woff[t] == kDeadOfs ? kDeadOfs : woff[t] + (uint32_t)(w + MID_P) * 64u, 0, 2 /* nt */));
         bf16x8 B[NQ];
         if constexpr (FMT == AFF4) {
 #pragma unroll
