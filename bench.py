@@ -15,13 +15,14 @@ streaming read of the same bytes per launch on this device, timed the same
 way (the practical bound at this size).
 
 Also reported (extra): the M in {1,2,4,8,16} x {4,8}-bit decode sweep, the
-qmm prefill configs, mxfp4 gather_qmm (gpt-oss-20b MoE shapes), end-to-end
+qmm prefill configs, mxfp4 gather_qmm (gpt-oss-20b MoE shapes), the fused
+decode MoE (Qwen3-30B-A3B experts) against its gather_qmm chain, end-to-end
 decode of a Qwen3-8B-shaped model, the measured device copy ceiling, and the
 single-core CPU baseline (the oracle's restatement of MLX's CPU `_qmm_t`,
 overlays/cpu/mlx/backend/cpu/quantized.cpp:199-257).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
-                       [--extras copy,sweep,qmm,gather,e2e]
+                       [--extras copy,sweep,qmm,gather,moe,e2e]
        python bench.py --traffic-probe   (under rocprofv3 --pmc: copy calibration + gate launches)
 """
 from __future__ import annotations
@@ -312,6 +313,56 @@ def gather_moe(iters=100):
     return res
 
 
+def fused_moe(iters=200):
+    """Fused single-token decode MoE (mlxq_fused_moe_expert) on Qwen3-30B-A3B
+    experts: 128 experts, hidden 2048, expert intermediate 768, top-8, 4-bit
+    affine g64; two copies of the expert stacks and 16 routing sets rotate so
+    the selected experts stream from HBM.  Compared with the reference's
+    fallback on this library: gather_qmm for gate, up and down, torch for
+    SiLU * up and the score-weighted sum."""
+    E, din, dff, k, gs, bits = 128, 2048, 768, 8, 64, 4
+    copies, nsets = 2, 16
+    stacks = []
+    for c in range(copies):
+        stacks.append([make_affine(E * dff, din, bits, gs, 80 + 3 * c), make_affine(E * dff, din, bits, gs, 81 + 3 * c),
+                       make_affine(E * din, dff, bits, gs, 82 + 3 * c)])
+        g, u, d = stacks[-1]
+        stacks[-1] = [tuple(t.view(E, dff, -1) for t in g), tuple(t.view(E, dff, -1) for t in u),
+                      tuple(t.view(E, din, -1) for t in d)]
+    rng = np.random.default_rng(9)
+    ids = [torch.from_numpy(rng.permutation(E)[:k].astype(np.int32)).cuda() for _ in range(nsets)]
+    scs = [torch.softmax(torch.randn(k, device="cuda"), 0) for _ in range(nsets)]
+    x = randn_bf16((din,), 13)
+    out = torch.empty(din, dtype=torch.bfloat16, device="cuda")
+    per_expert = 2 * (dff * din * bits // 8 + dff * (din // gs) * 4) + din * dff * bits // 8 + din * (dff // gs) * 4
+    nbytes = k * per_expert + 2 * din * 2
+
+    def fused(j):
+        g, u, d = stacks[j % copies]
+        s = j % nsets
+        mq.fused_moe_expert(x, ids[s], *g, *u, *d, scs[s], din, dff, k, bits, bits, gs, out=out)
+
+    def chain(j):
+        g, u, d = stacks[j % copies]
+        s = j % nsets
+        x4 = x.view(1, 1, 1, din)
+        rhs = ids[s].view(1, k)
+        gt = mq.gather_qmm(x4, *g, None, rhs, True, gs, bits)
+        ut = mq.gather_qmm(x4, *u, None, rhs, True, gs, bits)
+        a = torch.nn.functional.silu(gt) * ut
+        dt = mq.gather_qmm(a, *d, None, rhs, True, gs, bits)
+        out.copy_((dt.view(k, din).float() * scs[s].view(k, 1)).sum(0))
+
+    res = {"workload": "qwen3-30b-a3b experts: E=128, din=2048, dff=768, top-8, 4-bit g64, one token",
+           "bytes_per_call": nbytes}
+    for name, fn in (("fused", fused), ("gather_chain", chain)):
+        graphs = [capture(lambda j=j: fn(j)) for j in range(copies * nsets)]
+        ms = timed_graphs(graphs, iters, 10)
+        res[name] = {"us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
+    return res
+
+
 # ---- end-to-end decode (BASELINE configs[4]) --------------------------------
 #
 # A Qwen3-8B-shaped decoder (36 layers, hidden 4096, 32 query / 8 key-value
@@ -557,8 +608,8 @@ def main():
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--extras", default="copy,sweep,qmm,gather,e2e",
-                    help="comma-separated extra sections: copy, sweep, qmm, gather, e2e")
+    ap.add_argument("--extras", default="copy,sweep,qmm,gather,moe,e2e",
+                    help="comma-separated extra sections: copy, sweep, qmm, gather, moe, e2e")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run 5 copies of 256 MiB and 5 gate launches, eager, for rocprofv3 --pmc")
@@ -610,6 +661,8 @@ def main():
             extra["qmm_prefill"] = qmm_prefill()
         if "gather" in want:
             extra["gather_mxfp4_moe"] = gather_moe()
+        if "moe" in want:
+            extra["fused_moe_decode"] = fused_moe()
         if "e2e" in want:
             extra["e2e_decode_qwen3_8b_shape"] = e2e_decode()
         line["extra"] = extra

@@ -12,6 +12,10 @@
  *                             -> mlx::core::dequantize, ops.cpp:5753-5805)
  *   mlxq_quantize          <- ffi::quantize_weights_* (mlx_cxx_bridge.cpp:7867-7900
  *                             -> mlx::core::quantize, ops.cpp:5454-5492)
+ *   mlxq_fused_moe_expert  <- ffi::fused_moe_expert_kernel (lib.rs:2336-2356,
+ *                             mlx_cxx_bridge.h:2061-2070, mlx_cxx_kernels.cpp:4078-4094)
+ *   mlxq_fused_moe_geglu   <- ffi::fused_moe_geglu_kernel  (lib.rs:2357-2380,
+ *                             mlx_cxx_bridge.h:2072-2084, mlx_cxx_kernels.cpp:4096-4112)
  *
  * Conventions (differences from the reference are deliberate and listed):
  *   - Eager and stream-ordered: work is enqueued on `stream` (a hipStream_t,
@@ -147,6 +151,41 @@ mlxq_status mlxq_dequantize(const mlxq_array* w, const mlxq_array* scales,
 mlxq_status mlxq_quantize(const mlxq_array* w, int32_t group_size, int32_t bits,
                           const char* mode, mlxq_array* wq_out, mlxq_array* scales_out,
                           mlxq_array* biases_out, void* stream);
+
+/* Fused single-token decode MoE with SwiGLU experts, as the reference's
+ * fused_moe_expert_kernel:
+ *   out[h] = sum_j scores[j] * down_e(silu(gate_e(x)) * up_e(x))[h],  e = indices[j]
+ * x: bfloat16, din elements.  indices, scores: k elements (32/64-bit
+ * integers; float32, bfloat16 or float16).  gate_w/up_w: uint32
+ * (E, dff, din*gu_bits/32) with bfloat16 scales/biases (E, dff, din/group_size);
+ * down_w: uint32 (E, din, dff*d_bits/32) with bfloat16 scales/biases
+ * (E, din, dff/group_size); affine quantization.  out: bfloat16 (din).
+ * Gate/up, the activation and every per-expert product are fp32; the sum over
+ * the k experts is fp32 in a fixed order and rounded to bfloat16 once
+ * (mlx_cxx_kernels.cpp:3886-3899).  Implemented: gu_bits 4/8, d_bits 4/6/8,
+ * group_size 32/64/128; other valid configurations return MLXQ_EUNSUPPORTED
+ * (the reference's callers then take their gather_qmm path).  Index values
+ * past the expert count are clamped to E-1.  Uses the per-stream workspace
+ * (k*dff fp32). */
+mlxq_status mlxq_fused_moe_expert(const mlxq_array* x, const mlxq_array* indices,
+                                  const mlxq_array* gate_w, const mlxq_array* gate_s,
+                                  const mlxq_array* gate_b, const mlxq_array* up_w,
+                                  const mlxq_array* up_s, const mlxq_array* up_b,
+                                  const mlxq_array* down_w, const mlxq_array* down_s,
+                                  const mlxq_array* down_b, const mlxq_array* scores, int32_t din,
+                                  int32_t dff, int32_t k, int32_t gu_bits, int32_t d_bits,
+                                  int32_t group_size, mlxq_array* out, void* stream);
+
+/* Same with GeGLU experts (gemma4): gelu_tanh(gate) * up, as the reference's
+ * fused_moe_geglu_kernel. */
+mlxq_status mlxq_fused_moe_geglu(const mlxq_array* x, const mlxq_array* indices,
+                                 const mlxq_array* gate_w, const mlxq_array* gate_s,
+                                 const mlxq_array* gate_b, const mlxq_array* up_w,
+                                 const mlxq_array* up_s, const mlxq_array* up_b,
+                                 const mlxq_array* down_w, const mlxq_array* down_s,
+                                 const mlxq_array* down_b, const mlxq_array* scores, int32_t din,
+                                 int32_t dff, int32_t k, int32_t gu_bits, int32_t d_bits,
+                                 int32_t group_size, mlxq_array* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -4,7 +4,9 @@ The product is the C-ABI library ``libmlxq.so`` (``include/mlxq.h``); this
 package holds its HIP sources (``csrc/``), the build script, and a Python
 mirror of the reference operator interface (``ops``).
 """
-from .ops import dequantize, gather_qmm, quantize, quantized_matmul  # noqa: F401
+from .ops import (dequantize, fused_moe_expert, fused_moe_geglu, gather_qmm, quantize,  # noqa: F401
+                  quantized_matmul)
 from ._lib import LIB_PATH, load as load_library  # noqa: F401
 
-__all__ = ["quantized_matmul", "gather_qmm", "dequantize", "quantize", "load_library", "LIB_PATH"]
+__all__ = ["quantized_matmul", "gather_qmm", "dequantize", "quantize", "fused_moe_expert", "fused_moe_geglu",
+           "load_library", "LIB_PATH"]

@@ -39,6 +39,8 @@ SYMBOLS = (
     "mlxq_gather_qmm_shape",
     "mlxq_dequantize",
     "mlxq_quantize",
+    "mlxq_fused_moe_expert",
+    "mlxq_fused_moe_geglu",
 )
 
 _lib = None
@@ -74,6 +76,8 @@ def load() -> ctypes.CDLL:
                                           ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(I32)]
     lib.mlxq_dequantize.argtypes = [A, A, A, I32, I32, S, I32, A, P]
     lib.mlxq_quantize.argtypes = [A, I32, I32, S, A, A, A, P]
+    lib.mlxq_fused_moe_expert.argtypes = [A] * 12 + [I32] * 6 + [A, P]
+    lib.mlxq_fused_moe_geglu.argtypes = [A] * 12 + [I32] * 6 + [A, P]
     for name in SYMBOLS[2:]:
         getattr(lib, name).restype = ctypes.c_int
     _lib = lib

@@ -44,6 +44,7 @@ SOURCES = {
     "qmv_mid.hip": [],
     "qmm_group.hip": [],
     "qmm.hip": [],
+    "moe.hip": [],
     "dequant.hip": ["-ffp-contract=off"],
 }
 

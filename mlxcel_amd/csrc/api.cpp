@@ -1351,3 +1351,135 @@ mlxq_status mlxq_quantize(const mlxq_array* w, int32_t group_size, int32_t bits,
 }
 
 }  // extern "C"
+
+// ---- fused single-token decode MoE -------------------------------------------
+//
+// fused_moe_expert_kernel / fused_moe_geglu_kernel (mlx_cxx_bridge.h:2061-2084,
+// lib.rs:2336-2380; host side mlx_cxx_kernels.cpp:3817-4112).  The reference
+// casts its inputs to the activation dtype and reads them unchecked; here the
+// shapes are checked (EINVAL) and configurations the kernels do not cover are
+// refused (EUNSUPPORTED), which the caller answers with its gather_qmm
+// fallback, as it answers the reference's "no kernel port" refusal.
+
+namespace {
+
+void fused_moe(const char* tag, const mlxq_array* x, const mlxq_array* indices, const mlxq_array* gate_w,
+               const mlxq_array* gate_s, const mlxq_array* gate_b, const mlxq_array* up_w, const mlxq_array* up_s,
+               const mlxq_array* up_b, const mlxq_array* down_w, const mlxq_array* down_s, const mlxq_array* down_b,
+               const mlxq_array* scores, int32_t din, int32_t dff, int32_t k, int32_t gu_bits, int32_t d_bits,
+               int32_t group_size, int act, mlxq_array* out, void* stream_) {
+  const mlxq_array* all[] = {x, indices, gate_w, gate_s, gate_b, up_w, up_s, up_b, down_w, down_s, down_b, scores, out};
+  const char* names[] = {"x",      "indices", "gate_w", "gate_s", "gate_b", "up_w", "up_s",
+                         "up_b",   "down_w",  "down_s", "down_b", "scores", "out"};
+  for (int i = 0; i < 13; i++) check_array(all[i], names[i]);
+  auto bad = [&](const std::string& what) {
+    std::ostringstream os;
+    os << "[" << tag << "] " << what;
+    invalid(os);
+  };
+  if (din <= 0 || dff <= 0 || k <= 0) bad("din, dff and k must be positive");
+  if (k > 65535) unsupported(std::string(tag) + ": at most 65535 experts per token");
+  if (gu_bits != 4 && gu_bits != 8)
+    unsupported(std::string(tag) + ": gate/up bits must be 4 or 8 (got " + std::to_string(gu_bits) + ")");
+  if (d_bits != 4 && d_bits != 6 && d_bits != 8)
+    unsupported(std::string(tag) + ": down bits must be 4, 6 or 8 (got " + std::to_string(d_bits) + ")");
+  if (group_size != 32 && group_size != 64 && group_size != 128)
+    unsupported(std::string(tag) + ": group_size must be 32, 64 or 128 (got " + std::to_string(group_size) + ")");
+  // (with group_size >= 32 this also gives whole uint32 columns at 6 bits)
+  if (din % group_size || dff % group_size) bad("din and dff must be multiples of group_size");
+
+  View xv{x}, iv{indices}, sv{scores}, ov{out};
+  if (xv.size() != din) bad("x must have din elements");
+  if (iv.size() != k) bad("indices must have k elements");
+  if (sv.size() != k) bad("scores must have k elements");
+  if (ov.ndim() != 1 || ov.dim(0) != din) bad("out must have shape (din)");
+  if (!is_integral(indices->dtype) || (dtype_size(indices->dtype) != 4 && dtype_size(indices->dtype) != 8))
+    unsupported(std::string(tag) + ": indices must be 32- or 64-bit integers");
+  if (x->dtype != MLXQ_BFLOAT16 || out->dtype != MLXQ_BFLOAT16)
+    unsupported(std::string(tag) + ": only bfloat16 activations are implemented");
+  if (scores->dtype != MLXQ_FLOAT32 && scores->dtype != MLXQ_BFLOAT16 && scores->dtype != MLXQ_FLOAT16)
+    unsupported(std::string(tag) + ": scores must be float32, bfloat16 or float16");
+
+  View gw{gate_w};
+  if (gw.ndim() != 3) bad("gate_w must have shape (E, dff, din * bits / 32)");
+  const int64_t E = gw.dim(0);
+  if (E <= 0) bad("the expert count must be positive");
+  auto want = [&](const mlxq_array* a, const char* name, Shape shape, int dtype) {
+    if (View{a}.shape() != shape) bad(std::string(name) + " must have shape " + fmt_shape(shape));
+    if (a->dtype != dtype) bad(std::string(name) + " must be " + dtype_name(dtype));
+    require_contiguous(a, name);
+  };
+  want(gate_w, "gate_w", {E, dff, (int64_t)din * gu_bits / 32}, MLXQ_UINT32);
+  want(up_w, "up_w", {E, dff, (int64_t)din * gu_bits / 32}, MLXQ_UINT32);
+  want(down_w, "down_w", {E, din, (int64_t)dff * d_bits / 32}, MLXQ_UINT32);
+  for (auto p : {std::make_pair(gate_s, "gate_s"), std::make_pair(gate_b, "gate_b"), std::make_pair(up_s, "up_s"),
+                 std::make_pair(up_b, "up_b")})
+    want(p.first, p.second, {E, dff, din / group_size}, MLXQ_BFLOAT16);
+  for (auto p : {std::make_pair(down_s, "down_s"), std::make_pair(down_b, "down_b")})
+    want(p.first, p.second, {E, din, dff / group_size}, MLXQ_BFLOAT16);
+  require_contiguous(x, "x");
+  require_contiguous(indices, "indices");
+  require_contiguous(scores, "scores");
+  require_contiguous(out, "out");
+  // 32-bit buffer offsets: one expert's gate matrix, its scales and the
+  // activation staging stay below 2 GiB
+  if ((int64_t)dff * din * gu_bits / 8 >= ((int64_t)1 << 31) || (int64_t)k * dff * 4 >= ((int64_t)1 << 31) ||
+      (int64_t)dff * (din / group_size) * 2 >= ((int64_t)1 << 31) || (int64_t)din * 2 >= ((int64_t)1 << 31))
+    unsupported(std::string(tag) + ": operands above 2 GiB per expert");
+
+  const int dev = current_device();
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  mlxq::MoeArgs a{};
+  a.x = static_cast<const uint16_t*>(x->data);
+  a.idx = static_cast<const uint32_t*>(indices->data);
+  a.idx_stride = dtype_size(indices->dtype) / 4;
+  a.scores = scores->data;
+  a.score_dt = scores->dtype == MLXQ_FLOAT32 ? 0 : (scores->dtype == MLXQ_BFLOAT16 ? 1 : 2);
+  a.gate_w = static_cast<const uint32_t*>(gate_w->data);
+  a.gate_s = static_cast<const uint16_t*>(gate_s->data);
+  a.gate_b = static_cast<const uint16_t*>(gate_b->data);
+  a.up_w = static_cast<const uint32_t*>(up_w->data);
+  a.up_s = static_cast<const uint16_t*>(up_s->data);
+  a.up_b = static_cast<const uint16_t*>(up_b->data);
+  a.down_w = static_cast<const uint32_t*>(down_w->data);
+  a.down_s = static_cast<const uint16_t*>(down_s->data);
+  a.down_b = static_cast<const uint16_t*>(down_b->data);
+  a.out = static_cast<uint16_t*>(out->data);
+  a.din = din;
+  a.dff = dff;
+  a.k = k;
+  a.E = (int)std::min<int64_t>(E, INT32_MAX);
+  a.gs_shift = group_size == 32 ? 5 : (group_size == 64 ? 6 : 7);
+  a.act = reinterpret_cast<float*>(workspace(dev, stream, (size_t)k * dff * sizeof(float)).data);
+  hip_check(mlxq::moe_launch(a, gu_bits, d_bits, act, stream), "fused MoE launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+mlxq_status mlxq_fused_moe_expert(const mlxq_array* x, const mlxq_array* indices, const mlxq_array* gate_w,
+                                  const mlxq_array* gate_s, const mlxq_array* gate_b, const mlxq_array* up_w,
+                                  const mlxq_array* up_s, const mlxq_array* up_b, const mlxq_array* down_w,
+                                  const mlxq_array* down_s, const mlxq_array* down_b, const mlxq_array* scores,
+                                  int32_t din, int32_t dff, int32_t k, int32_t gu_bits, int32_t d_bits,
+                                  int32_t group_size, mlxq_array* out, void* stream) {
+  return guarded([&] {
+    fused_moe("fused_moe_expert_kernel", x, indices, gate_w, gate_s, gate_b, up_w, up_s, up_b, down_w, down_s,
+              down_b, scores, din, dff, k, gu_bits, d_bits, group_size, mlxq::MOE_SWIGLU, out, stream);
+  });
+}
+
+mlxq_status mlxq_fused_moe_geglu(const mlxq_array* x, const mlxq_array* indices, const mlxq_array* gate_w,
+                                 const mlxq_array* gate_s, const mlxq_array* gate_b, const mlxq_array* up_w,
+                                 const mlxq_array* up_s, const mlxq_array* up_b, const mlxq_array* down_w,
+                                 const mlxq_array* down_s, const mlxq_array* down_b, const mlxq_array* scores,
+                                 int32_t din, int32_t dff, int32_t k, int32_t gu_bits, int32_t d_bits,
+                                 int32_t group_size, mlxq_array* out, void* stream) {
+  return guarded([&] {
+    fused_moe("fused_moe_geglu_kernel", x, indices, gate_w, gate_s, gate_b, up_w, up_s, up_b, down_w, down_s,
+              down_b, scores, din, dff, k, gu_bits, d_bits, group_size, mlxq::MOE_GEGLU, out, stream);
+  });
+}
+
+}  // extern "C"

@@ -254,4 +254,28 @@ struct GroupArgs {
 constexpr int kGroupMaxExperts = 8192;  // LDS: (3 E + 1024) words
 hipError_t launch_group_by_expert(const GroupArgs& a, hipStream_t stream);
 
+// ---- fused single-token decode MoE (moe.hip) -----------------------------------
+enum MoeAct : int { MOE_SWIGLU = 0, MOE_GEGLU = 1 };
+constexpr int kMoeMaxWaves = 8;  // waves per workgroup (more lane chunks loop)
+struct MoeArgs {
+  const uint16_t* x;        // bf16 [din]
+  const uint32_t* idx;      // expert per slot (32- or 64-bit, low word), [k]
+  int idx_stride;           // 32-bit words per index (1 or 2)
+  const void* scores;       // routing weight per slot, [k]
+  int score_dt;             // 0 fp32, 1 bf16, 2 fp16
+  const uint32_t* gate_w;   // [E][dff][din * gu_bits / 32]
+  const uint16_t* gate_s;   // bf16 [E][dff][din / gs]
+  const uint16_t* gate_b;
+  const uint32_t* up_w;
+  const uint16_t* up_s;
+  const uint16_t* up_b;
+  const uint32_t* down_w;   // [E][din][dff * d_bits / 32]
+  const uint16_t* down_s;   // bf16 [E][din][dff / gs]
+  const uint16_t* down_b;
+  float* act;               // fp32 [k][dff] workspace
+  uint16_t* out;            // bf16 [din]
+  int din, dff, k, E, gs_shift;
+};
+hipError_t moe_launch(const MoeArgs& a, int gu_bits, int d_bits, int act, hipStream_t stream);
+
 }  // namespace mlxq

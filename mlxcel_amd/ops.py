@@ -207,3 +207,39 @@ def quantize(w: torch.Tensor, group_size: Optional[int] = None, bits: Optional[i
     if st:
         _raise(st)
     return (wq, scales, biases) if mode == "affine" else (wq, scales)
+
+
+def _fused_moe(fn_name: str, x, indices, gate_w, gate_s, gate_b, up_w, up_s, up_b, down_w, down_s, down_b,
+               scores, din: int, dff: int, k: int, gu_bits: int, d_bits: int, group_size: int,
+               out: Optional[torch.Tensor]) -> torch.Tensor:
+    lib = _lib.load()
+    dev = _device_of(x)
+    if out is None:
+        out = torch.empty(max(int(din), 0), dtype=x.dtype, device=dev)
+    arrs = [_arr(t) for t in (x, indices, gate_w, gate_s, gate_b, up_w, up_s, up_b, down_w, down_s, down_b,
+                              scores, out)]
+    with torch.cuda.device(dev):
+        st = getattr(lib, fn_name)(*[_ref(a) for a in arrs[:12]], din, dff, k, gu_bits, d_bits, group_size,
+                                   _ref(arrs[12]), _stream(dev))
+    if st:
+        _raise(st)
+    return out
+
+
+def fused_moe_expert(x, indices, gate_w, gate_s, gate_b, up_w, up_s, up_b, down_w, down_s, down_b, scores,
+                     din: int, dff: int, k: int, gu_bits: int, d_bits: int, group_size: int, *,
+                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The reference's ``fused_moe_expert_kernel`` (SwiGLU experts, one decode
+    token): ``sum_j scores[j] * down_e(silu(gate_e(x)) * up_e(x))`` over
+    ``e = indices[j]``; returns a ``(din,)`` tensor in x's dtype."""
+    return _fused_moe("mlxq_fused_moe_expert", x, indices, gate_w, gate_s, gate_b, up_w, up_s, up_b, down_w,
+                      down_s, down_b, scores, din, dff, k, gu_bits, d_bits, group_size, out)
+
+
+def fused_moe_geglu(x, indices, gate_w, gate_s, gate_b, up_w, up_s, up_b, down_w, down_s, down_b, scores,
+                    din: int, dff: int, k: int, gu_bits: int, d_bits: int, group_size: int, *,
+                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The reference's ``fused_moe_geglu_kernel`` (GeGLU experts: tanh-approximated
+    GELU of the gate times up)."""
+    return _fused_moe("mlxq_fused_moe_geglu", x, indices, gate_w, gate_s, gate_b, up_w, up_s, up_b, down_w,
+                      down_s, down_b, scores, din, dff, k, gu_bits, d_bits, group_size, out)

@@ -51,6 +51,8 @@ def _declare(l: ctypes.CDLL) -> None:
         "oracle_qmm_affine": [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P],
         "oracle_fp_qmm_t_mxfp4": [_P, _P, _P, _I64, _I64, _I64, _P],
         "oracle_gather_qmm_t": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _I, _P],
+        "oracle_affine_dequantize_f32": [_P, _P, _P, _I64, _I64, _I, _I, _P],
+        "oracle_fused_moe": [_P] * 12 + [_I64] * 4 + [_I] * 4 + [_P],
     }
     for name, args in sig.items():
         fn = getattr(l, name)
@@ -110,6 +112,19 @@ def affine_dequantize(wq, scales, biases, group_size: int = 64, bits: int = 4, r
     _check(lib().oracle_affine_dequantize(_ptr(wq), _ptr(scales), _ptr(biases), rows, K,
                                           group_size, bits, rounding, _ptr(out)),
            "affine_dequantize")
+    return out
+
+
+def affine_dequantize_f32(wq, scales, biases, group_size: int = 64, bits: int = 4):
+    """s * q + b in float32 (no bf16 rounding)."""
+    wq = np.ascontiguousarray(wq, dtype=np.uint32)
+    scales = np.ascontiguousarray(scales, dtype=np.uint16)
+    biases = np.ascontiguousarray(biases, dtype=np.uint16)
+    K = wq.shape[-1] * 32 // bits
+    rows = wq.size // wq.shape[-1]
+    out = np.empty(wq.shape[:-1] + (K,), dtype=np.float32)
+    _check(lib().oracle_affine_dequantize_f32(_ptr(wq), _ptr(scales), _ptr(biases), rows, K, group_size, bits,
+                                              _ptr(out)), "affine_dequantize_f32")
     return out
 
 
@@ -202,6 +217,29 @@ def gather_qmm_t(x_bf16, wq, scales, biases, lhs, rhs, group_size=64, bits=4, mo
     _check(lib().oracle_gather_qmm_t(_ptr(x), _ptr(wq), _ptr(scales), bptr, _ptr(lhs), _ptr(rhs),
                                      lhs.size, M, N, K, group_size, bits, m, _ptr(out)),
            "gather_qmm_t")
+    return out
+
+
+def fused_moe(x_bf16, indices, scores, gate, up, down, group_size: int = 64, gu_bits: int = 4,
+              d_bits: int = 4, act: str = "swiglu") -> np.ndarray:
+    """Dense fp64 restatement of the reference's fused single-token decode MoE
+    (``fused_moe_expert_kernel`` / ``fused_moe_geglu_kernel``): gate, up and
+    down are ``(wq, scales, biases)`` stacks over experts; returns float32
+    ``(din,)``, not rounded."""
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16).reshape(-1)
+    idx = np.ascontiguousarray(np.asarray(indices).astype(np.int64).astype(np.uint32)).reshape(-1)
+    sc = np.ascontiguousarray(scores, dtype=np.float32).reshape(-1)
+    gw, gs_, gb = (np.ascontiguousarray(a) for a in gate)
+    uw, us, ub = (np.ascontiguousarray(a) for a in up)
+    dw, ds, db = (np.ascontiguousarray(a) for a in down)
+    E, dff = gw.shape[0], gw.shape[1]
+    din = x.size
+    assert idx.size == sc.size and gw.shape == uw.shape and dw.shape[:2] == (E, din)
+    out = np.empty(din, dtype=np.float32)
+    _check(lib().oracle_fused_moe(_ptr(x), _ptr(idx), _ptr(sc), _ptr(gw), _ptr(gs_), _ptr(gb), _ptr(uw),
+                                  _ptr(us), _ptr(ub), _ptr(dw), _ptr(ds), _ptr(db), din, dff, idx.size, E,
+                                  group_size, gu_bits, d_bits, 1 if act == "geglu" else 0, _ptr(out)),
+           "fused_moe")
     return out
 
 

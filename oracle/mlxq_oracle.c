@@ -60,11 +60,20 @@ static inline float std_max(float a, float b) { return (a < b) ? b : a; }
 static inline float std_min(float a, float b) { return (b < a) ? b : a; }
 
 static int pow2_bits(int bits) { return bits == 1 || bits == 2 || bits == 4 || bits == 8; }
+/* widths with an affine packing here: the power-of-two ones and 6 */
+static int affine_bits(int bits) { return pow2_bits(bits) || bits == 6; }
 static int valid_gs(int gs) { return gs == 32 || gs == 64 || gs == 128; }
 
-/* Code i of a packed row: power-of-two widths pack 32/bits codes per uint32,
- * low bits first (CPUQ:1283-1290; ROPS:5231-5238). */
+/* Code i of a packed row.  Power-of-two widths pack 32/bits codes per uint32,
+ * low bits first (CPUQ:1283-1290; ROPS:5231-5238); 6-bit packs 4 codes per 3
+ * bytes, little-endian, code k at bit 6k of the 24-bit pack (CPUQ:1238-1240,
+ * 1283-1297: pack factor 4, 3 bytes per pack). */
 static inline uint32_t code_at(const uint32_t* row, int bits, int64_t i) {
+  if (bits == 6) {
+    const uint8_t* b = (const uint8_t*)row + (i / 4) * 3;
+    uint32_t pack = (uint32_t)b[0] | ((uint32_t)b[1] << 8) | ((uint32_t)b[2] << 16);
+    return (pack >> ((i % 4) * 6)) & 63u;
+  }
   int per = 32 / bits;
   return (row[i / per] >> ((i % per) * bits)) & ((1u << bits) - 1u);
 }
@@ -73,11 +82,13 @@ static inline uint32_t code_at(const uint32_t* row, int bits, int64_t i) {
 
 int oracle_affine_quantize(const uint16_t* w, int64_t rows, int64_t K, int group_size,
                            int bits, uint32_t* wq, uint16_t* scales, uint16_t* biases) {
-  if (!pow2_bits(bits) || !valid_gs(group_size) || K % group_size) return -1;
+  if (!affine_bits(bits) || !valid_gs(group_size) || K % group_size) return -1;
   const float n_bins = (float)((1 << bits) - 1);
   const float eps = 1e-7f;
-  const int el_per_int = 32 / bits;
-  const int64_t int_per_group = (int64_t)group_size * bits / 32;
+  const int el_per_int = bits == 6 ? 4 : 32 / bits;     /* codes per pack */
+  const int bytes_per_pack = bits == 6 ? 3 : 4;
+  /* packs per group (each pack a uint32, or 3 bytes at 6 bits) */
+  const int64_t int_per_group = (int64_t)group_size / el_per_int;
   const int64_t n_groups = rows * (K / group_size);
 
   for (int64_t i = 0; i < n_groups; ++i) {
@@ -105,7 +116,7 @@ int oracle_affine_quantize(const uint16_t* w, int64_t rows, int64_t K, int group
         bias = edge;
       }
     }
-    uint32_t* out = wq + i * int_per_group;
+    uint8_t* out = (uint8_t*)wq + i * int_per_group * bytes_per_pack;
     for (int64_t j = 0; j < int_per_group; ++j) {
       uint64_t out_el = 0;
       for (int k = 0; k < el_per_int; ++k) {
@@ -114,7 +125,7 @@ int oracle_affine_quantize(const uint16_t* w, int64_t rows, int64_t K, int group
         w_el = std_min(std_max(w_el, 0.0f), n_bins);
         out_el |= (uint64_t)w_el << (k * bits);
       }
-      out[j] = (uint32_t)out_el;
+      for (int b = 0; b < bytes_per_pack; ++b) out[j * bytes_per_pack + b] = (uint8_t)(out_el >> (8 * b));
     }
     scales[i] = oracle_f32_to_bf16(scale);
     biases[i] = oracle_f32_to_bf16(bias);
@@ -127,7 +138,7 @@ int oracle_affine_quantize(const uint16_t* w, int64_t rows, int64_t K, int group
 int oracle_affine_dequantize(const uint32_t* wq, const uint16_t* scales,
                              const uint16_t* biases, int64_t rows, int64_t K,
                              int group_size, int bits, int rounding, uint16_t* out) {
-  if (!pow2_bits(bits) || group_size <= 0 || K % group_size) return -1;
+  if (!affine_bits(bits) || group_size <= 0 || K % group_size || (K * bits) % 32) return -1;
   const int64_t wcols = K * bits / 32;
   const int64_t G = K / group_size;
   for (int64_t r = 0; r < rows; r++) {
@@ -348,4 +359,83 @@ int oracle_gather_qmm_t(const uint16_t* x, const uint32_t* wq, const void* scale
     if (rc) return rc;
   }
   return 0;
+}
+
+/* ---- affine dequantize to fp32 -------------------------------------------
+ * s * q + b in float from the bf16 scale and bias: the weights of the
+ * reference's all-f32 ground truth for the fused decode MoE, whose scales and
+ * biases are cast to f32 before MLX's dequantize (fused_moe_parity_tests.rs:
+ * 241-282, mlx_cxx_kernels.cpp:4003-4011). */
+int oracle_affine_dequantize_f32(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
+                                 int64_t rows, int64_t K, int group_size, int bits, float* out) {
+  if (!affine_bits(bits) || group_size <= 0 || K % group_size || (K * bits) % 32) return -1;
+  const int64_t wcols = K * bits / 32;
+  const int64_t G = K / group_size;
+  for (int64_t r = 0; r < rows; r++) {
+    const uint32_t* row = wq + r * wcols;
+    for (int64_t k = 0; k < K; k++) {
+      float s = oracle_bf16_to_f32(scales[r * G + k / group_size]);
+      float b = oracle_bf16_to_f32(biases[r * G + k / group_size]);
+      out[r * K + k] = s * (float)code_at(row, bits, k) + b;
+    }
+  }
+  return 0;
+}
+
+/* ---- fused single-token decode MoE (dense, fp64) --------------------------
+ * out[h] = sum_j score[j] * sum_f A(g_j[f]) u_j[f] Wd[e_j][h][f],
+ * g_j[f] = sum_i x[i] Wg[e_j][f][i] (u_j with Wu), e_j = min(idx[j], E-1),
+ * A = SiLU (act 0) or tanh-approximated GELU (act 1): the math of the
+ * reference's fused kernels (mlx_cxx_kernels.cpp:3032-3170) and of its
+ * all-f32 ground truth (fused_moe_parity_tests.rs:241-282), carried in fp64
+ * over the fp32 dequantized weights.  Result in fp32 (not rounded). */
+static double act_fn(int act, double g, double u) {
+  if (act == 1) return 0.5 * g * (1.0 + tanh(0.7978845608028654 * (g + 0.044715 * g * g * g))) * u;
+  return g / (1.0 + exp(-g)) * u;
+}
+
+int oracle_fused_moe(const uint16_t* x, const uint32_t* idx, const float* scores, const uint32_t* gate_w,
+                     const uint16_t* gate_s, const uint16_t* gate_b, const uint32_t* up_w,
+                     const uint16_t* up_s, const uint16_t* up_b, const uint32_t* down_w,
+                     const uint16_t* down_s, const uint16_t* down_b, int64_t din, int64_t dff, int64_t k,
+                     int64_t E, int group_size, int gu_bits, int d_bits, int act, float* out) {
+  if (!affine_bits(gu_bits) || !affine_bits(d_bits) || din % group_size || dff % group_size) return -1;
+  float* wg = malloc(sizeof(float) * dff * din);
+  float* wu = malloc(sizeof(float) * dff * din);
+  float* wd = malloc(sizeof(float) * din * dff);
+  double* a = malloc(sizeof(double) * dff);
+  double* y = calloc((size_t)din, sizeof(double));
+  int rc = (wg && wu && wd && a && y) ? 0 : -2;
+  const int64_t gcols = din * gu_bits / 32, dcols = dff * d_bits / 32;
+  for (int64_t j = 0; j < k && rc == 0; j++) {
+    const int64_t e = idx[j] < (uint32_t)E ? (int64_t)idx[j] : E - 1;
+    oracle_affine_dequantize_f32(gate_w + e * dff * gcols, gate_s + e * dff * (din / group_size),
+                                 gate_b + e * dff * (din / group_size), dff, din, group_size, gu_bits, wg);
+    oracle_affine_dequantize_f32(up_w + e * dff * gcols, up_s + e * dff * (din / group_size),
+                                 up_b + e * dff * (din / group_size), dff, din, group_size, gu_bits, wu);
+    oracle_affine_dequantize_f32(down_w + e * din * dcols, down_s + e * din * (dff / group_size),
+                                 down_b + e * din * (dff / group_size), din, dff, group_size, d_bits, wd);
+    for (int64_t f = 0; f < dff; f++) {
+      double g = 0.0, u = 0.0;
+      for (int64_t i = 0; i < din; i++) {
+        const double xv = oracle_bf16_to_f32(x[i]);
+        g += xv * wg[f * din + i];
+        u += xv * wu[f * din + i];
+      }
+      a[f] = act_fn(act, g, u);
+    }
+    for (int64_t h = 0; h < din; h++) {
+      double d = 0.0;
+      for (int64_t f = 0; f < dff; f++) d += a[f] * wd[h * dff + f];
+      y[h] += (double)scores[j] * d;
+    }
+  }
+  if (rc == 0)
+    for (int64_t h = 0; h < din; h++) out[h] = (float)y[h];
+  free(wg);
+  free(wu);
+  free(wd);
+  free(a);
+  free(y);
+  return rc;
 }

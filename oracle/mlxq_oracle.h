@@ -78,6 +78,14 @@ int oracle_gather_qmm_t(const uint16_t* x, const uint32_t* wq, const void* scale
                         const uint32_t* rhs, int64_t B, int64_t M, int64_t N,
                         int64_t K, int group_size, int bits, int mode, uint16_t* out);
 
+int oracle_affine_dequantize_f32(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
+                                 int64_t rows, int64_t K, int group_size, int bits, float* out);
+int oracle_fused_moe(const uint16_t* x, const uint32_t* idx, const float* scores, const uint32_t* gate_w,
+                     const uint16_t* gate_s, const uint16_t* gate_b, const uint32_t* up_w,
+                     const uint16_t* up_s, const uint16_t* up_b, const uint32_t* down_w,
+                     const uint16_t* down_s, const uint16_t* down_b, int64_t din, int64_t dff, int64_t k,
+                     int64_t E, int group_size, int gu_bits, int d_bits, int act, float* out);
+
 #ifdef __cplusplus
 }
 #endif

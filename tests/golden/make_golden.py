@@ -8,7 +8,8 @@ numpy/torch arithmetic:
   the definition in overlays/rocm/mlx/ops.cpp:5646-5695 and the CPU scale
   decode overlays/cpu/mlx/backend/cpu/quantized.cpp:91-105.  float64 ldexp is
   exact for these values; bf16 conversion by torch.
-* affine ramp groups (quantized.cpp:1233-1305 worked by hand):
+* affine ramp groups (quantized.cpp:1233-1305 worked by hand; 6-bit codes
+  packed 4 per 3 bytes, the little-endian bit stream):
     c_k = k % 2^bits (last c = 2^bits - 1), T = 2^bits - 1:
     w_k = c_k * d  -> w_max edge, scale = -d, bias = T d, code = T - c_k
     w_k = -c_k * d -> w_min edge, scale = +d, bias = -T d, code = T - c_k
@@ -46,6 +47,12 @@ def mxfp4_table() -> np.ndarray:
 
 
 def pack(codes: np.ndarray, bits: int) -> np.ndarray:
+    if bits == 6:
+        # 4 codes per 3 bytes, i.e. the little-endian bit stream of the codes
+        # (quantized.cpp:1238-1240, 1283-1297)
+        b = (codes.astype(np.uint8)[..., None] >> np.arange(6, dtype=np.uint8)) & 1
+        by = np.packbits(b.reshape(codes.shape[0], -1).astype(np.uint8), axis=1, bitorder="little")
+        return np.ascontiguousarray(by).view(np.uint32)
     per = 32 // bits
     codes = codes.reshape(codes.shape[0], -1, per).astype(np.uint64)
     shifts = (np.arange(per, dtype=np.uint64) * bits)[None, None, :]
@@ -84,7 +91,7 @@ def dequant_d2_cases():
 
 def main():
     out = {"mxfp4_table": mxfp4_table()}
-    for bits in (2, 4, 8):
+    for bits in (2, 4, 6, 8):
         for gs in (32, 64, 128):
             w, wq, s, b = affine_ramps(bits, gs)
             out[f"ramp_w_b{bits}_g{gs}"] = w

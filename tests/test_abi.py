@@ -239,3 +239,37 @@ def test_unimplemented_combinations_say_so(lib):
     st = lib.mlxq_quantized_matmul(ctypes.byref(x3), ctypes.byref(w3), ctypes.byref(s3), ctypes.byref(s3), True, 64,
                                    3, b"affine", ctypes.byref(out), None)
     assert st == _lib.EUNSUPPORTED
+
+
+def moe_args(din=256, dff=128, E=4, k=2, gu=4, db=4, gs=64, x_dtype=BF, idx_dtype=_lib.INT32, sc_dtype=_lib.FLOAT32):
+    return [arr([din], x_dtype), arr([k], idx_dtype),
+            arr([E, dff, din * gu // 32], U32), arr([E, dff, din // gs], BF), arr([E, dff, din // gs], BF),
+            arr([E, dff, din * gu // 32], U32), arr([E, dff, din // gs], BF), arr([E, dff, din // gs], BF),
+            arr([E, din, dff * db // 32], U32), arr([E, din, dff // gs], BF), arr([E, din, dff // gs], BF),
+            arr([k], sc_dtype)]
+
+
+def call_moe(lib, args, din, dff, k, gu, db, gs, out=None, geglu=False):
+    out = out if out is not None else arr([din], BF)
+    fn = lib.mlxq_fused_moe_geglu if geglu else lib.mlxq_fused_moe_expert
+    return fn(*[ctypes.byref(a) for a in args], din, dff, k, gu, db, gs, ctypes.byref(out), None)
+
+
+def test_fused_moe_validation(lib):
+    # shapes that disagree with din / dff / k are argument errors
+    a = moe_args()
+    assert call_moe(lib, a, 256, 128, 3, 4, 4, 64) == _lib.EINVAL
+    assert "indices must have k elements" in _lib.last_error()
+    assert call_moe(lib, a, 256, 192, 2, 4, 4, 64) == _lib.EINVAL
+    assert "gate_w must have shape (4,192,32)" in _lib.last_error()
+    assert call_moe(lib, a, 256, 128, 2, 4, 4, 64, out=arr([128], BF)) == _lib.EINVAL
+    assert call_moe(lib, moe_args(din=96), 96, 128, 2, 4, 4, 64, geglu=True) == _lib.EINVAL
+    assert "multiples of group_size" in _lib.last_error()
+    # valid for the reference's callers but not implemented: they fall back
+    assert call_moe(lib, moe_args(gu=2), 256, 128, 2, 2, 4, 64) == _lib.EUNSUPPORTED
+    assert call_moe(lib, moe_args(db=3), 256, 128, 2, 4, 3, 64) == _lib.EUNSUPPORTED
+    assert call_moe(lib, moe_args(gs=16), 256, 128, 2, 4, 4, 16) == _lib.EUNSUPPORTED
+    assert call_moe(lib, moe_args(x_dtype=_lib.FLOAT16), 256, 128, 2, 4, 4, 64) == _lib.EUNSUPPORTED
+    assert call_moe(lib, moe_args(sc_dtype=_lib.INT32), 256, 128, 2, 4, 4, 64) == _lib.EUNSUPPORTED
+    assert call_moe(lib, moe_args(idx_dtype=_lib.INT16), 256, 128, 2, 4, 4, 64) == _lib.EUNSUPPORTED
+    assert "fused_moe_expert_kernel" in _lib.last_error()

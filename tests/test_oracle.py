@@ -55,7 +55,7 @@ def test_bf16_rne_matches_torch(orc):
 
 # ---- affine quantize ---------------------------------------------------------
 
-@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("bits", [2, 4, 6, 8])
 @pytest.mark.parametrize("gs", [32, 64, 128])
 def test_affine_quantize_known_answers(orc, kat, bits, gs):
     wq, s, b = orc.affine_quantize(kat[f"ramp_w_b{bits}_g{gs}"], gs, bits)
@@ -64,7 +64,7 @@ def test_affine_quantize_known_answers(orc, kat, bits, gs):
     np.testing.assert_array_equal(b, kat[f"ramp_b_b{bits}_g{gs}"])
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [4, 6, 8])
 @pytest.mark.parametrize("gs", [32, 64, 128])
 def test_affine_quantize_invariants(orc, bits, gs):
     w = orc.normal_bf16((64, 512), 0.02, 7 + bits + gs)
@@ -88,7 +88,7 @@ def test_affine_quantize_invariants(orc, bits, gs):
 
 def test_affine_packing_is_little_endian_bitstream(orc):
     w = orc.normal_bf16((8, 256), 0.02, 11)
-    for bits in (2, 4, 8):
+    for bits in (2, 4, 6, 8):
         wq, s, b = orc.affine_quantize(w, 64, bits)
         codes = codes_bytestream(wq, bits, 256).astype(np.float32)
         # D2 rebuilt from byte-stream codes with torch's bf16 ops
@@ -97,6 +97,20 @@ def test_affine_packing_is_little_endian_bitstream(orc):
         ref = (torch.from_numpy(codes).to(torch.bfloat16) * st) + bt
         np.testing.assert_array_equal(orc.affine_dequantize(wq, s, b, 64, bits, 2),
                                       ref.view(torch.int16).numpy().astype(np.uint16))
+
+
+def test_six_bit_pack_layout_known_answer(orc):
+    # the 3-byte pack of 4 codes as the reference's kernels read it
+    # (mlx_cxx_kernels.cpp:3136-3151): v0 = b0 & 0x3f, v1 = (b0 >> 6) | ((b1 & 0xf) << 2),
+    # v2 = (b1 >> 4) | ((b2 & 3) << 4), v3 = b2 >> 2.  Bytes ff 00 ff -> 63, 3, 48, 63.
+    by = np.zeros(24, np.uint8)  # one group of 32 codes
+    by[:3] = [0xFF, 0x00, 0xFF]
+    by[3:6] = [0x41, 0x10, 0x04]  # codes 1, 1, 1, 1
+    wq = by.view(np.uint32).reshape(1, 6)
+    one, zero = np.array([[0x3F80]], np.uint16), np.zeros((1, 1), np.uint16)
+    d = orc.affine_dequantize_f32(wq, one, zero, 32, 6)[0]
+    np.testing.assert_array_equal(d[:8], [63, 3, 48, 63, 1, 1, 1, 1])
+    assert (d[8:] == 0).all()
 
 
 # ---- dequantize --------------------------------------------------------------
@@ -260,3 +274,119 @@ def test_gather_is_stack_of_matmuls(orc):
     outm = orc.gather_qmm_t(x, wm, sm, None, lhs, rhs, mode="mxfp4")
     for i in range(lhs.size):
         np.testing.assert_array_equal(outm[i], orc.fp_qmm_t_mxfp4(x[lhs[i]], wm[rhs[i]], sm[rhs[i]]))
+
+
+# ---- fused single-token decode MoE --------------------------------------------
+
+def moe_case(orc, din, dff, E, k, gu_bits, d_bits, gs, seed):
+    """Random experts quantized by the oracle, distinct expert ids, softmax-like
+    positive scores (fused_moe_parity_tests.rs:131-205)."""
+    x = orc.normal_bf16((din,), 1.0, seed)
+    gate = orc.affine_quantize(orc.normal_bf16((E, dff, din), 0.02, seed + 1), gs, gu_bits)
+    up = orc.affine_quantize(orc.normal_bf16((E, dff, din), 0.02, seed + 2), gs, gu_bits)
+    down = orc.affine_quantize(orc.normal_bf16((E, din, dff), 0.02, seed + 3), gs, d_bits)
+    rng = np.random.default_rng(seed)
+    idx = rng.permutation(E)[:k].astype(np.uint32)
+    sc = rng.random(k).astype(np.float32)
+    return x, idx, sc / sc.sum(), gate, up, down
+
+
+def norm_dev(a, b):
+    """(nrms, nmax) of a - b normalized by b's rms (fused_moe_parity_tests.rs:350-367)."""
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    rms = max(np.sqrt((b ** 2).mean()), 1e-20)
+    return np.sqrt(((a - b) ** 2).mean()) / rms, np.abs(a - b).max() / rms
+
+
+@pytest.mark.parametrize("act", ["swiglu", "geglu"])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_fused_moe_matches_the_gather_qmm_chain(orc, act, bits):
+    # The reference's graph fallback built from the oracle's (separately
+    # pinned) gather_qmm: gate/up per slot, activation, down per slot,
+    # score-weighted sum.  It rounds through bf16 between the products, so it
+    # agrees only to bf16 jitter (the reference's ceilings for it are nrms <
+    # 5e-2, nmax < 2e-1, fused_moe_parity_tests.rs:395-409; tighter bounds
+    # here); any mix-up of experts, rows, activation or scores is far outside.
+    din, dff, E, k, gs = 256, 128, 6, 4, 64
+    x, idx, sc, gate, up, down = moe_case(orc, din, dff, E, k, bits, bits, gs, 77 + bits)
+    fused = orc.fused_moe(x, idx, sc, gate, up, down, gs, bits, bits, act)
+    zero = np.zeros(k, np.uint32)
+    g = orc.bf16_to_f32(orc.gather_qmm_t(x.reshape(1, 1, din), *gate, zero, idx, gs, bits)).astype(np.float64)
+    u = orc.bf16_to_f32(orc.gather_qmm_t(x.reshape(1, 1, din), *up, zero, idx, gs, bits)).astype(np.float64)
+    if act == "geglu":
+        a = 0.5 * g * (1 + np.tanh(0.7978845608028654 * (g + 0.044715 * g ** 3))) * u
+    else:
+        a = g / (1 + np.exp(-g)) * u
+    a16 = orc.f32_to_bf16(a.astype(np.float32)).reshape(k, 1, dff)
+    d = orc.bf16_to_f32(orc.gather_qmm_t(a16, *down, np.arange(k, dtype=np.uint32), idx, gs, bits))
+    chain = (d.reshape(k, din).astype(np.float64) * sc[:, None]).sum(0)
+    nrms, nmax = norm_dev(chain, fused)
+    # measured here: nrms ~3e-3, nmax ~1e-2 (bf16 roundings of the chain)
+    assert nrms < 1e-2 and nmax < 4e-2, (nrms, nmax)
+    # pairing the scores with the wrong experts lands far outside the ceiling
+    bad = orc.fused_moe(x, idx[::-1].copy(), sc, gate, up, down, gs, bits, bits, act)
+    assert norm_dev(chain, bad)[0] > 0.1
+
+
+def pack_bitstream(codes, bits):
+    """Codes -> uint32 words of their little-endian bit stream (per row)."""
+    b = (codes.astype(np.uint8)[..., None] >> np.arange(bits, dtype=np.uint8)) & 1
+    by = np.packbits(b.reshape(codes.shape[0], -1).astype(np.uint8), axis=1, bitorder="little")
+    return np.ascontiguousarray(by).view(np.uint32)
+
+
+@pytest.mark.parametrize("d_bits", [4, 6, 8])
+@pytest.mark.parametrize("act", ["swiglu", "geglu"])
+def test_fused_moe_closed_form_identity_experts(orc, act, d_bits):
+    # Hand-packed experts with scale 1, bias -8 (4-bit gate/up) so weights are
+    # code - 8; x is one-hot at position 0.  Gate row f has weight
+    # (f % 16) - 8 there and up rows weight 1, so g_f = (f % 16) - 8, u_f = 1;
+    # down is the identity (weight 1 on h == f, 0 elsewhere).  Hence
+    # out[h] = score * A((h % 16) - 8), checked against the activations'
+    # published values.
+    din = dff = gs = 32
+    one = 0x3F80
+    x = np.zeros(din, np.uint16)
+    x[0] = one
+    gcodes = np.full((dff, din), 8, np.uint8)
+    gcodes[:, 0] = np.arange(dff) % 16
+    ucodes = np.full((dff, din), 8, np.uint8)
+    ucodes[:, 0] = 9
+    dbias = 8
+    dcodes = np.full((din, dff), dbias, np.uint8) + np.eye(din, dtype=np.uint8)
+    s1 = np.full((1, 32, 1), one, np.uint16)
+    m8 = np.full((1, 32, 1), 0xC100, np.uint16)  # -8.0
+    gate = (pack_bitstream(gcodes, 4)[None], s1, m8)
+    up = (pack_bitstream(ucodes, 4)[None], s1, m8)
+    down = (pack_bitstream(dcodes, d_bits)[None], s1, m8)
+    out = orc.fused_moe(x, np.array([0], np.uint32), np.array([0.5], np.float32), gate, up, down, gs, 4, d_bits,
+                        act)
+    g = (np.arange(din) % 16 - 8).astype(np.float64)
+    if act == "geglu":
+        want = 0.5 * 0.5 * g * (1 + np.tanh(np.sqrt(2 / np.pi) * (g + 0.044715 * g ** 3)))
+        anchors = {1: 0.8411919906082768, -1: -0.15880800939172324}
+    else:
+        want = 0.5 * g / (1 + np.exp(-g))
+        anchors = {1: 0.7310585786300049, -1: -0.2689414213699951}
+    np.testing.assert_allclose(out, want, rtol=1e-6, atol=1e-7)
+    for gv, av in anchors.items():
+        h = int(gv + 8)  # rows with g = gv
+        assert abs(out[h] - 0.5 * av) < 1e-6
+    assert out[8] == 0.0  # A(0) = 0
+
+
+def test_fused_moe_invariants(orc):
+    # linear in the scores, independent of slot order, and a repeated expert
+    # equals one slot carrying the summed score
+    din, dff, E, gs = 128, 64, 5, 32
+    x, _, _, gate, up, down = moe_case(orc, din, dff, E, 3, 4, 4, gs, 91)
+    idx = np.array([3, 1, 4], np.uint32)
+    s1 = np.array([0.2, 0.5, 0.3], np.float32)
+    s2 = np.array([0.1, -0.25, 0.75], np.float32)
+    f = lambda i, s: orc.fused_moe(x, i, s, gate, up, down, gs, 4, 4).astype(np.float64)
+    np.testing.assert_allclose(f(idx, s1 + s2), f(idx, s1) + f(idx, s2), rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(f(idx[[2, 0, 1]], s1[[2, 0, 1]]), f(idx, s1), rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(f(np.array([2, 2], np.uint32), np.array([0.25, 0.5], np.float32)),
+                               f(np.array([2], np.uint32), np.array([0.75], np.float32)), rtol=1e-5, atol=1e-6)
+    # out-of-range expert ids are clamped to the last expert
+    np.testing.assert_array_equal(f(np.array([9], np.uint32), s1[:1]), f(np.array([E - 1], np.uint32), s1[:1]))
