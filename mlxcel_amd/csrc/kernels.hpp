@@ -256,7 +256,9 @@ hipError_t launch_group_by_expert(const GroupArgs& a, hipStream_t stream);
 
 // ---- fused single-token decode MoE (moe.hip) -----------------------------------
 enum MoeAct : int { MOE_SWIGLU = 0, MOE_GEGLU = 1 };
-constexpr int kMoeMaxWaves = 8;  // waves per workgroup (more lane chunks loop)
+constexpr int kMoeMaxWaves = 8;     // waves per workgroup (more lane chunks loop)
+constexpr int kMoeGateupRows = 4;   // gate/up output rows per workgroup
+constexpr int kMoeDownRows = 8;     // down output rows per workgroup
 struct MoeArgs {
   const uint16_t* x;        // bf16 [din]
   const uint32_t* idx;      // expert per slot (32- or 64-bit, low word), [k]

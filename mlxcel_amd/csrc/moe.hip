@@ -21,7 +21,13 @@
 // and serve all 2R rows.  Codes widen to bf16 pairs (4-bit: "128 + q", one
 // byte permute per pair; 8-bit: exact via f32) and meet the bf16 activations
 // in v_dot2_f32_bf16; a lane chunk lies in one quantization group, so
-// y += s * sum(q' x) + b' * sum(x) once per chunk and row.
+// y += s * sum(q' x) + b' * sum(x) once per chunk and row.  The scales and
+// biases of the wave's rows and chunk range come in with loads of up to 4
+// groups and are staged in LDS as (s, b') pairs, one 8-byte read per row.
+//
+// Latency, not bandwidth, bounds both launches at decode sizes (about 14 MB
+// and 7 MB for Qwen3-30B-A3B experts): each waits for the expert ids before
+// its weight loads can start, a full memory round trip per launch.
 //
 // moe_down_kernel: one workgroup per R output rows h.  Its lanes cover the
 // (expert slot, lane chunk) pairs of those rows, so all slots of a row are
@@ -82,15 +88,25 @@ __device__ __forceinline__ float moe_total(const float* red, int V, int i, int n
 
 }  // namespace
 
-// GB: gate/up bits (4 or 8); ACT: MOE_SWIGLU or MOE_GEGLU; R: output rows per
-// workgroup (gate and up rows each).
-template <int GB, int ACT, int R>
+// LDS of a gate/up workgroup: per wave, the cross-wave partials (4 lane rows
+// x 2R) and the (scale, bias') pairs of its chunk range (2R rows x GC groups).
+__host__ __device__ inline uint32_t moe_gateup_lds(int nw, int gc) {
+  return (uint32_t)nw * (4 * 2 * kMoeGateupRows * 4 + 2 * kMoeGateupRows * gc * 8);
+}
+
+// GB: gate/up bits (4 or 8); ACT: MOE_SWIGLU or MOE_GEGLU; UPW: quantization
+// groups per scale load (1, 2 or 4: the widest load every row's scales stay
+// aligned for, from din / group_size).
+template <int GB, int ACT, int UPW>
 __global__ __launch_bounds__(512) void moe_gateup_kernel(const MoeArgs a) {
+  constexpr int R = kMoeGateupRows;
   constexpr int KL = 128 / GB;  // K positions per 16-byte lane chunk
   constexpr int XV = KL / 8;    // 16-byte activation pieces per chunk
   constexpr int NP = KL / 2;    // bf16 pairs per chunk
-  constexpr int V = 2 * R;      // partials per lane: gate rows, then up rows
-  __shared__ float red[kMoeMaxWaves * 4 * V];
+  constexpr int V = 2 * R;      // rows per workgroup: gate rows, then up rows
+  constexpr int SW = UPW == 4 ? 2 : 1;  // 32-bit words per scale load
+  constexpr int MAXLD = 4 / UPW;        // scale loads per lane and array (at most)
+  extern __shared__ __align__(16) unsigned char smem[];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -101,7 +117,11 @@ __global__ __launch_bounds__(512) void moe_gateup_kernel(const MoeArgs a) {
   const int nlc = din / KL;
   const uint32_t RB = (uint32_t)nlc * 16u;  // bytes per weight row
   const int G = din >> a.gs_shift;
+  const int GC = (64 * KL) >> a.gs_shift;   // groups per 64-lane chunk range (8 .. 64)
+  const int upr = GC / UPW;                 // scale units per row and range
   const int f0 = blockIdx.x * R;
+  float* red = reinterpret_cast<float*>(smem);
+  float2* scl = reinterpret_cast<float2*>(smem + NW * 4 * V * 4) + wave * V * GC;
 
   // Rows past dff read as 0 (scale and bias too) and add exactly 0.
   const int64_t wb = (int64_t)e * dff * (RB / 4), sb = (int64_t)e * dff * G;
@@ -114,9 +134,9 @@ __global__ __launch_bounds__(512) void moe_gateup_kernel(const MoeArgs a) {
   const __amdgpu_buffer_rsrc_t ubr = buffer_rsrc(a.up_b + sb, sbytes);
   const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.x, (uint32_t)din * 2u);
 
-  float yg[R], yu[R];
+  float y[V];
 #pragma unroll
-  for (int r = 0; r < R; r++) yg[r] = yu[r] = 0.f;
+  for (int r = 0; r < V; r++) y[r] = 0.f;
 
   for (int c0 = wave * 64; c0 < nlc; c0 += NW * 64) {  // wave-uniform
     const int c = c0 + lane;
@@ -126,24 +146,58 @@ __global__ __launch_bounds__(512) void moe_gateup_kernel(const MoeArgs a) {
 #pragma unroll
     for (int v = 0; v < XV; v++)
       xv[v] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo + v * 16u, 0, 0));
-    const int g = (c * KL) >> a.gs_shift;
-    uint32_t gs[R], gbi[R], us[R], ubi[R];
+
+    // Scales and biases of the range's groups for the R gate and R up rows:
+    // unit u = (row r = u / upr, groups gl*UPW .. +UPW-1), four loads (gate
+    // s, b, up s, b) per unit; lanes past the units load nothing.
+    const int gbase = (c0 * KL) >> a.gs_shift;
+    uint32_t ld[MAXLD][4][SW];
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-      const uint32_t so = live ? (uint32_t)((f0 + r) * G + g) * 2u : kDeadOfs;
-      gs[r] = __builtin_amdgcn_raw_buffer_load_b16(gsr, so, 0, 0);
-      gbi[r] = __builtin_amdgcn_raw_buffer_load_b16(gbr, so, 0, 0);
-      us[r] = __builtin_amdgcn_raw_buffer_load_b16(usr, so, 0, 0);
-      ubi[r] = __builtin_amdgcn_raw_buffer_load_b16(ubr, so, 0, 0);
+    for (int i = 0; i < MAXLD; i++) {
+      const int u = lane + 64 * i;
+      const int r = u / upr, gl = u - r * upr;
+      const uint32_t so = (u < R * upr) ? (uint32_t)((f0 + r) * G + gbase + gl * UPW) * 2u : kDeadOfs;
+      const __amdgpu_buffer_rsrc_t rs[4] = {gsr, gbr, usr, ubr};
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        if constexpr (UPW == 4) {
+          const u32x2 t = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs[q], so, 0, 0));
+          ld[i][q][0] = t[0];
+          ld[i][q][SW - 1] = t[1];
+        } else if constexpr (UPW == 2) {
+          ld[i][q][0] = __builtin_amdgcn_raw_buffer_load_b32(rs[q], so, 0, 0);
+        } else {
+          ld[i][q][0] = __builtin_amdgcn_raw_buffer_load_b16(rs[q], so, 0, 0);
+        }
+      }
     }
-    u32x4 wg[R], wu[R];
+    u32x4 wv[V];
 #pragma unroll
     for (int r = 0; r < R; r++) {
       const uint32_t wo = live ? (uint32_t)(f0 + r) * RB + (uint32_t)c * 16u : kDeadOfs;
-      wg[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(gwr, wo, 0, 2 /* nt */));
-      wu[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(uwr, wo, 0, 2 /* nt */));
+      wv[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(gwr, wo, 0, 2 /* nt */));
+      wv[R + r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(uwr, wo, 0, 2 /* nt */));
     }
     __builtin_amdgcn_sched_barrier(0);  // keep the arithmetic below the loads
+
+    // stage (s, b') per (row, group); 4-bit codes carry +128: b' = b - 128 s
+#pragma unroll
+    for (int i = 0; i < MAXLD; i++) {
+      const int u = lane + 64 * i;
+      if (u < R * upr) {
+        const int r = u / upr, gl = u - r * upr;
+#pragma unroll
+        for (int h = 0; h < UPW; h++) {
+#pragma unroll
+          for (int half = 0; half < 2; half++) {  // gate, up
+            const uint32_t sw = ld[i][2 * half][h >> 1], bw = ld[i][2 * half + 1][h >> 1];
+            const float sv = bf16_bits_to_f32((sw >> (16 * (h & 1))) & 0xFFFFu);
+            const float bv = bf16_bits_to_f32((bw >> (16 * (h & 1))) & 0xFFFFu);
+            scl[(half * R + r) * GC + gl * UPW + h] = float2{sv, GB == 4 ? __builtin_fmaf(-128.0f, sv, bv) : bv};
+          }
+        }
+      }
+    }
 
     float xs = 0.f;
 #pragma unroll
@@ -154,9 +208,17 @@ __global__ __launch_bounds__(512) void moe_gateup_kernel(const MoeArgs a) {
 #pragma unroll
       for (int v = 0; v < XV; v++) xv[v] = perm_aff4_v(xv[v]);
     }
+    // the wave reads only what it wrote, and its LDS operations complete in
+    // order (this also fences the compiler)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
-    auto row_dot = [&](const u32x4 w) -> float {
+    const int gme = (lane * KL) >> a.gs_shift;  // this lane's group within the range
+#pragma unroll
+    for (int r = 0; r < V; r++) {
+      float2 sbp = scl[r * GC + gme];
+      if (!live) sbp = float2{0.f, 0.f};  // lanes past the row add exactly 0
       uint32_t pr[NP];
+      const u32x4 w = wv[r];
       if constexpr (GB == 8) {
         uint32_t t[4];
         unpack_aff8(w[0], w[1], t);
@@ -177,28 +239,11 @@ __global__ __launch_bounds__(512) void moe_gateup_kernel(const MoeArgs a) {
       float d = 0.f;
 #pragma unroll
       for (int p = 0; p < NP; p++) d = dot2(pr[p], xv[p / 4][p % 4], d);
-      return d;
-    };
-    // 4-bit codes carry +128 (bf16 0x43xx): b' = b - 128 s removes it
-    auto fold = [&](float acc, float d, uint32_t sbits, uint32_t bbits) -> float {
-      const float s = bf16_bits_to_f32(sbits & 0xFFFFu), b = bf16_bits_to_f32(bbits & 0xFFFFu);
-      const float bp = GB == 4 ? __builtin_fmaf(-128.0f, s, b) : b;
-      return __builtin_fmaf(s, d, __builtin_fmaf(bp, xs, acc));
-    };
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-      yg[r] = fold(yg[r], row_dot(wg[r]), gs[r], gbi[r]);
-      yu[r] = fold(yu[r], row_dot(wu[r]), us[r], ubi[r]);
+      y[r] = __builtin_fmaf(sbp.x, d, __builtin_fmaf(sbp.y, xs, y[r]));
     }
   }
 
-  float v[V];
-#pragma unroll
-  for (int r = 0; r < R; r++) {
-    v[r] = yg[r];
-    v[R + r] = yu[r];
-  }
-  moe_stage<V>(v, red, lane, wave);
+  moe_stage<V>(y, red, lane, wave);
   __syncthreads();
   if ((int)threadIdx.x < R) {
     const int r = threadIdx.x;
@@ -269,6 +314,12 @@ __global__ __launch_bounds__(512) void moe_down_kernel(const MoeArgs a) {
     const bool live = t < T;
     const int slot = live ? t / nlc : 0;
     const int c = live ? t - slot * nlc : 0;
+    // the activations do not depend on the expert id: in flight first
+    const uint32_t ao = live ? (uint32_t)(slot * dff + c * KL) * 4u : kDeadOfs;
+    f32x4 av[AV];
+#pragma unroll
+    for (int v = 0; v < AV; v++)
+      av[v] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ar, ao + v * 16u, 0, 0));
     const int e = moe_expert(a, slot);
     const float sc = live ? moe_score(a, slot) : 0.f;
     // Rows past din and dead lanes read row din-1 / chunk 0 of a valid
@@ -292,11 +343,6 @@ __global__ __launch_bounds__(512) void moe_down_kernel(const MoeArgs a) {
         for (int i = 0; i < CW; i++) wv[r][i] = __builtin_nontemporal_load(wp + i);
       }
     }
-    const uint32_t ao = live ? (uint32_t)(slot * dff + c * KL) * 4u : kDeadOfs;
-    f32x4 av[AV];
-#pragma unroll
-    for (int v = 0; v < AV; v++)
-      av[v] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ar, ao + v * 16u, 0, 0));
     __builtin_amdgcn_sched_barrier(0);  // keep the arithmetic below the loads
 
     float as = 0.f;
@@ -330,10 +376,18 @@ __global__ __launch_bounds__(512) void moe_down_kernel(const MoeArgs a) {
 
 namespace {
 
-constexpr int kGateupRows = 4;  // gate/up output rows per workgroup
-constexpr int kDownRows = 8;    // down output rows per workgroup
+int moe_waves(int64_t lane_chunks) {
+  return (int)std::min<int64_t>(kMoeMaxWaves, std::max<int64_t>(1, (lane_chunks + 63) / 64));
+}
 
-int moe_waves(int64_t lane_chunks) { return (int)std::min<int64_t>(kMoeMaxWaves, std::max<int64_t>(1, (lane_chunks + 63) / 64)); }
+template <int GB, int ACT>
+void launch_gateup(const MoeArgs& a, dim3 block, uint32_t lds, hipStream_t stream) {
+  const dim3 grid((unsigned)((a.dff + kMoeGateupRows - 1) / kMoeGateupRows), (unsigned)a.k);
+  const int64_t G = a.din >> a.gs_shift;
+  if (G % 4 == 0) hipLaunchKernelGGL((moe_gateup_kernel<GB, ACT, 4>), grid, block, lds, stream, a);
+  else if (G % 2 == 0) hipLaunchKernelGGL((moe_gateup_kernel<GB, ACT, 2>), grid, block, lds, stream, a);
+  else hipLaunchKernelGGL((moe_gateup_kernel<GB, ACT, 1>), grid, block, lds, stream, a);
+}
 
 }  // namespace
 
@@ -341,19 +395,20 @@ hipError_t moe_launch(const MoeArgs& a, int gu_bits, int d_bits, int act, hipStr
   if (a.din <= 0 || a.dff <= 0 || a.k <= 0) return hipSuccess;
   const int klg = 128 / gu_bits;
   const int kld = d_bits == 6 ? 16 : 128 / d_bits;
-  const dim3 ga((unsigned)((a.dff + kGateupRows - 1) / kGateupRows), (unsigned)a.k);
-  const dim3 ba((unsigned)(64 * moe_waves(a.din / klg)));
-  const dim3 gd((unsigned)((a.din + kDownRows - 1) / kDownRows));
+  const int nwa = moe_waves(a.din / klg);
+  const dim3 ba((unsigned)(64 * nwa));
+  const uint32_t lds = moe_gateup_lds(nwa, (64 * klg) >> a.gs_shift);
   const dim3 bd((unsigned)(64 * moe_waves((int64_t)a.k * (a.dff / kld))));
-  if (gu_bits == 4 && act == MOE_SWIGLU) hipLaunchKernelGGL((moe_gateup_kernel<4, MOE_SWIGLU, kGateupRows>), ga, ba, 0, stream, a);
-  else if (gu_bits == 4) hipLaunchKernelGGL((moe_gateup_kernel<4, MOE_GEGLU, kGateupRows>), ga, ba, 0, stream, a);
-  else if (act == MOE_SWIGLU) hipLaunchKernelGGL((moe_gateup_kernel<8, MOE_SWIGLU, kGateupRows>), ga, ba, 0, stream, a);
-  else hipLaunchKernelGGL((moe_gateup_kernel<8, MOE_GEGLU, kGateupRows>), ga, ba, 0, stream, a);
+  if (gu_bits == 4 && act == MOE_SWIGLU) launch_gateup<4, MOE_SWIGLU>(a, ba, lds, stream);
+  else if (gu_bits == 4) launch_gateup<4, MOE_GEGLU>(a, ba, lds, stream);
+  else if (act == MOE_SWIGLU) launch_gateup<8, MOE_SWIGLU>(a, ba, lds, stream);
+  else launch_gateup<8, MOE_GEGLU>(a, ba, lds, stream);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  if (d_bits == 4) hipLaunchKernelGGL((moe_down_kernel<4, kDownRows>), gd, bd, 0, stream, a);
-  else if (d_bits == 6) hipLaunchKernelGGL((moe_down_kernel<6, kDownRows>), gd, bd, 0, stream, a);
-  else hipLaunchKernelGGL((moe_down_kernel<8, kDownRows>), gd, bd, 0, stream, a);
+  const dim3 gd((unsigned)((a.din + kMoeDownRows - 1) / kMoeDownRows));
+  if (d_bits == 4) hipLaunchKernelGGL((moe_down_kernel<4, kMoeDownRows>), gd, bd, 0, stream, a);
+  else if (d_bits == 6) hipLaunchKernelGGL((moe_down_kernel<6, kMoeDownRows>), gd, bd, 0, stream, a);
+  else hipLaunchKernelGGL((moe_down_kernel<8, kMoeDownRows>), gd, bd, 0, stream, a);
   return hipGetLastError();
 }
 

@@ -139,6 +139,17 @@ def test_group_sizes(gs, gu_bits, d_bits, act):
                    f"gs {gs} {gu_bits}/{d_bits} {act}")
 
 
+@pytest.mark.parametrize("din", [2880, 1152])
+@pytest.mark.parametrize("gu_bits", [4, 8])
+def test_scale_rows_not_a_multiple_of_four_groups(din, gu_bits):
+    # din / 64 = 45 (odd: one group per scale load) or 18 (two per load)
+    announce("moe_scale_units", din, gu_bits)
+    dff, E, k, gs = 256, 6, 3, 64
+    x, idx, sc, gate, up, down = moe_case(din, dff, E, k, gu_bits, 4, gs, 120 + din + gu_bits)
+    dense = orc.fused_moe(x, idx, sc, gate, up, down, gs, gu_bits, 4)
+    check_vs_dense(run_fused(x, idx, sc, gate, up, down, gs, gu_bits, 4), dense, f"din {din} {gu_bits}-bit")
+
+
 def test_long_rows_loop_over_lane_chunks():
     # din 40960 at 4 bits: 1280 lane chunks per gate/up row, 8 waves x 64
     # lanes -> three passes of the chunk loop
