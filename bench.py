@@ -391,8 +391,10 @@ class QwenShape:
 class QuantDecoder:
     """Random-weight quantized decoder; decode steps capture into HIP graphs."""
 
-    def __init__(self, shape: QwenShape, batch: int, max_ctx: int, seed: int = 0, gs: int = 64, bits: int = 4):
+    def __init__(self, shape: QwenShape, batch: int, max_ctx: int, seed: int = 0, gs: int = 64, bits: int = 4,
+                 multi: bool = True):
         self.c, self.B, self.T, self.gs, self.bits = shape, batch, max_ctx, gs, bits
+        self.multi = multi  # q/k/v and gate/up through quantized_matmul_multi
         c = shape
         dev = "cuda"
         gen = torch.Generator(device=dev).manual_seed(seed)
@@ -427,6 +429,12 @@ class QuantDecoder:
     def qmm(self, x, w):
         return mq.quantized_matmul(x, *w, True, self.gs, self.bits)
 
+    def qmm_n(self, x, ws):
+        if self.multi:
+            return mq.quantized_matmul_multi(x, [w[0] for w in ws], [w[1] for w in ws], [w[2] for w in ws],
+                                             self.gs, self.bits)
+        return [self.qmm(x, w) for w in ws]
+
     def rms(self, x, w):
         xf = x.float()
         return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.c.eps) * w.float()).to(torch.bfloat16)
@@ -451,9 +459,8 @@ class QuantDecoder:
         """h [B*S, hidden] at positions pos0 .. pos0+S-1 (pos0: device scalar)."""
         c, B = self.c, self.B
         x = self.rms(h, L["n1"])
-        q = self.qmm(x, L["q"]).view(B, S, c.nq, c.hd)
-        k = self.qmm(x, L["k"]).view(B, S, c.nkv, c.hd)
-        v = self.qmm(x, L["v"]).view(B, S, c.nkv, c.hd)
+        q, k, v = self.qmm_n(x, [L["q"], L["k"], L["v"]])
+        q, k, v = q.view(B, S, c.nq, c.hd), k.view(B, S, c.nkv, c.hd), v.view(B, S, c.nkv, c.hd)
         q, k = self.rms(q, L["qn"]), self.rms(k, L["kn"])
         idx = pos0 + torch.arange(S, device=h.device)
         cos, sin = self.cos.index_select(0, idx), self.sin.index_select(0, idx)
@@ -466,7 +473,8 @@ class QuantDecoder:
         o = o.view(B, c.nkv, G, S, c.hd).permute(0, 3, 1, 2, 4).reshape(B * S, c.nq * c.hd)
         h = h + self.qmm(o, L["o"])
         x = self.rms(h, L["n2"])
-        a = torch.nn.functional.silu(self.qmm(x, L["g"]).float()) * self.qmm(x, L["u"]).float()
+        gt, ut = self.qmm_n(x, [L["g"], L["u"]])
+        a = torch.nn.functional.silu(gt.float()) * ut.float()
         return h + self.qmm(a.to(torch.bfloat16), L["d"])
 
     def forward(self, tokens, pos0, S, T, mask):
@@ -544,16 +552,19 @@ class QuantDecoder:
         return out, t_pre, time.perf_counter() - t0
 
 
-def e2e_decode(batches=(1, 16), prompt_len=512, steps=256, layers=36):
-    """Decode tokens/s of the Qwen3-8B-shaped 4-bit model at each batch."""
+def e2e_decode(batches=(1, 16), prompt_len=512, steps=256, layers=36, separate_at=(1,)):
+    """Decode tokens/s of the Qwen3-8B-shaped 4-bit model at each batch (q/k/v
+    and gate/up through quantized_matmul_multi; at the batches in
+    `separate_at` also with one quantized_matmul call per projection)."""
     res = []
-    for B in batches:
-        model = QuantDecoder(QwenShape(layers=layers), B, prompt_len + steps, seed=11)
+    runs = [(B, True) for B in batches] + [(B, False) for B in separate_at]
+    for B, multi in runs:
+        model = QuantDecoder(QwenShape(layers=layers), B, prompt_len + steps, seed=11, multi=multi)
         g = torch.Generator(device="cuda").manual_seed(12)
         prompt = torch.randint(0, model.c.vocab, (B, prompt_len), device="cuda", generator=g)
         model.generate(prompt[:, :64], 8)  # warm-up (kernels, allocator)
         toks, t_pre, t_dec = model.generate(prompt, steps)
-        res.append({"batch": B, "prompt": prompt_len, "decode_tokens": steps,
+        res.append({"batch": B, "multi_projection": multi, "prompt": prompt_len, "decode_tokens": steps,
                     "decode_tok_s": round(B * steps / t_dec, 1), "ms_per_step": round(t_dec / steps * 1e3, 3),
                     "prefill_tok_s": round(B * prompt_len / t_pre, 1),
                     "weight_GB": round(model.weight_bytes / 1e9, 3),

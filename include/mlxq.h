@@ -12,6 +12,8 @@
  *                             -> mlx::core::dequantize, ops.cpp:5753-5805)
  *   mlxq_quantize          <- ffi::quantize_weights_* (mlx_cxx_bridge.cpp:7867-7900
  *                             -> mlx::core::quantize, ops.cpp:5454-5492)
+ *   mlxq_quantized_matmul_multi <- the fused q/k/v and gate/up GEMVs of mlxcel-xla
+ *                             (src/lib/mlxcel-xla/csrc/qmv4.hip:265-387)
  *   mlxq_fused_moe_expert  <- ffi::fused_moe_expert_kernel (lib.rs:2336-2356,
  *                             mlx_cxx_bridge.h:2061-2070, mlx_cxx_kernels.cpp:4078-4094)
  *   mlxq_fused_moe_geglu   <- ffi::fused_moe_geglu_kernel  (lib.rs:2357-2380,
@@ -98,6 +100,21 @@ mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w,
                                   const mlxq_array* scales, const mlxq_array* biases,
                                   bool transpose, int32_t group_size, int32_t bits,
                                   const char* mode, mlxq_array* out, void* stream);
+
+/* Several projections of one activation in one call (q/k/v, gate/up):
+ * out[i] = quantized_matmul(x, w[i], scales[i], biases[i], transpose = true,
+ * group_size, bits, mode) for i < n, 1 <= n <= 4, every w[i] 2-D and of the
+ * same format.  Results are bit for bit those of n mlxq_quantized_matmul
+ * calls; at decode row counts the n projections run as one launch that reads
+ * x once.  `biases` (the array of pointers) may be NULL for mxfp4.  No
+ * counterpart in the MLX op layer: it replaces the fused q/k/v and gate/up
+ * GEMV launches of the reference's native decode path
+ * (src/lib/mlxcel-xla/csrc/qmv4.hip:265-387, src/native_qmv.rs:250-330). */
+mlxq_status mlxq_quantized_matmul_multi(const mlxq_array* x, int32_t n, const mlxq_array* const* w,
+                                        const mlxq_array* const* scales,
+                                        const mlxq_array* const* biases, int32_t group_size,
+                                        int32_t bits, const char* mode, mlxq_array* const* out,
+                                        void* stream);
 
 /* Output shape/dtype the reference would give quantized_matmul, after the same
  * validation (no device work). */

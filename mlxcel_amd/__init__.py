@@ -5,8 +5,8 @@ package holds its HIP sources (``csrc/``), the build script, and a Python
 mirror of the reference operator interface (``ops``).
 """
 from .ops import (dequantize, fused_moe_expert, fused_moe_geglu, gather_qmm, quantize,  # noqa: F401
-                  quantized_matmul)
+                  quantized_matmul, quantized_matmul_multi)
 from ._lib import LIB_PATH, load as load_library  # noqa: F401
 
-__all__ = ["quantized_matmul", "gather_qmm", "dequantize", "quantize", "fused_moe_expert", "fused_moe_geglu",
+__all__ = ["quantized_matmul", "quantized_matmul_multi", "gather_qmm", "dequantize", "quantize", "fused_moe_expert", "fused_moe_geglu",
            "load_library", "LIB_PATH"]

@@ -677,6 +677,140 @@ void run_qmv(const QmmSpec& sp, mlxq::QmvArgs a, int nseg, int max_rows, hipStre
   hip_check(mlxq::qmv_launch(fmt, sp.gs, a, nseg, p, stream), "qmv launch");
 }
 
+// Argument checks of one quantized_matmul call (the reference's validation,
+// then what the kernels here cover); returns the call's spec.
+QmmSpec check_quantized_matmul(const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+                               const mlxq_array* biases, bool transpose, int32_t group_size, int32_t bits,
+                               const char* mode, const mlxq_array* out, const char* tag) {
+  QmmSpec sp = spec_quantized_matmul(x, w, scales, biases, transpose, group_size, bits, mode);
+  check_out(out, sp.out_shape, sp.out_dtype, tag);
+  require_kernel_support(sp, transpose, tag);
+  require_dtype(x, MLXQ_BFLOAT16, "x", tag);
+  if (sp.mode == AFFINE) {
+    require_dtype(scales, MLXQ_BFLOAT16, "scales", tag);
+    require_dtype(biases, MLXQ_BFLOAT16, "biases", tag);
+  }
+  require_contiguous(x, "x");
+  require_contiguous(w, "w");
+  require_contiguous(scales, "scales");
+  require_contiguous(biases, "biases");
+  return sp;
+}
+
+// Enqueues one checked quantized_matmul call.
+void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+                          const mlxq_array* biases, mlxq_array* out, hipStream_t stream) {
+  const int64_t rows_total = View{out}.size() / std::max<int64_t>(sp.N, 1);
+  if (rows_total == 0 || sp.N == 0) return;
+  if (sp.K == 0) unsupported("quantized_matmul: K == 0");
+
+  mlxq::QmvArgs a{};
+  a.x = static_cast<const uint16_t*>(x->data);
+  a.w = static_cast<const uint32_t*>(w->data);
+  a.scales = scales->data;
+  a.biases = biases ? static_cast<const uint16_t*>(biases->data) : nullptr;
+  a.out = static_cast<uint16_t*>(out->data);
+  a.N = (int)sp.N;
+  a.K = (int)sp.K;
+  a.out_rows = (int)rows_total;
+  const int fmt = fmt_of(sp.mode, sp.bits);
+  const int cap = mlxq::qmv_max_rows(fmt, sp.gs);
+  View wv{w}, xv{x};
+  if (wv.ndim() == 2 && rows_total <= 16 && use_mid((int)rows_total, fmt, sp.K)) {
+    // 5-16 rows: activations staged once per 128 weight rows (qmv_mid.hip)
+    const int dev = current_device();
+    const mlxq::QmvMidPlan mp = mlxq::qmv_mid_plan(fmt, sp.gs, sp.N, sp.K, (int)rows_total);
+    if (mp.ok) {
+      mlxq::QmvMidArgs m{};
+      m.x = a.x;
+      m.w = a.w;
+      m.scales = static_cast<const uint16_t*>(a.scales);
+      m.biases = a.biases;
+      m.out = a.out;
+      m.M = (int)rows_total;
+      m.N = (int)sp.N;
+      m.K = (int)sp.K;
+      int shift = 0;
+      while ((1 << shift) < sp.gs) shift++;
+      m.gs_shift = shift;
+      m.ks = mp.ks;
+      if (mp.ks > 1)
+        m.ws = reinterpret_cast<float*>(
+            workspace(dev, stream, (size_t)mp.ks * rows_total * sp.N * sizeof(float)).data);
+      hip_check(mlxq::qmv_mid_launch(fmt, m, mp, stream), "qmv_mid launch");
+      return;
+    }
+  }
+  if (wv.ndim() == 2 && rows_total >= env_int("MLXQ_QMM_MIN_ROWS", kQmmMinRows)) {
+    // prefill: one GEMM over all rows (every leading dim of x folds into rows)
+    const int dev = current_device();
+    // MLXQ_QMM_TILE / MLXQ_QMM_KSPLIT: A/B overrides of the tile shape and K split
+    const mlxq::QmmPlan qp = mlxq::qmm_plan(fmt, sp.gs, rows_total, sp.N, sp.K, device_info(dev).cus,
+                                            env_int("MLXQ_QMM_TILE", -1), env_int("MLXQ_QMM_KSPLIT", 0));
+    if (qp.ok) {
+      mlxq::QmmArgs q{};
+      q.x = a.x;
+      q.w = a.w;
+      q.scales = a.scales;
+      q.biases = a.biases;
+      q.out = a.out;
+      q.M = (int)rows_total;
+      q.x_rows = (int)rows_total;
+      q.N = (int)sp.N;
+      q.K = (int)sp.K;
+      int shift = 0;
+      while ((1 << shift) < sp.gs) shift++;
+      q.gs_shift = shift;
+      q.ksplit = qp.ksplit;
+      q.ksteps_per_split = qp.ksteps_per_split;
+      if (qp.ksplit > 1)
+        q.ws = reinterpret_cast<float*>(
+            workspace(dev, stream, (size_t)qp.ksplit * rows_total * sp.N * sizeof(float)).data);
+      hip_check(mlxq::qmm_launch(fmt, q, qp, stream), "qmm launch");
+      return;
+    }
+  }
+  if (wv.ndim() == 2) {
+    // every leading dim of x folds into rows (qmm.hip:3606-3620 does the same fold)
+    a.E = 1;
+    a.X = 1;
+    a.w_expert_stride = 0;
+    a.s_expert_stride = 0;
+    int rps = (int)std::min<int64_t>(rows_total, cap);
+    {
+      int nw, pf;
+      qmv_shape_choice(sp.N, sp.K, nw, pf);
+      const DevInfo di = device_info(current_device());
+      while (rps > 1 && mlxq::qmv_plan(fmt, sp.gs, sp.N, sp.K, rps, 1, di.cus, nw, pf).lds > mlxq::kQmvLdsMax)
+        rps = (rps + 1) / 2;
+    }
+    a.rps = rps;
+    a.total_rows = (int)rows_total;
+    a.X = (int)((rows_total + rps - 1) / rps);
+    const int nseg = a.X;
+    run_qmv(sp, a, nseg, rps, stream);
+  } else {
+    // batched weights: each batch element is a segment of x.shape[-2] rows
+    const Shape wsh = wv.shape(), xsh = xv.shape();
+    Shape wb(wsh.begin(), wsh.end() - 2);
+    Shape ob(sp.out_shape.begin(), sp.out_shape.end() - 2);
+    Shape xb = xv.ndim() > 2 ? Shape(xsh.begin(), xsh.end() - 2) : Shape{};
+    if (xv.ndim() <= 2 || wb != ob || xb != ob)
+      unsupported("quantized_matmul: batched w needs x with the same batch shape (use gather_qmm to broadcast)");
+    const int64_t M = xv.dim(-2);
+    if (M > cap) unsupported("quantized_matmul: batched w with more than " + std::to_string(cap) + " rows per batch");
+    int64_t nb = 1;
+    for (auto d : wb) nb *= d;
+    a.E = (int)nb;
+    a.X = (int)nb;
+    a.w_expert_stride = wv.dim(-2) * wv.dim(-1);
+    a.s_expert_stride = View{scales}.dim(-2) * View{scales}.dim(-1);
+    a.rps = (int)M;
+    a.total_rows = (int)rows_total;
+    run_qmv(sp, a, (int)nb, (int)M, stream);
+  }
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -700,129 +834,77 @@ mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w, cons
                                   const mlxq_array* biases, bool transpose, int32_t group_size, int32_t bits,
                                   const char* mode, mlxq_array* out, void* stream_) {
   return guarded([&] {
-    const char* tag = "quantized_matmul";
-    QmmSpec sp = spec_quantized_matmul(x, w, scales, biases, transpose, group_size, bits, mode);
-    check_out(out, sp.out_shape, sp.out_dtype, tag);
-    require_kernel_support(sp, transpose, tag);
-    require_dtype(x, MLXQ_BFLOAT16, "x", tag);
-    if (sp.mode == AFFINE) {
-      require_dtype(scales, MLXQ_BFLOAT16, "scales", tag);
-      require_dtype(biases, MLXQ_BFLOAT16, "biases", tag);
-    }
-    require_contiguous(x, "x");
-    require_contiguous(w, "w");
-    require_contiguous(scales, "scales");
-    require_contiguous(biases, "biases");
-    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
-    const int64_t rows_total = View{out}.size() / std::max<int64_t>(sp.N, 1);
-    if (rows_total == 0 || sp.N == 0) return;
-    if (sp.K == 0) unsupported("quantized_matmul: K == 0");
+    const QmmSpec sp =
+        check_quantized_matmul(x, w, scales, biases, transpose, group_size, bits, mode, out, "quantized_matmul");
+    run_quantized_matmul(sp, x, w, scales, biases, out, reinterpret_cast<hipStream_t>(stream_));
+  });
+}
 
+mlxq_status mlxq_quantized_matmul_multi(const mlxq_array* x, int32_t n, const mlxq_array* const* w,
+                                        const mlxq_array* const* scales, const mlxq_array* const* biases,
+                                        int32_t group_size, int32_t bits, const char* mode, mlxq_array* const* out,
+                                        void* stream_) {
+  return guarded([&] {
+    const char* tag = "quantized_matmul_multi";
+    if (n < 1 || n > mlxq::kQmvMultiMax) {
+      std::ostringstream os;
+      os << "[" << tag << "] n must be between 1 and " << mlxq::kQmvMultiMax << " but is " << n << ".";
+      invalid(os);
+    }
+    if (!w || !scales || !out) fail(MLXQ_EINVAL, std::string("[") + tag + "] w, scales and out must not be NULL");
+    std::vector<QmmSpec> sp;
+    for (int i = 0; i < n; i++) {
+      const mlxq_array* b = biases ? biases[i] : nullptr;
+      sp.push_back(check_quantized_matmul(x, w[i], scales[i], b, true, group_size, bits, mode, out[i], tag));
+      if (View{w[i]}.ndim() != 2) unsupported(std::string(tag) + ": 2-D weights only");
+    }
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    // One launch of the row-streaming kernel over every projection when each
+    // call alone would run it with the same plan (decode rows, no kernel
+    // override): the results are then those of the separate calls, bit for
+    // bit.  Otherwise the calls run one after another.
+    const int fmt = fmt_of(sp[0].mode, sp[0].bits);
+    const int64_t rows = View{out[0]}.size() / std::max<int64_t>(sp[0].N, 1);
+    bool fused = n > 1 && sp[0].K > 0 && rows >= 1 && rows < env_int("MLXQ_QMM_MIN_ROWS", kQmmMinRows) &&
+                 rows <= mlxq::qmv_max_rows(fmt, sp[0].gs) && !use_mid((int)rows, fmt, sp[0].K) &&
+                 skinny_choice((int)rows, fmt, sp[0].K) == Skinny::RS && env_int("MLXQ_QMV_MULTI", 1) != 0;
+    mlxq::QmvRsPlan plan{};
+    mlxq::QmvMulti mp{};
+    mp.n = n;
+    for (int i = 0; i < n && fused; i++) {
+      if (sp[i].N == 0) fused = false;
+      const mlxq::QmvRsPlan p =
+          mlxq::qmv_rs_plan(fmt, sp[i].gs, sp[i].N, sp[i].K, (int)rows, env_int("MLXQ_QMV_R", 0));
+      if (!p.ok || (i > 0 && (p.mr != plan.mr || p.r != plan.r || p.cpw != plan.cpw || p.nw != plan.nw ||
+                              p.lds != plan.lds)))
+        fused = false;
+      if (i == 0) plan = p;
+      mp.tile_end[i] = (i ? mp.tile_end[i - 1] : 0) + p.tiles;
+      mp.N[i] = (int)sp[i].N;
+      mp.w[i] = static_cast<const uint32_t*>(w[i]->data);
+      mp.scales[i] = scales[i]->data;
+      mp.biases[i] = biases && biases[i] ? static_cast<const uint16_t*>(biases[i]->data) : nullptr;
+      mp.out[i] = static_cast<uint16_t*>(out[i]->data);
+    }
+    if (!fused) {
+      for (int i = 0; i < n; i++)
+        run_quantized_matmul(sp[i], x, w[i], scales[i], biases ? biases[i] : nullptr, out[i], stream);
+      return;
+    }
     mlxq::QmvArgs a{};
     a.x = static_cast<const uint16_t*>(x->data);
-    a.w = static_cast<const uint32_t*>(w->data);
-    a.scales = scales->data;
-    a.biases = biases ? static_cast<const uint16_t*>(biases->data) : nullptr;
-    a.out = static_cast<uint16_t*>(out->data);
-    a.N = (int)sp.N;
-    a.K = (int)sp.K;
-    a.out_rows = (int)rows_total;
-    const int fmt = fmt_of(sp.mode, sp.bits);
-    const int cap = mlxq::qmv_max_rows(fmt, sp.gs);
-    View wv{w}, xv{x};
-    if (wv.ndim() == 2 && rows_total <= 16 && use_mid((int)rows_total, fmt, sp.K)) {
-      // 5-16 rows: activations staged once per 128 weight rows (qmv_mid.hip)
-      const int dev = current_device();
-      const mlxq::QmvMidPlan mp = mlxq::qmv_mid_plan(fmt, sp.gs, sp.N, sp.K, (int)rows_total);
-      if (mp.ok) {
-        mlxq::QmvMidArgs m{};
-        m.x = a.x;
-        m.w = a.w;
-        m.scales = static_cast<const uint16_t*>(a.scales);
-        m.biases = a.biases;
-        m.out = a.out;
-        m.M = (int)rows_total;
-        m.N = (int)sp.N;
-        m.K = (int)sp.K;
-        int shift = 0;
-        while ((1 << shift) < sp.gs) shift++;
-        m.gs_shift = shift;
-        m.ks = mp.ks;
-        if (mp.ks > 1)
-          m.ws = reinterpret_cast<float*>(
-              workspace(dev, stream, (size_t)mp.ks * rows_total * sp.N * sizeof(float)).data);
-        hip_check(mlxq::qmv_mid_launch(fmt, m, mp, stream), "qmv_mid launch");
-        return;
-      }
-    }
-    if (wv.ndim() == 2 && rows_total >= env_int("MLXQ_QMM_MIN_ROWS", kQmmMinRows)) {
-      // prefill: one GEMM over all rows (every leading dim of x folds into rows)
-      const int dev = current_device();
-      // MLXQ_QMM_TILE / MLXQ_QMM_KSPLIT: A/B overrides of the tile shape and K split
-      const mlxq::QmmPlan qp = mlxq::qmm_plan(fmt, sp.gs, rows_total, sp.N, sp.K, device_info(dev).cus,
-                                              env_int("MLXQ_QMM_TILE", -1), env_int("MLXQ_QMM_KSPLIT", 0));
-      if (qp.ok) {
-        mlxq::QmmArgs q{};
-        q.x = a.x;
-        q.w = a.w;
-        q.scales = a.scales;
-        q.biases = a.biases;
-        q.out = a.out;
-        q.M = (int)rows_total;
-        q.x_rows = (int)rows_total;
-        q.N = (int)sp.N;
-        q.K = (int)sp.K;
-        int shift = 0;
-        while ((1 << shift) < sp.gs) shift++;
-        q.gs_shift = shift;
-        q.ksplit = qp.ksplit;
-        q.ksteps_per_split = qp.ksteps_per_split;
-        if (qp.ksplit > 1)
-          q.ws = reinterpret_cast<float*>(
-              workspace(dev, stream, (size_t)qp.ksplit * rows_total * sp.N * sizeof(float)).data);
-        hip_check(mlxq::qmm_launch(fmt, q, qp, stream), "qmm launch");
-        return;
-      }
-    }
-    if (wv.ndim() == 2) {
-      // every leading dim of x folds into rows (qmm.hip:3606-3620 does the same fold)
-      a.E = 1;
-      a.X = 1;
-      a.w_expert_stride = 0;
-      a.s_expert_stride = 0;
-      int rps = (int)std::min<int64_t>(rows_total, cap);
-      {
-        int nw, pf;
-        qmv_shape_choice(sp.N, sp.K, nw, pf);
-        const DevInfo di = device_info(current_device());
-        while (rps > 1 && mlxq::qmv_plan(fmt, sp.gs, sp.N, sp.K, rps, 1, di.cus, nw, pf).lds > mlxq::kQmvLdsMax)
-          rps = (rps + 1) / 2;
-      }
-      a.rps = rps;
-      a.total_rows = (int)rows_total;
-      a.X = (int)((rows_total + rps - 1) / rps);
-      const int nseg = a.X;
-      run_qmv(sp, a, nseg, rps, stream);
-    } else {
-      // batched weights: each batch element is a segment of x.shape[-2] rows
-      const Shape wsh = wv.shape(), xsh = xv.shape();
-      Shape wb(wsh.begin(), wsh.end() - 2);
-      Shape ob(sp.out_shape.begin(), sp.out_shape.end() - 2);
-      Shape xb = xv.ndim() > 2 ? Shape(xsh.begin(), xsh.end() - 2) : Shape{};
-      if (xv.ndim() <= 2 || wb != ob || xb != ob)
-        unsupported("quantized_matmul: batched w needs x with the same batch shape (use gather_qmm to broadcast)");
-      const int64_t M = xv.dim(-2);
-      if (M > cap) unsupported("quantized_matmul: batched w with more than " + std::to_string(cap) + " rows per batch");
-      int64_t nb = 1;
-      for (auto d : wb) nb *= d;
-      a.E = (int)nb;
-      a.X = (int)nb;
-      a.w_expert_stride = wv.dim(-2) * wv.dim(-1);
-      a.s_expert_stride = View{scales}.dim(-2) * View{scales}.dim(-1);
-      a.rps = (int)M;
-      a.total_rows = (int)rows_total;
-      run_qmv(sp, a, (int)nb, (int)M, stream);
-    }
+    a.w = mp.w[0];
+    a.scales = mp.scales[0];
+    a.biases = mp.biases[0];
+    a.out = mp.out[0];
+    a.N = mp.N[0];
+    a.K = (int)sp[0].K;
+    a.out_rows = (int)rows;
+    a.E = 1;
+    a.X = 1;
+    a.rps = (int)rows;
+    a.total_rows = (int)rows;
+    hip_check(mlxq::qmv_rs_launch(fmt, sp[0].gs, a, 1, plan, stream, &mp), "qmv launch");
   });
 }
 

@@ -72,6 +72,19 @@ hipError_t qmv_launch(int fmt, int gs, const QmvArgs& a, int nseg_slots, const Q
 // Row-streaming decode kernel (qmv_rs.hip) for 1 to 4 activation rows per
 // weight matrix: R weight rows per workgroup, one wave per 1 KiB chunk of a
 // row (CPW chunks per wave when a row has more than 8).
+// Several projections of the same activations in one row-streaming launch
+// (q/k/v, gate/up): matrix p owns the workgroups [tile_end[p-1], tile_end[p])
+// of the grid's x dimension; n <= 1 means the QmvArgs matrix alone.
+constexpr int kQmvMultiMax = 4;
+struct QmvMulti {
+  int n;
+  int tile_end[kQmvMultiMax];
+  int N[kQmvMultiMax];
+  const uint32_t* w[kQmvMultiMax];
+  const void* scales[kQmvMultiMax];
+  const uint16_t* biases[kQmvMultiMax];
+  uint16_t* out[kQmvMultiMax];
+};
 struct QmvRsPlan {
   bool ok = false;  // false: use qmv_plan / qmv_launch
   int mr = 1;       // activation rows compiled for (1, 2 or 4)
@@ -83,7 +96,8 @@ struct QmvRsPlan {
 };
 // r_req: requested rows per workgroup (0 or invalid -> default).
 QmvRsPlan qmv_rs_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int r_req);
-hipError_t qmv_rs_launch(int fmt, int gs, const QmvArgs& a, int nseg, const QmvRsPlan& p, hipStream_t stream);
+hipError_t qmv_rs_launch(int fmt, int gs, const QmvArgs& a, int nseg, const QmvRsPlan& p, hipStream_t stream,
+                         const QmvMulti* multi = nullptr);
 
 // Block-MFMA decode kernel (qmv_b4.hip) for 1 to 16 activation rows per
 // weight matrix: v_mfma_f32_4x4x4bf16_1k over 4 weight rows x 256-byte pieces

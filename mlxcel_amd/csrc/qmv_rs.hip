@@ -50,7 +50,7 @@ __host__ __device__ inline uint32_t qmv_rs_lds(int fmt, int r, int mr, int nw, i
 // a branch join there makes the compiler wait for the loads before it issues
 // the weight stream.
 template <int FMT, int MR, int R, int CPW, int UPW>
-__global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shift) {
+__global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shift, const QmvMulti mp) {
   constexpr bool AFF = FMT != MXFP4;
   constexpr int BITS = FMT == AFF8 ? 8 : 4;
   constexpr int KL = 128 / BITS;  // K positions per lane chunk (16 bytes)
@@ -92,9 +92,26 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
   }
   const int xbatch = seg_index(a.lhs, a.lhs_stride, sidx, a.X, a.lhs_div > 1 ? sidx / a.lhs_div : sidx);
 
-  const int N = a.N;
+  // The weight matrix of this workgroup: a's, or with several projections of
+  // the same activations (mp.n > 1) the one whose row tiles hold blockIdx.x.
+  const uint32_t* Wm = a.w;
+  const void* Sm = a.scales;
+  const uint16_t* Bm = a.biases;
+  uint16_t* Om = a.out;
+  int N = a.N;
+  int tile = blockIdx.x;
+  if (mp.n > 1) {  // workgroup-uniform
+    int p = 0;
+    while (p < mp.n - 1 && tile >= mp.tile_end[p]) p++;
+    tile -= p > 0 ? mp.tile_end[p - 1] : 0;
+    Wm = mp.w[p];
+    Sm = mp.scales[p];
+    Bm = mp.biases[p];
+    Om = mp.out[p];
+    N = mp.N[p];
+  }
   const int K = a.K;
-  const int row0 = blockIdx.x * R;
+  const int row0 = tile * R;
   const int nlc = K / KL;  // lane chunks per row
   const uint32_t RB = (uint32_t)nlc * 16u;  // bytes per weight row
   const int G = K >> gs_shift;
@@ -104,13 +121,13 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
 
   // Buffer resources: bounds-checked loads return 0 past the end, which
   // covers rows past N, activation rows past `count` and dead lanes.
-  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.w + (int64_t)expert * a.w_expert_stride, (uint32_t)N * RB);
+  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(Wm + (int64_t)expert * a.w_expert_stride, (uint32_t)N * RB);
   const __amdgpu_buffer_rsrc_t xr =
       buffer_rsrc(a.x + (int64_t)xbatch * a.rps * K, (uint32_t)count * (uint32_t)K * 2u);
   const int64_t sb0 = (int64_t)expert * a.s_expert_stride;
   const __amdgpu_buffer_rsrc_t sr =
-      buffer_rsrc(reinterpret_cast<const uint8_t*>(a.scales) + sb0 * ESZ, (uint32_t)(N * G * ESZ));
-  const __amdgpu_buffer_rsrc_t br = buffer_rsrc(AFF ? (const void*)(a.biases + sb0) : a.scales,
+      buffer_rsrc(reinterpret_cast<const uint8_t*>(Sm) + sb0 * ESZ, (uint32_t)(N * G * ESZ));
+  const __amdgpu_buffer_rsrc_t br = buffer_rsrc(AFF ? (const void*)(Bm + sb0) : Sm,
                                                 (uint32_t)(AFF ? N * G * 2 : 0));
 
   int kc[CPW];
@@ -320,7 +337,7 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
     for (int q = 0; q < NW * 4; q++) tot += red[q * V + idx];
     const int r = idx / MR, m = idx % MR;
     const int row = row0 + r;
-    if (row < N && m < count) a.out[((int64_t)sidx * a.rps + m) * N + row] = (uint16_t)f32_to_bf16_bits(tot);
+    if (row < N && m < count) Om[((int64_t)sidx * a.rps + m) * N + row] = (uint16_t)f32_to_bf16_bits(tot);
   }
 }
 
@@ -329,12 +346,13 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
 namespace {
 
 template <int FMT, int UPW>
-hipError_t rs_launch_upw(const QmvRsPlan& p, const QmvArgs& a, int gs_shift, dim3 grid, hipStream_t stream) {
+hipError_t rs_launch_upw(const QmvRsPlan& p, const QmvArgs& a, int gs_shift, dim3 grid, const QmvMulti& mp,
+                         hipStream_t stream) {
   const dim3 block((unsigned)(p.nw * 64));
-#define RS_CASE(MR_, R_, CPW_)                                                                             \
-  if (p.mr == MR_ && p.r == R_ && p.cpw == CPW_) {                                                         \
-    hipLaunchKernelGGL((qmv_rs_kernel<FMT, MR_, R_, CPW_, UPW>), grid, block, p.lds, stream, a, gs_shift); \
-    return hipGetLastError();                                                                              \
+#define RS_CASE(MR_, R_, CPW_)                                                                                 \
+  if (p.mr == MR_ && p.r == R_ && p.cpw == CPW_) {                                                             \
+    hipLaunchKernelGGL((qmv_rs_kernel<FMT, MR_, R_, CPW_, UPW>), grid, block, p.lds, stream, a, gs_shift, mp); \
+    return hipGetLastError();                                                                                  \
   }
   RS_CASE(1, 4, 1)
   RS_CASE(1, 8, 1)
@@ -359,11 +377,12 @@ int rs_upw(int fmt, int64_t G) {
 }
 
 template <int FMT>
-hipError_t rs_launch_fmt(const QmvRsPlan& p, const QmvArgs& a, int gs_shift, dim3 grid, hipStream_t stream) {
+hipError_t rs_launch_fmt(const QmvRsPlan& p, const QmvArgs& a, int gs_shift, dim3 grid, const QmvMulti& mp,
+                         hipStream_t stream) {
   const int upw = rs_upw(FMT, (int64_t)a.K >> gs_shift);
-  if (upw == 1) return rs_launch_upw<FMT, 1>(p, a, gs_shift, grid, stream);
-  if (upw == 4) return rs_launch_upw<FMT, 4>(p, a, gs_shift, grid, stream);
-  return rs_launch_upw<FMT, 2>(p, a, gs_shift, grid, stream);
+  if (upw == 1) return rs_launch_upw<FMT, 1>(p, a, gs_shift, grid, mp, stream);
+  if (upw == 4) return rs_launch_upw<FMT, 4>(p, a, gs_shift, grid, mp, stream);
+  return rs_launch_upw<FMT, 2>(p, a, gs_shift, grid, mp, stream);
 }
 
 bool rs_valid(int mr, int r, int cpw) {
@@ -404,14 +423,21 @@ QmvRsPlan qmv_rs_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int r_req
   return p;
 }
 
-hipError_t qmv_rs_launch(int fmt, int gs, const QmvArgs& a, int nseg, const QmvRsPlan& p, hipStream_t stream) {
+hipError_t qmv_rs_launch(int fmt, int gs, const QmvArgs& a, int nseg, const QmvRsPlan& p, hipStream_t stream,
+                         const QmvMulti* multi) {
   if (!p.ok) return hipErrorInvalidValue;
+  QmvMulti mp{};
+  int tiles = p.tiles;
+  if (multi && multi->n > 1) {
+    mp = *multi;
+    tiles = mp.tile_end[mp.n - 1];
+  }
   const int gs_shift = log2i(gs);
-  const dim3 grid((unsigned)p.tiles, (unsigned)nseg, 1);
+  const dim3 grid((unsigned)tiles, (unsigned)nseg, 1);
   switch (fmt) {
-    case AFF4: return rs_launch_fmt<AFF4>(p, a, gs_shift, grid, stream);
-    case AFF8: return rs_launch_fmt<AFF8>(p, a, gs_shift, grid, stream);
-    default: return rs_launch_fmt<MXFP4>(p, a, gs_shift, grid, stream);
+    case AFF4: return rs_launch_fmt<AFF4>(p, a, gs_shift, grid, mp, stream);
+    case AFF8: return rs_launch_fmt<AFF8>(p, a, gs_shift, grid, mp, stream);
+    default: return rs_launch_fmt<MXFP4>(p, a, gs_shift, grid, mp, stream);
   }
 }
 

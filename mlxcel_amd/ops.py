@@ -120,6 +120,43 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     return out
 
 
+def quantized_matmul_multi(x: torch.Tensor, ws: Sequence[torch.Tensor], scales: Sequence[torch.Tensor],
+                           biases: Optional[Sequence[Optional[torch.Tensor]]] = None,
+                           group_size: Optional[int] = None, bits: Optional[int] = None, mode: str = "affine", *,
+                           out: Optional[Sequence[torch.Tensor]] = None) -> list:
+    """``[quantized_matmul(x, w_i, s_i, b_i) for i]`` (transpose=True) in one
+    call; at decode sizes one launch that reads x once (q/k/v, gate/up)."""
+    lib = _lib.load()
+    n = len(ws)
+    gs, b = _opt(group_size), _opt(bits)
+    dev = _device_of(x)
+    if out is None:
+        out = []
+        for w_, s_, b_ in zip(ws, scales, biases if biases is not None else [None] * n):
+            nd, sh, dt = ctypes.c_int32(), (ctypes.c_int64 * _lib.MAX_DIMS)(), ctypes.c_int32()
+            st = lib.mlxq_quantized_matmul_shape(_ref(_arr(x)), _ref(_arr(w_)), _ref(_arr(s_)), _ref(_arr(b_)),
+                                                 True, gs, b, _mode(mode), ctypes.byref(nd), sh, ctypes.byref(dt))
+            if st:
+                _raise(st)
+            out.append(_empty(nd, sh, dt, dev))
+    P = ctypes.POINTER(_lib.MlxqArray)
+
+    def ptrs(ts):  # (pointer array, the structs it points to: kept alive by the caller)
+        structs = [_arr(t)[1] if t is not None else None for t in ts]
+        return (P * n)(*[ctypes.pointer(v) if v is not None else None for v in structs]), structs
+
+    pw, kw = ptrs(ws)
+    ps, ks = ptrs(scales)
+    po, ko = ptrs(out)
+    pb, kb = ptrs(biases) if biases is not None else (None, None)
+    ax = _arr(x)
+    with torch.cuda.device(dev):
+        st = lib.mlxq_quantized_matmul_multi(_ref(ax), n, pw, ps, pb, gs, b, _mode(mode), po, _stream(dev))
+    if st:
+        _raise(st)
+    return list(out)
+
+
 def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
                biases: Optional[torch.Tensor] = None, lhs_indices: Optional[torch.Tensor] = None,
                rhs_indices: Optional[torch.Tensor] = None, transpose: bool = True,

@@ -39,6 +39,9 @@ class DequantDecoder(bench.QuantDecoder):
         wd = mq.dequantize(*w, self.gs, self.bits).float()
         return (x.float() @ wd.t()).to(torch.bfloat16)
 
+    def qmm_n(self, x, ws):
+        return [self.qmm(x, w) for w in ws]
+
 
 def rel(a, b):
     a, b = a.float(), b.float()
@@ -85,3 +88,18 @@ def test_graph_replay_matches_eager_step():
         ar = torch.arange(T, device="cuda")
         mask = torch.where(ar[None, :] <= pos, 0.0, float("-inf")).expand(G, T)
         tok = torch.argmax(e.forward(tok, pos, 1, T, mask), -1)
+
+
+def test_multi_projection_decoder_is_bitwise_the_separate_calls():
+    # q/k/v and gate/up through quantized_matmul_multi (one launch each at
+    # decode) against one quantized_matmul call per projection
+    announce("e2e_multi_vs_separate")
+    shape = bench.QwenShape(layers=2, hidden=512, nq=8, nkv=2, hd=64, inter=1024, vocab=2000)
+    g = torch.Generator(device="cuda").manual_seed(9)
+    prompt = torch.randint(0, shape.vocab, (1, 40), device="cuda", generator=g)
+    a = bench.QuantDecoder(shape, 1, 64, seed=10, multi=True)
+    b = bench.QuantDecoder(shape, 1, 64, seed=10, multi=False)
+    ta, _, _ = a.generate(prompt, 6, bucket=16)
+    tb, _, _ = b.generate(prompt, 6, bucket=16)
+    assert torch.equal(ta, tb)
+    assert torch.equal(a.logits, b.logits)

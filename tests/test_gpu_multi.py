@@ -1,0 +1,142 @@
+"""GPU checks of mlxq_quantized_matmul_multi (several projections of one
+activation: q/k/v, gate/up): every output is bit for bit the separate
+mlxq_quantized_matmul call's, and within max|y - y_ref| / max|y_ref| <= 1e-2
+of the oracle.  Decode rows (1-2, and 3-4 over long rows) take the single
+row-streaming launch over all projections; other row counts, and forced
+kernels, run the calls one after another and must give the same bytes.
+"""
+import numpy as np
+import pytest
+import torch
+
+import mlxcel_amd as mq
+import oracle as orc
+from helpers import TOL, announce, dev_bf16, dev_u32, dev_u8, host_u16, max_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def affine_sets(Ns, K, bits, gs, seed):
+    sets = []
+    for i, N in enumerate(Ns):
+        wq, s, b = orc.affine_quantize(orc.normal_bf16((N, K), 0.02, seed + i), gs, bits)
+        sets.append((wq, s, b))
+    return sets
+
+
+def run_both(x, sets, gs, bits, mode="affine"):
+    xd = dev_bf16(x)
+    if mode == "affine":
+        dev = [(dev_u32(w), dev_bf16(s), dev_bf16(b)) for w, s, b in sets]
+    else:
+        dev = [(dev_u32(w), dev_u8(s), None) for w, s in sets]
+    multi = mq.quantized_matmul_multi(xd, [d[0] for d in dev], [d[1] for d in dev],
+                                      [d[2] for d in dev] if mode == "affine" else None, gs, bits, mode)
+    single = [mq.quantized_matmul(xd, d[0], d[1], d[2], True, gs, bits, mode) for d in dev]
+    torch.cuda.synchronize()
+    return [host_u16(t) for t in multi], [host_u16(t) for t in single]
+
+
+def check(x, sets, gs, bits, mode="affine"):
+    multi, single = run_both(x, sets, gs, bits, mode)
+    for i, (m, s) in enumerate(zip(multi, single)):
+        np.testing.assert_array_equal(m, s, err_msg=f"projection {i}")
+        if mode == "affine":
+            want = orc.qmm_t_affine(x, *sets[i], gs, bits)
+        else:
+            want = orc.fp_qmm_t_mxfp4(x, *sets[i])
+        assert max_rel(m, want) <= TOL, (i, max_rel(m, want))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M", [1, 2, 4])
+def test_qkv_llama3_8b(bits, M):
+    announce("multi_qkv", bits, M)
+    K = 4096
+    x = orc.normal_bf16((M, K), 1.0, 900 + M)
+    check(x, affine_sets([4096, 1024, 1024], K, bits, 64, 910 + bits), 64, bits)
+
+
+@pytest.mark.parametrize("M", [1, 2])
+def test_gate_up_qwen3_8b(M):
+    announce("multi_gate_up", M)
+    K = 4096
+    x = orc.normal_bf16((1, M, K), 1.0, 920 + M)  # leading dims fold into rows
+    check(x, affine_sets([12288, 12288], K, 4, 64, 930), 64, 4)
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 4])
+@pytest.mark.parametrize("gs", [32, 128])
+def test_ragged_widths_and_counts(n, gs):
+    # partial row tiles in every projection, one of them a single row
+    announce("multi_ragged", n, gs)
+    K = 1536
+    Ns = [200, 77, 1, 333][:n]
+    x = orc.normal_bf16((1, K), 1.0, 940 + n)
+    check(x, affine_sets(Ns, K, 4, gs, 950 + n + gs), gs, 4)
+
+
+def test_mxfp4_projections():
+    announce("multi_mxfp4")
+    K = 2880
+    x = orc.normal_bf16((1, K), 1.0, 960)
+    sets = [orc.mxfp4_quantize(orc.normal_bf16((N, K), 0.02, 961 + i)) for i, N in enumerate([4096, 512, 512])]
+    check(x, sets, 32, 4, "mxfp4")
+
+
+@pytest.mark.parametrize("M", [3, 8, 20])
+def test_other_row_counts_run_separately(M):
+    # 3 rows over short rows (block-MFMA), 8 (mid-size kernel), 20 (prefill GEMM)
+    announce("multi_rows", M)
+    K = 2048
+    x = orc.normal_bf16((M, K), 1.0, 970 + M)
+    check(x, affine_sets([512, 256], K, 4, 64, 975 + M), 64, 4)
+
+
+@pytest.mark.parametrize("kernel", ["fr", "b4", "mfma"])
+def test_forced_kernels(monkeypatch, kernel):
+    monkeypatch.setenv("MLXQ_QMV_KERNEL", kernel)
+    announce("multi_forced", kernel)
+    K = 4096
+    x = orc.normal_bf16((1, K), 1.0, 980)
+    check(x, affine_sets([1024, 512, 512], K, 4, 64, 981), 64, 4)
+
+
+def test_graph_replays():
+    announce("multi_graph")
+    K = 4096
+    sets = affine_sets([4096, 1024, 1024], K, 4, 64, 990)
+    dev = [(dev_u32(w), dev_bf16(s), dev_bf16(b)) for w, s, b in sets]
+    xs = [orc.normal_bf16((1, K), 1.0, 991 + i) for i in range(3)]
+    xd = dev_bf16(xs[0])
+    outs = [torch.empty(1, N, dtype=torch.bfloat16, device="cuda") for N in (4096, 1024, 1024)]
+    args = ([d[0] for d in dev], [d[1] for d in dev], [d[2] for d in dev], 64, 4)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        mq.quantized_matmul_multi(xd, *args, out=outs)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        mq.quantized_matmul_multi(xd, *args, out=outs)
+    torch.cuda.synchronize()
+    for i in (0, 1, 2, 1):
+        xd.copy_(dev_bf16(xs[i]))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, (w, s, b) in zip(outs, dev):
+            np.testing.assert_array_equal(host_u16(o), host_u16(mq.quantized_matmul(xd, w, s, b)))
+
+
+def test_argument_errors():
+    announce("multi_errors")
+    K = 256
+    sets = affine_sets([64, 64], K, 4, 64, 999)
+    dev = [(dev_u32(w), dev_bf16(s), dev_bf16(b)) for w, s, b in sets]
+    xd = dev_bf16(orc.normal_bf16((1, K), 1.0, 998))
+    with pytest.raises(ValueError):  # K of the second weight disagrees with x
+        bad = dev_u32(orc.affine_quantize(orc.normal_bf16((64, 512), 0.02, 997), 64, 4)[0])
+        mq.quantized_matmul_multi(xd, [dev[0][0], bad], [d[1] for d in dev], [d[2] for d in dev], 64, 4)
+    with pytest.raises(ValueError):  # more than four projections
+        mq.quantized_matmul_multi(xd, [dev[0][0]] * 5, [dev[0][1]] * 5, [dev[0][2]] * 5, 64, 4)
