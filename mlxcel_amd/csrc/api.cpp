@@ -1318,8 +1318,8 @@ mlxq_status mlxq_dequantize(const mlxq_array* w, const mlxq_array* scales, const
     oshape.back() = wv.dim(-1) * 32 / bits;
     check_out(out, oshape, out_type, tag);
     if (mode == NVFP4_M || mode == MXFP8_M) unsupported("dequantize: only affine and mxfp4 are implemented");
-    if (mode == AFFINE && bits != 2 && bits != 4 && bits != 8)
-      unsupported("dequantize: affine bits 2, 4 and 8 are implemented");
+    if (mode == AFFINE && bits != 2 && bits != 4 && bits != 6 && bits != 8)
+      unsupported("dequantize: affine bits 2, 4, 6 and 8 are implemented");
     if (out_type != MLXQ_BFLOAT16) unsupported("dequantize: only bfloat16 output is implemented");
     if (mode == AFFINE) {
       require_dtype(scales, MLXQ_BFLOAT16, "scales", tag);
@@ -1408,8 +1408,8 @@ mlxq_status mlxq_quantize(const mlxq_array* w, int32_t group_size, int32_t bits,
     check_out(scales_out, ss, mode == AFFINE ? w->dtype : (int)MLXQ_UINT8, tag);
     if (mode == AFFINE) check_out(biases_out, ss, w->dtype, tag);
     if (mode == NVFP4_M || mode == MXFP8_M) unsupported("quantize: only affine and mxfp4 are implemented");
-    if (mode == AFFINE && bits != 2 && bits != 4 && bits != 8)
-      unsupported("quantize: affine bits 2, 4 and 8 are implemented");
+    if (mode == AFFINE && bits != 2 && bits != 4 && bits != 6 && bits != 8)
+      unsupported("quantize: affine bits 2, 4, 6 and 8 are implemented");
     if (w->dtype != MLXQ_BFLOAT16) unsupported("quantize: only bfloat16 weights are implemented");
     require_contiguous(w, "w");
     const int64_t K = wv.dim(-1);

@@ -8,7 +8,8 @@
 //    hardware's float denormal mode.
 //  * affine quantize: overlays/cpu/mlx/backend/cpu/quantized.cpp:1233-1305
 //    (`quantize<bfloat16_t, uint32_t>`), including the edge snapping and the
-//    codes computed with the unrounded float scale/bias.
+//    codes computed with the unrounded float scale/bias; bits 2, 4, 6 and 8
+//    (6-bit codes go out as 3-byte packs of 4, the bit stream of the codes).
 //  * mxfp4 quantize: the graph fallback ops.cpp:5364-5431, every op rounded to
 //    bf16 as MLX evaluates it; the shared exponent is the smallest e with
 //    2^e >= bf16(max|w| / 6), which is what round(log2) + the round-up step
@@ -54,9 +55,48 @@ __global__ __launch_bounds__(256) void affine_dequant_kernel(const uint32_t* __r
   for (int p = 0; p < PER / 2; p++) dst[p] = packed[p];
 }
 
+// 6-bit: one lane per 12-byte unit of 16 codes (four 3-byte packs; code j is
+// bits 6j .. 6j+5 of the little-endian unit, quantized.cpp:1283-1297).
+__global__ __launch_bounds__(256) void affine_dequant6_kernel(const uint32_t* __restrict__ w,
+                                                              const uint16_t* __restrict__ scales,
+                                                              const uint16_t* __restrict__ biases,
+                                                              uint16_t* __restrict__ out, int64_t nunits,
+                                                              int64_t upr, int gs) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nunits) return;
+  const int64_t row = i / upr;
+  const int64_t k0 = (i - row * upr) * 16;
+  const int64_t gi = row * (upr * 16 / gs) + k0 / gs;
+  const float s = bf16_bits_to_f32(scales[gi]);
+  const float b = bf16_bits_to_f32(biases[gi]);
+  const uint32_t u[3] = {w[3 * i], w[3 * i + 1], w[3 * i + 2]};
+  u32x4 o[2];
+#pragma unroll
+  for (int p = 0; p < 16; p += 2) {
+    uint32_t h[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int bit = 6 * (p + j), wi = bit >> 5, sh = bit & 31;
+      const uint32_t c = sh <= 26 ? (u[wi] >> sh) & 63u : ((u[wi] >> sh) | (u[wi + 1] << (32 - sh))) & 63u;
+      h[j] = f32_to_bf16_bits(bfr((float)c * s) + b);
+    }
+    o[p / 8][(p / 2) % 4] = h[0] | (h[1] << 16);
+  }
+  u32x4* dst = reinterpret_cast<u32x4*>(out + row * (upr * 16) + k0);
+  dst[0] = o[0];
+  dst[1] = o[1];
+}
+
 hipError_t launch_affine_dequantize(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                                     uint16_t* out, int64_t rows, int64_t K, int gs, int bits,
                                     hipStream_t stream) {
+  if (bits == 6) {
+    const int64_t nunits = rows * (K / 16);
+    if (nunits == 0) return hipSuccess;
+    hipLaunchKernelGGL(affine_dequant6_kernel, dim3((unsigned)((nunits + 255) / 256)), dim3(256), 0, stream, w,
+                       scales, biases, out, nunits, K / 16, gs);
+    return hipGetLastError();
+  }
   const int64_t Kw = K * bits / 32;
   const int64_t nwords = rows * Kw;
   if (nwords == 0) return hipSuccess;
@@ -171,22 +211,27 @@ __global__ __launch_bounds__(256) void affine_quant_kernel(const uint16_t* __res
     scale = edge / q0;
     bias = edge;
   }
-  uint32_t codes = 0;  // 8 codes of BITS bits (BITS == 8: low 4 in `codes`, high 4 in `codes_hi`)
-  uint32_t codes_hi = 0;
+  // 8 codes of BITS bits, low bits first (8-bit: low 4 in `codes`, high 4 in
+  // `codes_hi`; 6-bit: bits 0-31 in `codes`, 32-47 in `codes_hi`)
+  uint64_t all = 0;
 #pragma unroll
   for (int i = 0; i < 8; i++) {
     float q = rintf((vals[i] - bias) / scale);
     q = (q < 0.0f) ? 0.0f : q;
     q = (n_bins < q) ? n_bins : q;
-    const uint32_t c = (uint32_t)q;
-    if (BITS == 8) {
-      if (i < 4) codes |= c << (8 * i);
-      else codes_hi |= c << (8 * (i - 4));
-    } else {
-      codes |= c << (BITS * i);
-    }
+    all |= (uint64_t)(uint32_t)q << (BITS * i);
   }
-  if (BITS == 2) {
+  const uint32_t codes = (uint32_t)all, codes_hi = (uint32_t)(all >> 32);
+  if (BITS == 6) {
+    // two lanes (16 codes, 12 bytes: MLX's 3-byte packs of 4) per 3 words
+    const uint32_t olo = __shfl_xor(codes, 1), ohi = __shfl_xor(codes_hi, 1);
+    if (live && (piece & 1) == 0) {
+      uint32_t* d = wq + (piece >> 1) * 3;
+      d[0] = codes;
+      d[1] = codes_hi | (olo << 16);
+      d[2] = (olo >> 16) | (ohi << 16);
+    }
+  } else if (BITS == 2) {
     // two lanes (16 codes) per word
     const uint32_t other = __shfl_xor(codes, 1);
     if (live && (piece & 1) == 0) wq[piece >> 1] = codes | (other << 16);
@@ -219,6 +264,7 @@ hipError_t launch_affine_quantize(const uint16_t* w, uint32_t* wq, uint16_t* sca
   if (pieces == 0) return hipSuccess;
   if (bits == 2) launch_aq_bits<2>(w, wq, scales, biases, pieces, gs, stream);
   else if (bits == 4) launch_aq_bits<4>(w, wq, scales, biases, pieces, gs, stream);
+  else if (bits == 6) launch_aq_bits<6>(w, wq, scales, biases, pieces, gs, stream);
   else launch_aq_bits<8>(w, wq, scales, biases, pieces, gs, stream);
   return hipGetLastError();
 }

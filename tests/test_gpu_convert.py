@@ -5,7 +5,8 @@
 * quantize vs the MLX CPU quantizer (overlays/cpu/mlx/backend/cpu/
   quantized.cpp:1233-1305) and the mxfp4 graph quantizer (ops.cpp:5364-5431),
   plus the hand-derived ramp fixtures;
-* dequantize(slice) == slice(dequantize) (src/lib/mlxcel-core/src/ffi_tests.rs:5108-5170).
+* dequantize(slice) == slice(dequantize) (src/lib/mlxcel-core/src/ffi_tests.rs:5108-5170);
+* affine bits 2, 4, 6 (MLX's 3-byte packs of 4 codes) and 8.
 """
 import os
 
@@ -21,7 +22,7 @@ pytestmark = pytest.mark.gpu
 KAT = np.load(os.path.join(os.path.dirname(__file__), "golden", "kat.npz"))
 
 
-@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("bits", [2, 4, 6, 8])
 @pytest.mark.parametrize("gs", [32, 64, 128])
 def test_affine_dequantize_bitexact(bits, gs):
     announce("dequant", bits, gs)
@@ -65,7 +66,7 @@ def test_dequantize_commutes_with_row_slice():
     np.testing.assert_array_equal(full[16:40], part)
 
 
-@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("bits", [2, 4, 6, 8])
 @pytest.mark.parametrize("gs", [32, 64, 128])
 def test_affine_quantize_bitexact(bits, gs):
     announce("quant", bits, gs)
