@@ -12,6 +12,10 @@
  *                             -> mlx::core::dequantize, ops.cpp:5753-5805)
  *   mlxq_quantize          <- ffi::quantize_weights_* (mlx_cxx_bridge.cpp:7867-7900
  *                             -> mlx::core::quantize, ops.cpp:5454-5492)
+ *   mlxq_quantized_linear  <- ffi::quantized_linear_forward (lib.rs:697-707,
+ *                             mlx_cxx_bridge.cpp:1707-1746)
+ *   mlxq_quantized_matmul_matches_dense_gemm <- ffi::quantized_matmul_matches_dense_gemm
+ *                             (lib.rs:2925-2940)
  *   mlxq_quantized_matmul_multi <- the fused q/k/v and gate/up GEMVs of mlxcel-xla
  *                             (src/lib/mlxcel-xla/csrc/qmv4.hip:265-387)
  *   mlxq_fused_moe_expert  <- ffi::fused_moe_expert_kernel (lib.rs:2336-2356,
@@ -100,6 +104,26 @@ mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w,
                                   const mlxq_array* scales, const mlxq_array* biases,
                                   bool transpose, int32_t group_size, int32_t bits,
                                   const char* mode, mlxq_array* out, void* stream);
+
+/* A quantized linear layer, as the reference's quantized_linear_forward
+ * (lib.rs:697-707, mlx_cxx_bridge.cpp:1707-1746): quantized_matmul with
+ * transpose = true, then `+ linear_bias` as MLX adds two bf16 arrays (fp32
+ * sum, one rounding).  `linear_bias` may be NULL; otherwise of shape (N) (or
+ * (1, ..., N)) or the output's shape, in the output's dtype (other layouts
+ * return MLXQ_EUNSUPPORTED). */
+mlxq_status mlxq_quantized_linear(const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+                                  const mlxq_array* biases, const mlxq_array* linear_bias,
+                                  int32_t group_size, int32_t bits, const char* mode,
+                                  mlxq_array* out, void* stream);
+
+/* Whether quantized_matmul on these inputs returns the bytes of dequantize +
+ * a dense GEMM, as the reference's quantized_matmul_matches_dense_gemm
+ * (lib.rs:2925-2940, rocm qmm.hip:3493-3542) answers for its routes.  Always
+ * 0 here: every route dequantizes inside the matmul kernel.  No device work. */
+int32_t mlxq_quantized_matmul_matches_dense_gemm(const mlxq_array* x, const mlxq_array* w,
+                                                 const mlxq_array* scales,
+                                                 const mlxq_array* biases, int32_t group_size,
+                                                 int32_t bits);
 
 /* Several projections of one activation in one call (q/k/v, gate/up):
  * out[i] = quantized_matmul(x, w[i], scales[i], biases[i], transpose = true,

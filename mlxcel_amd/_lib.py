@@ -36,6 +36,8 @@ SYMBOLS = (
     "mlxq_quantized_matmul",
     "mlxq_quantized_matmul_shape",
     "mlxq_quantized_matmul_multi",
+    "mlxq_quantized_linear",
+    "mlxq_quantized_matmul_matches_dense_gemm",
     "mlxq_gather_qmm",
     "mlxq_gather_qmm_shape",
     "mlxq_dequantize",
@@ -74,6 +76,8 @@ def load() -> ctypes.CDLL:
                                                 ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(I32)]
     AA = ctypes.POINTER(A)
     lib.mlxq_quantized_matmul_multi.argtypes = [A, I32, AA, AA, AA, I32, I32, S, AA, P]
+    lib.mlxq_quantized_linear.argtypes = [A, A, A, A, A, I32, I32, S, A, P]
+    lib.mlxq_quantized_matmul_matches_dense_gemm.argtypes = [A, A, A, A, I32, I32]
     lib.mlxq_gather_qmm.argtypes = [A, A, A, A, A, A, B, I32, I32, B, S, A, A, P]
     lib.mlxq_gather_qmm_shape.argtypes = [A, A, A, A, A, A, B, I32, I32, S, ctypes.POINTER(I32),
                                           ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(I32)]

@@ -45,6 +45,7 @@ SOURCES = {
     "qmm_group.hip": [],
     "qmm.hip": [],
     "moe.hip": [],
+    "bias.hip": [],
     "dequant.hip": ["-ffp-contract=off"],
 }
 

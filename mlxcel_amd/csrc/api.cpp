@@ -840,6 +840,56 @@ mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w, cons
   });
 }
 
+mlxq_status mlxq_quantized_linear(const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+                                  const mlxq_array* biases, const mlxq_array* linear_bias, int32_t group_size,
+                                  int32_t bits, const char* mode, mlxq_array* out, void* stream_) {
+  return guarded([&] {
+    const char* tag = "quantized_linear";
+    const QmmSpec sp = check_quantized_matmul(x, w, scales, biases, true, group_size, bits, mode, out, tag);
+    int64_t bias_n = 0;
+    if (linear_bias) {
+      check_array(linear_bias, "linear_bias");
+      View lb{linear_bias}, ov{out};
+      // MLX's add broadcasts the bias against the (..., N) product; the two
+      // layouts a linear layer uses are covered: (N) / (1, ..., N), and the
+      // product's own shape
+      Shape osh = ov.shape();
+      Shape lsh = lb.shape();
+      while (!lsh.empty() && lsh.front() == 1 && (int)lsh.size() > 1) lsh.erase(lsh.begin());
+      if (lsh == Shape{sp.N}) bias_n = sp.N;
+      else if (lb.shape() == osh) bias_n = ov.size();
+      else
+        unsupported(std::string(tag) + ": linear_bias must have shape (N) or the output's shape (got " +
+                    fmt_shape(lb.shape()) + ")");
+      if (linear_bias->dtype != out->dtype)
+        unsupported(std::string(tag) + ": linear_bias must have the output's dtype (" + dtype_name(out->dtype) +
+                    "; the reference's add would promote)");
+      require_contiguous(linear_bias, "linear_bias");
+    }
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    run_quantized_matmul(sp, x, w, scales, biases, out, stream);
+    if (bias_n > 0 && View{out}.size() > 0)
+      hip_check(mlxq::launch_bias_add(static_cast<uint16_t*>(out->data),
+                                      static_cast<const uint16_t*>(linear_bias->data), View{out}.size(), bias_n,
+                                      stream),
+                "bias add launch");
+  });
+}
+
+int32_t mlxq_quantized_matmul_matches_dense_gemm(const mlxq_array* x, const mlxq_array* w,
+                                                 const mlxq_array* scales, const mlxq_array* biases,
+                                                 int32_t group_size, int32_t bits) {
+  (void)x;
+  (void)w;
+  (void)scales;
+  (void)biases;
+  (void)group_size;
+  (void)bits;
+  // Every route here dequantizes inside the matmul kernel (no dequantize +
+  // dense GEMM route), so no call returns the bytes of dequantize + matmul.
+  return 0;
+}
+
 mlxq_status mlxq_quantized_matmul_multi(const mlxq_array* x, int32_t n, const mlxq_array* const* w,
                                         const mlxq_array* const* scales, const mlxq_array* const* biases,
                                         int32_t group_size, int32_t bits, const char* mode, mlxq_array* const* out,

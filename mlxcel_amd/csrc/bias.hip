@@ -1,0 +1,42 @@
+// bias.hip — the linear bias of a quantized linear layer on gfx950.
+//
+// out[r][n] = bf16(out[r][n] + bias[n]) (or bias[r][n] for a full-shape bias):
+// MLX's `add` of two bf16 arrays, computed in fp32 and rounded to nearest even
+// once, as quantized_linear_forward applies it after quantized_matmul
+// (src/lib/mlxcel-core/cpp/mlx_cxx_bridge.cpp:1707-1746).  HBM-bound: one
+// read and one write of the output, one read of the bias; 8 elements a lane.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace mlxq {
+
+__global__ __launch_bounds__(256) void bias_add_kernel(uint16_t* __restrict__ out, const uint16_t* __restrict__ bias,
+                                                       int64_t n, int64_t bias_n) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (i >= n) return;
+  if (i + 8 <= n && bias_n % 8 == 0) {
+    u32x4 o = *reinterpret_cast<const u32x4*>(out + i);
+    const u32x4 b = *reinterpret_cast<const u32x4*>(bias + i % bias_n);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const uint32_t lo = f32_to_bf16_bits(bf16_bits_to_f32(o[q] & 0xFFFFu) + bf16_bits_to_f32(b[q] & 0xFFFFu));
+      const uint32_t hi = f32_to_bf16_bits(bf16_bits_to_f32(o[q] >> 16) + bf16_bits_to_f32(b[q] >> 16));
+      o[q] = lo | (hi << 16);
+    }
+    *reinterpret_cast<u32x4*>(out + i) = o;
+  } else {
+    for (int64_t j = i; j < n && j < i + 8; j++)
+      out[j] = (uint16_t)f32_to_bf16_bits(bf16_bits_to_f32(out[j]) + bf16_bits_to_f32(bias[j % bias_n]));
+  }
+}
+
+hipError_t launch_bias_add(uint16_t* out, const uint16_t* bias, int64_t n, int64_t bias_n, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  if (bias_n <= 0) return hipErrorInvalidValue;
+  const int64_t lanes = (n + 7) / 8;
+  hipLaunchKernelGGL(bias_add_kernel, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, stream, out, bias, n,
+                     bias_n);
+  return hipGetLastError();
+}
+
+}  // namespace mlxq

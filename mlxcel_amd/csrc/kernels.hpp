@@ -294,4 +294,7 @@ struct MoeArgs {
 };
 hipError_t moe_launch(const MoeArgs& a, int gu_bits, int d_bits, int act, hipStream_t stream);
 
+// out[i] = bf16(out[i] + bias[i % bias_n]) over n bf16 elements (bias.hip).
+hipError_t launch_bias_add(uint16_t* out, const uint16_t* bias, int64_t n, int64_t bias_n, hipStream_t stream);
+
 }  // namespace mlxq

@@ -120,6 +120,40 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     return out
 
 
+def quantized_linear(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: Optional[torch.Tensor] = None,
+                     linear_bias: Optional[torch.Tensor] = None, group_size: Optional[int] = None,
+                     bits: Optional[int] = None, mode: str = "affine", *,
+                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The reference's ``quantized_linear_forward``: ``x @ W^T + linear_bias``."""
+    lib = _lib.load()
+    gs, b = _opt(group_size), _opt(bits)
+    ax, aw, as_, ab, alb = _arr(x), _arr(w), _arr(scales), _arr(biases), _arr(linear_bias)
+    if out is None:
+        nd, sh, dt = ctypes.c_int32(), (ctypes.c_int64 * _lib.MAX_DIMS)(), ctypes.c_int32()
+        st = lib.mlxq_quantized_matmul_shape(_ref(ax), _ref(aw), _ref(as_), _ref(ab), True, gs, b, _mode(mode),
+                                             ctypes.byref(nd), sh, ctypes.byref(dt))
+        if st:
+            _raise(st)
+        out = _empty(nd, sh, dt, _device_of(x))
+    ao = _arr(out)
+    dev = _device_of(x)
+    with torch.cuda.device(dev):
+        st = lib.mlxq_quantized_linear(_ref(ax), _ref(aw), _ref(as_), _ref(ab), _ref(alb), gs, b, _mode(mode),
+                                       _ref(ao), _stream(dev))
+    if st:
+        _raise(st)
+    return out
+
+
+def quantized_matmul_matches_dense_gemm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                                        biases: Optional[torch.Tensor] = None, group_size: int = 64,
+                                        bits: int = 4) -> bool:
+    """The reference's predicate of the same name (no device work)."""
+    lib = _lib.load()
+    return bool(lib.mlxq_quantized_matmul_matches_dense_gemm(_ref(_arr(x)), _ref(_arr(w)), _ref(_arr(scales)),
+                                                             _ref(_arr(biases)), group_size, bits))
+
+
 def quantized_matmul_multi(x: torch.Tensor, ws: Sequence[torch.Tensor], scales: Sequence[torch.Tensor],
                            biases: Optional[Sequence[Optional[torch.Tensor]]] = None,
                            group_size: Optional[int] = None, bits: Optional[int] = None, mode: str = "affine", *,

@@ -273,3 +273,22 @@ def test_fused_moe_validation(lib):
     assert call_moe(lib, moe_args(sc_dtype=_lib.INT32), 256, 128, 2, 4, 4, 64) == _lib.EUNSUPPORTED
     assert call_moe(lib, moe_args(idx_dtype=_lib.INT16), 256, 128, 2, 4, 4, 64) == _lib.EUNSUPPORTED
     assert "fused_moe_expert_kernel" in _lib.last_error()
+
+
+def test_quantized_linear_and_dense_gemm_predicate(lib):
+    x, w, s = arr([1, 64], BF), arr([64, 8], U32), arr([64, 1], BF)
+    assert lib.mlxq_quantized_matmul_matches_dense_gemm(ctypes.byref(x), ctypes.byref(w), ctypes.byref(s),
+                                                        ctypes.byref(s), 64, 4) == 0
+    out = arr([1, 64], BF)
+
+    def lin(bias):
+        return lib.mlxq_quantized_linear(ctypes.byref(x), ctypes.byref(w), ctypes.byref(s), ctypes.byref(s),
+                                         ctypes.byref(bias), 64, 4, b"affine", ctypes.byref(out), None)
+
+    assert lin(arr([32], BF)) == _lib.EUNSUPPORTED and "linear_bias must have shape" in _lib.last_error()
+    assert lin(arr([64], F32)) == _lib.EUNSUPPORTED and "dtype" in _lib.last_error()
+    # argument errors of the matmul itself come first, with the reference's text
+    bad = arr([1, 32], BF)
+    st = lib.mlxq_quantized_linear(ctypes.byref(bad), ctypes.byref(w), ctypes.byref(s), ctypes.byref(s), None, 64, 4,
+                                   b"affine", ctypes.byref(out), None)
+    assert st == _lib.EINVAL
