@@ -10,11 +10,13 @@
 
 namespace mlxq {
 
+// vec: out and bias 16-byte aligned and bias_n a multiple of 8 (16-byte
+// accesses), else one element at a time.
 __global__ __launch_bounds__(256) void bias_add_kernel(uint16_t* __restrict__ out, const uint16_t* __restrict__ bias,
-                                                       int64_t n, int64_t bias_n) {
+                                                       int64_t n, int64_t bias_n, int vec) {
   const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
   if (i >= n) return;
-  if (i + 8 <= n && bias_n % 8 == 0) {
+  if (vec && i + 8 <= n) {
     u32x4 o = *reinterpret_cast<const u32x4*>(out + i);
     const u32x4 b = *reinterpret_cast<const u32x4*>(bias + i % bias_n);
 #pragma unroll
@@ -34,8 +36,10 @@ hipError_t launch_bias_add(uint16_t* out, const uint16_t* bias, int64_t n, int64
   if (n == 0) return hipSuccess;
   if (bias_n <= 0) return hipErrorInvalidValue;
   const int64_t lanes = (n + 7) / 8;
+  const int vec = ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(bias)) & 15u) == 0 &&
+                  bias_n % 8 == 0;
   hipLaunchKernelGGL(bias_add_kernel, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, stream, out, bias, n,
-                     bias_n);
+                     bias_n, vec);
   return hipGetLastError();
 }
 

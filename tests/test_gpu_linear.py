@@ -19,9 +19,10 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("M", [1, 3, 20])
 @pytest.mark.parametrize("bias_shape", ["n", "1n", "full"])
-def test_affine_linear_is_matmul_then_add(M, bias_shape):
-    announce("linear_affine", M, bias_shape)
-    N, K = 328, 1024
+@pytest.mark.parametrize("N", [328, 333])  # 16-byte bias rows, and an odd width (element path)
+def test_affine_linear_is_matmul_then_add(M, bias_shape, N):
+    announce("linear_affine", M, bias_shape, N)
+    K = 1024
     x, wq, s, b = orc.normal_bf16((M, K), 1.0, 1100 + M), *orc.affine_quantize(orc.normal_bf16((N, K), 0.02, 1101), 64, 4)
     shape = {"n": (N,), "1n": (1, N), "full": (M, N)}[bias_shape]
     lb = orc.normal_bf16(shape, 0.5, 1102)
