@@ -178,7 +178,18 @@ def headline(steps, warmup, layers=8):
     gate_graph = capture(lambda: [mq.quantized_matmul(x, *mlp[l][0], True, 64, 4, out=out_g) for l in range(layers)])
     reps = max(1, steps // layers)
     gate_us = timed_graphs([gate_graph], reps, max(1, warmup // layers)) * 1e3 / layers
-    return value, ms, ms * 1e3 / 3, per_launch, gate_us, mlp[0][0]
+    # the same steps with gate and up as one quantized_matmul_multi launch
+    # (two launches per step instead of three; same bytes)
+    def multi_step(l):
+        gate, up, down = mlp[l]
+        mq.quantized_matmul_multi(x, [gate[0], up[0]], [gate[1], up[1]], [gate[2], up[2]], 64, 4,
+                                  out=[out_g, out_u])
+        mq.quantized_matmul(h, *down, True, 64, 4, out=out_d)
+
+    multi_graph = capture(lambda: [multi_step(l) for l in range(layers)])
+    multi_ms = timed_graphs([multi_graph], reps, max(1, warmup // layers)) / layers
+    multi_value = 3 * per_launch / (multi_ms * 1e-3) / 1e9
+    return value, ms, ms * 1e3 / 3, per_launch, gate_us, mlp[0][0], multi_value, multi_ms
 
 
 # ---- extras -------------------------------------------------------------------
@@ -645,7 +656,7 @@ def main():
         traffic_probe()
         return
 
-    value, ms, launch_us, per_launch, gate_us, gate = headline(args.steps, args.warmup)
+    value, ms, launch_us, per_launch, gate_us, gate, multi_value, multi_ms = headline(args.steps, args.warmup)
     achieved = per_launch / (gate_us * 1e-6) / 1e9
     ceiling = read_ceiling(per_launch)
     line = {
@@ -672,7 +683,9 @@ def main():
     }
     if not args.no_extra:
         want = set(args.extras.split(","))
-        extra = {}
+        extra = {"mlp_step_gate_up_multi": {"GBps": round(multi_value, 1), "ms_per_step": round(multi_ms, 5),
+                                            "note": "the headline step with gate+up as one quantized_matmul_multi "
+                                                    "launch (2 launches per step instead of 3)"}}
         if "copy" in want:
             extra["copy_ceiling_GBps"] = round(copy_ceiling(), 1)
         if "sweep" in want:
