@@ -102,8 +102,9 @@ __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGrou
   // matrix: zeros); they meet activations that are zero there, and fp4 codes
   // are finite, so they add exactly 0.  Their scales are not read (dead: 0,
   // a finite 2^-127), since the next row's could be NaN.
+  // Blocks past the last are dead offsets: no memory traffic, zeros.
   auto wload = [&](int b, int t, int v) -> u32x4 {
-    const uint32_t o = wrow[t] + (uint32_t)((2 * b + v) * 4 + g) * 16u;
+    const uint32_t o = b < nblk ? wrow[t] + (uint32_t)((2 * b + v) * 4 + g) * 16u : kDeadOfs;
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, o, 0, 2 /* nt */));
   };
   auto sload = [&](int b, int t, int v) -> uint32_t {
