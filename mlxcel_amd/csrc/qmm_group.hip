@@ -19,9 +19,16 @@
 // 4-chunk (128 k) window; a chunk is exactly one mxfp4 group (32 codes), so
 // the lane widens its codes with the group's e8m0 scale folded into the gfx950
 // fp4 conversion (fp4 code points times a power of two are exact in bf16) and
-// the MFMAs accumulate over all of K with no per-group fold.  Activations: a
-// 256-k block of the chunk's rows is staged in LDS (the next block's loads and
-// the next block's weights are in flight while the current one is used).
+// the MFMAs accumulate over all of K with no per-group fold.
+//
+// Pipelining: K runs in 128-k blocks.  A block's activations (64 rows x 256
+// bytes) go straight from memory into one of 4 LDS buffers with
+// buffer_load_dwordx4 ... lds (lane L of a load lands at M0 + 16 L, so each
+// wave load fills 4 rows; the row's 16-byte chunks are stored XOR-swizzled by
+// the row index, which keeps the 16 rows an MFMA operand read touches on
+// distinct banks), and its weights and scales into one of 4 register slots;
+// both run 3 blocks ahead of the block being multiplied, with no registers
+// spent on activations in flight.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -33,10 +40,11 @@ constexpr int GQ_NW = 4;                     // waves per workgroup
 constexpr int GQ_T = 2;                      // 16-row weight tiles per wave
 constexpr int GQ_ROWS = GQ_NW * GQ_T * 16;   // weight rows per workgroup (128)
 constexpr int GQ_MC = 64;                    // activation rows per chunk (4 A tiles)
-constexpr int GQ_KB = 256;                   // k per staged block (2 windows)
+constexpr int GQ_KB = 128;                   // k per block (one 4-group window)
 constexpr int GQ_NT = 64 * GQ_NW;
-constexpr int GQ_XPITCH = GQ_KB + 8;         // bf16 per staged row (16 bytes of padding)
-constexpr int GQ_XP = GQ_MC * GQ_KB / 8 / GQ_NT;  // 16-byte activation pieces per thread and block (8)
+constexpr int GQ_RING = 4;                   // blocks in the activation / weight rings
+constexpr int GQ_XB = GQ_MC * GQ_KB * 2;     // activation bytes per block (16 KiB, 256 per row)
+constexpr int GQ_XI = GQ_XB / 1024 / GQ_NW;  // 1 KiB direct-to-LDS loads per wave and block (4)
 
 // First entry whose (clamped) expert is >= v in the sorted index array;
 // wave-uniform.  Each step samples 64 evenly spaced entries of [lo, hi).
@@ -65,7 +73,11 @@ __device__ __forceinline__ int lower_bound_sorted(const uint32_t* idx, int strid
 }  // namespace
 
 __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGroupArgs a) {
-  __shared__ __align__(16) uint16_t xl[GQ_MC * GQ_XPITCH];
+  // the ring as four LDS objects, so the compiler's wait analysis sees that
+  // a buffer being refilled is not the one being read
+  __shared__ __align__(16) unsigned char xl0[GQ_XB], xl1[GQ_XB], xl2[GQ_XB], xl3[GQ_XB];
+  static_assert(GQ_RING == 4, "four ring buffers");
+  auto ring = [&](int slot) -> unsigned char* { return slot == 0 ? xl0 : slot == 1 ? xl1 : slot == 2 ? xl2 : xl3; };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -82,8 +94,7 @@ __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGrou
 
   const int nchunk = K / 32;                     // 16-byte code chunks (mxfp4 groups) per row
   const uint32_t RB = (uint32_t)nchunk * 16u;    // bytes per weight row
-  const int nwin = (nchunk + 3) / 4;             // 128-k windows
-  const int nblk = (nwin + 1) / 2;               // 256-k blocks
+  const int nblk = (nchunk + 3) / 4;             // 128-k blocks
   const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.w + (int64_t)e * N * (nchunk * 4), (uint32_t)N * RB);
   const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(a.scales + (int64_t)e * N * nchunk, (uint32_t)(N * nchunk));
 
@@ -97,32 +108,60 @@ __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGrou
     srow[t] = n < N ? (uint32_t)(n * nchunk) : kDeadOfs;
   }
 
-  // weights + scales of block b for tile t, window v (0/1) of the block
+  // weights + scales of block b for tile t.
   // Chunks past the end of a row read the next row's codes (or past the
   // matrix: zeros); they meet activations that are zero there, and fp4 codes
   // are finite, so they add exactly 0.  Their scales are not read (dead: 0,
   // a finite 2^-127), since the next row's could be NaN.
   // Blocks past the last are dead offsets: no memory traffic, zeros.
-  auto wload = [&](int b, int t, int v) -> u32x4 {
-    const uint32_t o = b < nblk ? wrow[t] + (uint32_t)((2 * b + v) * 4 + g) * 16u : kDeadOfs;
+  auto wload = [&](int b, int t) -> u32x4 {
+    const uint32_t o = b < nblk ? wrow[t] + (uint32_t)(b * 4 + g) * 16u : kDeadOfs;
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, o, 0, 2 /* nt */));
   };
-  auto sload = [&](int b, int t, int v) -> uint32_t {
-    const int c = (2 * b + v) * 4 + g;
+  auto sload = [&](int b, int t) -> uint32_t {
+    const int c = b * 4 + g;
     const uint32_t o = (srow[t] != kDeadOfs && c < nchunk) ? srow[t] + (uint32_t)c : kDeadOfs;
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(sr, o, 0, 0);
   };
+  // LDS layout of a block: row r at r * 256 bytes, its logical 16-byte chunk
+  // c at position c ^ (r & 15).  Wave load j of wave w fills rows
+  // 4 (w GQ_XI + j) .. +3: lane L writes row rr = 4 (w GQ_XI + j) + L / 16,
+  // position L % 16, so it fetches logical chunk (L % 16) ^ (rr & 15).
+  constexpr int GQ_VMEM = GQ_XI + 2 * GQ_T;  // vector-memory instructions per block and wave
 
   for (int r0 = lo; r0 < hi; r0 += GQ_MC) {
     const int cnt = min(GQ_MC, hi - r0);
     const int nat = (cnt + 15) / 16;  // live A tiles (uniform)
     const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.x + (int64_t)r0 * K, (uint32_t)cnt * (uint32_t)K * 2u);
-    auto xload = [&](int b, int i) -> u32x4 {
-      const int p = tid + i * GQ_NT;
-      const int m = p / (GQ_KB / 8), c = p % (GQ_KB / 8);
-      const int k = b * GQ_KB + 8 * c;
-      const uint32_t o = (m < cnt && k < K) ? (uint32_t)(m * K + k) * 2u : kDeadOfs;
-      return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, o, 0, 0));
+    // Per wave load j: the lane's byte offset at block 0 (dead past the
+    // chunk's rows), fixed for the whole chunk; block b adds b * 256 bytes
+    // through the scalar offset (the range check covers the vector offset
+    // only, and every live offset stays inside the chunk's rows: the one
+    // block reaching past K kills its chunks past K).  Address registers
+    // that are never rewritten keep the compiler from waiting on the ring.
+    uint32_t xo[GQ_XI];
+    int xk[GQ_XI];
+#pragma unroll
+    for (int j = 0; j < GQ_XI; j++) {
+      const int rr = 4 * (wave * GQ_XI + j) + (lane >> 4);
+      xk[j] = 8 * ((lane & 15) ^ (rr & 15));
+      xo[j] = rr < cnt ? (uint32_t)(rr * K + xk[j]) * 2u : kDeadOfs;
+    }
+    auto issue = [&](int b, int slot, u32x4 (&wn)[GQ_RING][GQ_T], uint32_t (&sn)[GQ_RING][GQ_T]) {
+      const bool tail = (b + 1) * GQ_KB > K;  // uniform
+#pragma unroll
+      for (int j = 0; j < GQ_XI; j++) {
+        uint32_t o = xo[j];
+        if (tail) o = b * GQ_KB + xk[j] < K ? o : kDeadOfs;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            xr, (__attribute__((address_space(3))) void*)(ring(slot) + (wave * GQ_XI + j) * 1024), 16, o,
+            b * GQ_KB * 2, 0, 0);
+      }
+#pragma unroll
+      for (int t = 0; t < GQ_T; t++) {
+        wn[slot][t] = wload(b, t);
+        sn[slot][t] = sload(b, t);
+      }
     };
 
     f32x4 acc[4][GQ_T];
@@ -131,72 +170,55 @@ __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGrou
 #pragma unroll
       for (int t = 0; t < GQ_T; t++) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // block 0 loads
-    u32x4 xn[GQ_XP];
+    u32x4 wn[GQ_RING][GQ_T];
+    uint32_t sn[GQ_RING][GQ_T];
 #pragma unroll
-    for (int i = 0; i < GQ_XP; i++) xn[i] = xload(0, i);
-    u32x4 wn[GQ_T][2];
-    uint32_t sn[GQ_T][2];
-#pragma unroll
-    for (int t = 0; t < GQ_T; t++)
-#pragma unroll
-      for (int v = 0; v < 2; v++) {
-        wn[t][v] = wload(0, t, v);
-        sn[t][v] = sload(0, t, v);
-      }
+    for (int d = 0; d < GQ_RING - 1; d++) issue(d, d, wn, sn);
 
-    for (int b = 0; b < nblk; b++) {
-      // stage block b's activations (the previous block's readers are done)
-      __syncthreads();
+    // Whole ring turns: the blocks past the last (at most GQ_RING - 1) still
+    // wait, synchronise and issue (dead offsets: no memory traffic) but skip
+    // their MFMAs.  A loop without an early exit keeps every ring slot in the
+    // same registers across the back edge; an exit inside the unrolled turn
+    // made the compiler copy the slots there, waiting for every load in
+    // flight once a turn.
+    for (int b0 = 0; b0 < nblk; b0 += GQ_RING) {
 #pragma unroll
-      for (int i = 0; i < GQ_XP; i++) {
-        const int p = tid + i * GQ_NT;
-        const int m = p / (GQ_KB / 8), c = p % (GQ_KB / 8);
-        *reinterpret_cast<u32x4*>(xl + m * GQ_XPITCH + 8 * c) = xn[i];
-      }
-      u32x4 wc[GQ_T][2];
-      uint32_t sc[GQ_T][2];
-#pragma unroll
-      for (int t = 0; t < GQ_T; t++)
-#pragma unroll
-        for (int v = 0; v < 2; v++) {
-          wc[t][v] = wn[t][v];
-          sc[t][v] = sn[t][v];
-        }
-      __syncthreads();
-      // next block's loads in flight while this one is used (past the last
-      // block every offset is dead: no branch, so no wait at a join)
-#pragma unroll
-      for (int i = 0; i < GQ_XP; i++) xn[i] = xload(b + 1, i);
-#pragma unroll
-      for (int t = 0; t < GQ_T; t++)
-#pragma unroll
-        for (int v = 0; v < 2; v++) {
-          wn[t][v] = wload(b + 1, t, v);
-          sn[t][v] = sload(b + 1, t, v);
-        }
-#pragma unroll
-      for (int v = 0; v < 2; v++) {
+      for (int d = 0; d < GQ_RING; d++) {
+        const int b = b0 + d;
+        // block b's loads were issued GQ_RING - 1 blocks ago: wait until at most
+        // the GQ_RING - 2 later blocks' instructions are outstanding, then all
+        // waves' activations of block b are in LDS and every wave is done
+        // with the buffer block b + GQ_RING - 1 refills
+        // (one statement: nothing moves between the wait and the barrier, and
+        // no LDS read moves across either; a plain barrier, because the
+        // workgroup fences of __syncthreads would also wait for the ring's
+        // younger activation loads)
+        static_assert(GQ_VMEM * (GQ_RING - 2) == 16, "the wait below counts 2 blocks of 8 instructions");
+        asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+        issue(b + GQ_RING - 1, (d + GQ_RING - 1) % GQ_RING, wn, sn);
+        if (b >= nblk) continue;  // workgroup-uniform
+        const unsigned char* xb = ring(d);
         // B operands: the lane's chunk widened with its group scale folded in
         bf16x8 B[GQ_T][4];
 #pragma unroll
         for (int t = 0; t < GQ_T; t++) {
-          const float s = e8m0_to_f32(sc[t][v]);
+          const float sc = e8m0_to_f32(sn[d][t]);
 #pragma unroll
           for (int q = 0; q < 4; q++) {
             uint32_t pr[4];
-            unpack_mxfp4_scaled(wc[t][v][q], s, pr);
+            unpack_mxfp4_scaled(wn[d][t][q], sc, pr);
             B[t][q] = as_bf16x8(pr);
           }
         }
 #pragma unroll
         for (int u = 0; u < 4; u++) {
           if (u < nat) {
-            // A: activation row 16u + (lane & 15), k = window base + 32 g + 8 q
-            const uint16_t* src = xl + (16 * u + nl) * GQ_XPITCH + v * 128 + g * 32;
+            // A: activation row 16u + nl, logical chunk 4g + q at position (4g + q) ^ nl
+            const unsigned char* row = xb + (16 * u + nl) * 256;
             bf16x8 A[4];
 #pragma unroll
-            for (int q = 0; q < 4; q++) A[q] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(src + 8 * q));
+            for (int q = 0; q < 4; q++)
+              A[q] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(row + 16 * ((4 * g + q) ^ nl)));
 #pragma unroll
             for (int t = 0; t < GQ_T; t++)
 #pragma unroll
@@ -205,6 +227,10 @@ __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGrou
         }
       }
     }
+    // the ring's loads past the last block (dead, zeros) land before the next
+    // chunk or the end of the workgroup reuses the buffers
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
 
     // ---- store: D row 4 g + i of A tile u is activation row 16u + 4g + i ------
 #pragma unroll
