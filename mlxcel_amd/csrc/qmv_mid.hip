@@ -166,7 +166,7 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
     for (int t = 0; t < MID_T; t++)
       wbuf[p][t] = __builtin_bit_cast(
           u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, woff[t] == kDeadOfs ? kDeadOfs : woff[t] + p * 64u, 0,
-                                                       2 /* nt */));
+                                                       0 /* default cache policy: faster than nt */));
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- 2. stage activations (AFF4 pair order), scales, a zero piece ---------
@@ -260,7 +260,7 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
         if (w + MID_P < MID_WIN)
           wbuf[w % MID_P][t] = __builtin_bit_cast(
               u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                         wr, woff[t] == kDeadOfs ? kDeadOfs : woff[t] + (uint32_t)(w + MID_P) * 64u, 0, 2 /* nt */));
+                         wr, woff[t] == kDeadOfs ? kDeadOfs : woff[t] + (uint32_t)(w + MID_P) * 64u, 0, 0));
         bf16x8 B[NQ];
         if constexpr (FMT == AFF4) {
 #pragma unroll
