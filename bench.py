@@ -23,7 +23,7 @@ overlays/cpu/mlx/backend/cpu/quantized.cpp:199-257).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
                        [--extras copy,sweep,qmm,gather,moe,e2e]
-       python bench.py --traffic-probe   (under rocprofv3 --pmc: copy calibration + gate launches)
+       python bench.py --traffic-probe   (under rocprofv3 --pmc: copy calibration + gate and gather launches)
 """
 from __future__ import annotations
 
@@ -615,8 +615,9 @@ def cpu_baseline(gate, budget_s=10.0):
 
 def traffic_probe():
     """Dispatches whose HBM counters calibrate and measure traffic: a device
-    copy of exactly 256 MiB (reads 256 MiB, writes 256 MiB), then the gate
-    projection over 5 distinct weight sets (33,067,008 algorithmic bytes each)."""
+    copy of exactly 256 MiB (reads 256 MiB, writes 256 MiB), the gate
+    projection over 5 distinct weight sets (33,067,008 algorithmic bytes each),
+    then 5 sorted mxfp4 MoE gathers at T=256 (gate/up, 299,704,320 bytes each)."""
     n = 256 << 20
     src = torch.empty(n, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
@@ -630,7 +631,22 @@ def traffic_probe():
     for g in gates:
         mq.quantized_matmul(x, *g, True, 64, 4, out=out)
     torch.cuda.synchronize()
-    print(json.dumps({"traffic_probe": {"copy_bytes": n, "gate_algorithmic_bytes": qmv_bytes(1, 14336, 4096, 4, 64)}}))
+    del gates
+    # the sorted MoE gather at T=256 (gate/up, 32 mxfp4 experts, top-4): 5
+    # launches of qmm_group_mxfp4_kernel over one weight set
+    E, H, I2, T = 32, 2880, 5760, 256
+    gu = make_mxfp4(E, I2, H, 60)
+    ids = np.stack([np.random.default_rng(5 + t).permutation(E)[:4] for t in range(T)]).reshape(-1)
+    order = np.argsort(ids, kind="stable")
+    rhs = torch.from_numpy(ids[order].astype(np.int32)).cuda()
+    xg = randn_bf16((T, 1, H), 11)[torch.from_numpy(order // 4).cuda()]
+    torch.cuda.synchronize()
+    for _ in range(5):
+        mq.gather_qmm(xg, *gu, None, None, rhs, True, 32, 4, "mxfp4", sorted_indices=True)
+    torch.cuda.synchronize()
+    gather_bytes = E * (I2 * H // 2 + I2 * H // 32) + T * 4 * (H + I2) * 2
+    print(json.dumps({"traffic_probe": {"copy_bytes": n, "gate_algorithmic_bytes": qmv_bytes(1, 14336, 4096, 4, 64),
+                                        "gather_t256_gate_up_algorithmic_bytes": gather_bytes}}))
 
 
 def main():
