@@ -16,7 +16,15 @@
  * mxfp4 table vs ldexp, f64 matmul of the dequantized weights (the
  * reference's own test method, cpu_qmm_accum_tests.rs:237-287), one-hot and
  * all-ones activations with exact closed forms, and quantizer invariants.
- * Unpinned beyond invariants: the exact bits of MLX's bf16 log2 inside the
+ * The affine quantizer is pinned by hand-worked groups (bf16-unrepresentable
+ * scales, rint ties of both parities in the codes and in q0, the
+ * |w_min| == |w_max| branch, a clamped extreme) and by an independent numpy
+ * float32 restatement on random data; the mxfp4 quantizer by hand-worked
+ * groups (exponent round-up, first-minimum ties) and an exact argmin check.
+ * tests/test_oracle_mutants.py plants one mistake at a time in a copy of this
+ * file (bf16 scale in the codes, roundf for rint, >= for >, no clamp, no
+ * snap, last-minimum ties, no exponent round-up) and requires the pins to
+ * reject each.  Unpinned beyond invariants: the exact bits of MLX's bf16 log2 inside the
  * mxfp4 graph quantizer (shown not to change the chosen exponent for normal
  * scales), and MLX's NaN sign on conversion.
  */

@@ -15,6 +15,14 @@ numpy/torch arithmetic:
     w_k = -c_k * d -> w_min edge, scale = +d, bias = -T d, code = T - c_k
     all-zero group      -> scale = bf16(-1e-7), bias = 0, code = 0
   with d a power of two, so every quantity is exact.
+* affine hand cases (quantized.cpp:1251-1303 worked by hand in float32 steps,
+  see HAND_CASES): groups whose float32 scale is not a bf16 value (so codes
+  computed from bf16(scale) differ), exact rint ties of either parity in the
+  codes and in q0 = rint(edge / scale), the |w_min| == |w_max| branch and a
+  clamped far extreme, at bits 2/4/6/8.
+* mxfp4 hand cases (ops.cpp:5364-5431 worked by hand): the e8m0 exponent is
+  ceil(log2(bf16(max|w| / 6))), the codes the first index of the minimum
+  distance in FP4_LUT order (ties between neighbours, +0 before -0).
 * dequant_d2: bf16(bf16(q * s) + b) evaluated with torch's bfloat16 ops (an
   independent implementation of MLX's bf16 arithmetic), on halfway cases.
 
@@ -75,6 +83,103 @@ def affine_ramps(bits: int, gs: int):
     return w, pack(codes, bits), scales, biases
 
 
+# Hand-worked groups of MLX's CPU affine quantizer (quantized.cpp:1251-1303).
+# T = 2^bits - 1; scale0 = max((w_max - w_min) / T, 1e-7), negated unless
+# |w_min| > |w_max|; edge = w_min if |w_min| > |w_max| else w_max;
+# q0 = rint(edge / scale0); if q0 != 0: scale = edge / q0, bias = edge;
+# code = clamp(rint((w - bias) / scale), 0, T); scale and bias are stored as
+# bf16 only after the codes are computed.  Each group is 32 values: the listed
+# head, whose first value is the edge, then the edge repeated (code 0).  Values: (bits, head, codes of the
+# head, bf16 bits of the stored scale, bf16 bits of the stored bias).
+HAND_CASES = {
+    # T=3, edge w_min=-0.75: scale0 = 0.75/3 = 0.25 exactly, q0 = rint(-3) = -3,
+    # scale = 0.25, bias = -0.75; (w+0.75)/0.25 = 0.5, 1.5, 2.5 at -0.625,
+    # -0.375, -0.125: rint ties to 0, 2, 2 (round-half-away would give 1, 2, 3).
+    "tie2": (2, [-0.75, 0.0, -0.625, -0.375, -0.125, -0.5, -0.25],
+             [0, 3, 0, 2, 2, 1, 2], 0x3E80, 0xBF40),
+    # T=15, |w_min| = 0 < w_max = 0.9375: edge = w_max, scale0 = -0.0625,
+    # q0 = rint(0.9375 / -0.0625) = -15, scale = -0.0625, bias = 0.9375;
+    # (0.9375 - w) * 16 = 0.5, 1.5, 2.5, 7.5, 14.5 -> 0, 2, 2, 8, 14.
+    "tie4": (4, [0.9375, 0.0, 0.90625, 0.84375, 0.78125, 0.46875, 0.03125],
+             [0, 15, 0, 2, 2, 8, 14], 0xBD80, 0x3F70),
+    # T=3, w_min=-1, w_max=0: scale0 = fl(1/3) = 0x3EAAAAAB, q0 = -3,
+    # scale = fl(-1/-3) = 0x3EAAAAAB, bias = -1.  w = -0.166015625:
+    # 0.833984375 / 0.33333334 = 2.50195 -> 3 (bf16(scale) = 0.333984375 would
+    # give 2.4970 -> 2).
+    "scale2": (2, [-1.0, 0.0, -0.166015625], [0, 3, 3], 0x3EAB, 0xBF80),
+    # T=15: scale = fl(1/15) = 0x3D888889 (q0 = rint(-14.999999) = -15).
+    # w = -0.03125: 0.96875 / 0.06666667 = 14.53125 -> 15 (bf16 scale
+    # 0.06689453125: 14.4817 -> 14).
+    "scale4": (4, [-1.0, 0.0, -0.03125], [0, 15, 15], 0x3D89, 0xBF80),
+    # T=63: scale = fl(1/63) = 0x3C820821 (q0 = rint(-62.999996) = -63), whose
+    # bf16 0x3C82 = 0.015869140625 is smaller.  w = -0.008056640625:
+    # 0.991943359375 / 0.015873017 = 62.4924 -> 62 (bf16 scale: 62.5080 -> 63).
+    "scale6": (6, [-1.0, 0.0, -0.008056640625], [0, 63, 62], 0x3C82, 0xBF80),
+    # T=255: scale = fl(1/255) = 0x3B808081.  w = 0: 1 / 0.003921569 = 254.99999
+    # -> 255 (bf16 scale 0.003936767578125: 254.0186 -> 254).
+    "scale8": (8, [-1.0, 0.0], [0, 255], 0x3B81, 0xBF80),
+    # |w_min| == |w_max| = 1 takes the w_max branch: scale0 = -fl(2/15) =
+    # -0.13333334, 1 / -0.13333334 = -7.4999995 -> q0 = -7, scale = fl(1/-7) =
+    # 0xBE124925, bias = 1; codes (1-w)/0.14285715: 1 -> 0, -1 -> 14, 0 -> 7.
+    "equal4": (4, [1.0, -1.0, 0.0], [0, 14, 7], 0xBE12, 0x3F80),
+    # rint tie in q0: w_min = -0.53125, w_max = 0.40625: scale0 = 0.9375/15 =
+    # 0.0625, edge/scale0 = -8.5 exactly -> q0 = -8 (not -9), scale = 0.06640625,
+    # bias = -0.53125; w_max: 0.9375 / 0.06640625 = 14.1176 -> 14 (q0 = -9 would
+    # give scale 0.0590278 and 15.88 -> 15).
+    "q0tie4": (4, [-0.53125, 0.40625], [0, 14], 0x3D88, 0xBF08),
+    # q0 tie of the other parity and a clamped far extreme: w_min = -0.59375,
+    # w_max = 0.34375: scale0 = 0.0625, edge/scale0 = -9.5 -> q0 = -10,
+    # scale = fl(0.059375) = 0x3D733333, bias = -0.59375; w_max:
+    # 0.9375 / 0.059375 = 15.79 -> 16, clamped to 15.
+    "clamp4": (4, [-0.59375, 0.34375], [0, 15], 0x3D73, 0xBF18),
+}
+
+
+def affine_hand_cases():
+    out = {}
+    for name, (bits, head, codes, s_bits, b_bits) in HAND_CASES.items():
+        w = np.full(32, head[0], np.float32)
+        w[: len(head)] = head
+        c = np.zeros(32, np.int64)
+        c[: len(codes)] = codes
+        wb = bf16_bits(w[None])
+        # every listed value is a bf16 value (the quantizer's input)
+        assert np.array_equal(torch.from_numpy(wb.astype(np.int16)).view(torch.bfloat16).float().numpy()[0], w)
+        out[f"hand_w_{name}_b{bits}"] = wb
+        out[f"hand_wq_{name}_b{bits}"] = pack(c[None], bits)
+        out[f"hand_s_{name}_b{bits}"] = np.array([[s_bits]], np.uint16)
+        out[f"hand_b_{name}_b{bits}"] = np.array([[b_bits]], np.uint16)
+    return out
+
+
+# mxfp4 graph quantizer (ops.cpp:5364-5431) by hand.  Group 0: max|w| = 6,
+# scale bf16(6/6) = 1, exponent 0 (byte 127), v = w.  Ties go to the first
+# index of FP4_LUT = [0, .5, 1, 1.5, 2, 3, 4, 6, -0, -.5, -1, -1.5, -2, -3, -4, -6]:
+# 5 -> 4 (index 6), 0.75 -> 0.5 (1), -0.25 -> +0 (0), -0 -> +0 (0), ...
+# Group 1: max|w| = 3, scale 0.5, exponent -1 (byte 126), v = 2w.
+# Group 2: max|w| = 7, scale bf16(7/6) = 1.1640625, exponent ceil(log2) = 1
+# (byte 128), v = w/2: 7 -> 3.5 -> 3 (index 5).
+MXFP4_HAND = [
+    ([6, -6, 5, -5, 0.25, -0.25, 0.75, -0.75, 2.5, -2.5, 3.5, -3.5, 1.25, -1.25, 1.75, -1.75,
+      0.10009765625, -0.10009765625, 0.0, -0.0, 4.5, -4.5, 5.5, -5.5, 0.5, -0.5, 1, -1, 3, -3, 6, 6],
+     [7, 15, 6, 14, 0, 0, 1, 9, 4, 12, 5, 13, 2, 10, 3, 11,
+      0, 0, 0, 0, 6, 14, 7, 15, 1, 9, 2, 10, 5, 13, 7, 7], 127),
+    ([3, -3, 2.5, -2.5, 0.125, -0.125, 0.375, -0.375, 1.25, -1.25, 1.75, -1.75] + [0.0] * 20,
+     [7, 15, 6, 14, 0, 0, 1, 9, 4, 12, 5, 13] + [0] * 20, 126),
+    ([7, -7, 5, -5, 1, -1, 0.5, -0.5] + [0.0] * 24,
+     [5, 13, 4, 12, 1, 9, 0, 0] + [0] * 24, 128),
+]
+
+
+def mxfp4_hand_cases():
+    w = np.array([g[0] for g in MXFP4_HAND], np.float32).reshape(1, -1)
+    codes = np.array([g[1] for g in MXFP4_HAND], np.int64).reshape(1, -1)
+    wb = bf16_bits(w)
+    assert np.array_equal(torch.from_numpy(wb.astype(np.int16)).view(torch.bfloat16).float().numpy(), w)
+    return {"mxfp4_hand_w": wb, "mxfp4_hand_wq": pack(codes, 4),
+            "mxfp4_hand_scales": np.array([[g[2] for g in MXFP4_HAND]], np.uint8)}
+
+
 def dequant_d2_cases():
     rng = np.random.default_rng(2248)
     n = 4096
@@ -98,6 +203,8 @@ def main():
             out[f"ramp_wq_b{bits}_g{gs}"] = wq
             out[f"ramp_s_b{bits}_g{gs}"] = s
             out[f"ramp_b_b{bits}_g{gs}"] = b
+    out.update(affine_hand_cases())
+    out.update(mxfp4_hand_cases())
     q, s, b, d2 = dequant_d2_cases()
     out.update(d2_q=q, d2_s=s, d2_b=b, d2_out=d2)
     np.savez_compressed(os.path.join(HERE, "kat.npz"), **out)

@@ -82,6 +82,28 @@ def test_affine_quantize_bitexact(bits, gs):
     np.testing.assert_array_equal(host_u16(kb), KAT[f"ramp_b_b{bits}_g{gs}"])
 
 
+HAND = sorted({k[len("hand_w_"):] for k in KAT.files if k.startswith("hand_w_")})
+
+
+@pytest.mark.parametrize("case", HAND)
+def test_affine_quantize_hand_cases(case):
+    # hand-worked groups: bf16-unrepresentable scales, rint ties, the
+    # |w_min| == |w_max| branch, a clamped far extreme
+    announce("quant_hand", case)
+    bits = int(case.rsplit("_b", 1)[1])
+    wq, s, b = mq.quantize(dev_bf16(KAT[f"hand_w_{case}"]), 32, bits)
+    np.testing.assert_array_equal(wq.cpu().numpy(), KAT[f"hand_wq_{case}"])
+    np.testing.assert_array_equal(host_u16(s), KAT[f"hand_s_{case}"])
+    np.testing.assert_array_equal(host_u16(b), KAT[f"hand_b_{case}"])
+
+
+def test_mxfp4_quantize_hand_cases():
+    announce("quant_mxfp4_hand")
+    wq, sc = mq.quantize(dev_bf16(KAT["mxfp4_hand_w"]), mode="mxfp4")
+    np.testing.assert_array_equal(wq.cpu().numpy(), KAT["mxfp4_hand_wq"])
+    np.testing.assert_array_equal(sc.cpu().numpy(), KAT["mxfp4_hand_scales"])
+
+
 def test_mxfp4_quantize_bitexact():
     announce("quant_mxfp4")
     w = orc.normal_bf16((256, 2880), 0.02, 540)

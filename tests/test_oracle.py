@@ -86,6 +86,63 @@ def test_affine_quantize_invariants(orc, bits, gs):
     assert np.all(err <= np.abs(sf) * (1.5 + 2 * qmax * 2.0 ** -9) + np.abs(wf) * 2.0 ** -8 + 1e-12)
 
 
+HAND = sorted({k[len("hand_w_"):] for k in np.load(GOLD).files if k.startswith("hand_w_")})
+
+
+@pytest.mark.parametrize("case", HAND)
+def test_affine_quantize_hand_cases(orc, kat, case):
+    # worked by hand in float32 steps (tests/golden/make_golden.py HAND_CASES):
+    # bf16-unrepresentable scales, rint ties of both parities in the codes and
+    # in q0, the |w_min| == |w_max| branch, a clamped far extreme
+    bits = int(case.rsplit("_b", 1)[1])
+    wq, s, b = orc.affine_quantize(kat[f"hand_w_{case}"], 32, bits)
+    np.testing.assert_array_equal(codes_bytestream(wq, bits, 32), codes_bytestream(kat[f"hand_wq_{case}"], bits, 32))
+    np.testing.assert_array_equal(s, kat[f"hand_s_{case}"])
+    np.testing.assert_array_equal(b, kat[f"hand_b_{case}"])
+
+
+def numpy_affine_quantize(wf, gs, bits):
+    """MLX's CPU affine quantizer (quantized.cpp:1251-1303) restated with
+    vectorised numpy float32 arithmetic (IEEE division, np.rint = round half to
+    even, like std::rint): codes, float32 scale and bias per group."""
+    g = wf.reshape(-1, gs).astype(np.float32)
+    T = np.float32((1 << bits) - 1)
+    mn, mx = g.min(1), g.max(1)
+    mask = np.abs(mn) > np.abs(mx)
+    s0 = np.maximum((mx - mn) / T, np.float32(1e-7))
+    s = np.where(mask, s0, -s0)
+    edge = np.where(mask, mn, mx)
+    q0 = np.rint(edge / s)
+    nz = q0 != 0
+    s = np.where(nz, edge / np.where(nz, q0, np.float32(1)), s).astype(np.float32)
+    b = np.where(nz, edge, np.float32(0)).astype(np.float32)
+    codes = np.clip(np.rint((g - b[:, None]) / s[:, None]), 0, T)
+    return codes.astype(np.uint32).reshape(wf.shape), s, b
+
+
+@pytest.mark.parametrize("bits", [2, 4, 6, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_affine_quantize_matches_numpy_restatement(orc, bits, gs):
+    # random bf16 groups at scales from 1e-4 to 1e2, all-positive and
+    # all-negative groups, constant and all-zero groups
+    rng = np.random.default_rng(100 * bits + gs)
+    rows, K = 48, 512
+    x = rng.standard_normal((rows, K)).astype(np.float32)
+    x *= (10.0 ** rng.uniform(-4, 2, (rows, 1))).astype(np.float32)
+    x[8:12] = np.abs(x[8:12])
+    x[12:16] = -np.abs(x[12:16])
+    x[16, :gs] = 0.375
+    x[17, :gs] = 0.0
+    x[18, :gs] = -x[18, 0]
+    w = bf16_from_torch(x)
+    wf = torch_from_bits(w).float().numpy()
+    codes, s, b = numpy_affine_quantize(wf, gs, bits)
+    wq, so, bo = orc.affine_quantize(w, gs, bits)
+    np.testing.assert_array_equal(codes_bytestream(wq, bits, K), codes)
+    np.testing.assert_array_equal(so.reshape(-1), bf16_from_torch(s))
+    np.testing.assert_array_equal(bo.reshape(-1), bf16_from_torch(b))
+
+
 def test_affine_packing_is_little_endian_bitstream(orc):
     w = orc.normal_bf16((8, 256), 0.02, 11)
     for bits in (2, 4, 6, 8):
@@ -173,12 +230,21 @@ def test_mxfp4_quantize_nearest_code_and_roundtrip(orc):
     v = wf / scale
     codes = codes_bytestream(wq, 4, 2880).reshape(64, -1, 32)
     lut = np.array([0, .5, 1, 1.5, 2, 3, 4, 6, -0., -.5, -1, -1.5, -2, -3, -4, -6])
+    # v = w / 2^e is exact, and so is every |v - lut| in float64: the code is
+    # the first index of the exact minimum distance (argmin order)
     dist = np.abs(v[..., None] - lut)
-    chosen = np.take_along_axis(dist, codes[..., None].astype(np.int64), -1)[..., 0]
-    assert np.all(chosen <= dist.min(-1) * (1 + 2 ** -7) + 1e-30)
-    assert np.all(np.abs(v).max(-1) <= 6.0 * (1 + 2 ** -7))  # round-up keeps the block maximum representable
+    np.testing.assert_array_equal(codes, dist.argmin(-1))
+    assert np.all(np.abs(v).max(-1) <= 6.0)  # round-up keeps the block maximum representable
     d = orc.bf16_to_f32(orc.mxfp4_dequantize(wq, sc)).reshape(64, -1, 32)
     np.testing.assert_array_equal(d, (lut[codes.astype(np.int64)] * scale).astype(np.float32))
+
+
+def test_mxfp4_quantize_hand_cases(orc, kat):
+    # tests/golden/make_golden.py MXFP4_HAND: exponents ceil(log2(max|w|/6)),
+    # ties to the first LUT index (+0 before -0)
+    wq, sc = orc.mxfp4_quantize(kat["mxfp4_hand_w"])
+    np.testing.assert_array_equal(codes_bytestream(wq, 4, 96), codes_bytestream(kat["mxfp4_hand_wq"], 4, 96))
+    np.testing.assert_array_equal(sc, kat["mxfp4_hand_scales"])
 
 
 def test_mxfp4_quantize_zero_group(orc):
