@@ -44,6 +44,7 @@
 #define MLXQ_H
 
 #include <stdbool.h>
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -86,6 +87,34 @@ typedef struct mlxq_array {
   int64_t shape[MLXQ_MAX_DIMS];
   int64_t strides[MLXQ_MAX_DIMS];
 } mlxq_array;
+
+/* Device scratch.  Calls that need scratch (split-K partials of the 5-16-row
+ * decode kernel and of the prefill GEMM, gather index lists, the fused MoE's
+ * activations) use a per-(device, stream) workspace that grows on demand.  A
+ * grown workspace never frees the buffer it replaces (a HIP graph captured
+ * earlier may still use it); no call synchronizes a stream, and a call that
+ * would have to grow the workspace of a stream under capture returns
+ * MLXQ_ENOMEM instead of allocating.  Callers that capture either run each
+ * call shape once before the capture or reserve the workspace up front. */
+
+/* Grows `stream`'s workspace on the current device to at least `bytes`.  No
+ * counterpart in the reference (MLX allocates inside each eval). */
+mlxq_status mlxq_workspace_reserve(size_t bytes, void* stream);
+
+/* Bytes of device memory held by the workspaces (current and replaced
+ * buffers), like the reference's get_cache_memory (lib.rs:2720). */
+size_t mlxq_get_cache_memory(void);
+
+/* Synchronizes every device that holds a workspace and frees all workspace
+ * buffers, like the reference's clear_memory_cache (lib.rs:2666).  HIP graphs
+ * captured earlier that ran library calls must not be replayed afterwards. */
+mlxq_status mlxq_clear_cache(void);
+
+/* The MLXQ_* environment switches (forced kernels, tile shapes: A/B
+ * measurement and tests only) are read once, at the first call; this re-reads
+ * them.  No counterpart in the reference, which latches its knobs in function
+ * statics (rocm/quantized/qmm.hip:392-452). */
+void mlxq_reload_options(void);
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* mlxq_last_error(void);
@@ -152,10 +181,13 @@ mlxq_status mlxq_quantized_matmul_shape(const mlxq_array* x, const mlxq_array* w
  * shape, as mlx::core::gather_qmm (ops.cpp:5841-5948): out.shape =
  * broadcast(lhs, rhs).shape + [x.shape[-2], N].  NULL lhs/rhs default to
  * arange over the batch dims of x/w; both NULL is quantized_matmul.
- * `sorted_indices` is the reference's promise that rhs is non-decreasing in
- * the flat order of the broadcast batch; as in the reference's expert-run
- * kernels (rocm/quantized/qmm.hip:4705-4740, found by binary search) the
- * result is unspecified when the promise is false.  Sorted and unsorted
+ * `sorted_indices` is the reference's promise that rhs, cast to uint32 as
+ * the reference casts indices (ops.cpp:100), is non-decreasing in the flat
+ * order of the broadcast batch; as in the reference's expert-run kernels
+ * (rocm/quantized/qmm.hip:4705-4740, found by binary search) the result is
+ * unspecified when the promise is false (the sorted mxfp4 route then leaves
+ * some output rows unwritten: negative int32 values, for instance, are not
+ * sorted after the cast).  Sorted and unsorted
  * routes differ only in summation order (same tolerance).  `global_scale` (nvfp4 only in the reference) must be
  * NULL.  Index arrays may be any integer dtype and any strides
  * (broadcasting included). */

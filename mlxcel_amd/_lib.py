@@ -44,6 +44,10 @@ SYMBOLS = (
     "mlxq_quantize",
     "mlxq_fused_moe_expert",
     "mlxq_fused_moe_geglu",
+    "mlxq_workspace_reserve",
+    "mlxq_get_cache_memory",
+    "mlxq_clear_cache",
+    "mlxq_reload_options",
 )
 
 _lib = None
@@ -85,8 +89,14 @@ def load() -> ctypes.CDLL:
     lib.mlxq_quantize.argtypes = [A, I32, I32, S, A, A, A, P]
     lib.mlxq_fused_moe_expert.argtypes = [A] * 12 + [I32] * 6 + [A, P]
     lib.mlxq_fused_moe_geglu.argtypes = [A] * 12 + [I32] * 6 + [A, P]
+    lib.mlxq_workspace_reserve.argtypes = [ctypes.c_size_t, P]
+    lib.mlxq_get_cache_memory.argtypes = []
+    lib.mlxq_clear_cache.argtypes = []
+    lib.mlxq_reload_options.argtypes = []
     for name in SYMBOLS[2:]:
         getattr(lib, name).restype = ctypes.c_int
+    lib.mlxq_get_cache_memory.restype = ctypes.c_size_t
+    lib.mlxq_reload_options.restype = None
     _lib = lib
     return lib
 

@@ -46,6 +46,7 @@ SOURCES = {
     "qmm.hip": [],
     "moe.hip": [],
     "bias.hip": [],
+    "scratch.hip": [],
     "dequant.hip": ["-ffp-contract=off"],
 }
 

@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 #include <cstdarg>
 #include <cstring>
@@ -415,9 +416,17 @@ struct DevInfo {
 std::mutex g_mu;
 std::map<int, DevInfo> g_dev;
 
+// Per-(device, stream) scratch.  A buffer is never freed while the library
+// may still use it: when a call needs more, a larger buffer replaces it and
+// the old one moves to `retired`, which only mlxq_clear_cache() frees (a HIP
+// graph captured earlier, or a launch another thread has not issued yet, may
+// still hold the old pointer).  No call synchronizes a stream, and none
+// allocates while its stream is being captured.
 struct Workspace {
   void* data = nullptr;
   size_t bytes = 0;
+  std::vector<void*> retired;
+  size_t retired_bytes = 0;
 };
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
@@ -438,41 +447,118 @@ DevInfo device_info(int dev) {
   return d;
 }
 
-// Scratch that stays allocated for the stream's lifetime; grows (after a
-// stream synchronize, so no queued kernel still uses the old buffer) when a
-// call needs more.
-Workspace& workspace(int dev, hipStream_t stream, size_t bytes) {
-  std::lock_guard<std::mutex> lk(g_mu);
-  Workspace& w = g_ws[{dev, stream}];
-  if (w.bytes < bytes) {
-    if (w.data) {
-      hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
-      hip_check(hipFree(w.data), "hipFree");
-      w.data = nullptr;
-      w.bytes = 0;
-    }
-    size_t sz = 1 << 20;
-    while (sz < bytes) sz <<= 1;
-    if (hipMalloc(&w.data, sz) != hipSuccess) fail(MLXQ_ENOMEM, "[mlxq] workspace allocation failed");
-    w.bytes = sz;
-  }
-  return w;
+bool stream_capturing(hipStream_t stream) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  hip_check(hipStreamIsCapturing(stream, &st), "hipStreamIsCapturing");
+  return st != hipStreamCaptureStatusNone;
 }
 
-// A/B overrides for the skinny kernel's shape (waves per workgroup, K-steps
-// per wave); unset or invalid values keep the defaults.
+// Grows the stream's workspace to at least `bytes` (a power of two from
+// 1 MiB); the caller must not be capturing `stream`.
+void* grow_workspace(Workspace& w, size_t bytes) {
+  size_t sz = 1 << 20;
+  while (sz < bytes) sz <<= 1;
+  void* p = nullptr;
+  if (hipMalloc(&p, sz) != hipSuccess) {
+    (void)hipGetLastError();
+    fail(MLXQ_ENOMEM, "[mlxq] workspace allocation of " + std::to_string(sz) + " bytes failed");
+  }
+  if (w.data) {
+    w.retired.push_back(w.data);
+    w.retired_bytes += w.bytes;
+  }
+  w.data = p;
+  w.bytes = sz;
+  return p;
+}
+
+// Scratch source of one call: the per-stream workspace, or a fixed buffer
+// (the no-allocation entry point's device array) of at most `max` bytes.
+struct ScratchSrc {
+  void* fixed = nullptr;
+  size_t max = 0;
+};
+
+void* workspace(int dev, hipStream_t stream, size_t bytes, const ScratchSrc& src = ScratchSrc{}) {
+  if (src.fixed) {
+    if (bytes > src.max)
+      fail(MLXQ_ENOMEM, "[mlxq] this call needs " + std::to_string(bytes) +
+                            " bytes of scratch; the no-allocation entry point has " + std::to_string(src.max));
+    return src.fixed;
+  }
+  std::lock_guard<std::mutex> lk(g_mu);
+  Workspace& w = g_ws[{dev, stream}];
+  if (w.bytes >= bytes) return w.data;
+  if (stream_capturing(stream))
+    fail(MLXQ_ENOMEM, "[mlxq] this call needs " + std::to_string(bytes) + " bytes of workspace on a stream that is "
+                      "being captured (which holds " + std::to_string(w.bytes) +
+                      "); run it once before the capture or reserve with mlxq_workspace_reserve");
+  return grow_workspace(w, bytes);
+}
+
+// Rows from which a dense quantized_matmul runs the prefill GEMM (qmm.hip):
+// at 9-16 rows its 128 x 128 tiles already beat the skinny kernels on
+// MI355X (MLXQ_QMM_MIN_ROWS overrides, for tests and measurements).
+constexpr int kQmmMinRows = 9;
+
+// Environment switches for A/B measurement and tests, latched at the first
+// call (mlxq_reload_options re-reads them).
+struct Knobs {
+  int qmv_nw = 0, qmv_tk = 0, qmv_r = 0, b4_rg = 0, b4_cpw = 0;
+  int qmm_min_rows = kQmmMinRows, qmm_tile = -1, qmm_ksplit = 0;
+  int qmv_mid = 1, qmv_multi = 1;
+  int gather_sorted = 1, gather_group = -1, gather_runs = 1, gather_direct = 1;
+  std::string qmv_kernel;  // "", "rs", "b4", "mid", "fr", "mfma"
+};
+
 int env_int(const char* name, int dflt) {
   const char* v = std::getenv(name);
   if (!v || !*v) return dflt;
   return std::atoi(v);
 }
 
+const Knobs* read_knobs() {
+  Knobs* k = new Knobs;
+  k->qmv_nw = env_int("MLXQ_QMV_NW", 0);
+  k->qmv_tk = env_int("MLXQ_QMV_TK", 0);
+  k->qmv_r = env_int("MLXQ_QMV_R", 0);
+  k->b4_rg = env_int("MLXQ_QMV_B4_RG", 0);
+  k->b4_cpw = env_int("MLXQ_QMV_B4_CPW", 0);
+  k->qmm_min_rows = env_int("MLXQ_QMM_MIN_ROWS", kQmmMinRows);
+  k->qmm_tile = env_int("MLXQ_QMM_TILE", -1);
+  k->qmm_ksplit = env_int("MLXQ_QMM_KSPLIT", 0);
+  k->qmv_mid = env_int("MLXQ_QMV_MID", 1);
+  k->qmv_multi = env_int("MLXQ_QMV_MULTI", 1);
+  k->gather_sorted = env_int("MLXQ_GATHER_SORTED", 1);
+  k->gather_group = env_int("MLXQ_GATHER_GROUP", -1);
+  k->gather_runs = env_int("MLXQ_GATHER_RUNS", 1);
+  k->gather_direct = env_int("MLXQ_GATHER_DIRECT", 1);
+  const char* v = std::getenv("MLXQ_QMV_KERNEL");
+  k->qmv_kernel = v ? v : "";
+  return k;
+}
+
+// Replaced snapshots are kept (a concurrent call may still read one).
+std::atomic<const Knobs*> g_knobs{nullptr};
+
+const Knobs& knobs() {
+  const Knobs* k = g_knobs.load(std::memory_order_acquire);
+  if (k) return *k;
+  const Knobs* fresh = read_knobs();
+  if (!g_knobs.compare_exchange_strong(k, fresh, std::memory_order_acq_rel)) {
+    delete fresh;
+    return *k;
+  }
+  return *fresh;
+}
+
 // Default (waves per workgroup, loads in flight) by shape.
 void qmv_shape_choice(int64_t N, int64_t K, int& nw, int& p) {
   (void)N;
   (void)K;
-  nw = env_int("MLXQ_QMV_NW", 0);
-  p = env_int("MLXQ_QMV_TK", 0);
+  // A/B overrides (waves per workgroup, K-steps per wave); 0 keeps the defaults
+  nw = knobs().qmv_nw;
+  p = knobs().qmv_tk;
 }
 
 // Broadcast strides of an index array (or of the default arange over `dshape`)
@@ -578,10 +664,6 @@ void require_dtype(const mlxq_array* a, int dt, const char* name, const char* ta
 // tests and measurements.
 enum class Skinny { FR, RS, B4, MFMA };
 
-// Rows from which a dense quantized_matmul runs the prefill GEMM (qmm.hip):
-// at 9-16 rows its 128 x 128 tiles already beat the skinny kernels on
-// MI355X (MLXQ_QMM_MIN_ROWS overrides, for tests and measurements).
-constexpr int kQmmMinRows = 9;
 // The mid-size decode kernel takes 5-16 rows (affine), where it beats the
 // block-MFMA, skinny-MFMA and prefill kernels (MI355X, Llama-3-8B MLP shapes:
 // 4-bit gate M=8 13.4 us vs 17.7, down M=8 16.5 us vs 33.6, gate M=16 22 us
@@ -594,11 +676,11 @@ constexpr int kMidMinRows = 5;
 // otherwise.  (Above 8 rows a dense quantized_matmul goes to the prefill
 // GEMM instead, see kQmmMinRows.)
 Skinny skinny_choice(int rows, int fmt = mlxq::AFF4, int64_t K = 0) {
-  const char* k = std::getenv("MLXQ_QMV_KERNEL");
-  if (k && std::strcmp(k, "mfma") == 0) return Skinny::MFMA;
-  if (k && std::strcmp(k, "rs") == 0) return rows <= 4 ? Skinny::RS : Skinny::MFMA;
-  if (k && std::strcmp(k, "fr") == 0) return rows <= 2 ? Skinny::FR : Skinny::MFMA;
-  if (k && std::strcmp(k, "b4") == 0) return rows <= 16 ? Skinny::B4 : Skinny::MFMA;
+  const std::string& k = knobs().qmv_kernel;
+  if (k == "mfma") return Skinny::MFMA;
+  if (k == "rs") return rows <= 4 ? Skinny::RS : Skinny::MFMA;
+  if (k == "fr") return rows <= 2 ? Skinny::FR : Skinny::MFMA;
+  if (k == "b4") return rows <= 16 ? Skinny::B4 : Skinny::MFMA;
   // 3-4 rows over short affine rows (one 16-piece chunk per wave): the
   // block-MFMA kernel with 32 weight rows per workgroup is ~4% faster
   if (rows >= 3 && rows <= 4 && fmt != mlxq::MXFP4 && K * (fmt == mlxq::AFF8 ? 8 : 4) <= 16384) return Skinny::B4;
@@ -612,10 +694,10 @@ Skinny skinny_choice(int rows, int fmt = mlxq::AFF4, int64_t K = 0) {
 // another MLXQ_QMV_KERNEL value or MLXQ_QMV_MID=0 keeps it off.
 bool use_mid(int rows, int fmt, int64_t K) {
   if (fmt == mlxq::MXFP4 || rows > 16) return false;
-  const char* k = std::getenv("MLXQ_QMV_KERNEL");
-  if (k && std::strcmp(k, "mid") == 0) return true;
-  if (k && *k) return false;
-  if (env_int("MLXQ_QMV_MID", 1) == 0) return false;
+  const std::string& k = knobs().qmv_kernel;
+  if (k == "mid") return true;
+  if (!k.empty()) return false;
+  if (knobs().qmv_mid == 0) return false;
   (void)K;
   return rows >= kMidMinRows;
 }
@@ -625,7 +707,7 @@ bool use_mid(int rows, int fmt, int64_t K) {
 bool try_fr_rs(const QmmSpec& sp, const mlxq::QmvArgs& a, int nseg, int rows, hipStream_t stream) {
   const int fmt = fmt_of(sp.mode, sp.bits);
   Skinny c = skinny_choice(rows, fmt, sp.K);
-  const int r_req = env_int("MLXQ_QMV_R", 0);
+  const int r_req = knobs().qmv_r;
   if (c == Skinny::FR) {
     const mlxq::QmvFrPlan p = mlxq::qmv_fr_plan(fmt, sp.gs, sp.N, sp.K, rows, r_req);
     if (p.ok) {
@@ -636,8 +718,8 @@ bool try_fr_rs(const QmmSpec& sp, const mlxq::QmvArgs& a, int nseg, int rows, hi
     c = Skinny::RS;
   }
   if (c == Skinny::B4) {
-    const mlxq::QmvB4Plan p = mlxq::qmv_b4_plan(fmt, sp.gs, sp.N, sp.K, rows, env_int("MLXQ_QMV_B4_RG", 0),
-                                                env_int("MLXQ_QMV_B4_CPW", 0));
+    const mlxq::QmvB4Plan p = mlxq::qmv_b4_plan(fmt, sp.gs, sp.N, sp.K, rows, knobs().b4_rg,
+                                                knobs().b4_cpw);
     if (p.ok) {
       if (nseg > 65535) unsupported("too many segments for one launch");
       hip_check(mlxq::qmv_b4_launch(fmt, sp.gs, a, nseg, p, stream), "qmv launch");
@@ -657,7 +739,8 @@ bool try_fr_rs(const QmmSpec& sp, const mlxq::QmvArgs& a, int nseg, int rows, hi
 }
 
 // Launch the skinny kernel over `nseg` segments of at most `max_rows` rows.
-void run_qmv(const QmmSpec& sp, mlxq::QmvArgs a, int nseg, int max_rows, hipStream_t stream) {
+void run_qmv(const QmmSpec& sp, mlxq::QmvArgs a, int nseg, int max_rows, hipStream_t stream,
+             const ScratchSrc& ss) {
   if (max_rows <= 16 && try_fr_rs(sp, a, nseg, max_rows, stream)) return;
   const int fmt = fmt_of(sp.mode, sp.bits);
   const int dev = current_device();
@@ -671,7 +754,7 @@ void run_qmv(const QmmSpec& sp, mlxq::QmvArgs a, int nseg, int max_rows, hipStre
   a.kst_per_wg = p.kst_per_wg;
   if (p.ks > 1) {
     const size_t ws_bytes = (size_t)p.ks * a.out_rows * sp.N * sizeof(float);
-    a.ws = reinterpret_cast<float*>(workspace(dev, stream, ws_bytes).data);
+    a.ws = reinterpret_cast<float*>(workspace(dev, stream, ws_bytes, ss));
   }
   if (nseg > 65535) unsupported("too many segments for one launch");
   hip_check(mlxq::qmv_launch(fmt, sp.gs, a, nseg, p, stream), "qmv launch");
@@ -699,7 +782,8 @@ QmmSpec check_quantized_matmul(const mlxq_array* x, const mlxq_array* w, const m
 
 // Enqueues one checked quantized_matmul call.
 void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
-                          const mlxq_array* biases, mlxq_array* out, hipStream_t stream) {
+                          const mlxq_array* biases, mlxq_array* out, hipStream_t stream,
+                          const ScratchSrc& ss = ScratchSrc{}) {
   const int64_t rows_total = View{out}.size() / std::max<int64_t>(sp.N, 1);
   if (rows_total == 0 || sp.N == 0) return;
   if (sp.K == 0) unsupported("quantized_matmul: K == 0");
@@ -735,18 +819,17 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
       m.gs_shift = shift;
       m.ks = mp.ks;
       if (mp.ks > 1)
-        m.ws = reinterpret_cast<float*>(
-            workspace(dev, stream, (size_t)mp.ks * rows_total * sp.N * sizeof(float)).data);
+        m.ws = reinterpret_cast<float*>(workspace(dev, stream, (size_t)mp.ks * rows_total * sp.N * sizeof(float), ss));
       hip_check(mlxq::qmv_mid_launch(fmt, m, mp, stream), "qmv_mid launch");
       return;
     }
   }
-  if (wv.ndim() == 2 && rows_total >= env_int("MLXQ_QMM_MIN_ROWS", kQmmMinRows)) {
+  if (wv.ndim() == 2 && rows_total >= knobs().qmm_min_rows) {
     // prefill: one GEMM over all rows (every leading dim of x folds into rows)
     const int dev = current_device();
     // MLXQ_QMM_TILE / MLXQ_QMM_KSPLIT: A/B overrides of the tile shape and K split
     const mlxq::QmmPlan qp = mlxq::qmm_plan(fmt, sp.gs, rows_total, sp.N, sp.K, device_info(dev).cus,
-                                            env_int("MLXQ_QMM_TILE", -1), env_int("MLXQ_QMM_KSPLIT", 0));
+                                            knobs().qmm_tile, knobs().qmm_ksplit);
     if (qp.ok) {
       mlxq::QmmArgs q{};
       q.x = a.x;
@@ -765,7 +848,7 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
       q.ksteps_per_split = qp.ksteps_per_split;
       if (qp.ksplit > 1)
         q.ws = reinterpret_cast<float*>(
-            workspace(dev, stream, (size_t)qp.ksplit * rows_total * sp.N * sizeof(float)).data);
+            workspace(dev, stream, (size_t)qp.ksplit * rows_total * sp.N * sizeof(float), ss));
       hip_check(mlxq::qmm_launch(fmt, q, qp, stream), "qmm launch");
       return;
     }
@@ -788,7 +871,7 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
     a.total_rows = (int)rows_total;
     a.X = (int)((rows_total + rps - 1) / rps);
     const int nseg = a.X;
-    run_qmv(sp, a, nseg, rps, stream);
+    run_qmv(sp, a, nseg, rps, stream, ss);
   } else {
     // batched weights: each batch element is a segment of x.shape[-2] rows
     const Shape wsh = wv.shape(), xsh = xv.shape();
@@ -807,7 +890,7 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
     a.s_expert_stride = View{scales}.dim(-2) * View{scales}.dim(-1);
     a.rps = (int)M;
     a.total_rows = (int)rows_total;
-    run_qmv(sp, a, (int)nb, (int)M, stream);
+    run_qmv(sp, a, (int)nb, (int)M, stream, ss);
   }
 }
 
@@ -837,6 +920,52 @@ mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w, cons
     const QmmSpec sp =
         check_quantized_matmul(x, w, scales, biases, transpose, group_size, bits, mode, out, "quantized_matmul");
     run_quantized_matmul(sp, x, w, scales, biases, out, reinterpret_cast<hipStream_t>(stream_));
+  });
+}
+
+void mlxq_reload_options(void) {
+  // the previous snapshot stays allocated: a concurrent call may still read it
+  g_knobs.store(read_knobs(), std::memory_order_release);
+}
+
+mlxq_status mlxq_workspace_reserve(size_t bytes, void* stream_) {
+  return guarded([&] {
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    const int dev = current_device();
+    std::lock_guard<std::mutex> lk(g_mu);
+    Workspace& w = g_ws[{dev, stream}];
+    if (w.bytes >= bytes) return;
+    if (stream_capturing(stream)) unsupported("mlxq_workspace_reserve: the stream is being captured");
+    grow_workspace(w, bytes);
+  });
+}
+
+size_t mlxq_get_cache_memory(void) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  size_t total = 0;
+  for (auto& kv : g_ws) total += kv.second.bytes + kv.second.retired_bytes;
+  return total;
+}
+
+mlxq_status mlxq_clear_cache(void) {
+  return guarded([&] {
+    std::lock_guard<std::mutex> lk(g_mu);
+    int cur = 0;
+    hip_check(hipGetDevice(&cur), "hipGetDevice");
+    std::map<int, bool> synced;
+    for (auto& kv : g_ws) {
+      const int dev = kv.first.first;
+      if (!synced[dev]) {
+        hip_check(hipSetDevice(dev), "hipSetDevice");
+        hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        synced[dev] = true;
+      }
+      hip_check(hipSetDevice(dev), "hipSetDevice");
+      for (void* p : kv.second.retired) hip_check(hipFree(p), "hipFree");
+      if (kv.second.data) hip_check(hipFree(kv.second.data), "hipFree");
+    }
+    g_ws.clear();
+    hip_check(hipSetDevice(cur), "hipSetDevice");
   });
 }
 
@@ -915,16 +1044,16 @@ mlxq_status mlxq_quantized_matmul_multi(const mlxq_array* x, int32_t n, const ml
     // bit.  Otherwise the calls run one after another.
     const int fmt = fmt_of(sp[0].mode, sp[0].bits);
     const int64_t rows = View{out[0]}.size() / std::max<int64_t>(sp[0].N, 1);
-    bool fused = n > 1 && sp[0].K > 0 && rows >= 1 && rows < env_int("MLXQ_QMM_MIN_ROWS", kQmmMinRows) &&
+    bool fused = n > 1 && sp[0].K > 0 && rows >= 1 && rows < knobs().qmm_min_rows &&
                  rows <= mlxq::qmv_max_rows(fmt, sp[0].gs) && !use_mid((int)rows, fmt, sp[0].K) &&
-                 skinny_choice((int)rows, fmt, sp[0].K) == Skinny::RS && env_int("MLXQ_QMV_MULTI", 1) != 0;
+                 skinny_choice((int)rows, fmt, sp[0].K) == Skinny::RS && knobs().qmv_multi != 0;
     mlxq::QmvRsPlan plan{};
     mlxq::QmvMulti mp{};
     mp.n = n;
     for (int i = 0; i < n && fused; i++) {
       if (sp[i].N == 0) fused = false;
       const mlxq::QmvRsPlan p =
-          mlxq::qmv_rs_plan(fmt, sp[i].gs, sp[i].N, sp[i].K, (int)rows, env_int("MLXQ_QMV_R", 0));
+          mlxq::qmv_rs_plan(fmt, sp[i].gs, sp[i].N, sp[i].K, (int)rows, knobs().qmv_r);
       if (!p.ok || (i > 0 && (p.mr != plan.mr || p.r != plan.r || p.cpw != plan.cpw || p.nw != plan.nw ||
                               p.lds != plan.lds)))
         fused = false;
@@ -976,7 +1105,8 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq
                             const mlxq_array* biases, const mlxq_array* lhs_indices, const mlxq_array* rhs_indices,
                             bool transpose, int32_t group_size, int32_t bits, bool sorted_indices, const char* mode,
                             const mlxq_array* global_scale, mlxq_array* out, void* stream_) {
-  // sorted_indices only selects a faster launch shape; results never depend on it
+  // sorted_indices selects the routes that rely on rhs being non-decreasing
+  // (after the uint32 cast); with a false promise their rows are unspecified
   if (!lhs_indices && !rhs_indices) {
     if (global_scale) {
       g_last_error = "[gather_qmm] Global scale is not supported without indices.";
@@ -1040,7 +1170,7 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq
     // rows per expert run as segments of up to 4 entries (below).  Like the reference's sorted route, it
     // relies on sorted_indices being true.  MLXQ_GATHER_SORTED=0 turns it off.
     if (sorted_indices && M == 1 && fmt == mlxq::MXFP4 && B >= 32 && B >= 4 * E &&
-        env_int("MLXQ_GATHER_SORTED", 1) != 0) {
+        knobs().gather_sorted != 0) {
       const DirectIdx dl = direct_index(lhs_indices, dsh[0], g.idx_shape);
       const DirectIdx dr = direct_index(rhs_indices, dsh[1], g.idx_shape);
       const mlxq::QmmGroupPlan gp = mlxq::qmm_group_plan(fmt, sp.N, sp.K, E, B);
@@ -1066,7 +1196,7 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq
     // tile of rows (qmm.hip), instead of once per index entry.  Auto when the
     // entries average >= 8 rows per touched expert; MLXQ_GATHER_GROUP=0|1
     // forces the choice (A/B switch for tests).
-    const int grp_env = env_int("MLXQ_GATHER_GROUP", -1);
+    const int grp_env = knobs().gather_group;
     const int64_t rows = B * M;
     const bool want_group = grp_env == 1 || (grp_env != 0 && rows >= 8 * std::min<int64_t>(E, B));
     if (E <= mlxq::kGroupMaxExperts && want_group) {
@@ -1092,8 +1222,7 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq
       const size_t o_n = o_seg + al((size_t)maxseg * 3 * sizeof(uint32_t));
       const size_t o_part = o_n + 256;
       const size_t part = (!use_qmm && p.ks > 1) ? (size_t)p.ks * rows * sp.N * sizeof(float) : 0;
-      Workspace& ws = workspace(dev, stream, o_part + part);
-      char* base = static_cast<char*>(ws.data);
+      char* base = static_cast<char*>(workspace(dev, stream, o_part + part));
       uint32_t* flat = reinterpret_cast<uint32_t*>(base);
       ip.out[0] = flat;
       ip.out[1] = flat + B;
@@ -1168,12 +1297,12 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq
     // mlxcel's callers) run over runs of equal experts: each run streams its
     // expert's weights once per 4 entries instead of once per entry.
     // MLXQ_GATHER_RUNS=0 turns it off.
-    const int r_req = env_int("MLXQ_QMV_R", 0);
+    const int r_req = knobs().qmv_r;
     {
       const DirectIdx dl = direct_index(lhs_indices, dsh[0], g.idx_shape);
       const DirectIdx dr = direct_index(rhs_indices, dsh[1], g.idx_shape);
       if (sorted_indices && M == 1 && B >= 8 && dr.ok && dr.p && dl.ok && !dl.p && dl.div == 1 &&
-          env_int("MLXQ_GATHER_RUNS", 1) != 0) {
+          knobs().gather_runs != 0) {
         // runs of up to 4 entries on the block-MFMA kernel (gpt-oss MoE shapes,
         // T=16: 9% faster than one segment per entry; runs of 8 or 16 are
         // slower), else the row-streaming kernel
@@ -1215,8 +1344,8 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq
     const mlxq::QmvFrPlan fp =
         kind == Skinny::FR ? mlxq::qmv_fr_plan(fmt, sp.gs, sp.N, sp.K, (int)M, r_req) : mlxq::QmvFrPlan{};
     const mlxq::QmvB4Plan bp =
-        kind == Skinny::B4 ? mlxq::qmv_b4_plan(fmt, sp.gs, sp.N, sp.K, (int)M, env_int("MLXQ_QMV_B4_RG", 0),
-                                               env_int("MLXQ_QMV_B4_CPW", 0))
+        kind == Skinny::B4 ? mlxq::qmv_b4_plan(fmt, sp.gs, sp.N, sp.K, (int)M, knobs().b4_rg,
+                                               knobs().b4_cpw)
                            : mlxq::QmvB4Plan{};
     const mlxq::QmvRsPlan rp =
         (kind == Skinny::RS || (kind == Skinny::FR && !fp.ok) || (kind == Skinny::B4 && !bp.ok && M <= 4))
@@ -1233,11 +1362,11 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq
     // indices the kernels can read in place skip the index_prep launch
     const DirectIdx dl = direct_index(lhs_indices, dsh[0], g.idx_shape);
     const DirectIdx dr = direct_index(rhs_indices, dsh[1], g.idx_shape);
-    const bool direct = dl.ok && dr.ok && dr.div == 1 && env_int("MLXQ_GATHER_DIRECT", 1) != 0;
+    const bool direct = dl.ok && dr.ok && dr.div == 1 && knobs().gather_direct != 0;
     const size_t idx_bytes = direct ? 0 : ((size_t)B * 2 * sizeof(uint32_t) + 255) & ~(size_t)255;
     const size_t part_bytes = p.ks > 1 ? (size_t)p.ks * B * M * sp.N * sizeof(float) : 0;
     char* wsb = nullptr;
-    if (idx_bytes + part_bytes > 0) wsb = static_cast<char*>(workspace(dev, stream, idx_bytes + part_bytes).data);
+    if (idx_bytes + part_bytes > 0) wsb = static_cast<char*>(workspace(dev, stream, idx_bytes + part_bytes));
     const uint32_t* lhs_p = dl.p;
     const uint32_t* rhs_p = dr.p;
     int lhs_stride = dl.stride, rhs_stride = dr.stride, lhs_div = dl.div;
@@ -1582,7 +1711,7 @@ void fused_moe(const char* tag, const mlxq_array* x, const mlxq_array* indices, 
   a.k = k;
   a.E = (int)std::min<int64_t>(E, INT32_MAX);
   a.gs_shift = group_size == 32 ? 5 : (group_size == 64 ? 6 : 7);
-  a.act = reinterpret_cast<float*>(workspace(dev, stream, (size_t)k * dff * sizeof(float)).data);
+  a.act = reinterpret_cast<float*>(workspace(dev, stream, (size_t)k * dff * sizeof(float)));
   hip_check(mlxq::moe_launch(a, gu_bits, d_bits, act, stream), "fused MoE launch");
 }
 

@@ -314,3 +314,26 @@ def fused_moe_geglu(x, indices, gate_w, gate_s, gate_b, up_w, up_s, up_b, down_w
     GELU of the gate times up)."""
     return _fused_moe("mlxq_fused_moe_geglu", x, indices, gate_w, gate_s, gate_b, up_w, up_s, up_b, down_w,
                       down_s, down_b, scores, din, dff, k, gu_bits, d_bits, group_size, out)
+
+
+def workspace_reserve(nbytes: int, device: Optional[torch.device] = None) -> None:
+    """Grow the current stream's workspace to ``nbytes`` before a HIP-graph
+    capture (a call under capture never allocates; it fails instead)."""
+    lib = _lib.load()
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    with torch.cuda.device(dev):
+        st = lib.mlxq_workspace_reserve(int(nbytes), _stream(dev))
+    if st:
+        _raise(st)
+
+
+def get_cache_memory() -> int:
+    """Device bytes held by the library's workspaces (``get_cache_memory``)."""
+    return int(_lib.load().mlxq_get_cache_memory())
+
+
+def clear_cache() -> None:
+    """Free every workspace after synchronizing (``clear_memory_cache``)."""
+    st = _lib.load().mlxq_clear_cache()
+    if st:
+        _raise(st)

@@ -10,6 +10,14 @@ import oracle as orc
 TOL = 1e-2  # north-star gate: max|y - y_ref| / max|y_ref|, bf16 output, fp32 accumulate
 
 
+def setknob(monkeypatch, name, value):
+    """Set an MLXQ_* switch for this test; the library latches the switches,
+    so re-read them (the conftest re-reads them again before the next test)."""
+    monkeypatch.setenv(name, value)
+    import mlxcel_amd._lib as L
+    L.load().mlxq_reload_options()
+
+
 def announce(*parts):
     """Name the GPU case before it runs (a fault then still says which case)."""
     print("[gpu case]", *parts, flush=True)

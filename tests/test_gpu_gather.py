@@ -14,7 +14,7 @@ import torch
 
 import mlxcel_amd as mq
 import oracle as orc
-from helpers import TOL, announce, dev_bf16, dev_u32, dev_u8, host_u16, max_rel
+from helpers import TOL, announce, dev_bf16, dev_u32, dev_u8, host_u16, max_rel, setknob
 
 pytestmark = pytest.mark.gpu
 
@@ -122,7 +122,7 @@ def test_grouped_by_expert_matches_stack(monkeypatch, K, group, E, T, M, mode):
     # (CPUQ:792-812); E=2, T=160 gives segments of more than 64 rows
     if mode == "mxfp4" and K % 32:
         pytest.skip("mxfp4 needs K % 32 == 0")
-    monkeypatch.setenv("MLXQ_GATHER_GROUP", str(group))
+    setknob(monkeypatch, "MLXQ_GATHER_GROUP", str(group))
     announce("gather_grouped", K, group, E, T, M, mode)
     N = 264
     rng = np.random.default_rng(1700 + E + T + M)
@@ -155,11 +155,11 @@ def test_grouped_gather_is_deterministic_and_matches_per_entry(monkeypatch):
     lhs = torch.from_numpy(np.repeat(np.arange(T), 4).astype(np.int32)).cuda()
     rhs = torch.from_numpy(ids.astype(np.int32)).cuda()
     args = (dev_bf16(x), dev_u32(wq), dev_u8(sc), None, lhs, rhs, True, 32, 4, "mxfp4")
-    monkeypatch.setenv("MLXQ_GATHER_GROUP", "1")
+    setknob(monkeypatch, "MLXQ_GATHER_GROUP", "1")
     g1 = host_u16(mq.gather_qmm(*args))
     g2 = host_u16(mq.gather_qmm(*args))
     np.testing.assert_array_equal(g1, g2)
-    monkeypatch.setenv("MLXQ_GATHER_GROUP", "0")
+    setknob(monkeypatch, "MLXQ_GATHER_GROUP", "0")
     per_entry = host_u16(mq.gather_qmm(*args))
     assert max_rel(g1, per_entry) <= TOL
     want = orc.gather_qmm_t(x, wq, sc, None, np.repeat(np.arange(T), 4).astype(np.uint32), ids.astype(np.uint32),
@@ -199,7 +199,7 @@ def test_direct_indices_match_index_prep(monkeypatch, dtype, case):
         lhs, rhs = None, torch.from_numpy(bad).to(dtype).cuda()
     outs = []
     for direct in ("1", "0"):
-        monkeypatch.setenv("MLXQ_GATHER_DIRECT", direct)
+        setknob(monkeypatch, "MLXQ_GATHER_DIRECT", direct)
         y = mq.gather_qmm(x, W, S, Bi, lhs, rhs, True, 64, 4)
         torch.cuda.synchronize()
         outs.append(host_u16(y))
@@ -224,7 +224,7 @@ def test_sorted_runs(monkeypatch, pattern, dtype):
     # gathers, test_sorted_grouped_mxfp4) relies on sorted_indices the way
     # the reference's sorted route does, and "pairs" (wrapping at E),
     # "alternating" and "unsorted" are not sorted
-    monkeypatch.setenv("MLXQ_GATHER_SORTED", "0")
+    setknob(monkeypatch, "MLXQ_GATHER_SORTED", "0")
     if pattern == "random_sorted":
         rhs = np.sort(rng.integers(0, E, B))
     elif pattern == "one_expert":
@@ -244,7 +244,7 @@ def test_sorted_runs(monkeypatch, pattern, dtype):
     assert max_rel(got, want) <= TOL
     again = host_u16(mq.gather_qmm(X, W, S, None, None, R, True, 32, 4, "mxfp4", sorted_indices=True))
     np.testing.assert_array_equal(got, again)
-    monkeypatch.setenv("MLXQ_GATHER_RUNS", "0")
+    setknob(monkeypatch, "MLXQ_GATHER_RUNS", "0")
     per_entry = host_u16(mq.gather_qmm(X, W, S, None, None, R, True, 32, 4, "mxfp4", sorted_indices=True))
     assert max_rel(per_entry, got) <= TOL
 

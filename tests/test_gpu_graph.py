@@ -11,7 +11,7 @@ import torch
 
 import mlxcel_amd as mq
 import oracle as orc
-from helpers import TOL, affine_case, announce, dev_bf16, dev_u32, dev_u8, host_u16, max_rel, mxfp4_case
+from helpers import TOL, affine_case, announce, dev_bf16, dev_u32, dev_u8, host_u16, max_rel, mxfp4_case, setknob
 
 pytestmark = pytest.mark.gpu
 
@@ -43,7 +43,7 @@ def replay_and_check(g, out, want_u16, other_work):
 
 @pytest.mark.parametrize("kernel,M", [("rs", 1), ("rs", 2), ("fr", 1), ("mfma", 1), ("mfma", 8)])
 def test_quantized_matmul_graph(monkeypatch, kernel, M):
-    monkeypatch.setenv("MLXQ_QMV_KERNEL", kernel)
+    setknob(monkeypatch, "MLXQ_QMV_KERNEL", kernel)
     announce("graph_qmm", kernel, M)
     N, K = 1024, 4096
     x, wq, s, b = affine_case(M, N, K, 64, 4, 1200 + M)
@@ -99,3 +99,72 @@ def test_graph_sees_new_inputs_in_place():
     torch.cuda.synchronize()
     want = host_u16(mq.quantized_matmul(dev_bf16(x2), W, S, B, True, 64, 4))
     np.testing.assert_array_equal(host_u16(out), want)
+
+
+def test_capture_without_warmup_gets_a_status_and_an_intact_capture():
+    # a call that needs workspace on a stream under capture returns
+    # MLXQ_ENOMEM (no allocation, no synchronize) and the capture goes on
+    announce("graph_no_warmup")
+    M, N, K = 256, 256, 8192
+    x, wq, s, b = affine_case(M, N, K, 64, 4, 1260)
+    X, W, S, B = dev_bf16(x), dev_u32(wq), dev_bf16(s), dev_bf16(b)
+    out = torch.zeros(M, N, dtype=torch.bfloat16, device="cuda")
+    marker = torch.zeros(4, device="cuda")
+    st = torch.cuda.Stream()  # never used: its workspace is empty
+    g = torch.cuda.CUDAGraph()
+    err = None
+    with torch.cuda.graph(g, stream=st):
+        try:
+            mq.quantized_matmul(X, W, S, B, True, 64, 4, out=out)
+        except mq.ops.QuantizedOpError as e:
+            err = str(e)
+        marker.add_(1.0)
+    assert err is not None and "captured" in err, err
+    for rep in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert float(marker[0]) == rep + 1
+    # reserving up front makes the same capture work
+    eager = host_u16(mq.quantized_matmul(X, W, S, B, True, 64, 4))
+    st2 = torch.cuda.Stream()
+    with torch.cuda.stream(st2):
+        mq.workspace_reserve(64 << 20)
+    torch.cuda.synchronize()
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2, stream=st2):
+        mq.quantized_matmul(X, W, S, B, True, 64, 4, out=out)
+    junk = torch.randn(1 << 20, device="cuda")
+    replay_and_check(g2, out, eager, lambda: junk.mul_(0.5))
+
+
+def test_replay_after_the_workspace_grew():
+    # a graph captured with a small workspace still replays correctly after a
+    # larger call on the same stream replaced the workspace (the old buffer
+    # is kept, not freed)
+    announce("graph_ws_growth")
+    M, N, K = 8, 2048, 4096  # 5-16-row decode kernel: K-range partials in the workspace
+    x, wq, s, b = affine_case(M, N, K, 64, 4, 1270)
+    X, W, S, B = dev_bf16(x), dev_u32(wq), dev_bf16(s), dev_bf16(b)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    eager = host_u16(mq.quantized_matmul(X, W, S, B, True, 64, 4))
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        mq.quantized_matmul(X, W, S, B, True, 64, 4, out=out)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        mq.quantized_matmul(X, W, S, B, True, 64, 4, out=out)
+    held = mq.get_cache_memory()
+    # a split-K prefill with much larger partials on the same stream
+    M2, N2, K2 = 512, 4096, 14336
+    x2, wq2, s2, b2 = affine_case(M2, N2, K2, 64, 4, 1271)
+    X2, W2, S2, B2 = dev_bf16(x2), dev_u32(wq2), dev_bf16(s2), dev_bf16(b2)
+    with torch.cuda.stream(st):
+        big = mq.quantized_matmul(X2, W2, S2, B2, True, 64, 4)
+    torch.cuda.synchronize()
+    assert mq.get_cache_memory() >= held
+    junk = torch.randn(1 << 22, device="cuda")
+    replay_and_check(g, out, eager, lambda: junk.mul_(1.5))
+    want_big = host_u16(mq.quantized_matmul(X2, W2, S2, B2, True, 64, 4))
+    np.testing.assert_array_equal(host_u16(big), want_big)

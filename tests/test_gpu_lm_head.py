@@ -17,7 +17,7 @@ import pytest
 
 import mlxcel_amd as mq
 import oracle as orc
-from helpers import TOL, announce, dev_bf16, dev_u32, host_u16, max_rel
+from helpers import TOL, announce, dev_bf16, dev_u32, host_u16, max_rel, setknob
 
 pytestmark = pytest.mark.gpu
 
@@ -71,7 +71,7 @@ def test_qwen3_8b_head():
 
 @pytest.mark.parametrize("kernel", ["rs", "fr", "b4", "mfma", "mid"])
 def test_every_decode_kernel_at_a_ragged_width(monkeypatch, kernel):
-    monkeypatch.setenv("MLXQ_QMV_KERNEL", kernel)
+    setknob(monkeypatch, "MLXQ_QMV_KERNEL", kernel)
     announce("lm_head_kernel", kernel)
     x, wq, s, b, want = head_case(262147, 576)
     got = host_u16(mq.quantized_matmul(dev_bf16(x), dev_u32(wq), dev_bf16(s), dev_bf16(b), True, 64, 4))

@@ -11,7 +11,7 @@ import torch
 
 import mlxcel_amd as mq
 import oracle as orc
-from helpers import TOL, announce, dev_bf16, dev_u32, dev_u8, host_u16, max_rel
+from helpers import TOL, announce, dev_bf16, dev_u32, dev_u8, host_u16, max_rel, setknob
 
 pytestmark = pytest.mark.gpu
 
@@ -95,7 +95,7 @@ def test_other_row_counts_run_separately(M):
 
 @pytest.mark.parametrize("kernel", ["fr", "b4", "mfma"])
 def test_forced_kernels(monkeypatch, kernel):
-    monkeypatch.setenv("MLXQ_QMV_KERNEL", kernel)
+    setknob(monkeypatch, "MLXQ_QMV_KERNEL", kernel)
     announce("multi_forced", kernel)
     K = 4096
     x = orc.normal_bf16((1, K), 1.0, 980)

@@ -11,7 +11,7 @@ import torch
 
 import mlxcel_amd as mq
 import oracle as orc
-from helpers import TOL, affine_case, announce, dev_bf16, dev_u32, dev_u8, host_u16, max_rel, mxfp4_case
+from helpers import TOL, affine_case, announce, dev_bf16, dev_u32, dev_u8, host_u16, max_rel, mxfp4_case, setknob
 
 pytestmark = pytest.mark.gpu
 
@@ -30,7 +30,7 @@ def test_affine_qmm_vs_oracle(monkeypatch, tile, bits, gs, M, N, K):
     # every output-tile shape (MLXQ_QMM_TILE: 16x16-MFMA kernel 0 = 256x128,
     # 1 = 256x256, 2 = 128x128; 32x32-MFMA tile kernel 4 = 256x256,
     # 5 = 256x128, 6 = 128x128; -1 = by shape)
-    monkeypatch.setenv("MLXQ_QMM_TILE", str(tile))
+    setknob(monkeypatch, "MLXQ_QMM_TILE", str(tile))
     announce("qmm_affine", tile, bits, gs, M, N, K)
     x, wq, s, b = affine_case(M, N, K, gs, bits, 2100 + M + N + bits + gs)
     assert max_rel(run(x, wq, s, b, gs, bits), orc.qmm_t_affine(x, wq, s, b, gs, bits)) <= TOL
@@ -42,7 +42,7 @@ def test_affine_qmm_unaligned_scale_rows(monkeypatch, tile, bits, gs):
     # K = 2880 (gpt-oss): K / gs groups per row = 90 or 45, so scale rows are
     # 180 or 90 bytes apart and the tile kernel's 16-byte scale chunks start
     # off their natural alignment
-    monkeypatch.setenv("MLXQ_QMM_TILE", str(tile))
+    setknob(monkeypatch, "MLXQ_QMM_TILE", str(tile))
     announce("qmm_unaligned_scales", tile, bits, gs)
     M, N, K = 130, 160, 2880
     x, wq, s, b = affine_case(M, N, K, gs, bits, 2150 + bits + gs)
@@ -53,8 +53,8 @@ def test_affine_qmm_unaligned_scale_rows(monkeypatch, tile, bits, gs):
 def test_affine_qmm_split_k_and_batch_fold(monkeypatch, tile, ksplit):
     # few output tiles and a long K: the K range is split across workgroups
     # (uneven splits included); x given as [2, 128, K] folds into 256 rows
-    monkeypatch.setenv("MLXQ_QMM_TILE", str(tile))
-    monkeypatch.setenv("MLXQ_QMM_KSPLIT", str(ksplit))
+    setknob(monkeypatch, "MLXQ_QMM_TILE", str(tile))
+    setknob(monkeypatch, "MLXQ_QMM_KSPLIT", str(ksplit))
     announce("qmm_splitk", tile, ksplit)
     M, N, K = 256, 256, 8192
     x, wq, s, b = affine_case(M, N, K, 64, 4, 2201)
@@ -68,7 +68,7 @@ def test_affine_qmm_split_k_and_batch_fold(monkeypatch, tile, ksplit):
 
 @pytest.mark.parametrize("tile", [0, 1, 2, 4, 5, 6, 7])
 def test_mxfp4_qmm_vs_oracle(monkeypatch, tile):
-    monkeypatch.setenv("MLXQ_QMM_TILE", str(tile))
+    setknob(monkeypatch, "MLXQ_QMM_TILE", str(tile))
     announce("qmm_mxfp4", tile)
     M, N, K = 192, 576, 2880
     x, wq, sc = mxfp4_case(M, N, K, 2301)

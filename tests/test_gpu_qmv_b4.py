@@ -15,7 +15,7 @@ import torch
 
 import mlxcel_amd as mq
 import oracle as orc
-from helpers import TOL, affine_case, announce, dev_bf16, dev_u32, dev_u8, host_u16, max_rel, mxfp4_case
+from helpers import TOL, affine_case, announce, dev_bf16, dev_u32, dev_u8, host_u16, max_rel, mxfp4_case, setknob
 
 pytestmark = pytest.mark.gpu
 
@@ -36,11 +36,11 @@ def mxfp4(x, wq, sc):
 
 @pytest.fixture
 def b4(monkeypatch):
-    monkeypatch.setenv("MLXQ_QMV_KERNEL", "b4")
+    setknob(monkeypatch, "MLXQ_QMV_KERNEL", "b4")
 
     def shape(rg, cpw):
-        monkeypatch.setenv("MLXQ_QMV_B4_RG", str(rg))
-        monkeypatch.setenv("MLXQ_QMV_B4_CPW", str(cpw))
+        setknob(monkeypatch, "MLXQ_QMV_B4_RG", str(rg))
+        setknob(monkeypatch, "MLXQ_QMV_B4_CPW", str(cpw))
     return shape
 
 

@@ -17,14 +17,14 @@ import torch
 
 import mlxcel_amd as mq
 import oracle as orc
-from helpers import TOL, affine_case, announce, dev_bf16, dev_u32, host_u16, max_rel
+from helpers import TOL, affine_case, announce, dev_bf16, dev_u32, host_u16, max_rel, setknob
 
 pytestmark = pytest.mark.gpu
 
 
 @pytest.fixture
 def mid(monkeypatch):
-    monkeypatch.setenv("MLXQ_QMV_KERNEL", "mid")
+    setknob(monkeypatch, "MLXQ_QMV_KERNEL", "mid")
 
 
 def run(x, wq, s, b, gs, bits):

@@ -16,7 +16,7 @@ import torch
 
 import mlxcel_amd as mq
 import oracle as orc
-from helpers import TOL, affine_case, announce, dev_bf16, dev_u32, dev_u8, host_u16, max_rel, mxfp4_case
+from helpers import TOL, affine_case, announce, dev_bf16, dev_u32, dev_u8, host_u16, max_rel, mxfp4_case, setknob
 
 pytestmark = pytest.mark.gpu
 
@@ -39,8 +39,8 @@ def mxfp4(x, wq, sc):
 @pytest.mark.parametrize("bits,gs", [(4, 32), (4, 64), (4, 128), (8, 32), (8, 64), (8, 128)])
 @pytest.mark.parametrize("M", [1, 2, 3, 4])
 def test_affine_kernels(monkeypatch, kernel, R, bits, gs, M):
-    monkeypatch.setenv("MLXQ_QMV_KERNEL", kernel)
-    monkeypatch.setenv("MLXQ_QMV_R", str(R))
+    setknob(monkeypatch, "MLXQ_QMV_KERNEL", kernel)
+    setknob(monkeypatch, "MLXQ_QMV_R", str(R))
     N, K = 200, 2304  # 4-bit: 2 chunks per row, the second one ends mid-chunk
     announce("skinny_affine", kernel, R, bits, gs, M)
     x, wq, s, b = affine_case(M, N, K, gs, bits, 900 + M + bits + gs + R)
@@ -52,7 +52,7 @@ def test_affine_kernels(monkeypatch, kernel, R, bits, gs, M):
 @pytest.mark.parametrize("bits,K", [(4, 1024), (4, 512), (4, 6144), (8, 6144), (4, 16384), (8, 2048)])
 def test_affine_chunk_counts(monkeypatch, kernel, M, bits, K):
     # 1, 4, 8 and 16 chunks per row (compiled chunk bounds 1/4/8/16)
-    monkeypatch.setenv("MLXQ_QMV_KERNEL", kernel)
+    setknob(monkeypatch, "MLXQ_QMV_KERNEL", kernel)
     announce("skinny_chunks", kernel, M, bits, K)
     x, wq, s, b = affine_case(M, 72, K, 64, bits, 970 + M + bits + K)
     assert max_rel(affine(x, wq, s, b, 64, bits), orc.qmm_t_affine(x, wq, s, b, 64, bits)) <= TOL
@@ -63,7 +63,7 @@ def test_affine_chunk_counts(monkeypatch, kernel, M, bits, K):
 @pytest.mark.parametrize("bits,K", [(4, 28672), (8, 14336), (8, 9216)])
 def test_affine_two_chunks_per_wave(monkeypatch, kernel, M, bits, K):
     # rows longer than 8 KiB: each wave streams two chunks of every row
-    monkeypatch.setenv("MLXQ_QMV_KERNEL", kernel)
+    setknob(monkeypatch, "MLXQ_QMV_KERNEL", kernel)
     announce("rs_two_chunks", kernel, M, bits, K)
     x, wq, s, b = affine_case(M, 136, K, 64, bits, 950 + M + bits)
     assert max_rel(affine(x, wq, s, b, 64, bits), orc.qmm_t_affine(x, wq, s, b, 64, bits)) <= TOL
@@ -72,8 +72,8 @@ def test_affine_two_chunks_per_wave(monkeypatch, kernel, M, bits, K):
 @pytest.mark.parametrize("kernel,R", KERNEL_R)
 @pytest.mark.parametrize("M", [1, 2, 4])
 def test_mxfp4_kernels(monkeypatch, kernel, R, M):
-    monkeypatch.setenv("MLXQ_QMV_KERNEL", kernel)
-    monkeypatch.setenv("MLXQ_QMV_R", str(R))
+    setknob(monkeypatch, "MLXQ_QMV_KERNEL", kernel)
+    setknob(monkeypatch, "MLXQ_QMV_R", str(R))
     announce("rs_mxfp4", kernel, R, M)
     x, wq, sc = mxfp4_case(M, 5760 + 8, 2880, 980 + M + R)
     assert max_rel(mxfp4(x, wq, sc), orc.fp_qmm_t_mxfp4(x, wq, sc)) <= TOL
