@@ -67,6 +67,36 @@ def _compile(name: str, extra: list[str]) -> str:
     return obj
 
 
+def _verify_group_ring_waits() -> None:
+    """qmm_group.hip waits for its LDS ring with a hand-counted
+    `s_waitcnt vmcnt(16)`: 2 younger blocks of 8 vector-memory instructions
+    each (4 direct-to-LDS activation loads, 2 weight and 2 scale loads per
+    wave).  If the compiler ever emitted a different number per block the
+    wait would be wrong, so check the kernel's AMD assembly (built here): 3
+    blocks before the first wait, then exactly 8 loads after each of the 4
+    waits of a ring turn."""
+    src = os.path.join(CSRC, "qmm_group.hip")
+    asm = os.path.join(BUILD, "qmm_group.device.s")
+    cmd = [HIPCC, *COMMON, "--cuda-device-only", "-S", src, "-o", asm]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc -S failed for qmm_group.hip:\n{r.stderr}")
+    lines = open(asm).read().splitlines()
+    start = next(i for i, l in enumerate(lines) if l.startswith("_ZN4mlxq22qmm_group_mxfp4_kernel"))
+    end = next(i for i in range(start, len(lines)) if "s_endpgm" in lines[i])
+    body = [l.strip() for l in lines[start:end]]
+    marks = [i for i, l in enumerate(body) if l.startswith("s_waitcnt vmcnt(16)")]
+    if len(marks) != 4:
+        raise RuntimeError(f"qmm_group ring check: expected 4 ring waits, found {len(marks)}")
+    loads = lambda a, b: sum(1 for l in body[a:b] if l.startswith("buffer_load"))
+    bounds = marks + [next(i for i in range(marks[-1], len(body)) if body[i].startswith("s_waitcnt vmcnt(0)"))]
+    per = [loads(bounds[k] + 1, bounds[k + 1]) for k in range(4)]
+    pro = loads(0, marks[0])
+    if per != [8, 8, 8, 8] or pro != 24:
+        raise RuntimeError(f"qmm_group ring check: loads per ring step {per}, prologue {pro} "
+                           "(the kernel's vmcnt(16) assumes 8 per step and 24 before the first wait)")
+
+
 def build(verbose: bool = True) -> str:
     """Compile every source and link libmlxq.so; always rebuilds."""
     if not os.path.exists(HIPCC) and shutil.which("hipcc") is None:
@@ -81,6 +111,7 @@ def build(verbose: bool = True) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    _verify_group_ring_waits()
     bobjs = [_compile(k, v) for k, v in BENCH_SOURCES.items()]
     tmp = BENCH_LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *bobjs]

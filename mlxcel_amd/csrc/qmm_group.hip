@@ -197,6 +197,7 @@ __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGrou
         // no LDS read moves across either; a plain barrier, because the
         // workgroup fences of __syncthreads would also wait for the ring's
         // younger activation loads)
+        // (mlxcel_amd/build.py checks the emitted assembly for exactly 8 loads per block)
         static_assert(GQ_VMEM * (GQ_RING - 2) == 16, "the wait below counts 2 blocks of 8 instructions");
         asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
         issue(b + GQ_RING - 1, (d + GQ_RING - 1) % GQ_RING, wn, sn);
