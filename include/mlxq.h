@@ -134,6 +134,21 @@ mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w,
                                   bool transpose, int32_t group_size, int32_t bits,
                                   const char* mode, mlxq_array* out, void* stream);
 
+/* quantized_matmul without any allocation: the same validation, kernels and
+ * result bits as mlxq_quantized_matmul, but the scratch some routes need
+ * (split-K partials of the 5-16-row decode kernel and of the prefill GEMM)
+ * lives in a fixed 64 MiB device array of the library (one per GPU, held
+ * until the process ends) instead of the per-stream workspace.  Calls that
+ * would need more return MLXQ_ENOMEM with the size in mlxq_last_error().
+ * Every call on one GPU shares that array: calls that overlap in time on one
+ * GPU (several streams, threads or replays of graphs in flight together) race.
+ * No counterpart in the reference; it is for callers that cannot allocate
+ * (code under HIP-graph capture, tight serving loops). */
+mlxq_status mlxq_quantized_matmul_noalloc(const mlxq_array* x, const mlxq_array* w,
+                                          const mlxq_array* scales, const mlxq_array* biases,
+                                          bool transpose, int32_t group_size, int32_t bits,
+                                          const char* mode, mlxq_array* out, void* stream);
+
 /* A quantized linear layer, as the reference's quantized_linear_forward
  * (lib.rs:697-707, mlx_cxx_bridge.cpp:1707-1746): quantized_matmul with
  * transpose = true, then `+ linear_bias` as MLX adds two bf16 arrays (fp32

@@ -48,6 +48,7 @@ SYMBOLS = (
     "mlxq_get_cache_memory",
     "mlxq_clear_cache",
     "mlxq_reload_options",
+    "mlxq_quantized_matmul_noalloc",
 )
 
 _lib = None
@@ -89,6 +90,7 @@ def load() -> ctypes.CDLL:
     lib.mlxq_quantize.argtypes = [A, I32, I32, S, A, A, A, P]
     lib.mlxq_fused_moe_expert.argtypes = [A] * 12 + [I32] * 6 + [A, P]
     lib.mlxq_fused_moe_geglu.argtypes = [A] * 12 + [I32] * 6 + [A, P]
+    lib.mlxq_quantized_matmul_noalloc.argtypes = [A, A, A, A, B, I32, I32, S, A, P]
     lib.mlxq_workspace_reserve.argtypes = [ctypes.c_size_t, P]
     lib.mlxq_get_cache_memory.argtypes = []
     lib.mlxq_clear_cache.argtypes = []

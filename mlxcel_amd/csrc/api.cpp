@@ -923,6 +923,19 @@ mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w, cons
   });
 }
 
+mlxq_status mlxq_quantized_matmul_noalloc(const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+                                          const mlxq_array* biases, bool transpose, int32_t group_size,
+                                          int32_t bits, const char* mode, mlxq_array* out, void* stream_) {
+  return guarded([&] {
+    const QmmSpec sp = check_quantized_matmul(x, w, scales, biases, transpose, group_size, bits, mode, out,
+                                              "quantized_matmul_noalloc");
+    ScratchSrc ss;
+    hip_check(mlxq::static_scratch(current_device(), &ss.fixed), "hipGetSymbolAddress(scratch)");
+    ss.max = mlxq::static_scratch_bytes();
+    run_quantized_matmul(sp, x, w, scales, biases, out, reinterpret_cast<hipStream_t>(stream_), ss);
+  });
+}
+
 void mlxq_reload_options(void) {
   // the previous snapshot stays allocated: a concurrent call may still read it
   g_knobs.store(read_knobs(), std::memory_order_release);

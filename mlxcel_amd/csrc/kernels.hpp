@@ -297,4 +297,8 @@ hipError_t moe_launch(const MoeArgs& a, int gu_bits, int d_bits, int act, hipStr
 // out[i] = bf16(out[i] + bias[i % bias_n]) over n bf16 elements (bias.hip).
 hipError_t launch_bias_add(uint16_t* out, const uint16_t* bias, int64_t n, int64_t bias_n, hipStream_t stream);
 
+// ---- scratch.hip: the no-allocation entry point's device array ----
+size_t static_scratch_bytes();
+hipError_t static_scratch(int dev, void** ptr);
+
 }  // namespace mlxq
