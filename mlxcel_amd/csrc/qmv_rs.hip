@@ -24,6 +24,8 @@
 // Partial sums of all (row, activation-row) pairs are reduced across the 64
 // lanes with a halving butterfly and across waves through LDS in a fixed
 // order, so results are bitwise reproducible.
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -42,15 +44,44 @@ __host__ __device__ inline uint32_t qmv_rs_lds(int fmt, int r, int mr, int nw, i
 }
 
 
-// FMT: weight format; MR: activation rows (>= rows of any segment);
+// Compact launch arguments of the dense and multi-projection entries: every
+// field a wave needs before its first weight load sits in the first few
+// scalar-cache lines and no branch depends on a loaded value before the
+// weight stream is issued (each dependent round of kernel-argument loads
+// costs a memory latency at the start of every workgroup).
+struct RsDenseArgs {
+  const uint16_t* x;     // count rows of K
+  const uint32_t* w;     // [N][K*bits/32]
+  const void* scales;
+  const uint16_t* biases;
+  uint16_t* out;         // count rows of N
+  int N, K, count, gs_shift;
+};
+struct RsMultiArgs {
+  const uint16_t* x;
+  int K, count, gs_shift, n;
+  int tile_end[kQmvMultiMax];
+  int N[kQmvMultiMax];
+  const uint32_t* w[kQmvMultiMax];
+  const void* scales[kQmvMultiMax];
+  const uint16_t* biases[kQmvMultiMax];
+  uint16_t* out[kQmvMultiMax];
+};
+
+// FMT: weight format; MR: activation rows (>= `count`);
 // R: weight rows per workgroup (power of two); CPW: 1 KiB chunks per wave and
 // row; UPW: quantization groups per scale load (1, 2 or 4: the widest load
 // every row's scales stay aligned for, chosen on the host from K / gs).  The
 // load width is a template parameter so the scale loads carry no branches:
 // a branch join there makes the compiler wait for the loads before it issues
 // the weight stream.
+//
+// One row tile: output rows [tile*R, tile*R + R) of the `count` activation
+// rows at x (row stride K) against the matrix Wm (N rows), written to Om
+// (row stride N).
 template <int FMT, int MR, int R, int CPW, int UPW>
-__global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shift, const QmvMulti mp) {
+__device__ __forceinline__ void rs_tile(const uint16_t* x, int count, const uint32_t* Wm, const void* Sm,
+                                        const uint16_t* Bm, uint16_t* Om, int N, int K, int gs_shift, int tile) {
   constexpr bool AFF = FMT != MXFP4;
   constexpr int BITS = FMT == AFF8 ? 8 : 4;
   constexpr int KL = 128 / BITS;  // K positions per lane chunk (16 bytes)
@@ -70,47 +101,6 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int NW = blockDim.x >> 6;
-  const int NT = blockDim.x;
-  const int sidx = blockIdx.y;
-
-  // ---- segment (workgroup-uniform) ----------------------------------------
-  int count = min(a.rps, a.total_rows - sidx * a.rps);
-  if (count <= 0) return;
-  const int expert = seg_index(a.rhs, a.rhs_stride, sidx, a.E, a.w_expert_stride ? sidx : 0);
-  if (a.runs) {
-    // Expert runs of a sorted gather (one activation row per entry, MR >= 4):
-    // entry sidx starts a segment where the expert changes or at a multiple
-    // of 4, and the segment takes the following entries of the same expert
-    // up to the next multiple of 4; every other entry's workgroup exits.  So
-    // each entry is computed once and each run of an expert streams its
-    // weights once per 4 entries instead of once per entry.
-    if ((sidx & 3) != 0 && seg_index(a.rhs, a.rhs_stride, sidx - 1, a.E, 0) == expert) return;
-    count = 1;
-    while (count < 4 && ((sidx + count) & 3) != 0 && sidx + count < a.total_rows &&
-           seg_index(a.rhs, a.rhs_stride, sidx + count, a.E, 0) == expert)
-      count++;
-  }
-  const int xbatch = seg_index(a.lhs, a.lhs_stride, sidx, a.X, a.lhs_div > 1 ? sidx / a.lhs_div : sidx);
-
-  // The weight matrix of this workgroup: a's, or with several projections of
-  // the same activations (mp.n > 1) the one whose row tiles hold blockIdx.x.
-  const uint32_t* Wm = a.w;
-  const void* Sm = a.scales;
-  const uint16_t* Bm = a.biases;
-  uint16_t* Om = a.out;
-  int N = a.N;
-  int tile = blockIdx.x;
-  if (mp.n > 1) {  // workgroup-uniform
-    int p = 0;
-    while (p < mp.n - 1 && tile >= mp.tile_end[p]) p++;
-    tile -= p > 0 ? mp.tile_end[p - 1] : 0;
-    Wm = mp.w[p];
-    Sm = mp.scales[p];
-    Bm = mp.biases[p];
-    Om = mp.out[p];
-    N = mp.N[p];
-  }
-  const int K = a.K;
   const int row0 = tile * R;
   const int nlc = K / KL;  // lane chunks per row
   const uint32_t RB = (uint32_t)nlc * 16u;  // bytes per weight row
@@ -121,14 +111,10 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
 
   // Buffer resources: bounds-checked loads return 0 past the end, which
   // covers rows past N, activation rows past `count` and dead lanes.
-  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(Wm + (int64_t)expert * a.w_expert_stride, (uint32_t)N * RB);
-  const __amdgpu_buffer_rsrc_t xr =
-      buffer_rsrc(a.x + (int64_t)xbatch * a.rps * K, (uint32_t)count * (uint32_t)K * 2u);
-  const int64_t sb0 = (int64_t)expert * a.s_expert_stride;
-  const __amdgpu_buffer_rsrc_t sr =
-      buffer_rsrc(reinterpret_cast<const uint8_t*>(Sm) + sb0 * ESZ, (uint32_t)(N * G * ESZ));
-  const __amdgpu_buffer_rsrc_t br = buffer_rsrc(AFF ? (const void*)(Bm + sb0) : Sm,
-                                                (uint32_t)(AFF ? N * G * 2 : 0));
+  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(Wm, (uint32_t)N * RB);
+  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(x, (uint32_t)count * (uint32_t)K * 2u);
+  const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(Sm, (uint32_t)(N * G * ESZ));
+  const __amdgpu_buffer_rsrc_t br = buffer_rsrc(AFF ? (const void*)Bm : Sm, (uint32_t)(AFF ? N * G * 2 : 0));
 
   int kc[CPW];
   bool live[CPW];
@@ -337,22 +323,120 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
     for (int q = 0; q < NW * 4; q++) tot += red[q * V + idx];
     const int r = idx / MR, m = idx % MR;
     const int row = row0 + r;
-    if (row < N && m < count) Om[((int64_t)sidx * a.rps + m) * N + row] = (uint16_t)f32_to_bf16_bits(tot);
+    if (row < N && m < count) Om[(int64_t)m * N + row] = (uint16_t)f32_to_bf16_bits(tot);
   }
+}
+
+// General entry: segments of a gather or of batched weights (segment
+// blockIdx.y: expert rhs[s], x batch lhs[s], runs of a sorted gather), and
+// the multi-projection table of QmvMulti.
+template <int FMT, int MR, int R, int CPW, int UPW>
+__global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shift, const QmvMulti mp) {
+  constexpr bool AFF = FMT != MXFP4;
+  constexpr int ESZ = AFF ? 2 : 1;
+  const int sidx = blockIdx.y;
+  int count = min(a.rps, a.total_rows - sidx * a.rps);
+  if (count <= 0) return;
+  const int expert = seg_index(a.rhs, a.rhs_stride, sidx, a.E, a.w_expert_stride ? sidx : 0);
+  if (a.runs) {
+    // Expert runs of a sorted gather (one activation row per entry, MR >= 4):
+    // entry sidx starts a segment where the expert changes or at a multiple
+    // of 4, and the segment takes the following entries of the same expert
+    // up to the next multiple of 4; every other entry's workgroup exits.  So
+    // each entry is computed once and each run of an expert streams its
+    // weights once per 4 entries instead of once per entry.
+    if ((sidx & 3) != 0 && seg_index(a.rhs, a.rhs_stride, sidx - 1, a.E, 0) == expert) return;
+    count = 1;
+    while (count < 4 && ((sidx + count) & 3) != 0 && sidx + count < a.total_rows &&
+           seg_index(a.rhs, a.rhs_stride, sidx + count, a.E, 0) == expert)
+      count++;
+  }
+  const int xbatch = seg_index(a.lhs, a.lhs_stride, sidx, a.X, a.lhs_div > 1 ? sidx / a.lhs_div : sidx);
+  const uint32_t* Wm = a.w;
+  const void* Sm = a.scales;
+  const uint16_t* Bm = a.biases;
+  uint16_t* Om = a.out;
+  int N = a.N;
+  int tile = blockIdx.x;
+  if (mp.n > 1) {  // workgroup-uniform
+    int p = 0;
+    while (p < mp.n - 1 && tile >= mp.tile_end[p]) p++;
+    tile -= p > 0 ? mp.tile_end[p - 1] : 0;
+    Wm = mp.w[p];
+    Sm = mp.scales[p];
+    Bm = mp.biases[p];
+    Om = mp.out[p];
+    N = mp.N[p];
+  }
+  const int64_t sb0 = (int64_t)expert * a.s_expert_stride;
+  rs_tile<FMT, MR, R, CPW, UPW>(a.x + (int64_t)xbatch * a.rps * a.K, count, Wm + (int64_t)expert * a.w_expert_stride,
+                                reinterpret_cast<const uint8_t*>(Sm) + sb0 * ESZ, Bm ? Bm + sb0 : Bm,
+                                Om + (int64_t)sidx * a.rps * N, N, a.K, gs_shift, tile);
+}
+
+// Dense entry: one 2-D matrix, `count` <= MR activation rows.
+template <int FMT, int MR, int R, int CPW, int UPW>
+__global__ __launch_bounds__(512) void qmv_rs_dense_kernel(const RsDenseArgs a) {
+  rs_tile<FMT, MR, R, CPW, UPW>(a.x, a.count, a.w, a.scales, a.biases, a.out, a.N, a.K, a.gs_shift, blockIdx.x);
+}
+
+// Several 2-D matrices of the same activations: matrix p owns the row tiles
+// [tile_end[p-1], tile_end[p]).  Every table entry is read unconditionally
+// and selected, so the kernel-argument loads form one round.
+template <int FMT, int MR, int R, int CPW, int UPW>
+__global__ __launch_bounds__(512) void qmv_rs_multi_kernel(const RsMultiArgs a) {
+  int tile = blockIdx.x;
+  int p = 0;
+#pragma unroll
+  for (int i = 0; i < kQmvMultiMax - 1; i++) p += (i < a.n - 1 && tile >= a.tile_end[i]) ? 1 : 0;
+  const uint32_t* Wm = a.w[0];
+  const void* Sm = a.scales[0];
+  const uint16_t* Bm = a.biases[0];
+  uint16_t* Om = a.out[0];
+  int N = a.N[0];
+  int t0 = 0;
+#pragma unroll
+  for (int i = 1; i < kQmvMultiMax; i++) {
+    const bool on = p == i;
+    Wm = on ? a.w[i] : Wm;
+    Sm = on ? a.scales[i] : Sm;
+    Bm = on ? a.biases[i] : Bm;
+    Om = on ? a.out[i] : Om;
+    N = on ? a.N[i] : N;
+    t0 = on ? a.tile_end[i - 1] : t0;
+  }
+  rs_tile<FMT, MR, R, CPW, UPW>(a.x, a.count, Wm, Sm, Bm, Om, N, a.K, a.gs_shift, tile - t0);
 }
 
 // ---- host ------------------------------------------------------------------
 
 namespace {
 
+enum RsEntry { RS_GENERAL, RS_DENSE, RS_MULTI };
+
+struct RsLaunch {
+  RsEntry entry;
+  dim3 grid;
+  const QmvArgs* a;
+  int gs_shift;
+  const QmvMulti* mp;
+  RsDenseArgs dense;
+  RsMultiArgs multi;
+};
+
 template <int FMT, int UPW>
-hipError_t rs_launch_upw(const QmvRsPlan& p, const QmvArgs& a, int gs_shift, dim3 grid, const QmvMulti& mp,
-                         hipStream_t stream) {
+hipError_t rs_launch_upw(const QmvRsPlan& p, const RsLaunch& L, hipStream_t stream) {
   const dim3 block((unsigned)(p.nw * 64));
-#define RS_CASE(MR_, R_, CPW_)                                                                                 \
-  if (p.mr == MR_ && p.r == R_ && p.cpw == CPW_) {                                                             \
-    hipLaunchKernelGGL((qmv_rs_kernel<FMT, MR_, R_, CPW_, UPW>), grid, block, p.lds, stream, a, gs_shift, mp); \
-    return hipGetLastError();                                                                                  \
+#define RS_CASE(MR_, R_, CPW_)                                                                                     \
+  if (p.mr == MR_ && p.r == R_ && p.cpw == CPW_) {                                                                 \
+    if (L.entry == RS_DENSE)                                                                                       \
+      hipLaunchKernelGGL((qmv_rs_dense_kernel<FMT, MR_, R_, CPW_, UPW>), L.grid, block, p.lds, stream, L.dense);   \
+    else if (L.entry == RS_MULTI)                                                                                  \
+      hipLaunchKernelGGL((qmv_rs_multi_kernel<FMT, MR_, R_, CPW_, UPW>), L.grid, block, p.lds, stream, L.multi);   \
+    else                                                                                                           \
+      hipLaunchKernelGGL((qmv_rs_kernel<FMT, MR_, R_, CPW_, UPW>), L.grid, block, p.lds, stream, *L.a, L.gs_shift, \
+                         *L.mp);                                                                                   \
+    return hipGetLastError();                                                                                      \
   }
   RS_CASE(1, 4, 1)
   RS_CASE(1, 8, 1)
@@ -377,12 +461,11 @@ int rs_upw(int fmt, int64_t G) {
 }
 
 template <int FMT>
-hipError_t rs_launch_fmt(const QmvRsPlan& p, const QmvArgs& a, int gs_shift, dim3 grid, const QmvMulti& mp,
-                         hipStream_t stream) {
-  const int upw = rs_upw(FMT, (int64_t)a.K >> gs_shift);
-  if (upw == 1) return rs_launch_upw<FMT, 1>(p, a, gs_shift, grid, mp, stream);
-  if (upw == 4) return rs_launch_upw<FMT, 4>(p, a, gs_shift, grid, mp, stream);
-  return rs_launch_upw<FMT, 2>(p, a, gs_shift, grid, mp, stream);
+hipError_t rs_launch_fmt(const QmvRsPlan& p, const RsLaunch& L, int K, hipStream_t stream) {
+  const int upw = rs_upw(FMT, (int64_t)K >> L.gs_shift);
+  if (upw == 1) return rs_launch_upw<FMT, 1>(p, L, stream);
+  if (upw == 4) return rs_launch_upw<FMT, 4>(p, L, stream);
+  return rs_launch_upw<FMT, 2>(p, L, stream);
 }
 
 bool rs_valid(int mr, int r, int cpw) {
@@ -431,18 +514,52 @@ QmvRsPlan qmv_rs_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int r_req
 hipError_t qmv_rs_launch(int fmt, int gs, const QmvArgs& a, int nseg, const QmvRsPlan& p, hipStream_t stream,
                          const QmvMulti* multi) {
   if (!p.ok) return hipErrorInvalidValue;
-  QmvMulti mp{};
+  RsLaunch L{};
+  L.a = &a;
+  L.gs_shift = log2i(gs);
+  QmvMulti none{};
+  L.mp = &none;
   int tiles = p.tiles;
   if (multi && multi->n > 1) {
-    mp = *multi;
-    tiles = mp.tile_end[mp.n - 1];
+    // several 2-D matrices of one activation block (segment 0)
+    tiles = multi->tile_end[multi->n - 1];
+    L.entry = RS_MULTI;
+    RsMultiArgs& m = L.multi;
+    m.x = a.x;
+    m.K = a.K;
+    m.count = std::min(a.rps, a.total_rows);
+    m.gs_shift = L.gs_shift;
+    m.n = multi->n;
+    for (int i = 0; i < kQmvMultiMax; i++) {
+      const int j = i < multi->n ? i : multi->n - 1;  // unused entries repeat the last one
+      m.tile_end[i] = multi->tile_end[j];
+      m.N[i] = multi->N[j];
+      m.w[i] = multi->w[j];
+      m.scales[i] = multi->scales[j];
+      m.biases[i] = multi->biases[j];
+      m.out[i] = multi->out[j];
+    }
+    nseg = 1;
+  } else if (nseg == 1 && !a.rhs && !a.lhs && !a.runs && a.w_expert_stride == 0) {
+    L.entry = RS_DENSE;
+    RsDenseArgs& d = L.dense;
+    d.x = a.x;
+    d.w = a.w;
+    d.scales = a.scales;
+    d.biases = a.biases;
+    d.out = a.out;
+    d.N = a.N;
+    d.K = a.K;
+    d.count = std::min(a.rps, a.total_rows);
+    d.gs_shift = L.gs_shift;
+  } else {
+    L.entry = RS_GENERAL;
   }
-  const int gs_shift = log2i(gs);
-  const dim3 grid((unsigned)tiles, (unsigned)nseg, 1);
+  L.grid = dim3((unsigned)tiles, (unsigned)nseg, 1);
   switch (fmt) {
-    case AFF4: return rs_launch_fmt<AFF4>(p, a, gs_shift, grid, mp, stream);
-    case AFF8: return rs_launch_fmt<AFF8>(p, a, gs_shift, grid, mp, stream);
-    default: return rs_launch_fmt<MXFP4>(p, a, gs_shift, grid, mp, stream);
+    case AFF4: return rs_launch_fmt<AFF4>(p, L, a.K, stream);
+    case AFF8: return rs_launch_fmt<AFF8>(p, L, a.K, stream);
+    default: return rs_launch_fmt<MXFP4>(p, L, a.K, stream);
   }
 }
 
