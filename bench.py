@@ -649,6 +649,26 @@ def traffic_probe():
                                         "gather_t256_gate_up_algorithmic_bytes": gather_bytes}}))
 
 
+def prefill_probe():
+    """Dispatches for rocprofv3 counter passes over the prefill GEMM: the 8
+    configs[2] cases (4/8-bit x gate/up and down x M=512/2048), two launches
+    each on distinct weights, in the order printed."""
+    cases = []
+    for bits in (4, 8):
+        for (N, K, name) in ((14336, 4096, "gate_up"), (4096, 14336, "down")):
+            ws = [make_affine(N, K, bits, 64, 90 + c) for c in range(2)]
+            for M in (512, 2048):
+                x = randn_bf16((M, K), 13)
+                out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+                torch.cuda.synchronize()
+                for w in ws:
+                    mq.quantized_matmul(x, *w, True, 64, bits, out=out)
+                torch.cuda.synchronize()
+                cases.append({"bits": bits, "shape": name, "M": M, "N": N, "K": K, "launches": len(ws)})
+            del ws
+    print(json.dumps({"prefill_probe": cases}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -660,6 +680,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run 5 copies of 256 MiB and 5 gate launches, eager, for rocprofv3 --pmc")
+    ap.add_argument("--prefill-probe", action="store_true",
+                    help="run the 8 prefill GEMM configs twice each, eager, for rocprofv3 --pmc")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build runs the quantized-matmul kernels on a single "
@@ -670,6 +692,9 @@ def main():
     mq.load_library()
     if args.traffic_probe:
         traffic_probe()
+        return
+    if args.prefill_probe:
+        prefill_probe()
         return
 
     value, ms, launch_us, per_launch, gate_us, gate, multi_value, multi_ms = headline(args.steps, args.warmup)

@@ -44,6 +44,7 @@ SOURCES = {
     "qmv_mid.hip": [],
     "qmm_group.hip": [],
     "qmm.hip": [],
+    "qmm_rb.hip": [],
     "moe.hip": [],
     "bias.hip": [],
     "scratch.hip": [],

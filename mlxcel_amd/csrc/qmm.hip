@@ -54,6 +54,8 @@ __device__ __forceinline__ float cvt_ubyte(uint32_t w) {
   return r;
 }
 
+__device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
+
 }  // namespace
 
 // BM x BN output tile per workgroup; each wave owns (BM/2) x (BN/2).
@@ -261,9 +263,10 @@ __global__ __launch_bounds__(NT) void qmm_kernel(const QmmArgs a) {
 //
 // Per 64-wide K-step, activations [BM][64] and dequantized weights [BN][64]
 // (bf16) sit in double-buffered LDS.  Rows are 128 bytes with the 16-byte
-// chunk c of row r stored at c ^ (r & 7), so the 8 lanes of one LDS cycle
-// (8 rows, same chunk) hit distinct banks for both the staging writes and the
-// fragment reads.  One K-step, one barrier: while the MFMAs of step ks run
+// chunk c of row r stored at c ^ swz(r), swz(r) = (r ^ (r >> 3)) & 7, so the
+// 16 rows that one LDS cycle of a fragment read touches (same chunk) hit
+// distinct banks; with c ^ (r & 7) rows r and r + 8 collided (37% of the LDS
+// cycles were bank conflicts by SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE).  One K-step, one barrier: while the MFMAs of step ks run
 // from buffer ks&1, the wave dequantizes step ks+1 from registers into the
 // other buffer and then issues the global loads of step ks+2, a whole K-step
 // ahead of their first use.
@@ -367,7 +370,10 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
     const uint32_t xrw = a.seg ? (tr < rows ? a.xrows[r0 + tr] : 0u) : (uint32_t)(m0 + tr);
     xoff[i] = tr < rows ? xrw * (uint32_t)K * 2u + (uint32_t)xch * 16u : kDeadOfs;
   }
-  const int xdst = xrow * RS + ((xch ^ (xrow & 7)) << 3);  // + XROWS i rows (same swizzle)
+  auto xdst = [&](int i) {  // LDS position of activation load i
+    const int r = xrow + XROWS * i;
+    return r * RS + ((xch ^ swz(r)) << 3);
+  };
 
   // weights: thread t dequantizes rows wrow + WROWS p, 16-byte piece wpc
   const int wrow = t / WT, wpc = t % WT;
@@ -442,7 +448,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
   auto store_part = [&](int buf, int p, int ks) {
 #pragma unroll
     for (int i = 0; i < XL; i++)
-      if (i * NPART / XL == p) *reinterpret_cast<u32x4*>(&xs[buf][xdst + XROWS * i * RS]) = xreg[i];
+      if (i * NPART / XL == p) *reinterpret_cast<u32x4*>(&xs[buf][xdst(i)]) = xreg[i];
     // this thread's group of step ks (one per 16-byte piece: VPL <= group size)
     const int g = ((ks * BK + wpc * VPL) >> gs_shift);
     const int gslot = ((g / CHG) & 1) * CHG + g % CHG;
@@ -453,7 +459,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
       const int r = wrow + WROWS * pp;
       const uint32_t w = wreg[pp][e % 4];
       uint16_t* rowp = &wsm[buf][r * RS];
-      const int r7 = r & 7;
+      const int r7 = swz(r);
       if constexpr (AFF) {
         const uint32_t sb = tbl[gslot * BN + r];
         const float sc = __uint_as_float(sb << 16);
@@ -503,13 +509,20 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
       for (int q = 0; q < 16; q++) acc[i][j][q] = 0.f;
 
   // fragment of 32 x 32 x 16: lane holds row/column (lane % 32), k 8 * (lane / 32) .. + 8;
-  // slice s reads logical chunk 2 s + lane / 32 of its row, stored at that ^ (row & 7)
+  // slice s reads logical chunk 2 s + lane / 32 of its row, stored at that ^
+  // swz(row); fragment tile i's rows are 32 i + fr past a multiple of 64, so
+  // swz(row) = (fr & 7) ^ (fr >> 3) ^ 4 (i & 1)
   const int fr = lane & 31;
-  const int c0 = (lane >> 5) ^ (fr & 7);
+  const int c0 = (lane >> 5) ^ (fr & 7) ^ (fr >> 3);
   const int arow = (wm * TM + fr) * RS, brow = (wn * TN + fr) * RS;
-  int soff[NPART];
+  static_assert(TM % 64 == 0 && TN % 64 == 0, "wave tiles start at multiples of 64 rows");
+  int soff2[2][NPART];
 #pragma unroll
-  for (int s = 0; s < NPART; s++) soff[s] = ((2 * s) ^ c0) << 3;
+  for (int s = 0; s < NPART; s++) {
+    soff2[0][s] = ((2 * s) ^ c0) << 3;
+    soff2[1][s] = ((2 * s) ^ c0 ^ 4) << 3;
+  }
+
 
   // Steady state: step ks computes from buffer ks&1 while step ks+1 goes to
   // the other buffer (first two slices) and step ks+2 is loaded.  A barrier
@@ -538,9 +551,9 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
     __syncthreads();
     bf16x8 af[2][FM], bv[2][FN];
 #pragma unroll
-    for (int i = 0; i < FM; i++) af[0][i] = *reinterpret_cast<const bf16x8*>(xs[0] + arow + i * 32 * RS + soff[0]);
+    for (int i = 0; i < FM; i++) af[0][i] = *reinterpret_cast<const bf16x8*>(xs[0] + arow + i * 32 * RS + soff2[i & 1][0]);
 #pragma unroll
-    for (int j = 0; j < FN; j++) bv[0][j] = *reinterpret_cast<const bf16x8*>(wsm[0] + brow + j * 32 * RS + soff[0]);
+    for (int j = 0; j < FN; j++) bv[0][j] = *reinterpret_cast<const bf16x8*>(wsm[0] + brow + j * 32 * RS + soff2[j & 1][0]);
     for (int ks = ks0; ks < ks1; ks++) {
       // scale chunks: table of step ks+2 written now (published by this
       // step's barriers), loads for step ks+3 issued a step ahead
@@ -555,20 +568,20 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
         if (s + 1 < NPART) {
 #pragma unroll
           for (int i = 0; i < FM; i++)
-            af[cur ^ 1][i] = *reinterpret_cast<const bf16x8*>(xb + arow + i * 32 * RS + soff[s + 1]);
+            af[cur ^ 1][i] = *reinterpret_cast<const bf16x8*>(xb + arow + i * 32 * RS + soff2[i & 1][s + 1]);
 #pragma unroll
           for (int j = 0; j < FN; j++)
-            bv[cur ^ 1][j] = *reinterpret_cast<const bf16x8*>(wb + brow + j * 32 * RS + soff[s + 1]);
+            bv[cur ^ 1][j] = *reinterpret_cast<const bf16x8*>(wb + brow + j * 32 * RS + soff2[j & 1][s + 1]);
         } else {
           // first fragments of step ks+1 (published by the barrier after slice 1)
           const uint16_t* xn = xs[buf ^ 1];
           const uint16_t* wnx = wsm[buf ^ 1];
 #pragma unroll
           for (int i = 0; i < FM; i++)
-            af[cur ^ 1][i] = *reinterpret_cast<const bf16x8*>(xn + arow + i * 32 * RS + soff[0]);
+            af[cur ^ 1][i] = *reinterpret_cast<const bf16x8*>(xn + arow + i * 32 * RS + soff2[i & 1][0]);
 #pragma unroll
           for (int j = 0; j < FN; j++)
-            bv[cur ^ 1][j] = *reinterpret_cast<const bf16x8*>(wnx + brow + j * 32 * RS + soff[0]);
+            bv[cur ^ 1][j] = *reinterpret_cast<const bf16x8*>(wnx + brow + j * 32 * RS + soff2[j & 1][0]);
         }
 #pragma unroll
         for (int i = 0; i < FM; i++)
