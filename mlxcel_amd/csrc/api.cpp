@@ -1534,7 +1534,6 @@ mlxq_status mlxq_dequantize(const mlxq_array* w, const mlxq_array* scales, const
     Shape oshape = wv.shape();
     oshape.back() = wv.dim(-1) * 32 / bits;
     check_out(out, oshape, out_type, tag);
-    if (mode == NVFP4_M || mode == MXFP8_M) unsupported("dequantize: only affine and mxfp4 are implemented");
     if (mode == AFFINE && bits != 2 && bits != 4 && bits != 6 && bits != 8)
       unsupported("dequantize: affine bits 2, 4, 6 and 8 are implemented");
     if (out_type != MLXQ_BFLOAT16) unsupported("dequantize: only bfloat16 output is implemented");
@@ -1556,10 +1555,16 @@ mlxq_status mlxq_dequantize(const mlxq_array* w, const mlxq_array* scales, const
                                                static_cast<const uint16_t*>(biases->data),
                                                static_cast<uint16_t*>(out->data), rows, K, group_size, bits, stream),
                 "dequantize launch");
-    } else {
+    } else if (mode == MXFP4_M) {
       hip_check(mlxq::launch_mxfp4_dequantize(static_cast<const uint32_t*>(w->data),
                                               static_cast<const uint8_t*>(scales->data),
                                               static_cast<uint16_t*>(out->data), rows, K, stream),
+                "dequantize launch");
+    } else {
+      hip_check(mlxq::launch_fp_dequantize(mode == MXFP8_M ? mlxq::FP_MXFP8 : mlxq::FP_NVFP4,
+                                           static_cast<const uint32_t*>(w->data),
+                                           static_cast<const uint8_t*>(scales->data),
+                                           static_cast<uint16_t*>(out->data), rows, K, stream),
                 "dequantize launch");
     }
   });
@@ -1624,7 +1629,6 @@ mlxq_status mlxq_quantize(const mlxq_array* w, int32_t group_size, int32_t bits,
     check_out(wq_out, qs, MLXQ_UINT32, tag);
     check_out(scales_out, ss, mode == AFFINE ? w->dtype : (int)MLXQ_UINT8, tag);
     if (mode == AFFINE) check_out(biases_out, ss, w->dtype, tag);
-    if (mode == NVFP4_M || mode == MXFP8_M) unsupported("quantize: only affine and mxfp4 are implemented");
     if (mode == AFFINE && bits != 2 && bits != 4 && bits != 6 && bits != 8)
       unsupported("quantize: affine bits 2, 4, 6 and 8 are implemented");
     if (w->dtype != MLXQ_BFLOAT16) unsupported("quantize: only bfloat16 weights are implemented");
@@ -1640,10 +1644,15 @@ mlxq_status mlxq_quantize(const mlxq_array* w, int32_t group_size, int32_t bits,
                                              static_cast<uint16_t*>(biases_out->data), rows, K, group_size, bits,
                                              stream),
                 "quantize launch");
-    } else {
+    } else if (mode == MXFP4_M) {
       hip_check(mlxq::launch_mxfp4_quantize(static_cast<const uint16_t*>(w->data),
                                             static_cast<uint32_t*>(wq_out->data),
                                             static_cast<uint8_t*>(scales_out->data), rows, K, stream),
+                "quantize launch");
+    } else {
+      hip_check(mlxq::launch_fp_quantize(mode == MXFP8_M ? mlxq::FP_MXFP8 : mlxq::FP_NVFP4,
+                                         static_cast<const uint16_t*>(w->data), static_cast<uint32_t*>(wq_out->data),
+                                         static_cast<uint8_t*>(scales_out->data), rows, K, stream),
                 "quantize launch");
     }
   });

@@ -14,7 +14,13 @@
 //    bf16 as MLX evaluates it; the shared exponent is the smallest e with
 //    2^e >= bf16(max|w| / 6), which is what round(log2) + the round-up step
 //    produce for every normal scale.
-// All four are HBM-bound streaming kernels (one word or one group per lane group).
+//  * mxfp8 / nvfp4 (e4m3 codes with e8m0 scales per 32 / e2m1 codes with e4m3
+//    scales per 16, no global scale): the same graph fallbacks, with MLX's
+//    to_fp8 as the ROCm backend evaluates it
+//    (overlays/rocm/mlx/backend/rocm/quantized/convert_fp8.hip:18-90: half-up
+//    mantissa rounding, saturation to 448 except the NaN code for [464, 496),
+//    zero below 2^-9, truncated subnormals) and from_fp8's exact decode.
+// All are HBM-bound streaming kernels (one word or one group per lane group).
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -338,6 +344,231 @@ hipError_t launch_mxfp4_quantize(const uint16_t* w, uint32_t* wq, uint8_t* scale
   if (pieces == 0) return hipSuccess;
   hipLaunchKernelGGL(mxfp4_quant_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, stream, w,
                      wq, scales, pieces);
+  return hipGetLastError();
+}
+
+// ---- fp8 e4m3 ----------------------------------------------------------------
+
+// MLX to_fp8 on the ROCm backend (convert_fp8.hip:18-66), integer steps.
+__device__ __forceinline__ uint32_t e4m3_encode(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7Fu;  // NaN
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const int e = (int)((u >> 23) & 0xFFu) - 127;
+  const uint32_t frac = u & 0x7FFFFFu;
+  if (e < -9) return sign;
+  if (e > 8) return sign | 0x7Eu;
+  int be = e + 7;
+  uint32_t m = (frac + 0x80000u) >> 20;
+  if (m > 7u) {
+    m = 0u;
+    if (++be > 15) return sign | 0x7Eu;
+  }
+  if (be <= 0) {
+    m = (frac | 0x800000u) >> (20 + (1 - be));
+    be = 0;
+  }
+  return sign | ((uint32_t)be << 3) | (m & 7u);
+}
+
+// e4m3 code c as sign * M * 2^E (M < 16); false for the NaN codes
+__device__ __forceinline__ bool e4m3_fields(uint32_t c, uint32_t& sign, uint32_t& M, int& E) {
+  const uint32_t e = (c >> 3) & 15u, m = c & 7u;
+  sign = (c & 0x80u) << 8;
+  if (e == 15u && m == 7u) return false;
+  if (e == 0u) {
+    M = m;
+    E = -9;
+  } else {
+    M = 8u + m;
+    E = (int)e - 10;
+  }
+  return true;
+}
+
+__device__ __forceinline__ float e4m3_decode(uint32_t c) {
+  uint32_t sign, M;
+  int E;
+  if (!e4m3_fields(c, sign, M, E)) return __uint_as_float(0x7FC00000u);
+  const float v = __builtin_ldexpf((float)M, E);  // >= 2^-9: a normal float
+  return sign ? -v : v;
+}
+
+// bf16 bits of sign * M * 2^E (M < 16), rounded to nearest even; integer
+// arithmetic, so bf16 subnormal results do not depend on the float denormal mode
+__device__ __forceinline__ uint32_t bf16_scaled(uint32_t sign, uint32_t M, int E) {
+  if (M == 0u) return sign;
+  const int p = 31 - __clz((int)M);  // M = 1.f * 2^p
+  const int ex = E + p;
+  if (ex > 127) return sign | 0x7F80u;
+  if (ex >= -126) return sign | ((uint32_t)(ex + 127) << 7) | ((M - (1u << p)) << (7 - p));
+  const int sh = E + 133;  // subnormal: value / 2^-133 = M * 2^sh
+  if (sh >= 0) return sign | (M << sh);
+  const int r = -sh;
+  if (r > 5) return sign;  // below half the smallest subnormal
+  uint32_t q = M >> r;
+  const uint32_t rem = M & ((1u << r) - 1u), half = 1u << (r - 1);
+  if (rem > half || (rem == half && (q & 1u))) q++;
+  return sign | q;
+}
+
+// ---- mxfp8 dequantize: from_fp8(code) * 2^(s-127), one bf16 rounding ---------
+
+__global__ __launch_bounds__(256) void mxfp8_dequant_kernel(const uint32_t* __restrict__ w,
+                                                            const uint8_t* __restrict__ scales,
+                                                            uint16_t* __restrict__ out, int64_t npairs) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // 8 codes (2 words)
+  if (i >= npairs) return;
+  const u32x2 wd = *reinterpret_cast<const u32x2*>(w + 2 * i);
+  const uint32_t s = scales[i >> 2];  // 32 codes per scale
+  u32x4 o;
+#pragma unroll
+  for (int q = 0; q < 8; q++) {
+    const uint32_t c = (wd[q >> 2] >> (8 * (q & 3))) & 0xFFu;
+    uint32_t sign, M, bits;
+    int E;
+    if (s == 255u || !e4m3_fields(c, sign, M, E)) bits = 0x7FC0u;
+    else bits = bf16_scaled(sign, M, E + (int)s - 127);
+    if (q & 1) o[q >> 1] |= bits << 16;
+    else o[q >> 1] = bits;
+  }
+  *reinterpret_cast<u32x4*>(out + 8 * i) = o;
+}
+
+// ---- nvfp4 dequantize: LUT[code] * from_fp8(scale), exact in bf16 ------------
+
+__global__ __launch_bounds__(256) void nvfp4_dequant_kernel(const uint32_t* __restrict__ w,
+                                                            const uint8_t* __restrict__ scales,
+                                                            uint16_t* __restrict__ out, int64_t nwords) {
+  const float lut[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nwords) return;
+  const uint32_t word = w[i];
+  const float sc = e4m3_decode(scales[i >> 1]);  // 16 codes per scale
+  u32x4 o;
+#pragma unroll
+  for (int q = 0; q < 8; q++) {
+    const uint32_t c = (word >> (4 * q)) & 15u;
+    float v = lut[c & 7u] * sc;  // products of <= 6 significant bits: exact
+    if (c & 8u) v = -v;
+    const uint32_t bits = f32_to_bf16_bits(v);
+    if (q & 1) o[q >> 1] |= bits << 16;
+    else o[q >> 1] = bits;
+  }
+  *reinterpret_cast<u32x4*>(out + 8 * i) = o;
+}
+
+hipError_t launch_fp_dequantize(int mode, const uint32_t* w, const uint8_t* scales, uint16_t* out, int64_t rows,
+                                int64_t K, hipStream_t stream) {
+  if (mode == FP_MXFP8) {
+    const int64_t n = rows * K / 8;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(mxfp8_dequant_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, w, scales,
+                       out, n);
+  } else {
+    const int64_t n = rows * K / 8;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(nvfp4_dequant_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, w, scales,
+                       out, n);
+  }
+  return hipGetLastError();
+}
+
+// ---- mxfp8 quantize: 4 lanes per group of 32, 8 values (2 words) per lane ----
+
+__global__ __launch_bounds__(256) void mxfp8_quant_kernel(const uint16_t* __restrict__ w,
+                                                          uint32_t* __restrict__ wq,
+                                                          uint8_t* __restrict__ scales, int64_t n_pieces) {
+  const int64_t piece = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool live = piece < n_pieces;
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (live) v = *reinterpret_cast<const u32x4*>(w + piece * 8);
+  float vals[8];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    vals[2 * i] = bf16_bits_to_f32(v[i] & 0xFFFFu);
+    vals[2 * i + 1] = bf16_bits_to_f32(v[i] >> 16);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const float a = fabsf(vals[i]);
+    amax = (amax < a) ? a : amax;
+  }
+#pragma unroll
+  for (int off = 1; off < 4; off <<= 1) {
+    const float o = __shfl_xor(amax, off);
+    amax = (amax < o) ? o : amax;
+  }
+  const float s = bfr(amax / 448.0f);
+  const int e = (s == 0.0f) ? 0 : ceil_log2_pos(s);
+  const float p = bf16_bits_to_f32(e >= -126 ? (uint32_t)(e + 127) << 7 : (0x40u >> (-127 - e)));
+  u32x2 out = {0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 8; i++) out[i >> 2] |= e4m3_encode(bfr(vals[i] / p)) << (8 * (i & 3));
+  if (live) *reinterpret_cast<u32x2*>(wq + 2 * piece) = out;
+  if (live && (piece & 3) == 0) scales[piece >> 2] = (uint8_t)(e + 127);
+}
+
+// ---- nvfp4 quantize: 2 lanes per group of 16, 8 values (1 word) per lane ----
+
+__global__ __launch_bounds__(256) void nvfp4_quant_kernel(const uint16_t* __restrict__ w,
+                                                          uint32_t* __restrict__ wq,
+                                                          uint8_t* __restrict__ scales, int64_t n_pieces) {
+  const float lut[16] = {+0.0f, +0.5f, +1.0f, +1.5f, +2.0f, +3.0f, +4.0f, +6.0f,
+                         -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
+  const int64_t piece = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool live = piece < n_pieces;
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (live) v = *reinterpret_cast<const u32x4*>(w + piece * 8);
+  float vals[8];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    vals[2 * i] = bf16_bits_to_f32(v[i] & 0xFFFFu);
+    vals[2 * i + 1] = bf16_bits_to_f32(v[i] >> 16);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const float a = fabsf(vals[i]);
+    amax = (amax < a) ? a : amax;
+  }
+  const float o = __shfl_xor(amax, 1);
+  amax = (amax < o) ? o : amax;
+  const uint32_t sc = e4m3_encode(bfr(amax / 6.0f));
+  const float d = e4m3_decode(sc);
+  uint32_t word = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    // bf16 quotient; float32 distances (exact); the first minimum wins, and a
+    // NaN or infinite quotient (zero scale) keeps code 0
+    const float x = bfr(vals[i] / d);
+    int best = 0;
+    float best_d = INFINITY;
+#pragma unroll
+    for (int c = 0; c < 16; c++) {
+      const float dist = fabsf(x - lut[c]);
+      if (dist < best_d) {
+        best_d = dist;
+        best = c;
+      }
+    }
+    word |= (uint32_t)best << (4 * i);
+  }
+  if (live) wq[piece] = word;
+  if (live && (piece & 1) == 0) scales[piece >> 1] = (uint8_t)sc;
+}
+
+hipError_t launch_fp_quantize(int mode, const uint16_t* w, uint32_t* wq, uint8_t* scales, int64_t rows, int64_t K,
+                              hipStream_t stream) {
+  const int64_t pieces = rows * K / 8;
+  if (pieces == 0) return hipSuccess;
+  if (mode == FP_MXFP8)
+    hipLaunchKernelGGL(mxfp8_quant_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, stream, w, wq,
+                       scales, pieces);
+  else
+    hipLaunchKernelGGL(nvfp4_quant_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, stream, w, wq,
+                       scales, pieces);
   return hipGetLastError();
 }
 

@@ -53,11 +53,17 @@ def _declare(l: ctypes.CDLL) -> None:
         "oracle_gather_qmm_t": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _I, _P],
         "oracle_affine_dequantize_f32": [_P, _P, _P, _I64, _I64, _I, _I, _P],
         "oracle_fused_moe": [_P] * 12 + [_I64] * 4 + [_I] * 4 + [_P],
+        "oracle_e4m3_encode_n": [_P, _P, _I64],
+        "oracle_e4m3_decode_n": [_P, _P, _I64],
+        "oracle_mxfp8_quantize": [_P, _I64, _I64, _P, _P],
+        "oracle_mxfp8_dequantize": [_P, _P, _I64, _I64, _P],
+        "oracle_nvfp4_quantize": [_P, _I64, _I64, _P, _P],
+        "oracle_nvfp4_dequantize": [_P, _P, _I64, _I64, _P],
     }
     for name, args in sig.items():
         fn = getattr(l, name)
         fn.argtypes = args
-        fn.restype = _I if name not in ("oracle_f32_to_bf16_n", "oracle_bf16_to_f32_n") else None
+        fn.restype = None if name.endswith("_n") else _I
     l.oracle_e8m0_to_bf16.argtypes = [ctypes.c_uint8]
     l.oracle_e8m0_to_bf16.restype = ctypes.c_uint16
 
@@ -251,3 +257,55 @@ def normal_bf16(shape, std: float, seed: int) -> np.ndarray:
     rng = np.random.Generator(np.random.Philox(seed))
     v = rng.standard_normal(n, dtype=np.float32) * np.float32(std)
     return f32_to_bf16(v).reshape(shape)
+
+
+# ---- fp8 e4m3, mxfp8, nvfp4 -------------------------------------------------
+
+def e4m3_encode(a) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.uint8)
+    lib().oracle_e4m3_encode_n(_ptr(a), _ptr(out), a.size)
+    return out
+
+
+def e4m3_decode(c) -> np.ndarray:
+    c = np.ascontiguousarray(c, dtype=np.uint8)
+    out = np.empty(c.shape, dtype=np.float32)
+    lib().oracle_e4m3_decode_n(_ptr(c), _ptr(out), c.size)
+    return out
+
+
+def _fp_quantize(fn, w_bf16, gs, bits):
+    w = np.ascontiguousarray(w_bf16, dtype=np.uint16)
+    K = w.shape[-1]
+    rows = w.size // K
+    wq = np.empty(w.shape[:-1] + (K * bits // 32,), dtype=np.uint32)
+    s = np.empty(w.shape[:-1] + (K // gs,), dtype=np.uint8)
+    _check(fn(_ptr(w), rows, K, _ptr(wq), _ptr(s)), "fp quantize")
+    return wq, s
+
+
+def _fp_dequantize(fn, wq, scales, bits):
+    wq = np.ascontiguousarray(wq, dtype=np.uint32)
+    scales = np.ascontiguousarray(scales, dtype=np.uint8)
+    K = wq.shape[-1] * 32 // bits
+    rows = wq.size // wq.shape[-1]
+    out = np.empty(wq.shape[:-1] + (K,), dtype=np.uint16)
+    _check(fn(_ptr(wq), _ptr(scales), rows, K, _ptr(out)), "fp dequantize")
+    return out
+
+
+def mxfp8_quantize(w_bf16):
+    return _fp_quantize(lib().oracle_mxfp8_quantize, w_bf16, 32, 8)
+
+
+def mxfp8_dequantize(wq, scales):
+    return _fp_dequantize(lib().oracle_mxfp8_dequantize, wq, scales, 8)
+
+
+def nvfp4_quantize(w_bf16):
+    return _fp_quantize(lib().oracle_nvfp4_quantize, w_bf16, 16, 4)
+
+
+def nvfp4_dequantize(wq, scales):
+    return _fp_dequantize(lib().oracle_nvfp4_dequantize, wq, scales, 4)

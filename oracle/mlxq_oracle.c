@@ -9,7 +9,8 @@
  * reference's scalar loops do on an x86 host without FMA contraction.
  * Citations: CPUQ = src/lib/mlxcelverse/overlays/cpu/mlx/backend/cpu/quantized.cpp,
  * ROPS = src/lib/mlxcelverse/overlays/rocm/mlx/ops.cpp,
- * QAFF = src/lib/mlxcelverse/overlays/rocm/mlx/backend/rocm/quantized/affine_quantize.hip.
+ * QAFF = src/lib/mlxcelverse/overlays/rocm/mlx/backend/rocm/quantized/affine_quantize.hip,
+ * FP8C = src/lib/mlxcelverse/overlays/rocm/mlx/backend/rocm/quantized/convert_fp8.hip.
  *
  * Parity pins (tests/test_oracle.py): hand-computed known answers, torch's
  * independent bf16 arithmetic for both dequantize roundings, exhaustive
@@ -243,6 +244,154 @@ int oracle_mxfp4_dequantize(const uint32_t* wq, const uint8_t* scales, int64_t r
         v = bf(FP4_LUT[code_at(row, 4, k)] * sc);
       }
       out[r * K + k] = oracle_f32_to_bf16(v);
+    }
+  }
+  return 0;
+}
+
+/* ---- fp8 e4m3 (MLX to_fp8 / from_fp8) ------------------------------------- */
+
+/* The ROCm backend's to_fp8 encoder, FP8C:18-66 (float_to_fp8_e4m3): NaN ->
+ * 0x7F; exponents below -9 -> signed zero; above 8 -> 0x7E (448); the 23-bit
+ * mantissa rounded to 3 bits by adding half a unit and truncating (ties away
+ * from zero); a carry into the exponent past 15 -> 0x7E; results below the
+ * normal range keep (1.mant) >> (1 - exponent) truncated. */
+uint8_t oracle_e4m3_encode(float f) {
+  if (isnan(f)) return 0x7F;
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  const uint8_t sign = (uint8_t)((u >> 31) << 7);
+  const int e = (int)((u >> 23) & 0xFFu) - 127;
+  const uint32_t frac = u & 0x7FFFFFu;
+  if (e < -9) return sign;
+  if (e > 8) return sign | 0x7E;
+  int be = e + 7;                      /* biased e4m3 exponent */
+  uint32_t m = (frac + 0x80000u) >> 20; /* 3 mantissa bits, half-up */
+  if (m > 7) {
+    m = 0;
+    if (++be > 15) return sign | 0x7E;
+  }
+  if (be <= 0) {
+    m = (frac | 0x800000u) >> (20 + (1 - be));
+    be = 0;
+  }
+  return sign | (uint8_t)((be & 0xF) << 3) | (uint8_t)(m & 7u);
+}
+
+/* FP8C:68-90 (fp8_e4m3_to_float): e4m3fn, exponent bias 7, no infinities,
+ * 0x7F / 0xFF NaN, subnormals m * 2^-9. */
+float oracle_e4m3_decode(uint8_t c) {
+  const int e = (c >> 3) & 0xF, m = c & 7;
+  float v;
+  if (e == 15 && m == 7) return NAN;
+  if (e == 0) v = ldexpf((float)m, -9);
+  else v = ldexpf((float)(8 + m), e - 10);
+  return (c & 0x80) ? -v : v;
+}
+
+void oracle_e4m3_encode_n(const float* in, uint8_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; i++) out[i] = oracle_e4m3_encode(in[i]);
+}
+
+void oracle_e4m3_decode_n(const uint8_t* in, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; i++) out[i] = oracle_e4m3_decode(in[i]);
+}
+
+/* The e8m0 exponent of the mx graph quantizers (ROPS:5384-5396) for the bf16
+ * scale s: round(log2(s)) in bf16, plus one when 2^that is below s; 0 for s == 0. */
+static int mx_exponent(float s) {
+  if (s == 0.0f) return 0;
+  int e = (int)rintf(bf(log2f(s)));
+  if (ldexpf(1.0f, e) < s) e += 1;
+  return e;
+}
+
+/* mxfp8 quantize, the graph fallback of ROPS:5364-5431 with bits 8, group 32:
+ * scale = bf16(max|w| / 448), e8m0 exponent as for mxfp4, codes =
+ * to_fp8(bf16(w / 2^e)) (FP8C encoder), 4 codes per uint32 low byte first
+ * (view as uint32). */
+int oracle_mxfp8_quantize(const uint16_t* w, int64_t rows, int64_t K, uint32_t* wq, uint8_t* scales) {
+  if (K % 32) return -1;
+  const int64_t n_groups = rows * (K / 32);
+  uint8_t* out = (uint8_t*)wq;
+  for (int64_t i = 0; i < n_groups; i++) {
+    const uint16_t* g = w + i * 32;
+    float amax = 0.0f;
+    for (int j = 0; j < 32; j++) amax = std_max(amax, fabsf(oracle_bf16_to_f32(g[j])));
+    const int e = mx_exponent(bf(amax / 448.0f));
+    const float p = bf(powf(2.0f, (float)e));
+    for (int j = 0; j < 32; j++) out[i * 32 + j] = oracle_e4m3_encode(bf(oracle_bf16_to_f32(g[j]) / p));
+    scales[i] = (uint8_t)(e + 127);
+  }
+  return 0;
+}
+
+/* mxfp8 dequantize, ROPS:5682, 5692-5695: from_fp8(byte) * 2^(s-127) in bf16,
+ * s == 0xFF -> NaN. */
+int oracle_mxfp8_dequantize(const uint32_t* wq, const uint8_t* scales, int64_t rows, int64_t K,
+                            uint16_t* out) {
+  if (K % 32) return -1;
+  const uint8_t* codes = (const uint8_t*)wq;
+  for (int64_t i = 0; i < rows * K; i++) {
+    const uint8_t s = scales[i / 32];
+    float v;
+    if (s == 0xFF) {
+      v = NAN;
+    } else {
+      const float sc = bf(powf(2.0f, bf((float)s - 127.0f)));
+      v = bf(bf(oracle_e4m3_decode(codes[i])) * sc);
+    }
+    out[i] = oracle_f32_to_bf16(v);
+  }
+  return 0;
+}
+
+/* nvfp4 quantize without a global scale, the graph fallback of
+ * ROPS:5364-5382, 5402-5424 with group 16: scale = bf16(max|w| / 6) (bf16
+ * divide), times the float32 1.0 of scale_encode (the product is float32),
+ * to_fp8 (FP8C encoder); w / from_fp8(scale) in bf16, times that float32 1.0
+ * (float32), so the LUT distances are float32 (exact); argmin keeps the first
+ * minimum (a zero scale gives NaN or infinite quotients whose distances never
+ * compare smaller: code 0). */
+int oracle_nvfp4_quantize(const uint16_t* w, int64_t rows, int64_t K, uint32_t* wq, uint8_t* scales) {
+  if (K % 16) return -1;
+  const int64_t n_groups = rows * (K / 16);
+  for (int64_t i = 0; i < n_groups; i++) {
+    const uint16_t* g = w + i * 16;
+    float amax = 0.0f;
+    for (int j = 0; j < 16; j++) amax = std_max(amax, fabsf(oracle_bf16_to_f32(g[j])));
+    const uint8_t sc = oracle_e4m3_encode(bf(amax / 6.0f));
+    const float d = bf(oracle_e4m3_decode(sc));
+    uint32_t words[2] = {0, 0};
+    for (int j = 0; j < 16; j++) {
+      const float v = bf(oracle_bf16_to_f32(g[j]) / d);
+      int best = 0;
+      float best_d = INFINITY;
+      for (int c = 0; c < 16; c++) {
+        const float dist = fabsf(v - FP4_LUT[c]);
+        if (dist < best_d) {
+          best_d = dist;
+          best = c;
+        }
+      }
+      words[j / 8] |= (uint32_t)best << (4 * (j % 8));
+    }
+    memcpy(wq + i * 2, words, sizeof(words));
+    scales[i] = sc;
+  }
+  return 0;
+}
+
+/* nvfp4 dequantize without a global scale, ROPS:5661-5690: LUT[nibble] *
+ * from_fp8(scale) in bf16 (exact). */
+int oracle_nvfp4_dequantize(const uint32_t* wq, const uint8_t* scales, int64_t rows, int64_t K,
+                            uint16_t* out) {
+  if (K % 16) return -1;
+  for (int64_t r = 0; r < rows; r++) {
+    const uint32_t* row = wq + r * (K / 8);
+    for (int64_t k = 0; k < K; k++) {
+      const float sc = bf(oracle_e4m3_decode(scales[r * (K / 16) + k / 16]));
+      out[r * K + k] = oracle_f32_to_bf16(bf(FP4_LUT[code_at(row, 4, k)] * sc));
     }
   }
   return 0;

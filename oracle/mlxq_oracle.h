@@ -53,6 +53,23 @@ int oracle_mxfp4_quantize(const uint16_t* w, int64_t rows, int64_t K, uint32_t* 
 int oracle_mxfp4_dequantize(const uint32_t* wq, const uint8_t* scales, int64_t rows,
                             int64_t K, uint16_t* out);
 
+/* fp8 e4m3 as MLX's to_fp8 / from_fp8 on the ROCm backend
+ * (overlays/rocm/mlx/backend/rocm/quantized/convert_fp8.hip:18-90). */
+uint8_t oracle_e4m3_encode(float f);
+float oracle_e4m3_decode(uint8_t c);
+void oracle_e4m3_encode_n(const float* in, uint8_t* out, int64_t n);
+void oracle_e4m3_decode_n(const uint8_t* in, float* out, int64_t n);
+
+/* mxfp8 (e4m3 codes, group 32, e8m0 scales) and nvfp4 (e2m1 codes, group 16,
+ * e4m3 scales, no global scale): the graph quantizer ROPS:5364-5431 and
+ * dequantizer ROPS:5646-5695.  wq: [rows, K*bits/32] u32, scales [rows, K/gs] u8. */
+int oracle_mxfp8_quantize(const uint16_t* w, int64_t rows, int64_t K, uint32_t* wq, uint8_t* scales);
+int oracle_mxfp8_dequantize(const uint32_t* wq, const uint8_t* scales, int64_t rows, int64_t K,
+                            uint16_t* out);
+int oracle_nvfp4_quantize(const uint16_t* w, int64_t rows, int64_t K, uint32_t* wq, uint8_t* scales);
+int oracle_nvfp4_dequantize(const uint32_t* wq, const uint8_t* scales, int64_t rows, int64_t K,
+                            uint16_t* out);
+
 /* `_qmm_t<bfloat16_t, bits, gs>`, CPUQ:199-257: y[m, n] = bf16(sum_k x*(s*q+b)),
  * float accumulation in MLX's loop order.  x: [M, K], w: [N, K*bits/32]. */
 int oracle_qmm_t_affine(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,

@@ -23,6 +23,11 @@ numpy/torch arithmetic:
 * mxfp4 hand cases (ops.cpp:5364-5431 worked by hand): the e8m0 exponent is
   ceil(log2(bf16(max|w| / 6))), the codes the first index of the minimum
   distance in FP4_LUT order (ties between neighbours, +0 before -0).
+* e4m3 hand cases (MLX to_fp8 on the ROCm backend, convert_fp8.hip:18-66,
+  worked by hand): half-up ties, saturation to 448 and the NaN code for
+  [464, 496), underflow below 2^-9, truncated subnormals and the subnormal
+  carry quirk.
+* mxfp8 / nvfp4 quantizer hand groups (ops.cpp:5364-5431 with those encoders).
 * dequant_d2: bf16(bf16(q * s) + b) evaluated with torch's bfloat16 ops (an
   independent implementation of MLX's bf16 arithmetic), on halfway cases.
 
@@ -180,6 +185,81 @@ def mxfp4_hand_cases():
             "mxfp4_hand_scales": np.array([[g[2] for g in MXFP4_HAND]], np.uint8)}
 
 
+# MLX to_fp8 on the ROCm backend (convert_fp8.hip:18-66) by hand: value ->
+# code.  The float's exponent e and 23-bit fraction f: e < -9 -> signed zero;
+# e > 8 -> 0x7E; else exponent field e + 7 and mantissa (f + 2^19) >> 20
+# (half-up), a mantissa of 8 carrying into the exponent (past 15 -> 0x7E);
+# an exponent field <= 0 instead takes (2^23 + f) >> (21 - field).
+E4M3_HAND = [
+    (1.0, 0x38),                  # field 7, mantissa 0
+    (1.0625, 0x39),               # 1 + 0.5/8: tie, half-up -> 1 (to-even would be 0)
+    (1.1875, 0x3A),               # 1 + 1.5/8 -> 2
+    (1.3125, 0x3B),               # 1 + 2.5/8: tie -> 3 (to-even would be 2)
+    (-3.0, 0xC4),                 # 1.5 * 2^1: field 8, mantissa 4, sign
+    (448.0, 0x7E),                # 1.75 * 2^8, the largest finite
+    (449.0, 0x7E),                # rounds to 1.75 * 2^8
+    (464.0, 0x7F),                # 1.8125 * 2^8 -> mantissa 7 in field 15: the NaN code
+    (495.0, 0x7F),
+    (496.0, 0x7E),                # mantissa 8 carries to field 16 -> 0x7E
+    (1.0e6, 0x7E), (float("inf"), 0x7E), (float("-inf"), 0xFE), (float("nan"), 0x7F),
+    (0.0, 0x00), (-0.0, 0x80),
+    (2.0 ** -6, 0x08),            # smallest normal
+    (2.0 ** -9, 0x01),            # smallest subnormal: field -2 -> (2^23) >> 23 = 1
+    (2.0 ** -10, 0x00),           # e = -10 < -9: zero
+    (1.5 * 2.0 ** -10, 0x00),     # also zero (nearest would be 2^-9)
+    (1.75 * 2.0 ** -9, 0x01),     # field -2: (1.75 * 2^23) >> 23 = 1, truncated
+    (1.5 * 2.0 ** -8, 0x03),      # field -1: (1.5 * 2^23) >> 22 = 3
+    (1.96875 * 2.0 ** -8, 0x07),  # mantissa carries to field 0, then (1.96875 * 2^23) >> 21 = 7
+    (1.96875 * 2.0 ** -9, 0x03),  # carries to field -1: >> 22 = 3
+    (1.96875 * 2.0 ** -7, 0x08),  # carries to field 1: the smallest normal
+]
+
+# mxfp8 groups (32 values): G1 max 448 -> scale bf16(448/448) = 1, exponent 0
+# (byte 127), codes = to_fp8(w); G2 max 1 -> bf16(1/448) = 1.140625 * 2^-9,
+# log2 = -8.81 -> bf16 -8.8125 -> round -9, 2^-9 < scale -> exponent -8 (byte
+# 119), codes = to_fp8(w * 256): 1 -> 256 = 0x78, -0.5 -> -128 = 0xF0,
+# 0.25 -> 64 = 0x68, 2^-16 -> 2^-8 = 2 * 2^-9 = 0x02; G3 zeros -> byte 127, codes 0.
+MXFP8_HAND = [
+    ([448.0, -448.0, 1.0, 1.0625, 1.3125, -3.0, 2.0 ** -9, 1.75 * 2.0 ** -9, 1.5 * 2.0 ** -8,
+      1.96875 * 2.0 ** -8, 2.0 ** -6, 0.0, -0.0] + [0.0] * 19,
+     [0x7E, 0xFE, 0x38, 0x39, 0x3B, 0xC4, 0x01, 0x01, 0x03, 0x07, 0x08, 0x00, 0x80] + [0x00] * 19, 127),
+    ([1.0, -0.5, 0.25, 2.0 ** -16] + [0.0] * 28, [0x78, 0xF0, 0x68, 0x02] + [0x00] * 28, 119),
+    ([0.0] * 32, [0x00] * 32, 127),
+]
+
+# nvfp4 groups (16 values, no global scale): N1 max 6 -> bf16(6/6) = 1 ->
+# to_fp8 0x38, divisor 1, codes = first nearest FP4_LUT index; N2 max 7 ->
+# bf16(7/6) = 1.1640625 -> to_fp8 0x39 (1.125): 7/1.125 -> bf16 6.21875 -> 6
+# (7), 1/1.125 -> 0.88671875 -> 1 (2), -2.8125/1.125 = -2.5: tie -> -2 (12),
+# 0.5625/1.125 = 0.5 (1); N3 zeros -> scale 0, 0/0 -> NaN -> code 0; N4 max
+# 6 * 2^-12 -> 2^-12 -> to_fp8 0 -> w/0 = +-inf -> code 0.
+NVFP4_HAND = [
+    ([6.0, -6.0, 5.0, 0.25, -0.25, 0.75, -0.75, 2.5, 3.5, 1.25, 1.75, -5.0, 0.0, -0.0, 1.0, -1.0],
+     [7, 15, 6, 0, 0, 1, 9, 4, 5, 2, 3, 14, 0, 0, 2, 10], 0x38),
+    ([7.0, 1.0, -2.8125, 0.5625] + [0.0] * 12, [7, 2, 12, 1] + [0] * 12, 0x39),
+    ([0.0] * 16, [0] * 16, 0x00),
+    ([6.0 * 2.0 ** -12, -2.0 ** -12] + [0.0] * 14, [0] * 16, 0x00),
+]
+
+
+def fp_hand_cases():
+    enc = np.array([v for v, _ in E4M3_HAND], np.float32)
+    out = {"e4m3_hand_in": enc, "e4m3_hand_code": np.array([c for _, c in E4M3_HAND], np.uint8)}
+    w = np.array([g[0] for g in MXFP8_HAND], np.float32)
+    wb = bf16_bits(w)
+    assert np.array_equal(torch.from_numpy(wb.astype(np.int16)).view(torch.bfloat16).float().numpy(), w)
+    out["mxfp8_hand_w"] = wb
+    out["mxfp8_hand_wq"] = np.ascontiguousarray(np.array([g[1] for g in MXFP8_HAND], np.uint8)).view(np.uint32)
+    out["mxfp8_hand_scales"] = np.array([[g[2]] for g in MXFP8_HAND], np.uint8)
+    w = np.array([g[0] for g in NVFP4_HAND], np.float32)
+    wb = bf16_bits(w)
+    assert np.array_equal(torch.from_numpy(wb.astype(np.int16)).view(torch.bfloat16).float().numpy(), w)
+    out["nvfp4_hand_w"] = wb
+    out["nvfp4_hand_wq"] = pack(np.array([g[1] for g in NVFP4_HAND], np.int64), 4)
+    out["nvfp4_hand_scales"] = np.array([[g[2]] for g in NVFP4_HAND], np.uint8)
+    return out
+
+
 def dequant_d2_cases():
     rng = np.random.default_rng(2248)
     n = 4096
@@ -205,6 +285,7 @@ def main():
             out[f"ramp_b_b{bits}_g{gs}"] = b
     out.update(affine_hand_cases())
     out.update(mxfp4_hand_cases())
+    out.update(fp_hand_cases())
     q, s, b, d2 = dequant_d2_cases()
     out.update(d2_q=q, d2_s=s, d2_b=b, d2_out=d2)
     np.savez_compressed(os.path.join(HERE, "kat.npz"), **out)

@@ -6,7 +6,11 @@
   quantized.cpp:1233-1305) and the mxfp4 graph quantizer (ops.cpp:5364-5431),
   plus the hand-derived ramp fixtures;
 * dequantize(slice) == slice(dequantize) (src/lib/mlxcel-core/src/ffi_tests.rs:5108-5170);
-* affine bits 2, 4, 6 (MLX's 3-byte packs of 4 codes) and 8.
+* affine bits 2, 4, 6 (MLX's 3-byte packs of 4 codes) and 8;
+* mxfp8 and nvfp4 (e4m3 as the ROCm backend's to_fp8 / from_fp8 evaluate it,
+  overlays/rocm/mlx/backend/rocm/quantized/convert_fp8.hip:18-90): quantize
+  on wide-range data and the hand fixtures, dequantize over every code and
+  every scale.
 """
 import os
 
@@ -121,3 +125,84 @@ def test_quantize_dequantize_roundtrip_full_size():
     d = mq.dequantize(wq, s, b, 64, 4).float()
     err = (d - w.float()).abs().reshape(14336, 64, 64)
     assert float((err / s.float().abs().unsqueeze(-1)).max()) <= 1.6
+
+
+# ---- mxfp8 / nvfp4 (e4m3 via the ROCm backend's to_fp8, convert_fp8.hip:18-90) ----
+
+def wide_bf16(rows, K, seed):
+    # N(0, 0.02) rows plus rows spanning 1e-6 .. 1e3 per group, zeros and a
+    # few groups with one large outlier (saturation, subnormal codes)
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((rows, K)).astype(np.float32) * np.float32(0.02)
+    x[rows // 2:] *= (10.0 ** rng.uniform(-4, 5, (rows - rows // 2, K // 16, 1))).repeat(16, -1).reshape(-1, K) \
+        .astype(np.float32)
+    x[0, :64] = 0.0
+    x[1, 5] = 300.0
+    return orc.f32_to_bf16(x)
+
+
+@pytest.mark.parametrize("mode", ["mxfp8", "nvfp4"])
+def test_fp_quantize_bitexact(mode):
+    announce("quant", mode)
+    w = wide_bf16(96, 2048, 560 + len(mode))
+    wq, sc = mq.quantize(dev_bf16(w), mode=mode)
+    ewq, esc = (orc.mxfp8_quantize if mode == "mxfp8" else orc.nvfp4_quantize)(w)
+    np.testing.assert_array_equal(sc.cpu().numpy(), esc)
+    np.testing.assert_array_equal(wq.cpu().numpy(), ewq)
+
+
+def test_fp_quantize_hand_cases():
+    announce("quant_fp_hand")
+    for mode in ("mxfp8", "nvfp4"):
+        wq, sc = mq.quantize(dev_bf16(KAT[f"{mode}_hand_w"]), mode=mode)
+        np.testing.assert_array_equal(wq.cpu().numpy(), KAT[f"{mode}_hand_wq"])
+        np.testing.assert_array_equal(sc.cpu().numpy(), KAT[f"{mode}_hand_scales"])
+
+
+def test_mxfp8_dequantize_every_code_and_scale():
+    # all 256 codes under all 256 scales (bf16 subnormal products included)
+    announce("dequant_mxfp8_table")
+    codes = np.tile(np.arange(256, dtype=np.uint8), (256, 1))
+    wq = np.ascontiguousarray(codes).view(np.uint32).reshape(256, 64)
+    sc = np.repeat(np.arange(256, dtype=np.uint8)[:, None], 8, 1)
+    got = host_u16(mq.dequantize(dev_u32(wq), dev_u8(sc), None, 32, 8, "mxfp8"))
+    np.testing.assert_array_equal(got, orc.mxfp8_dequantize(wq, sc))
+
+
+def test_nvfp4_dequantize_every_code_and_scale():
+    announce("dequant_nvfp4_table")
+    wq = np.zeros((256, 2), np.uint32)
+    for j in range(16):
+        wq[:, j // 8] |= np.uint32(j) << np.uint32(4 * (j % 8))
+    sc = np.arange(256, dtype=np.uint8).reshape(256, 1)
+    got = host_u16(mq.dequantize(dev_u32(wq), dev_u8(sc), None, 16, 4, "nvfp4"))
+    np.testing.assert_array_equal(got, orc.nvfp4_dequantize(wq, sc))
+
+
+@pytest.mark.parametrize("mode", ["mxfp8", "nvfp4"])
+def test_fp_dequantize_random_and_roundtrip(mode):
+    announce("dequant_fp", mode)
+    w = wide_bf16(64, 2880, 570 + len(mode))
+    wq, sc = (orc.mxfp8_quantize if mode == "mxfp8" else orc.nvfp4_quantize)(w)
+    got = host_u16(mq.dequantize(dev_u32(wq), dev_u8(sc), None, None, None, mode))
+    np.testing.assert_array_equal(got, (orc.mxfp8_dequantize if mode == "mxfp8" else orc.nvfp4_dequantize)(wq, sc))
+    # quantize -> dequantize on the GPU at a full expert shape, within the
+    # format's error: mxfp8 half a 3-bit mantissa step (2^-4 relative, 2^-3
+    # bound) plus the truncated subnormal codes (a few 2^-9 * 2^e, below
+    # 2^-12 * max|w| of the group); nvfp4, with d the decoded e4m3 scale of
+    # the group, half the largest code step (d) or, where |w| / d passed 6
+    # (the scale rounded down, or truncated in e4m3's subnormal range),
+    # |w| - 6 d
+    wd = torch.randn(2880, 5760, device="cuda").mul_(0.02).to(torch.bfloat16)
+    q, s = mq.quantize(wd, mode=mode)
+    d = mq.dequantize(q, s, None, None, None, mode).float()
+    err = (d - wd.float()).abs()
+    gs = 32 if mode == "mxfp8" else 16
+    amax = wd.float().abs().reshape(2880, -1, gs).amax(-1, keepdim=True).expand(-1, -1, gs).reshape(2880, -1)
+    if mode == "mxfp8":
+        bound = wd.float().abs() * 2.0 ** -3 + 2.0 ** -12 * amax
+    else:
+        table = torch.from_numpy(orc.e4m3_decode(np.arange(256, dtype=np.uint8))).cuda()
+        dsc = table[s.long()].repeat_interleave(gs, -1)
+        bound = torch.maximum(dsc, wd.float().abs() - 6 * dsc) * (1 + 2.0 ** -7)
+    assert bool((err <= bound).all())

@@ -456,3 +456,92 @@ def test_fused_moe_invariants(orc):
                                f(np.array([2], np.uint32), np.array([0.75], np.float32)), rtol=1e-5, atol=1e-6)
     # out-of-range expert ids are clamped to the last expert
     np.testing.assert_array_equal(f(np.array([9], np.uint32), s1[:1]), f(np.array([E - 1], np.uint32), s1[:1]))
+
+
+# ---- fp8 e4m3, mxfp8, nvfp4 ----------------------------------------------------
+
+def e4m3_value(c):
+    """e4m3fn code -> value from the format definition (bias 7, no infinities,
+    0x7F / 0xFF NaN, subnormals m * 2^-9), in float64."""
+    c = np.asarray(c, np.int64)
+    s = np.where(c & 0x80, -1.0, 1.0)
+    e, m = (c >> 3) & 15, c & 7
+    v = np.where(e == 0, np.ldexp(m.astype(np.float64), -9), np.ldexp((8 + m).astype(np.float64), e - 10))
+    v = s * v
+    return np.where((e == 15) & (m == 7), np.nan, v)
+
+
+def test_e4m3_decode_exhaustive(orc):
+    codes = np.arange(256, dtype=np.uint8)
+    np.testing.assert_array_equal(orc.e4m3_decode(codes), e4m3_value(codes).astype(np.float32))
+
+
+def test_e4m3_encode_round_trips_every_finite_code(orc):
+    codes = np.array([c for c in range(256) if c not in (0x7F, 0xFF)], np.uint8)
+    np.testing.assert_array_equal(orc.e4m3_encode(e4m3_value(codes).astype(np.float32)), codes)
+
+
+def test_e4m3_encode_hand_cases(orc, kat):
+    # tests/golden/make_golden.py E4M3_HAND: half-up ties, saturation and the
+    # [464, 496) NaN code, underflow, truncated subnormals, the carry quirk
+    np.testing.assert_array_equal(orc.e4m3_encode(kat["e4m3_hand_in"]), kat["e4m3_hand_code"])
+
+
+def test_e4m3_encode_normal_range_is_nearest_ties_up(orc):
+    # in the normal range [2^-6, 448] the encoder returns the nearest e4m3
+    # value, ties to the larger magnitude (brute force over the codes)
+    pos = np.arange(0x08, 0x7F)
+    vals = e4m3_value(pos)
+    rng = np.random.default_rng(7)
+    x = np.concatenate([np.exp(rng.uniform(np.log(2.0 ** -6), np.log(448.0), 20000)),
+                        (vals[:-1] + vals[1:]) / 2])  # every midpoint
+    x = x.astype(np.float32).astype(np.float64)
+    x = x[(x >= 2.0 ** -6) & (x <= 448.0)]
+    d = np.abs(x[:, None] - vals[None, :])
+    best = d.min(1, keepdims=True)
+    want = np.where(d == best, pos[None, :], -1).max(1)  # ties: the larger code
+    for sgn in (1, -1):
+        got = orc.e4m3_encode((sgn * x).astype(np.float32)).astype(np.int64)
+        np.testing.assert_array_equal(got, want | (0x80 if sgn < 0 else 0))
+
+
+def test_mxfp8_and_nvfp4_quantize_hand_cases(orc, kat):
+    wq, sc = orc.mxfp8_quantize(kat["mxfp8_hand_w"])
+    np.testing.assert_array_equal(wq, kat["mxfp8_hand_wq"])
+    np.testing.assert_array_equal(sc, kat["mxfp8_hand_scales"])
+    wq, sc = orc.nvfp4_quantize(kat["nvfp4_hand_w"])
+    np.testing.assert_array_equal(wq, kat["nvfp4_hand_wq"])
+    np.testing.assert_array_equal(sc, kat["nvfp4_hand_scales"])
+
+
+def assert_bf16_equal_nan_any_sign(got, want):
+    # MLX's NaN sign through from_fp8 and the bf16 conversion is not pinned:
+    # NaN positions must match, other bits exactly
+    isnan = lambda b: (b & 0x7FFF) > 0x7F80
+    np.testing.assert_array_equal(isnan(got), isnan(want))
+    np.testing.assert_array_equal(got[~isnan(want)], want[~isnan(want)])
+
+
+def test_mxfp8_dequantize_table(orc):
+    # every code under scales 0, 1, 100, 127, 254, 255: from_fp8(code) *
+    # 2^(s-127), one bf16 rounding (float64 ldexp is exact), NaN for s == 255
+    codes = np.arange(256, dtype=np.uint8)
+    for s in (0, 1, 100, 127, 254, 255):
+        wq = np.tile(codes, 1).reshape(8, 32).copy().view(np.uint32)
+        sc = np.full((8, 1), s, np.uint8)
+        got = orc.mxfp8_dequantize(wq, sc).reshape(-1)
+        want = e4m3_value(codes) * (np.nan if s == 255 else 2.0 ** (s - 127))
+        assert_bf16_equal_nan_any_sign(got, bf16_from_torch(want.astype(np.float32)).reshape(-1))
+
+
+def test_nvfp4_dequantize_table(orc):
+    # 16 codes x every e4m3 scale: LUT[code] * e4m3(scale), exact in bf16
+    lut = np.array([0, .5, 1, 1.5, 2, 3, 4, 6, -0., -.5, -1, -1.5, -2, -3, -4, -6])
+    codes = np.arange(16, dtype=np.uint32)
+    wq = np.zeros((256, 2), np.uint32)
+    for j in range(16):
+        wq[:, j // 8] |= codes[j] << (4 * (j % 8))
+    sc = np.arange(256, dtype=np.uint8).reshape(256, 1)
+    got = orc.nvfp4_dequantize(wq, sc)
+    want = lut[None, :] * e4m3_value(np.arange(256))[:, None]
+    assert_bf16_equal_nan_any_sign(got, bf16_from_torch(want.astype(np.float32)))

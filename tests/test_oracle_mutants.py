@@ -89,6 +89,29 @@ def mxfp4_pins_pass(orc):
             and np.array_equal(sc, kat["mxfp4_hand_scales"]))
 
 
+FP8_MUTANTS = {
+    # round to nearest even instead of half-up
+    "e4m3_rne": ("uint32_t m = (frac + 0x80000u) >> 20; /* 3 mantissa bits, half-up */",
+                 "uint32_t m = (frac + 0x7FFFFu + ((frac >> 20) & 1u)) >> 20;"),
+    # round subnormals to nearest instead of truncating
+    "e4m3_sub_round": ("m = (frac | 0x800000u) >> (20 + (1 - be));",
+                       "m = ((frac | 0x800000u) + (1u << (19 + (1 - be)))) >> (20 + (1 - be));"),
+    # saturate at 448 instead of the NaN code for [464, 496)
+    "e4m3_no_nan": ("return sign | (uint8_t)((be & 0xF) << 3) | (uint8_t)(m & 7u);",
+                    "return (be == 15 && m == 7) ? (sign | 0x7E) : (sign | (uint8_t)((be & 0xF) << 3) | (uint8_t)(m & 7u));"),
+    # underflow one exponent early (2^-9 would become zero)
+    "e4m3_underflow": ("if (e < -9) return sign;", "if (e < -8) return sign;"),
+}
+
+
+def fp8_pins_pass(orc):
+    kat = np.load(GOLD)
+    if not np.array_equal(orc.e4m3_encode(kat["e4m3_hand_in"]), kat["e4m3_hand_code"]):
+        return False
+    wq, sc = orc.mxfp8_quantize(kat["mxfp8_hand_w"])
+    return np.array_equal(wq, kat["mxfp8_hand_wq"]) and np.array_equal(sc, kat["mxfp8_hand_scales"])
+
+
 @pytest.fixture
 def swap_lib(monkeypatch):
     def swap(lib):
@@ -100,6 +123,7 @@ def test_unmodified_source_passes(tmp_path, swap_lib):
     swap_lib(build(tmp_path, "original", None))
     assert quantizer_pins_pass(oracle)
     assert mxfp4_pins_pass(oracle)
+    assert fp8_pins_pass(oracle)
 
 
 @pytest.mark.parametrize("name", sorted(MUTANTS))
@@ -112,3 +136,9 @@ def test_mutant_is_rejected(tmp_path, swap_lib, name):
 def test_mxfp4_mutant_is_rejected(tmp_path, swap_lib, name):
     swap_lib(build(tmp_path, name, MXFP4_MUTANTS[name]))
     assert not mxfp4_pins_pass(oracle), f"mutant {name} passes the mxfp4 pins"
+
+
+@pytest.mark.parametrize("name", sorted(FP8_MUTANTS))
+def test_fp8_mutant_is_rejected(tmp_path, swap_lib, name):
+    swap_lib(build(tmp_path, name, FP8_MUTANTS[name]))
+    assert not fp8_pins_pass(oracle), f"mutant {name} passes the fp8 pins"
