@@ -224,7 +224,10 @@ mlxq_status mlxq_gather_qmm_shape(const mlxq_array* x, const mlxq_array* w,
 /* w_hat = dequantize(w, scales, biases), as mlx::core::dequantize
  * (ops.cpp:5753-5805).  Affine output is bit-exact to the MLX CPU graph
  * (ops.cpp:5531-5573): bf16(bf16(q*s) + b).  mxfp4 output is
- * LUT[q] * 2^(s-127) (exact; s == 255 gives NaN, ops.cpp:5692-5695).
+ * LUT[q] * 2^(s-127) (exact; s == 255 gives NaN, ops.cpp:5692-5695); mxfp8
+ * is from_fp8(q) * 2^(s-127) rounded once to bf16; nvfp4 (no global scale)
+ * LUT[q] * from_fp8(s) (exact) (ops.cpp:5661-5695; e4m3 decoding as
+ * rocm/quantized/convert_fp8.hip:68-90).
  * `dtype` < 0 selects the reference default (scales' dtype for affine,
  * bfloat16 for fp modes); only bfloat16 output is implemented. */
 mlxq_status mlxq_dequantize(const mlxq_array* w, const mlxq_array* scales,
@@ -233,9 +236,11 @@ mlxq_status mlxq_dequantize(const mlxq_array* w, const mlxq_array* scales,
 
 /* (wq, scales[, biases]) = quantize(w), as mlx::core::quantize
  * (ops.cpp:5454-5492).  Affine follows the MLX CPU quantizer
- * (overlays/cpu/.../quantized.cpp:1233-1305) bit-exactly; mxfp4 follows the
- * graph quantizer (ops.cpp:5364-5431).  `biases_out` is ignored for fp
- * modes.  Implemented for bfloat16 w. */
+ * (overlays/cpu/.../quantized.cpp:1233-1305) bit-exactly; mxfp4, mxfp8 and
+ * nvfp4 (without a global scale) follow the graph quantizer
+ * (ops.cpp:5364-5431) as the ROCm backend evaluates it, to_fp8 included
+ * (rocm/quantized/convert_fp8.hip:18-66).  `biases_out` is ignored for fp
+ * modes.  Implemented for bfloat16 w; affine bits 2, 4, 6 and 8. */
 mlxq_status mlxq_quantize(const mlxq_array* w, int32_t group_size, int32_t bits,
                           const char* mode, mlxq_array* wq_out, mlxq_array* scales_out,
                           mlxq_array* biases_out, void* stream);
