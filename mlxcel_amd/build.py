@@ -44,9 +44,11 @@ SOURCES = {
     "qmv_mid.hip": [],
     "qmm_group.hip": [],
     "qmm.hip": [],
+    "qmm_gen.hip": [],
     "qmm_rb.hip": [],
     "moe.hip": [],
     "bias.hip": [],
+    "copy.hip": [],
     "scratch.hip": [],
     "dequant.hip": ["-ffp-contract=off"],
 }

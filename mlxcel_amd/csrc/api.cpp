@@ -272,6 +272,8 @@ struct QmmSpec {
   int64_t K, N;
   int out_dtype;
   Shape out_shape;
+  bool transpose = true;
+  bool fast = true;  // the specialised kernels take the call (else qmm_gen.hip)
 };
 
 QmmSpec spec_quantized_matmul(const mlxq_array* xa, const mlxq_array* wa, const mlxq_array* sa,
@@ -283,6 +285,7 @@ QmmSpec spec_quantized_matmul(const mlxq_array* xa, const mlxq_array* wa, const 
   if (ba) check_array(ba, "biases");
   const char* tag = "quantized_matmul";
   QmmSpec sp;
+  sp.transpose = transpose;
   sp.mode = parse_mode(mode_str, tag);
   int dtype = validate_mode_with_type(tag, sa, ba, -1, sp.mode, mode_str);
   params_from_mode(sp.mode, gs, bits);
@@ -349,6 +352,7 @@ GatherSpec spec_gather(const mlxq_array* xa, const mlxq_array* wa, const mlxq_ar
   const char* tag = "gather_qmm";
   GatherSpec g;
   QmmSpec& sp = g.q;
+  sp.transpose = transpose;
   sp.mode = parse_mode(mode_str, tag);
   int out_type = validate_mode_with_type(tag, sa, ba, -1, sp.mode, mode_str);
   params_from_mode(sp.mode, gs, bits);
@@ -397,7 +401,6 @@ void check_out(const mlxq_array* out, const Shape& shape, int dtype, const char*
        << " but has shape " << fmt_shape(View{out}.shape()) << " and dtype " << dtype_name(out->dtype) << ".";
     invalid(os);
   }
-  if (!View{out}.row_contiguous()) unsupported(std::string(tag) + ": out must be row-contiguous");
 }
 
 void require_contiguous(const mlxq_array* a, const char* name) {
@@ -428,7 +431,9 @@ struct Workspace {
   std::vector<void*> retired;
   size_t retired_bytes = 0;
 };
-std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+// key: (device, stream, slot); slot 0 holds kernel scratch, slot 1 the
+// row-contiguous copies of strided operands
+std::map<std::tuple<int, hipStream_t, int>, Workspace> g_ws;
 
 int current_device() {
   int dev = 0;
@@ -479,7 +484,7 @@ struct ScratchSrc {
   size_t max = 0;
 };
 
-void* workspace(int dev, hipStream_t stream, size_t bytes, const ScratchSrc& src = ScratchSrc{}) {
+void* workspace(int dev, hipStream_t stream, size_t bytes, const ScratchSrc& src = ScratchSrc{}, int slot = 0) {
   if (src.fixed) {
     if (bytes > src.max)
       fail(MLXQ_ENOMEM, "[mlxq] this call needs " + std::to_string(bytes) +
@@ -487,7 +492,7 @@ void* workspace(int dev, hipStream_t stream, size_t bytes, const ScratchSrc& src
     return src.fixed;
   }
   std::lock_guard<std::mutex> lk(g_mu);
-  Workspace& w = g_ws[{dev, stream}];
+  Workspace& w = g_ws[{dev, stream, slot}];
   if (w.bytes >= bytes) return w.data;
   if (stream_capturing(stream))
     fail(MLXQ_ENOMEM, "[mlxq] this call needs " + std::to_string(bytes) + " bytes of workspace on a stream that is "
@@ -507,6 +512,7 @@ struct Knobs {
   int qmv_nw = 0, qmv_tk = 0, qmv_r = 0, b4_rg = 0, b4_cpw = 0;
   int qmm_min_rows = kQmmMinRows, qmm_tile = -1, qmm_ksplit = 0;
   int qmv_mid = 1, qmv_multi = 1;
+  int gen_ks = 0;  // K splits of the general kernel (0: planner)
   int gather_sorted = 1, gather_group = -1, gather_runs = 1, gather_direct = 1;
   std::string qmv_kernel;  // "", "rs", "b4", "mid", "fr", "mfma"
 };
@@ -529,6 +535,7 @@ const Knobs* read_knobs() {
   k->qmm_ksplit = env_int("MLXQ_QMM_KSPLIT", 0);
   k->qmv_mid = env_int("MLXQ_QMV_MID", 1);
   k->qmv_multi = env_int("MLXQ_QMV_MULTI", 1);
+  k->gen_ks = env_int("MLXQ_GEN_KS", 0);
   k->gather_sorted = env_int("MLXQ_GATHER_SORTED", 1);
   k->gather_group = env_int("MLXQ_GATHER_GROUP", -1);
   k->gather_runs = env_int("MLXQ_GATHER_RUNS", 1);
@@ -632,21 +639,52 @@ int fmt_of(Mode m, int bits) {
   return bits == 8 ? mlxq::AFF8 : mlxq::AFF4;
 }
 
-void require_kernel_support(const QmmSpec& sp, bool transpose, const char* tag) {
+int gen_type(int dt) {
+  if (dt == MLXQ_BFLOAT16) return mlxq::GEN_BF16;
+  if (dt == MLXQ_FLOAT16) return mlxq::GEN_F16;
+  if (dt == MLXQ_FLOAT32) return mlxq::GEN_F32;
+  return -1;
+}
+
+// Whether the specialised kernels take a validated call: transpose=true,
+// bfloat16 activations, scales, biases and result, affine 4- or 8-bit codes
+// in groups of 32/64/128 or mxfp4, K a multiple of 32.  (Operands are made
+// row-contiguous before the kernels run.)
+bool fast_route(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* scales, const mlxq_array* biases) {
+  if (!sp.transpose || sp.out_dtype != MLXQ_BFLOAT16 || x->dtype != MLXQ_BFLOAT16 || sp.K % 32 != 0) return false;
+  if (sp.mode == AFFINE)
+    return (sp.bits == 4 || sp.bits == 8) && (sp.gs == 32 || sp.gs == 64 || sp.gs == 128) &&
+           scales->dtype == MLXQ_BFLOAT16 && (!biases || biases->dtype == MLXQ_BFLOAT16);
+  return sp.mode == MXFP4_M && sp.gs == 32 && sp.bits == 4;
+}
+
+// What the general kernel (qmm_gen.hip) covers; anything else is refused
+// with MLXQ_EUNSUPPORTED (the caller falls back).
+void require_gen_support(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* scales, const mlxq_array* biases,
+                         const char* tag) {
   if (sp.mode == NVFP4_M || sp.mode == MXFP8_M)
     unsupported(std::string(tag) + ": mode '" + (sp.mode == NVFP4_M ? "nvfp4" : "mxfp8") + "' is not implemented");
   if (sp.mode == MXFP4_M && (sp.gs != 32 || sp.bits != 4))
     unsupported(std::string(tag) + ": mxfp4 needs group_size 32 and bits 4");
-  if (sp.mode == AFFINE && sp.bits != 4 && sp.bits != 8)
-    unsupported(std::string(tag) + ": affine bits " + std::to_string(sp.bits) + " is not implemented (4 and 8 are)");
+  if (sp.mode == AFFINE && sp.bits != 2 && sp.bits != 3 && sp.bits != 4 && sp.bits != 5 && sp.bits != 6 &&
+      sp.bits != 8)
+    unsupported(std::string(tag) + ": affine bits " + std::to_string(sp.bits) + " is not implemented");
   if (sp.mode == AFFINE && sp.gs != 32 && sp.gs != 64 && sp.gs != 128)
     unsupported(std::string(tag) + ": group_size must be 32, 64 or 128");
-  if (!transpose) unsupported(std::string(tag) + ": transpose=false is not implemented");
-  if (sp.out_dtype != MLXQ_BFLOAT16)
-    unsupported(std::string(tag) + ": only bfloat16 compute is implemented (result dtype " +
-                dtype_name(sp.out_dtype) + ")");
-  if (sp.K % 32 != 0) unsupported(std::string(tag) + ": K must be a multiple of 32");
+  if (gen_type(sp.out_dtype) < 0)
+    unsupported(std::string(tag) + ": result dtype " + dtype_name(sp.out_dtype) +
+                " is not implemented (bfloat16, float16 and float32 are)");
+  if (gen_type(x->dtype) < 0) unsupported(std::string(tag) + ": x dtype " + dtype_name(x->dtype) + " is not implemented");
+  if (sp.mode == AFFINE && (gen_type(scales->dtype) < 0 || (biases && gen_type(biases->dtype) < 0)))
+    unsupported(std::string(tag) + ": scales/biases dtype is not implemented");
   if (sp.K > (int64_t)1 << 30 || sp.N > (int64_t)1 << 30) unsupported(std::string(tag) + ": dimension too large");
+}
+
+// Route of a validated call: sets sp.fast, or refuses what no kernel covers.
+void choose_route(QmmSpec& sp, const mlxq_array* x, const mlxq_array* scales, const mlxq_array* biases,
+                  const char* tag) {
+  sp.fast = fast_route(sp, x, scales, biases) && sp.K <= ((int64_t)1 << 30) && sp.N <= ((int64_t)1 << 30);
+  if (!sp.fast) require_gen_support(sp, x, scales, biases, tag);
 }
 
 void require_dtype(const mlxq_array* a, int dt, const char* name, const char* tag) {
@@ -767,17 +805,148 @@ QmmSpec check_quantized_matmul(const mlxq_array* x, const mlxq_array* w, const m
                                const char* mode, const mlxq_array* out, const char* tag) {
   QmmSpec sp = spec_quantized_matmul(x, w, scales, biases, transpose, group_size, bits, mode);
   check_out(out, sp.out_shape, sp.out_dtype, tag);
-  require_kernel_support(sp, transpose, tag);
-  require_dtype(x, MLXQ_BFLOAT16, "x", tag);
-  if (sp.mode == AFFINE) {
-    require_dtype(scales, MLXQ_BFLOAT16, "scales", tag);
-    require_dtype(biases, MLXQ_BFLOAT16, "biases", tag);
-  }
-  require_contiguous(x, "x");
-  require_contiguous(w, "w");
-  require_contiguous(scales, "scales");
-  require_contiguous(biases, "biases");
+  choose_route(sp, x, scales, biases, tag);
   return sp;
+}
+
+// ---- row-contiguous staging of strided operands --------------------------
+
+bool needs_staging(const mlxq_array* a) {
+  if (!a || View{a}.size() == 0) return false;
+  return !View{a}.row_contiguous() || (reinterpret_cast<uintptr_t>(a->data) & 15u) != 0;
+}
+
+mlxq_array contiguous_like(const mlxq_array* a, void* data) {
+  mlxq_array c = *a;
+  c.data = data;
+  int64_t st = 1;
+  for (int i = a->ndim - 1; i >= 0; i--) {
+    c.strides[i] = st;
+    st *= a->shape[i];
+  }
+  return c;
+}
+
+void copy_view(const mlxq_array* src, const mlxq_array* dst, hipStream_t stream) {
+  mlxq::CopyArgs c{};
+  c.src = src->data;
+  c.dst = dst->data;
+  c.ndim = src->ndim;
+  c.esz = dtype_size(src->dtype);
+  c.n = View{src}.size();
+  for (int i = 0; i < src->ndim; i++) {
+    c.shape[i] = src->shape[i];
+    c.src_strides[i] = src->strides[i];
+    c.dst_strides[i] = dst->strides[i];
+  }
+  hip_check(mlxq::launch_strided_copy(c, stream), "strided copy launch");
+}
+
+// The operands of one call as the kernels need them: row-contiguous and
+// 16-byte aligned.  Others are first copied into the stream's staging
+// workspace (as the reference copies them, rocm/quantized/qmm.hip:3557-3564);
+// a strided `out` is computed into the staging buffer and copied back by
+// finish().  With allow = false (the no-allocation entry point) such
+// operands are refused instead.
+struct Staged {
+  const mlxq_array* in[4] = {nullptr, nullptr, nullptr, nullptr};  // x, w, scales, biases
+  mlxq_array* out = nullptr;
+  mlxq_array copies[5];
+  mlxq_array* user_out = nullptr;
+  hipStream_t stream = nullptr;
+  void finish() {
+    if (user_out) copy_view(out, user_out, stream);
+  }
+};
+
+Staged stage_operands(const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+                      const mlxq_array* biases, mlxq_array* out, hipStream_t stream, bool allow, const char* tag) {
+  Staged st;
+  st.stream = stream;
+  const mlxq_array* ops[4] = {x, w, scales, biases};
+  auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  bool need[5];
+  size_t bytes = 0;
+  for (int i = 0; i < 4; i++) {
+    st.in[i] = ops[i];
+    need[i] = needs_staging(ops[i]);
+    if (need[i]) bytes += al((size_t)View{ops[i]}.size() * dtype_size(ops[i]->dtype));
+  }
+  st.out = out;
+  need[4] = needs_staging(out);
+  if (need[4]) bytes += al((size_t)View{out}.size() * dtype_size(out->dtype));
+  if (bytes == 0) return st;
+  if (!allow) unsupported(std::string(tag) + ": operands must be row-contiguous and 16-byte aligned");
+  char* base = static_cast<char*>(workspace(current_device(), stream, bytes, ScratchSrc{}, 1));
+  size_t off = 0;
+  for (int i = 0; i < 4; i++) {
+    if (!need[i]) continue;
+    st.copies[i] = contiguous_like(ops[i], base + off);
+    off += al((size_t)View{ops[i]}.size() * dtype_size(ops[i]->dtype));
+    copy_view(ops[i], &st.copies[i], stream);
+    st.in[i] = &st.copies[i];
+  }
+  if (need[4]) {
+    st.copies[4] = contiguous_like(out, base + off);
+    st.out = &st.copies[4];
+    st.user_out = out;
+  }
+  return st;
+}
+
+// The general kernel (qmm_gen.hip) over nseg segments of M rows: segment s
+// multiplies x batch lhs[s] by weight matrix rhs[s] (flat index lists built
+// by index_prep from `ip`), or, with no `ip`, x batch 0 by matrix 0.
+void run_gen(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+             const mlxq_array* biases, mlxq_array* out, int64_t M, int64_t nseg, int64_t X, int64_t E,
+             mlxq::IdxPrepArgs* ip, hipStream_t stream, const ScratchSrc& ss) {
+  if (nseg == 0 || M == 0 || sp.N == 0) return;
+  if (sp.K == 0) unsupported("quantized_matmul: K == 0");
+  const int dev = current_device();
+  const mlxq::GenPlan p = mlxq::gen_plan(M, sp.N, sp.K, nseg, device_info(dev).cus, knobs().gen_ks);
+  if (!p.ok) unsupported("quantized matmul: too many row tiles or segments for one launch");
+  const int tc = gen_type(sp.out_dtype);
+  const int64_t out_elems = nseg * M * sp.N;
+  auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  const size_t idx_bytes = ip ? al((size_t)nseg * 2 * sizeof(uint32_t)) : 0;
+  const size_t part_bytes = p.ks > 1 ? (size_t)p.ks * out_elems * sizeof(float) : 0;
+  char* base = idx_bytes + part_bytes ? static_cast<char*>(workspace(dev, stream, idx_bytes + part_bytes, ss))
+                                      : nullptr;
+  mlxq::GenArgs a{};
+  if (ip) {
+    uint32_t* flat = reinterpret_cast<uint32_t*>(base);
+    ip->out[0] = flat;
+    ip->out[1] = flat + nseg;
+    hip_check(mlxq::launch_index_prep(*ip, stream), "index_prep launch");
+    a.lhs = flat;
+    a.rhs = flat + nseg;
+  }
+  a.x = x->data;
+  a.w = static_cast<const uint32_t*>(w->data);
+  a.scales = scales->data;
+  a.biases = biases ? biases->data : nullptr;
+  a.out = out->data;
+  a.ws = part_bytes ? reinterpret_cast<float*>(base + idx_bytes) : nullptr;
+  a.x_dtype = gen_type(x->dtype);
+  a.s_dtype = sp.mode == AFFINE ? gen_type(scales->dtype) : mlxq::GEN_BF16;
+  a.b_dtype = sp.mode == AFFINE && biases ? gen_type(biases->dtype) : a.s_dtype;
+  a.mode = sp.mode == MXFP4_M ? mlxq::GEN_MXFP4 : mlxq::GEN_AFFINE;
+  a.bits = sp.bits;
+  int shift = 0;
+  while ((1 << shift) < sp.gs) shift++;
+  a.gs_shift = shift;
+  a.M = (int)M;
+  a.N = (int)sp.N;
+  a.K = (int)sp.K;
+  a.X = (int)std::max<int64_t>(X, 1);
+  a.E = (int)std::max<int64_t>(E, 1);
+  a.x_vec = sp.K % 8 == 0;
+  View wv{w}, sv{scales};
+  a.w_expert_stride = wv.dim(-2) * wv.dim(-1);
+  a.s_expert_stride = sv.dim(-2) * sv.dim(-1);
+  a.out_elems = out_elems;
+  hip_check(mlxq::qmm_gen_launch(a, p, tc, sp.transpose, nseg, stream), "qmm_gen launch");
+  if (p.ks > 1) hip_check(mlxq::launch_gen_reduce(a.ws, out->data, out_elems, p.ks, tc, stream), "reduce launch");
 }
 
 // Enqueues one checked quantized_matmul call.
@@ -787,6 +956,38 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
   const int64_t rows_total = View{out}.size() / std::max<int64_t>(sp.N, 1);
   if (rows_total == 0 || sp.N == 0) return;
   if (sp.K == 0) unsupported("quantized_matmul: K == 0");
+  if (!sp.fast) {
+    View wv{w}, xv{x};
+    if (wv.ndim() == 2) {
+      // every leading dim of x folds into rows
+      run_gen(sp, x, w, scales, biases, out, rows_total, 1, 1, 1, nullptr, stream, ss);
+      return;
+    }
+    // batched weights: the default indices of gather_qmm over the broadcast
+    // batch shape (x batches and weight matrices broadcast against it)
+    if (xv.ndim() <= 2) unsupported("quantized_matmul: batched w needs batched x");
+    const Shape ob(sp.out_shape.begin(), sp.out_shape.end() - 2);
+    if ((int)ob.size() > MLXQ_MAX_DIMS) unsupported("quantized_matmul: batch rank too large");
+    mlxq::IdxPrepArgs ip{};
+    ip.bnd = (int)ob.size();
+    int64_t B = 1;
+    for (int d = 0; d < ip.bnd; d++) {
+      ip.bshape[d] = ob[d];
+      B *= ob[d];
+    }
+    ip.B = B;
+    const Shape dx = default_index_shape(xv), dw = default_index_shape(wv);
+    bstrides_for(nullptr, dx, ob, ip.bstrides[0]);
+    bstrides_for(nullptr, dw, ob, ip.bstrides[1]);
+    ip.dtype[0] = ip.dtype[1] = MLXQ_UINT32;
+    int64_t X = 1, E = 1;
+    for (auto d : dx) X *= d;
+    for (auto d : dw) E *= d;
+    ip.clamp[0] = std::max<int64_t>(X, 1);
+    ip.clamp[1] = std::max<int64_t>(E, 1);
+    run_gen(sp, x, w, scales, biases, out, xv.dim(-2), B, X, E, &ip, stream, ss);
+    return;
+  }
 
   mlxq::QmvArgs a{};
   a.x = static_cast<const uint16_t*>(x->data);
@@ -944,7 +1145,10 @@ mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w, cons
   return guarded([&] {
     const QmmSpec sp =
         check_quantized_matmul(x, w, scales, biases, transpose, group_size, bits, mode, out, "quantized_matmul");
-    run_quantized_matmul(sp, x, w, scales, biases, out, reinterpret_cast<hipStream_t>(stream_));
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    Staged st = stage_operands(x, w, scales, biases, out, stream, true, "quantized_matmul");
+    run_quantized_matmul(sp, st.in[0], st.in[1], st.in[2], st.in[3], st.out, stream);
+    st.finish();
   });
 }
 
@@ -954,10 +1158,13 @@ mlxq_status mlxq_quantized_matmul_noalloc(const mlxq_array* x, const mlxq_array*
   return guarded([&] {
     const QmmSpec sp = check_quantized_matmul(x, w, scales, biases, transpose, group_size, bits, mode, out,
                                               "quantized_matmul_noalloc");
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    // no staging buffer here: strided or misaligned operands are refused
+    stage_operands(x, w, scales, biases, out, stream, false, "quantized_matmul_noalloc");
     ScratchSrc ss;
     hip_check(mlxq::static_scratch(current_device(), &ss.fixed), "hipGetSymbolAddress(scratch)");
     ss.max = mlxq::static_scratch_bytes();
-    run_quantized_matmul(sp, x, w, scales, biases, out, reinterpret_cast<hipStream_t>(stream_), ss);
+    run_quantized_matmul(sp, x, w, scales, biases, out, stream, ss);
   });
 }
 
@@ -971,7 +1178,7 @@ mlxq_status mlxq_workspace_reserve(size_t bytes, void* stream_) {
     hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
     const int dev = current_device();
     std::lock_guard<std::mutex> lk(g_mu);
-    Workspace& w = g_ws[{dev, stream}];
+    Workspace& w = g_ws[{dev, stream, 0}];
     if (w.bytes >= bytes) return;
     if (stream_capturing(stream)) unsupported("mlxq_workspace_reserve: the stream is being captured");
     grow_workspace(w, bytes);
@@ -992,7 +1199,7 @@ mlxq_status mlxq_clear_cache(void) {
     hip_check(hipGetDevice(&cur), "hipGetDevice");
     std::map<int, bool> synced;
     for (auto& kv : g_ws) {
-      const int dev = kv.first.first;
+      const int dev = std::get<0>(kv.first);
       if (!synced[dev]) {
         hip_check(hipSetDevice(dev), "hipSetDevice");
         hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
@@ -1034,12 +1241,13 @@ mlxq_status mlxq_quantized_linear(const mlxq_array* x, const mlxq_array* w, cons
       require_contiguous(linear_bias, "linear_bias");
     }
     hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
-    run_quantized_matmul(sp, x, w, scales, biases, out, stream);
+    Staged st = stage_operands(x, w, scales, biases, out, stream, true, tag);
+    run_quantized_matmul(sp, st.in[0], st.in[1], st.in[2], st.in[3], st.out, stream);
     if (bias_n > 0 && View{out}.size() > 0)
-      hip_check(mlxq::launch_bias_add(static_cast<uint16_t*>(out->data),
-                                      static_cast<const uint16_t*>(linear_bias->data), View{out}.size(), bias_n,
-                                      stream),
+      hip_check(mlxq::launch_bias_add(st.out->data, linear_bias->data, View{out}.size(), bias_n,
+                                      gen_type(out->dtype), stream),
                 "bias add launch");
+    st.finish();
   });
 }
 
@@ -1082,7 +1290,11 @@ mlxq_status mlxq_quantized_matmul_multi(const mlxq_array* x, int32_t n, const ml
     // bit.  Otherwise the calls run one after another.
     const int fmt = fmt_of(sp[0].mode, sp[0].bits);
     const int64_t rows = View{out[0]}.size() / std::max<int64_t>(sp[0].N, 1);
-    bool fused = n > 1 && sp[0].K > 0 && rows >= 1 && rows < knobs().qmm_min_rows &&
+    bool plain = true;  // every projection on the specialised kernels, no operand to stage
+    for (int i = 0; i < n; i++)
+      plain = plain && sp[i].fast && !needs_staging(x) && !needs_staging(w[i]) && !needs_staging(scales[i]) &&
+              !needs_staging(biases ? biases[i] : nullptr) && !needs_staging(out[i]);
+    bool fused = plain && n > 1 && sp[0].K > 0 && rows >= 1 && rows < knobs().qmm_min_rows &&
                  rows <= mlxq::qmv_max_rows(fmt, sp[0].gs) && !use_mid((int)rows, fmt, sp[0].K) &&
                  skinny_choice((int)rows, fmt, sp[0].K) == Skinny::RS && knobs().qmv_multi != 0;
     mlxq::QmvRsPlan plan{};
@@ -1104,8 +1316,11 @@ mlxq_status mlxq_quantized_matmul_multi(const mlxq_array* x, int32_t n, const ml
       mp.out[i] = static_cast<uint16_t*>(out[i]->data);
     }
     if (!fused) {
-      for (int i = 0; i < n; i++)
-        run_quantized_matmul(sp[i], x, w[i], scales[i], biases ? biases[i] : nullptr, out[i], stream);
+      for (int i = 0; i < n; i++) {
+        Staged st = stage_operands(x, w[i], scales[i], biases ? biases[i] : nullptr, out[i], stream, true, tag);
+        run_quantized_matmul(sp[i], st.in[0], st.in[1], st.in[2], st.in[3], st.out, stream);
+        st.finish();
+      }
       return;
     }
     mlxq::QmvArgs a{};
@@ -1139,10 +1354,10 @@ mlxq_status mlxq_gather_qmm_shape(const mlxq_array* x, const mlxq_array* w, cons
   });
 }
 
-mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
-                            const mlxq_array* biases, const mlxq_array* lhs_indices, const mlxq_array* rhs_indices,
+mlxq_status mlxq_gather_qmm(const mlxq_array* x_, const mlxq_array* w_, const mlxq_array* scales_,
+                            const mlxq_array* biases_, const mlxq_array* lhs_indices, const mlxq_array* rhs_indices,
                             bool transpose, int32_t group_size, int32_t bits, bool sorted_indices, const char* mode,
-                            const mlxq_array* global_scale, mlxq_array* out, void* stream_) {
+                            const mlxq_array* global_scale, mlxq_array* out_, void* stream_) {
   // sorted_indices selects the routes that rely on rhs being non-decreasing
   // (after the uint32 cast); with a false promise their rows are unspecified
   if (!lhs_indices && !rhs_indices) {
@@ -1150,35 +1365,30 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq
       g_last_error = "[gather_qmm] Global scale is not supported without indices.";
       return MLXQ_EINVAL;
     }
-    return mlxq_quantized_matmul(x, w, scales, biases, transpose, group_size, bits, mode, out, stream_);
+    return mlxq_quantized_matmul(x_, w_, scales_, biases_, transpose, group_size, bits, mode, out_, stream_);
   }
   return guarded([&] {
     const char* tag = "gather_qmm";
-    GatherSpec g = spec_gather(x, w, scales, biases, lhs_indices, rhs_indices, transpose, group_size, bits, mode,
-                               global_scale);
+    GatherSpec g = spec_gather(x_, w_, scales_, biases_, lhs_indices, rhs_indices, transpose, group_size, bits,
+                               mode, global_scale);
     QmmSpec& sp = g.q;
-    check_out(out, sp.out_shape, sp.out_dtype, tag);
-    require_kernel_support(sp, transpose, tag);
+    check_out(out_, sp.out_shape, sp.out_dtype, tag);
+    choose_route(sp, x_, scales_, biases_, tag);
     if (global_scale) unsupported("gather_qmm: global_scale (nvfp4) is not implemented");
-    require_dtype(x, MLXQ_BFLOAT16, "x", tag);
-    if (sp.mode == AFFINE) {
-      require_dtype(scales, MLXQ_BFLOAT16, "scales", tag);
-      require_dtype(biases, MLXQ_BFLOAT16, "biases", tag);
-    }
-    require_contiguous(x, "x");
-    require_contiguous(w, "w");
-    require_contiguous(scales, "scales");
-    require_contiguous(biases, "biases");
     hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    Staged st = stage_operands(x_, w_, scales_, biases_, out_, stream, true, tag);
+    const mlxq_array* x = st.in[0];
+    const mlxq_array* w = st.in[1];
+    const mlxq_array* scales = st.in[2];
+    const mlxq_array* biases = st.in[3];
+    mlxq_array* out = st.out;
+    [&] {
     View xv{x}, wv{w}, sv{scales};
     const int64_t M = xv.dim(-2);
     int64_t B = 1;
     for (auto d : g.idx_shape) B *= d;
     if (B == 0 || M == 0 || sp.N == 0) return;
     if ((int)g.idx_shape.size() > MLXQ_MAX_DIMS) unsupported("gather_qmm: index rank too large");
-    const int fmt = fmt_of(sp.mode, sp.bits);
-    const int cap = mlxq::qmv_max_rows(fmt, sp.gs);
-    if (M > cap) unsupported("gather_qmm: more than " + std::to_string(cap) + " rows per gathered matrix");
     if (B > 65535) unsupported("gather_qmm: more than 65535 index entries");
     const int64_t X = xv.size() / std::max<int64_t>(M * sp.K, 1);
     const int64_t E = wv.size() / std::max<int64_t>(wv.dim(-2) * wv.dim(-1), 1);
@@ -1197,6 +1407,19 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq
     }
     ip.clamp[0] = std::max<int64_t>(X, 1);
     ip.clamp[1] = std::max<int64_t>(E, 1);
+
+    if (!sp.fast) {
+      run_gen(sp, x, w, scales, biases, out, M, B, X, E, &ip, stream, ScratchSrc{});
+      return;
+    }
+    const int fmt = fmt_of(sp.mode, sp.bits);
+    const int cap = mlxq::qmv_max_rows(fmt, sp.gs);
+    if (M > cap) {
+      // more rows per gathered matrix than the decode kernels stage: the
+      // general kernel tiles any row count
+      run_gen(sp, x, w, scales, biases, out, M, B, X, E, &ip, stream, ScratchSrc{});
+      return;
+    }
 
     const int dev = current_device();
     const DevInfo di = device_info(dev);
@@ -1455,6 +1678,8 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w, const mlxq
     a.kst_per_wg = p.kst_per_wg;
     if (p.ks > 1) a.ws = reinterpret_cast<float*>(wsb + idx_bytes);
     hip_check(mlxq::qmv_launch(fmt, sp.gs, a, (int)B, p, stream), "gather qmv launch");
+    }();
+    st.finish();
   });
 }
 

@@ -1,8 +1,8 @@
 // bias.hip — the linear bias of a quantized linear layer on gfx950.
 //
-// out[r][n] = bf16(out[r][n] + bias[n]) (or bias[r][n] for a full-shape bias):
-// MLX's `add` of two bf16 arrays, computed in fp32 and rounded to nearest even
-// once, as quantized_linear_forward applies it after quantized_matmul
+// out[r][n] = T(out[r][n] + bias[n]) (or bias[r][n] for a full-shape bias):
+// MLX's `add` of two arrays of the output type T, computed in fp32 and rounded
+// to nearest even once, as quantized_linear_forward applies it after quantized_matmul
 // (src/lib/mlxcel-core/cpp/mlx_cxx_bridge.cpp:1707-1746).  HBM-bound: one
 // read and one write of the output, one read of the bias; 8 elements a lane.
 #include "common.hpp"
@@ -32,9 +32,31 @@ __global__ __launch_bounds__(256) void bias_add_kernel(uint16_t* __restrict__ ou
   }
 }
 
-hipError_t launch_bias_add(uint16_t* out, const uint16_t* bias, int64_t n, int64_t bias_n, hipStream_t stream) {
+// float16 / float32 outputs: the same add in fp32, one element a thread
+template <typename T>
+__global__ __launch_bounds__(256) void bias_add_any_kernel(T* __restrict__ out, const T* __restrict__ bias, int64_t n,
+                                                           int64_t bias_n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  out[i] = (T)((float)out[i] + (float)bias[i % bias_n]);
+}
+
+hipError_t launch_bias_add(void* out_, const void* bias_, int64_t n, int64_t bias_n, int tc, hipStream_t stream) {
   if (n == 0) return hipSuccess;
   if (bias_n <= 0) return hipErrorInvalidValue;
+  if (tc == GEN_F16 || tc == GEN_F32) {
+    const unsigned blocks = (unsigned)((n + 255) / 256);
+    if (tc == GEN_F16)
+      hipLaunchKernelGGL(bias_add_any_kernel<_Float16>, dim3(blocks), dim3(256), 0, stream,
+                         static_cast<_Float16*>(out_), static_cast<const _Float16*>(bias_), n, bias_n);
+    else
+      hipLaunchKernelGGL(bias_add_any_kernel<float>, dim3(blocks), dim3(256), 0, stream, static_cast<float*>(out_),
+                         static_cast<const float*>(bias_), n, bias_n);
+    return hipGetLastError();
+  }
+  if (tc != GEN_BF16) return hipErrorInvalidValue;
+  uint16_t* out = static_cast<uint16_t*>(out_);
+  const uint16_t* bias = static_cast<const uint16_t*>(bias_);
   const int64_t lanes = (n + 7) / 8;
   const int vec = ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(bias)) & 15u) == 0 &&
                   bias_n % 8 == 0;

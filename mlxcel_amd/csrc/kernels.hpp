@@ -99,6 +99,58 @@ QmvRsPlan qmv_rs_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int r_req
 hipError_t qmv_rs_launch(int fmt, int gs, const QmvArgs& a, int nseg, const QmvRsPlan& p, hipStream_t stream,
                          const QmvMulti* multi = nullptr);
 
+// Strided copy (copy.hip): dst[idx] = src[idx] over an N-d view, strides
+// in elements on both sides.
+struct CopyArgs {
+  const void* src;
+  void* dst;
+  int ndim, esz;
+  int64_t n;
+  int64_t shape[MLXQ_MAX_DIMS];
+  int64_t src_strides[MLXQ_MAX_DIMS];
+  int64_t dst_strides[MLXQ_MAX_DIMS];
+};
+hipError_t launch_strided_copy(const CopyArgs& a, hipStream_t stream);
+
+// General quantized matmul (qmm_gen.hip): float16 / bfloat16 / float32
+// activations and scales, affine codes of 2-8 bits, mxfp4, both transposes,
+// gather segments.  Element types of x / scales / result:
+enum GenType : int { GEN_BF16 = 0, GEN_F16 = 1, GEN_F32 = 2 };
+enum GenMode : int { GEN_AFFINE = 0, GEN_MXFP4 = 1 };
+struct GenArgs {
+  const void* x;            // [X][M][K] of x_dtype
+  const uint32_t* w;        // [E][N][K*bits/32] (transpose) or [E][K][N*bits/32]
+  const void* scales;       // [E][N][K/gs] or [E][K][N/gs] of s_dtype (uint8 e8m0 for mxfp4)
+  const void* biases;       // like scales (affine)
+  void* out;                // [nseg][M][N] of the compute type
+  float* ws;                // [ks][nseg*M*N] fp32 partials when ks > 1
+  const uint32_t* lhs;      // x batch per segment (null: segment s, or 0 when X == 1)
+  const uint32_t* rhs;      // weight matrix per segment (null: segment s, or 0 when E == 1)
+  int x_dtype, s_dtype, b_dtype;  // GenType
+  int mode;                 // GenMode
+  int bits, gs_shift;
+  int M, N, K;              // rows per segment, output columns, reduction length
+  int X, E;                 // index clamps
+  int x_vec;                // K % 8 == 0: 8 activations per vector load
+  int64_t w_expert_stride;  // words per weight matrix
+  int64_t s_expert_stride;  // scale elements per weight matrix
+  int64_t out_elems;        // nseg * M * N (partial stride)
+  int tiles_m, ks, ksteps_per_split;  // set by qmm_gen_launch from the plan
+};
+struct GenPlan {
+  bool ok = false;
+  int bm = 16;              // rows per tile (16 or 64)
+  int tiles_m = 1, tiles_n = 1;
+  int ks = 1;               // K splits
+  int ksteps_per_split = 1; // 32-position steps per split
+};
+// ks_req > 0 forces the K split (tests)
+GenPlan gen_plan(int64_t M, int64_t N, int64_t K, int64_t nseg, int cus, int ks_req);
+// tc: GenType of the MFMA inputs and of `out`
+hipError_t qmm_gen_launch(const GenArgs& a, const GenPlan& p, int tc, bool transpose, int64_t nseg,
+                          hipStream_t stream);
+hipError_t launch_gen_reduce(const float* ws, void* out, int64_t n, int ks, int tc, hipStream_t stream);
+
 // Block-MFMA decode kernel (qmv_b4.hip) for 1 to 16 activation rows per
 // weight matrix: v_mfma_f32_4x4x4bf16_1k over 4 weight rows x 256-byte pieces
 // per wave-load, RG groups of 4 rows per workgroup, waves split K in chunks
@@ -324,7 +376,7 @@ struct MoeArgs {
 hipError_t moe_launch(const MoeArgs& a, int gu_bits, int d_bits, int act, hipStream_t stream);
 
 // out[i] = bf16(out[i] + bias[i % bias_n]) over n bf16 elements (bias.hip).
-hipError_t launch_bias_add(uint16_t* out, const uint16_t* bias, int64_t n, int64_t bias_n, hipStream_t stream);
+hipError_t launch_bias_add(void* out, const void* bias, int64_t n, int64_t bias_n, int tc, hipStream_t stream);
 
 // ---- scratch.hip: the no-allocation entry point's device array ----
 size_t static_scratch_bytes();

@@ -228,17 +228,19 @@ def test_dequantize_and_quantize_errors(lib):
 
 
 def test_unimplemented_combinations_say_so(lib):
-    # transpose=false is valid for MLX but not implemented here
-    x, w, s = arr([1, 64], BF), arr([64, 8], U32), arr([64, 1], BF)
+    # mxfp8 matmuls are valid for MLX but not implemented here (refused before
+    # any device work, so the caller can fall back)
+    x, w, s = arr([1, 64], BF), arr([64, 16], U32), arr([64, 2], U8)
     out = arr([1, 64], BF)
-    st = lib.mlxq_quantized_matmul(ctypes.byref(x), ctypes.byref(w), ctypes.byref(s), ctypes.byref(s), False, 64, 4,
-                                   b"affine", ctypes.byref(out), None)
-    assert st == _lib.EUNSUPPORTED and "transpose=false" in _lib.last_error()
-    # 3-bit affine
-    x3, w3, s3 = arr([1, 64], BF), arr([64, 6], U32), arr([64, 1], BF)
-    st = lib.mlxq_quantized_matmul(ctypes.byref(x3), ctypes.byref(w3), ctypes.byref(s3), ctypes.byref(s3), True, 64,
-                                   3, b"affine", ctypes.byref(out), None)
-    assert st == _lib.EUNSUPPORTED
+    st = lib.mlxq_quantized_matmul(ctypes.byref(x), ctypes.byref(w), ctypes.byref(s), None, True, 32, 8,
+                                   b"mxfp8", ctypes.byref(out), None)
+    assert st == _lib.EUNSUPPORTED and "mxfp8" in _lib.last_error()
+    # float64 activations promote the result to float64
+    x64, w4, s4 = arr([1, 64], _lib.FLOAT64), arr([64, 8], U32), arr([64, 1], BF)
+    out64 = arr([1, 64], _lib.FLOAT64)
+    st = lib.mlxq_quantized_matmul(ctypes.byref(x64), ctypes.byref(w4), ctypes.byref(s4), ctypes.byref(s4), True, 64,
+                                   4, b"affine", ctypes.byref(out64), None)
+    assert st == _lib.EUNSUPPORTED and "float64" in _lib.last_error()
 
 
 def moe_args(din=256, dff=128, E=4, k=2, gu=4, db=4, gs=64, x_dtype=BF, idx_dtype=_lib.INT32, sc_dtype=_lib.FLOAT32):

@@ -108,6 +108,6 @@ def test_mxfp4_one_hot_is_exact():
 def test_unimplemented_raises():
     x, wq, s, b = affine_case(1, 64, 64, 64, 4, 3)
     with pytest.raises(NotImplementedError):
-        mq.quantized_matmul(dev_bf16(x).float(), dev_u32(wq), dev_bf16(s).float(), dev_bf16(b).float())
+        mq.quantized_matmul(dev_bf16(x).double(), dev_u32(wq), dev_bf16(s).double(), dev_bf16(b).double())
     with pytest.raises(ValueError, match="Biases must be provided"):
         mq.quantized_matmul(dev_bf16(x), dev_u32(wq), dev_bf16(s), None)
