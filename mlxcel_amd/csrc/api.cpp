@@ -1759,21 +1759,42 @@ mlxq_status mlxq_dequantize(const mlxq_array* w, const mlxq_array* scales, const
     Shape oshape = wv.shape();
     oshape.back() = wv.dim(-1) * 32 / bits;
     check_out(out, oshape, out_type, tag);
-    if (mode == AFFINE && bits != 2 && bits != 4 && bits != 6 && bits != 8)
-      unsupported("dequantize: affine bits 2, 4, 6 and 8 are implemented");
-    if (out_type != MLXQ_BFLOAT16) unsupported("dequantize: only bfloat16 output is implemented");
-    if (mode == AFFINE) {
-      require_dtype(scales, MLXQ_BFLOAT16, "scales", tag);
-      require_dtype(biases, MLXQ_BFLOAT16, "biases", tag);
+    // bfloat16 results of bfloat16 affine 2/4/6/8-bit and of the fp modes run
+    // the dedicated kernels; the general one takes float16/float32 scales or
+    // results, affine 3/5-bit codes and mxfp4 to float16/float32
+    const bool bf16_all = out_type == MLXQ_BFLOAT16 &&
+                          (mode != AFFINE || (scales->dtype == MLXQ_BFLOAT16 && biases->dtype == MLXQ_BFLOAT16));
+    const bool dedicated = bf16_all && (mode != AFFINE || bits == 2 || bits == 4 || bits == 6 || bits == 8);
+    if (!dedicated) {
+      if (mode == AFFINE && bits != 2 && bits != 3 && bits != 4 && bits != 5 && bits != 6 && bits != 8)
+        unsupported("dequantize: affine bits " + std::to_string(bits) + " is not implemented");
+      if (mode == MXFP8_M || mode == NVFP4_M) unsupported("dequantize: only bfloat16 output is implemented for this mode");
+      if (gen_type(out_type) < 0) unsupported("dequantize: output dtype " + std::string(dtype_name(out_type)) +
+                                              " is not implemented");
+      if (mode == AFFINE && (gen_type(scales->dtype) < 0 || biases->dtype != scales->dtype))
+        unsupported("dequantize: scales and biases of one float type (bfloat16, float16 or float32) are implemented");
+      if (mode == AFFINE && group_size != 32 && group_size != 64 && group_size != 128)
+        unsupported("dequantize: group_size must be 32, 64 or 128");
     }
-    require_contiguous(w, "w");
-    require_contiguous(scales, "scales");
-    require_contiguous(biases, "biases");
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    Staged st = stage_operands(nullptr, w, scales, biases, out, stream, true, tag);
+    w = st.in[1];
+    scales = st.in[2];
+    biases = st.in[3];
+    out = st.out;
     const int64_t K = oshape.back();
     const int64_t rows = View{out}.size() / std::max<int64_t>(K, 1);
     if (rows == 0 || K == 0) return;
     if (K % group_size) unsupported("dequantize: K must be a multiple of group_size");
-    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    if (!dedicated) {
+      hip_check(mlxq::launch_gen_dequantize(mode == MXFP4_M ? mlxq::GEN_MXFP4 : mlxq::GEN_AFFINE,
+                                            static_cast<const uint32_t*>(w->data), scales->data,
+                                            biases ? biases->data : nullptr, out->data, rows, K, group_size, bits,
+                                            mode == AFFINE ? gen_type(scales->dtype) : 0, gen_type(out_type), stream),
+                "dequantize launch");
+      st.finish();
+      return;
+    }
     if (mode == AFFINE) {
       hip_check(mlxq::launch_affine_dequantize(static_cast<const uint32_t*>(w->data),
                                                static_cast<const uint16_t*>(scales->data),
@@ -1792,6 +1813,7 @@ mlxq_status mlxq_dequantize(const mlxq_array* w, const mlxq_array* scales, const
                                            static_cast<uint16_t*>(out->data), rows, K, stream),
                 "dequantize launch");
     }
+    st.finish();
   });
 }
 

@@ -572,4 +572,112 @@ hipError_t launch_fp_quantize(int mode, const uint16_t* w, uint32_t* wq, uint8_t
   return hipGetLastError();
 }
 
+// ---- dequantize for every element type and code width -------------------
+// Affine (ops.cpp:5494-5586, then astype to the requested type at 5788-5793):
+// the graph multiplies the codes by the scales in the scales' type T and adds
+// the biases in T, each op rounded to T, then casts to the output type:
+//   out = To(T(T(q * s) + b))   (T, To in {bfloat16, float16, float32}).
+// mxfp4 to float16 / float32 (ops.cpp:5646-5695 with out_type): the scale
+// 2^(s-127) is formed in the output type (float16: rounded, so it is 0 below
+// 2^-25 and inf from 2^16), times the LUT value, rounded once; s == 255 -> NaN.
+// One thread per 32-code piece (`bits` words), codes read as the little-endian
+// bit stream of the packed row (quantized.cpp:107-137).
+
+namespace {
+
+template <int T>
+__device__ __forceinline__ float round_to(float f) {
+  if constexpr (T == GEN_BF16) return bfr(f);
+  else if constexpr (T == GEN_F16) return (float)(_Float16)f;
+  else return f;
+}
+
+template <int T>
+__device__ __forceinline__ float load_t(const void* p, int64_t i) {
+  if constexpr (T == GEN_F32) return static_cast<const float*>(p)[i];
+  else if constexpr (T == GEN_BF16) return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+  else return (float)__builtin_bit_cast(_Float16, static_cast<const uint16_t*>(p)[i]);
+}
+
+template <int T>
+__device__ __forceinline__ void store_t(void* p, int64_t i, float v) {
+  if constexpr (T == GEN_F32) static_cast<float*>(p)[i] = v;
+  else if constexpr (T == GEN_BF16) static_cast<uint16_t*>(p)[i] = (uint16_t)f32_to_bf16_bits(v);
+  else static_cast<uint16_t*>(p)[i] = __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+__device__ __forceinline__ uint32_t piece_code(const uint32_t* wp, int j, int bits) {
+  const int sb = j * bits, d = sb >> 5, sh = sb & 31;
+  uint64_t v = wp[d];
+  if (sh + bits > 32) v |= (uint64_t)wp[d + 1] << 32;
+  return (uint32_t)(v >> sh) & ((1u << bits) - 1u);
+}
+
+}  // namespace
+
+template <int TS, int TO>
+__global__ __launch_bounds__(256) void gen_affine_dequant_kernel(const uint32_t* __restrict__ w, const void* scales,
+                                                                 const void* biases, void* out, int64_t npieces,
+                                                                 int64_t ppr, int gs_shift, int bits) {
+  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= npieces) return;
+  const int64_t row = p / ppr, c = p - row * ppr;
+  const int64_t K = ppr * 32;
+  const int64_t g = row * (K >> gs_shift) + ((c * 32) >> gs_shift);
+  const float sc = load_t<TS>(scales, g), bi = load_t<TS>(biases, g);
+  const uint32_t* wp = w + p * bits;
+  for (int j = 0; j < 32; j++) {
+    const float q = (float)piece_code(wp, j, bits);
+    store_t<TO>(out, row * K + c * 32 + j, round_to<TS>(round_to<TS>(q * sc) + bi));
+  }
+}
+
+template <int TO>
+__global__ __launch_bounds__(256) void gen_mxfp4_dequant_kernel(const uint32_t* __restrict__ w,
+                                                                const uint8_t* __restrict__ scales, void* out,
+                                                                int64_t npieces) {
+  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= npieces) return;
+  const uint32_t s = scales[p];
+  // 2^(s-127) in the output type (exact in float32, whose subnormals reach 2^-149)
+  float scale = s == 255u ? __builtin_nanf("") : __builtin_ldexpf(1.0f, (int)s - 127);
+  scale = round_to<TO>(scale);
+  const uint32_t* wp = w + p * 4;
+  for (int j = 0; j < 32; j++) {
+    const uint32_t code = (wp[j >> 3] >> (4 * (j & 7))) & 15u;
+    const float mag = (code & 6u) == 0 ? 0.5f * (float)(code & 1u)
+                                       : (1.0f + 0.5f * (float)(code & 1u)) * (float)(1u << (((code >> 1) & 3u) - 1u));
+    store_t<TO>(out, p * 32 + j, ((code & 8u) ? -mag : mag) * scale);
+  }
+}
+
+hipError_t launch_gen_dequantize(int mode, const uint32_t* w, const void* scales, const void* biases, void* out,
+                                 int64_t rows, int64_t K, int gs, int bits, int ts, int to, hipStream_t stream) {
+  if (K % 32 != 0) return hipErrorInvalidValue;
+  const int64_t npieces = rows * (K / 32);
+  if (npieces == 0) return hipSuccess;
+  const dim3 grid((unsigned)((npieces + 255) / 256)), block(256);
+  if (mode == GEN_MXFP4) {
+    if (to == GEN_F32) hipLaunchKernelGGL(gen_mxfp4_dequant_kernel<GEN_F32>, grid, block, 0, stream, w,
+                                          static_cast<const uint8_t*>(scales), out, npieces);
+    else if (to == GEN_F16) hipLaunchKernelGGL(gen_mxfp4_dequant_kernel<GEN_F16>, grid, block, 0, stream, w,
+                                               static_cast<const uint8_t*>(scales), out, npieces);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+  }
+  int shift = 0;
+  while ((1 << shift) < gs) shift++;
+#define GDQ(TS_, TO_)                                                                                          \
+  if (ts == TS_ && to == TO_) {                                                                                \
+    hipLaunchKernelGGL((gen_affine_dequant_kernel<TS_, TO_>), grid, block, 0, stream, w, scales, biases, out, \
+                       npieces, K / 32, shift, bits);                                                          \
+    return hipGetLastError();                                                                                  \
+  }
+  GDQ(GEN_BF16, GEN_BF16) GDQ(GEN_BF16, GEN_F16) GDQ(GEN_BF16, GEN_F32)
+  GDQ(GEN_F16, GEN_BF16) GDQ(GEN_F16, GEN_F16) GDQ(GEN_F16, GEN_F32)
+  GDQ(GEN_F32, GEN_BF16) GDQ(GEN_F32, GEN_F16) GDQ(GEN_F32, GEN_F32)
+#undef GDQ
+  return hipErrorInvalidValue;
+}
+
 }  // namespace mlxq

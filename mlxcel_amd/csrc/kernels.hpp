@@ -150,6 +150,11 @@ GenPlan gen_plan(int64_t M, int64_t N, int64_t K, int64_t nseg, int cus, int ks_
 hipError_t qmm_gen_launch(const GenArgs& a, const GenPlan& p, int tc, bool transpose, int64_t nseg,
                           hipStream_t stream);
 hipError_t launch_gen_reduce(const float* ws, void* out, int64_t n, int ks, int tc, hipStream_t stream);
+// dequantize for every element type (dequant.hip): affine codes of 2-8 bits
+// with scales/biases of type ts, or mxfp4 (mode GEN_MXFP4) to float16/float32;
+// `to` is the output type.  K a multiple of 32.
+hipError_t launch_gen_dequantize(int mode, const uint32_t* w, const void* scales, const void* biases, void* out,
+                                 int64_t rows, int64_t K, int gs, int bits, int ts, int to, hipStream_t stream);
 
 // Block-MFMA decode kernel (qmv_b4.hip) for 1 to 16 activation rows per
 // weight matrix: v_mfma_f32_4x4x4bf16_1k over 4 weight rows x 256-byte pieces

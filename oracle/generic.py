@@ -64,6 +64,31 @@ def dequantize(wq, scales, biases, group_size: int, bits: int, n: int, mode: str
     return g * q + b
 
 
+def dequantize_graph(wq, scales, biases, group_size: int, bits: int, n: int, ts: str, to: str) -> np.ndarray:
+    """mlx::core::dequantize, affine (overlays/rocm/mlx/ops.cpp:5494-5586, then
+    astype(out_type) at 5788-5793): the codes times the scales in the scales'
+    type T, plus the biases in T, each op computed in float32 and rounded to T,
+    then cast to the output type:  To(T(f32(T(f32(q * s)) + b))).
+    scales / biases hold values of type ts; returns float64 values of type to."""
+    q = unpack_codes(wq, bits, n).astype(np.float64)
+    sc = np.repeat(np.asarray(scales, dtype=np.float64), group_size, axis=-1)
+    bi = np.repeat(np.asarray(biases, dtype=np.float64), group_size, axis=-1)
+    prod = round_to(round_to(q * sc, "float32"), ts)
+    tot = round_to(round_to(prod + bi, "float32"), ts)
+    return round_to(tot, to)
+
+
+def mxfp4_dequantize_graph(wq, scales, n: int, to: str) -> np.ndarray:
+    """mxfp4 dequantize to float16 / float32 (ops.cpp:5646-5695 with out_type):
+    the scale 2^(s-127) is formed in the output type (rounded to it), s == 255
+    gives NaN, and LUT[q] * scale is rounded once."""
+    q = unpack_codes(wq, 4, n)
+    s = np.asarray(scales, dtype=np.int64)
+    scale = np.where(s == 255, np.nan, np.ldexp(1.0, s - 127))
+    scale = round_to(scale, to)
+    return round_to(E2M1[q] * np.repeat(scale, 32, axis=-1), to)
+
+
 def qmm(x, wq, scales, biases, transpose: bool, group_size: int, bits: int, mode: str = "affine") -> np.ndarray:
     """y = x @ W^T (transpose) or x @ W for 2-D W, float64.
 

@@ -216,3 +216,51 @@ def test_strided_operands_bitwise(kind):
             mq.quantized_matmul(x, wq, s, b, True, 64, bits, out=y)
         torch.cuda.synchronize()
         np.testing.assert_array_equal(y.float().cpu().numpy(), want.float().cpu().numpy())
+
+
+# ---- dequantize for every type and width -------------------------------------
+# Bit for bit the reference's dequantize graph (ops.cpp:5494-5586 + astype at
+# 5788-5793, oracle/generic.py dequantize_graph): To(T(T(q * s) + b)).
+
+@pytest.mark.parametrize("ts", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("to", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("bits", [3, 4, 5])
+def test_dequantize_types_bitwise(ts, to, bits):
+    announce("gen_dequant", ts, to, bits)
+    rows, K, gs = 8, 256, 64
+    rng = np.random.default_rng(2900 + bits)
+    codes = rng.integers(0, 1 << bits, size=(rows, K))
+    wqn = og.pack_codes(codes, bits)
+    s, sv = dev(rng.uniform(-0.05, 0.05, size=(rows, K // gs)), ts)
+    b, bv = dev(rng.uniform(-0.2, 0.2, size=(rows, K // gs)), ts)
+    y = mq.dequantize(dev_u32(wqn), s, b, gs, bits, "affine", dtype=TD[to])
+    assert y.dtype == TD[to]
+    want = og.dequantize_graph(wqn, sv, bv, gs, bits, K, ts, to)
+    np.testing.assert_array_equal(y.float().cpu().numpy().astype(np.float64), want)
+
+
+@pytest.mark.parametrize("to", ["float16", "float32"])
+def test_mxfp4_dequantize_every_code_and_scale(to):
+    # row r has scale byte r (0..255) and codes 0..15 twice
+    announce("gen_mxfp4_dequant", to)
+    codes = np.tile(np.arange(32) % 16, (256, 1))
+    wqn = og.pack_codes(codes, 4)
+    sc = np.arange(256, dtype=np.uint8)[:, None]
+    y = mq.dequantize(dev_u32(wqn), torch.from_numpy(sc).cuda(), None, 32, 4, "mxfp4", dtype=TD[to])
+    want = og.mxfp4_dequantize_graph(wqn, sc, 32, to)
+    np.testing.assert_array_equal(y.float().cpu().numpy().astype(np.float64), want)
+
+
+def test_dequantize_strided_scales():
+    # a transposed (non-contiguous) scales view is copied first: same bits
+    announce("gen_dequant_strided")
+    rng = np.random.default_rng(2950)
+    codes = rng.integers(0, 16, size=(16, 128))
+    wqn = og.pack_codes(codes, 4)
+    s, _ = dev(rng.uniform(-0.05, 0.05, size=(16, 2)), "float16")
+    b, _ = dev(rng.uniform(-0.2, 0.2, size=(16, 2)), "float16")
+    want = mq.dequantize(dev_u32(wqn), s, b, 64, 4)
+    st = s.t().contiguous().t()
+    assert not st.is_contiguous()
+    got = mq.dequantize(dev_u32(wqn), st, b, 64, 4)
+    np.testing.assert_array_equal(got.float().cpu().numpy(), want.float().cpu().numpy())

@@ -118,3 +118,41 @@ def test_round_to_bfloat16_ties_to_even():
     # 1 + 3 * 2^-8 is halfway between 1 + 2^-7 and 1 + 2^-6: ties up
     y = np.array([1 + 2.0 ** -8, 1 + 3 * 2.0 ** -8, -(1 + 2.0 ** -8)])
     np.testing.assert_array_equal(og.round_to(y, "bfloat16"), [1.0, 1 + 2.0 ** -6, -1.0])
+
+
+@pytest.mark.parametrize("bits", [2, 4, 6, 8])
+def test_dequantize_graph_bfloat16_is_the_pinned_c_oracle(bits):
+    # bfloat16 scales and result: bit for bit the C oracle's dequantize
+    # (pinned against the reference's fixtures)
+    w = orc.normal_bf16((6, 256), 0.05, 80 + bits)
+    wq, s, b = orc.affine_quantize(w, 64, bits)
+    want = orc.bf16_to_f32(orc.affine_dequantize(wq, s, b, 64, bits)).astype(np.float64)
+    got = og.dequantize_graph(wq, orc.bf16_to_f32(s), orc.bf16_to_f32(b), 64, bits, 256, "bfloat16", "bfloat16")
+    np.testing.assert_array_equal(got, want)
+
+
+def test_dequantize_graph_float16_rounds_each_op():
+    # q = 3, s = f16(0.1) = 0.0999755859375, b = f16(-0.2) = -0.199951171875:
+    # q*s = 0.2999267578125 lies halfway between the float16 neighbours
+    # 1228 * 2^-12 and 1229 * 2^-12, so it rounds to the even 0.2998046875;
+    # + b = 0.099853515625 (= 1636 * 2^-14, exact).  A fused q*s + b would
+    # give 0.0999755859375 instead.
+    codes = np.zeros((1, 32), np.int64)
+    codes[0, 0] = 3
+    wq = og.pack_codes(codes, 4)
+    got = og.dequantize_graph(wq, np.array([[np.float16(0.1)]], np.float64),
+                              np.array([[np.float16(-0.2)]], np.float64), 32, 4, 32, "float16", "float16")
+    assert got[0, 0] == 0.099853515625
+    assert got[0, 1] == float(np.float16(-0.2))
+
+
+def test_mxfp4_dequantize_graph_float16_scale_range():
+    # scale 2^(s-127) formed in float16: 2^-25 rounds to 0 (tie to even),
+    # 2^-24 is the smallest subnormal, 2^16 overflows to inf; NaN for 255
+    codes = np.full((4, 32), 2, np.int64)  # LUT[2] = 1.0
+    wq = og.pack_codes(codes, 4)
+    sc = np.array([[102], [103], [143], [255]], np.uint8)
+    got = og.mxfp4_dequantize_graph(wq, sc, 32, "float16")[:, 0]
+    assert got[0] == 0.0 and got[1] == 2.0 ** -24 and np.isinf(got[2]) and np.isnan(got[3])
+    got32 = og.mxfp4_dequantize_graph(wq, sc, 32, "float32")[:, 0]
+    assert got32[0] == 2.0 ** -25 and got32[2] == 2.0 ** 16
