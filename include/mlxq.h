@@ -126,9 +126,17 @@ const char* mlxq_version(void);
  * transpose.  Shapes/dtypes exactly as mlx::core::quantized_matmul
  * (ops.cpp:4955-5008): out.shape = x.shape[:-1] + [N], out dtype =
  * promote(x, scales, biases) for affine and x.dtype for fp modes.
- * Implemented: transpose=true; mode "affine" with bits 4 or 8 and
- * group_size 32/64/128; mode "mxfp4"; bfloat16 activations; w 2-D, or
- * batched with the same batch shape as x.  Row-contiguous inputs. */
+ * Implemented: both transposes; mode "affine" with bits 2, 3, 4, 5, 6 or 8
+ * and group_size 32/64/128; mode "mxfp4"; bfloat16, float16 and float32
+ * activations, scales and biases (computed in the promoted type, fp32
+ * accumulation); w 2-D, or batched with batch dims that broadcast against
+ * x's.  Operands of any strides: ones that are not row-contiguous and
+ * 16-byte aligned are first copied into a per-stream staging workspace, as
+ * the reference copies them (rocm/quantized/qmm.hip:3557-3564), and a
+ * strided `out` is written through it.  bfloat16 4/8-bit affine and mxfp4
+ * with transpose=true run the specialised kernels; every other combination
+ * runs the general kernel (float16 results also round the dequantized
+ * weights to float16, as the reference's dequantize + GEMM route does). */
 mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w,
                                   const mlxq_array* scales, const mlxq_array* biases,
                                   bool transpose, int32_t group_size, int32_t bits,
@@ -142,6 +150,7 @@ mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w,
  * would need more return MLXQ_ENOMEM with the size in mlxq_last_error().
  * Every call on one GPU shares that array: calls that overlap in time on one
  * GPU (several streams, threads or replays of graphs in flight together) race.
+ * Operands must be row-contiguous and 16-byte aligned (no staging copies).
  * No counterpart in the reference; it is for callers that cannot allocate
  * (code under HIP-graph capture, tight serving loops). */
 mlxq_status mlxq_quantized_matmul_noalloc(const mlxq_array* x, const mlxq_array* w,
@@ -152,7 +161,8 @@ mlxq_status mlxq_quantized_matmul_noalloc(const mlxq_array* x, const mlxq_array*
 /* A quantized linear layer, as the reference's quantized_linear_forward
  * (lib.rs:697-707, mlx_cxx_bridge.cpp:1707-1746): quantized_matmul with
  * transpose = true, then `+ linear_bias` as MLX adds two bf16 arrays (fp32
- * sum, one rounding).  `linear_bias` may be NULL; otherwise of shape (N) (or
+ * sum, one rounding; float16 / float32 results likewise in their type).
+ * `linear_bias` may be NULL; otherwise row-contiguous, of shape (N) (or
  * (1, ..., N)) or the output's shape, in the output's dtype (other layouts
  * return MLXQ_EUNSUPPORTED). */
 mlxq_status mlxq_quantized_linear(const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
@@ -205,7 +215,8 @@ mlxq_status mlxq_quantized_matmul_shape(const mlxq_array* x, const mlxq_array* w
  * sorted after the cast).  Sorted and unsorted
  * routes differ only in summation order (same tolerance).  `global_scale` (nvfp4 only in the reference) must be
  * NULL.  Index arrays may be any integer dtype and any strides
- * (broadcasting included). */
+ * (broadcasting included).  Types, code widths, transposes and strides as
+ * for mlxq_quantized_matmul; any rows per gathered matrix. */
 mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w,
                             const mlxq_array* scales, const mlxq_array* biases,
                             const mlxq_array* lhs_indices, const mlxq_array* rhs_indices,
@@ -229,7 +240,11 @@ mlxq_status mlxq_gather_qmm_shape(const mlxq_array* x, const mlxq_array* w,
  * LUT[q] * from_fp8(s) (exact) (ops.cpp:5661-5695; e4m3 decoding as
  * rocm/quantized/convert_fp8.hip:68-90).
  * `dtype` < 0 selects the reference default (scales' dtype for affine,
- * bfloat16 for fp modes); only bfloat16 output is implemented. */
+ * bfloat16 for fp modes).  Affine: bits 2, 3, 4, 5, 6, 8 with scales/biases
+ * of one type T in {bfloat16, float16, float32} and any of those outputs,
+ * To(T(T(q*s) + b)) bit-exactly (ops.cpp:5494-5586 then astype).  mxfp4
+ * also to float16/float32 (the scale 2^(s-127) formed in the output type,
+ * ops.cpp:5680-5690); mxfp8 and nvfp4 to bfloat16.  Any strides. */
 mlxq_status mlxq_dequantize(const mlxq_array* w, const mlxq_array* scales,
                             const mlxq_array* biases, int32_t group_size, int32_t bits,
                             const char* mode, int32_t dtype, mlxq_array* out, void* stream);
