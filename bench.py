@@ -718,7 +718,9 @@ def main():
                    "bytes_per_step": 3 * per_launch, "avg_us_per_launch": round(launch_us, 3)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_GATE,
-                     "kernel": "qmv_rs_kernel<AFF4, MR=1, R=8, CPW=1, UPW=4> (gate, N=14336 K=4096 M=1)",
+                     "kernel": "qmv_rs_dense_kernel<AFF4, MR=1, R=8, CPW=1, UPW=4> (gate, N=14336 K=4096 M=1)",
+                     "timing": "graph replay of 8 back-to-back launches, HIP events on the replay stream; "
+                               "per-launch time includes the dispatch gap between dependent kernels",
                      "bytes_per_launch": per_launch, "avg_launch_us": round(gate_us, 3),
                      "read_ceiling": ceiling, "frac_of_read_ceiling": round(achieved / ceiling["GBps"], 3)},
     }
