@@ -262,21 +262,33 @@ def qmv_sweep(iters=200):
 
 def qmm_prefill(iters=20):
     """Prefill GEMM: M in {512, 2048}, 4/8-bit, the
-    Llama-3-8B gate/up and down shapes; TFLOPS = 2 M N K / time."""
+    Llama-3-8B gate/up and down shapes; TFLOPS = 2 M N K / time.  Beside
+    each, torch's bf16 GEMM (hipBLASLt) on the dequantized weights of the same
+    shape, timed the same way in the same run (`dense_bf16`): the library
+    GEMM the reference's prefill route calls after dequantizing."""
     res = []
     for bits in (4, 8):
         for (N, K, name) in ((14336, 4096, "gate_up"), (4096, 14336, "down")):
             ws = [make_affine(N, K, bits, 64, 80 + c) for c in range(3)]
+            # [K, N] contiguous bf16 copies of the dequantized weights
+            wts = [mq.dequantize(*w, 64, bits).t().contiguous() for w in ws]
             for M in (512, 2048):
                 x = randn_bf16((M, K), 13)
                 out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
                 g = capture(lambda: [mq.quantized_matmul(x, *w, True, 64, bits, out=out) for w in ws])
                 ms = timed_graphs([g], max(1, iters // len(ws)), 1) / len(ws)
-                tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-                res.append({"bits": bits, "shape": name, "M": M, "N": N, "K": K, "us": round(ms * 1e3, 1),
-                            "TFLOPS": round(tf, 1), "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 3)})
                 del g
-            del ws
+                gd = capture(lambda: [torch.mm(x, wt, out=out) for wt in wts])
+                ms_d = timed_graphs([gd], max(1, iters // len(wts)), 1) / len(wts)
+                del gd
+                tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+                tf_d = 2.0 * M * N * K / (ms_d * 1e-3) / 1e12
+                res.append({"bits": bits, "shape": name, "M": M, "N": N, "K": K, "us": round(ms * 1e3, 1),
+                            "TFLOPS": round(tf, 1), "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 3),
+                            "dense_bf16": {"us": round(ms_d * 1e3, 1), "TFLOPS": round(tf_d, 1),
+                                           "frac_mfma": round(tf_d / BF16_PEAK_TFLOPS, 3)},
+                            "vs_dense": round(ms_d / ms, 3)})
+            del ws, wts
     return res
 
 

@@ -45,7 +45,6 @@ SOURCES = {
     "qmm_group.hip": [],
     "qmm.hip": [],
     "qmm_gen.hip": [],
-    "qmm_rb.hip": [],
     "moe.hip": [],
     "bias.hip": [],
     "copy.hip": [],

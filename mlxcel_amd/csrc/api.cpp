@@ -1025,31 +1025,6 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
       return;
     }
   }
-  if (wv.ndim() == 2 && rows_total >= knobs().qmm_min_rows && (knobs().qmm_tile == 8 || knobs().qmm_tile == 9)) {
-    // prefill with the weights in registers (qmm_rb.hip)
-    const int dev = current_device();
-    const mlxq::QmmRbPlan rp = mlxq::qmm_rb_plan(fmt, sp.gs, rows_total, sp.N, sp.K, device_info(dev).cus,
-                                                 knobs().qmm_tile == 8 ? 256 : 128, knobs().qmm_ksplit);
-    if (rp.ok) {
-      mlxq::QmmRbArgs q{};
-      q.x = a.x;
-      q.w = a.w;
-      q.scales = a.scales;
-      q.biases = a.biases;
-      q.out = a.out;
-      q.M = (int)rows_total;
-      q.N = (int)sp.N;
-      q.K = (int)sp.K;
-      int shift = 0;
-      while ((1 << shift) < sp.gs) shift++;
-      q.gs_shift = shift;
-      if (rp.ksplit > 1)
-        q.ws = reinterpret_cast<float*>(
-            workspace(dev, stream, (size_t)rp.ksplit * rows_total * sp.N * sizeof(float), ss));
-      hip_check(mlxq::qmm_rb_launch(fmt, q, rp, stream), "qmm launch");
-      return;
-    }
-  }
   if (wv.ndim() == 2 && rows_total >= knobs().qmm_min_rows) {
     // prefill: one GEMM over all rows (every leading dim of x folds into rows)
     const int dev = current_device();

@@ -275,29 +275,6 @@ struct QmmPlan {
   int tiles_n = 1, tiles_m = 1, ksplit = 1, ksteps_per_split = 1;
   int m_fast = 0;  // tile kernel: consecutive workgroups walk along M
 };
-// Prefill GEMM with the weights in registers (qmm_rb.hip): BM x 256 output
-// tiles, 4 waves side by side along N, activations through a 4-stage LDS ring.
-struct QmmRbArgs {
-  const uint16_t* x;       // bf16 [M, K]
-  const uint32_t* w;       // packed codes [N, K*bits/32]
-  const void* scales;      // bf16 or e8m0 [N, K/gs]
-  const uint16_t* biases;  // bf16 [N, K/gs] (affine)
-  uint16_t* out;           // bf16 [M, N]
-  float* ws;               // fp32 partials [ksplit, M, N] when ksplit > 1
-  int M, N, K;
-  int gs_shift;
-  int ksplit, ksteps_per_split;
-  int tiles_m, tiles_n, m_fast;
-};
-struct QmmRbPlan {
-  bool ok = false;
-  int bm = 256;  // rows per tile (128 or 256)
-  int tiles_m = 1, tiles_n = 1, ksplit = 1, ksteps_per_split = 1, m_fast = 0;
-};
-// bm_req: 128 / 256 or 0 (by shape); ksplit_req: 0 = by shape
-QmmRbPlan qmm_rb_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus, int bm_req, int ksplit_req);
-hipError_t qmm_rb_launch(int fmt, const QmmRbArgs& a, const QmmRbPlan& p, hipStream_t stream);
-
 // rows of x per output tile of a tile code (0 if unknown)
 int qmm_tile_rows(int tile);
 // Grouped gather: tiles along N for `tile`; tiles_m = segments is set by the caller.

@@ -286,12 +286,10 @@ __device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-#ifndef QMM_VALU_PER_MFMA
-#define QMM_VALU_PER_MFMA 6
-#endif
-#ifndef QMM_DS_BURST
-#define QMM_DS_BURST 1
-#endif
+// Interleave of one slice: after each MFMA, up to this many VALU
+// instructions (measured on MI355X: 6 keeps the dequantization under the
+// MFMAs at both tile sizes).
+constexpr int kValuPerMfma = 6;
 
 template <int FMT, int BM, int BN, int NWM, int NWN>
 __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs a) {
@@ -445,6 +443,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
   // the weight words that fall in the p-th share.
   constexpr int NPART = BK / 16;
   constexpr int NWORD = WP * 4;  // weight words per thread and K-step
+  static_assert(BITS != 8 || WP % 2 == 0 || WP * 4 / NPART >= 2, "8-bit word pairs must fall in one part");
   auto store_part = [&](int buf, int p, int ks) {
 #pragma unroll
     for (int i = 0; i < XL; i++)
@@ -474,10 +473,18 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
           const int ch = wpc * 4 + (e % 4);  // logical 16-byte chunk (8 values)
           *reinterpret_cast<u32x4*>(rowp + ((ch ^ r7) << 3)) = o;
         } else {
-          const u32x2 o = {pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<0>(w), bi), __builtin_fmaf(sc, cvt_ubyte<1>(w), bi)),
-                           pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<2>(w), bi), __builtin_fmaf(sc, cvt_ubyte<3>(w), bi))};
-          const int v = wpc * 16 + (e % 4) * 4;  // first of the 4 values
-          *reinterpret_cast<u32x2*>(rowp + ((((v >> 3) ^ r7) << 3) | (v & 7))) = o;
+          // two words (8 codes) per 16-byte chunk, written with the even word:
+          // the same 16-byte LDS stores as the 4-bit path (8-byte stores of
+          // one word each conflicted on 16% of the LDS cycles)
+          if ((e & 1) == 0) {
+            const uint32_t w1 = wreg[pp][(e % 4) + 1];
+            const u32x4 o = {pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<0>(w), bi), __builtin_fmaf(sc, cvt_ubyte<1>(w), bi)),
+                             pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<2>(w), bi), __builtin_fmaf(sc, cvt_ubyte<3>(w), bi)),
+                             pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<0>(w1), bi), __builtin_fmaf(sc, cvt_ubyte<1>(w1), bi)),
+                             pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<2>(w1), bi), __builtin_fmaf(sc, cvt_ubyte<3>(w1), bi))};
+            const int ch = wpc * 2 + (e % 4) / 2;  // logical 16-byte chunk (8 values)
+            *reinterpret_cast<u32x4*>(rowp + ((ch ^ r7) << 3)) = o;
+          }
         }
       } else {
         // fp4 code points times a normal power of two are exact in bf16 (one
@@ -600,20 +607,15 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
         // interleave within the slice: one MFMA, then a share of the VALU,
         // LDS and global-load work; slices are scheduled one by one
         constexpr int NMF = FM * FN;
-#if QMM_DS_BURST
         // the next slice's fragment reads go out first, a whole slice of
         // MFMAs ahead of their use
         __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);  // DS read
-#endif
 #pragma unroll
         for (int q = 0; q < NMF; q++) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, QMM_VALU_PER_MFMA, 0);  // VALU
-#if !QMM_DS_BURST
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                  // DS read
-#endif
-          __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                  // DS write
-          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                  // VMEM read
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);             // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);  // VALU
+          __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);             // DS write
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);             // VMEM read
         }
         __builtin_amdgcn_sched_barrier(0);
         if (s == 1) __syncthreads();  // step ks+1's buffer complete
