@@ -949,6 +949,41 @@ void run_gen(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const 
   if (p.ks > 1) hip_check(mlxq::launch_gen_reduce(a.ws, out->data, out_elems, p.ks, tc, stream), "reduce launch");
 }
 
+// float16 decode (1-4 rows, 2-D weights): the row-streaming kernel's float16
+// instantiation, when x, scales, biases and result are all float16 (affine
+// 4/8-bit) or x and result are (mxfp4).  False: not covered.
+bool try_rs_f16(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+                const mlxq_array* biases, mlxq_array* out, int64_t rows, hipStream_t stream) {
+  if (!sp.transpose || rows < 1 || rows > 4 || sp.K % 32 != 0 || sp.out_dtype != MLXQ_FLOAT16 ||
+      x->dtype != MLXQ_FLOAT16)
+    return false;
+  if (sp.mode == AFFINE) {
+    if ((sp.bits != 4 && sp.bits != 8) || (sp.gs != 32 && sp.gs != 64 && sp.gs != 128)) return false;
+    if (scales->dtype != MLXQ_FLOAT16 || !biases || biases->dtype != MLXQ_FLOAT16) return false;
+  } else if (sp.mode != MXFP4_M || sp.gs != 32 || sp.bits != 4) {
+    return false;
+  }
+  const int fmt = fmt_of(sp.mode, sp.bits);
+  const mlxq::QmvRsPlan p = mlxq::qmv_rs_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, knobs().qmv_r);
+  if (!p.ok) return false;
+  mlxq::QmvArgs a{};
+  a.x = static_cast<const uint16_t*>(x->data);
+  a.w = static_cast<const uint32_t*>(w->data);
+  a.scales = scales->data;
+  a.biases = biases ? static_cast<const uint16_t*>(biases->data) : nullptr;
+  a.out = static_cast<uint16_t*>(out->data);
+  a.N = (int)sp.N;
+  a.K = (int)sp.K;
+  a.E = 1;
+  a.X = 1;
+  a.rps = (int)rows;
+  a.total_rows = (int)rows;
+  a.out_rows = (int)rows;
+  a.xt = 1;
+  hip_check(mlxq::qmv_rs_launch(fmt, sp.gs, a, 1, p, stream), "qmv launch");
+  return true;
+}
+
 // Enqueues one checked quantized_matmul call.
 void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
                           const mlxq_array* biases, mlxq_array* out, hipStream_t stream,
@@ -958,6 +993,7 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
   if (sp.K == 0) unsupported("quantized_matmul: K == 0");
   if (!sp.fast) {
     View wv{w}, xv{x};
+    if (wv.ndim() == 2 && try_rs_f16(sp, x, w, scales, biases, out, rows_total, stream)) return;
     if (wv.ndim() == 2) {
       // every leading dim of x folds into rows
       run_gen(sp, x, w, scales, biases, out, rows_total, 1, 1, 1, nullptr, stream, ss);

@@ -73,10 +73,10 @@ __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
 // invisible to the compiler's hazard checks: it inserted no wait states
 // between such a write and an MFMA reading the result, and the MFMA then read
 // stale operands.)
-__device__ __forceinline__ void unpack_aff4(uint32_t w, uint32_t (&v)[4]) {
+// (`c` = 0x64646464 gives the float16 pairs 1024 + q instead.)
+__device__ __forceinline__ void unpack_aff4(uint32_t w, uint32_t (&v)[4], uint32_t c = 0x43434343u) {
   const uint32_t lo = w & 0x0F0F0F0Fu;
   const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
-  const uint32_t c = 0x43434343u;
   v[0] = __builtin_amdgcn_perm(c, lo, 0x04020400u);  // (n0, n4): bytes lo.0, 0x43, lo.2, 0x43
   v[1] = __builtin_amdgcn_perm(c, hi, 0x04020400u);  // (n1, n5)
   v[2] = __builtin_amdgcn_perm(c, lo, 0x04030401u);  // (n2, n6)
@@ -94,6 +94,15 @@ __device__ __forceinline__ void unpack_mxfp4(uint32_t w, uint32_t (&v)[4]) {
   v[1] = __builtin_bit_cast(uint32_t, p1);
   v[2] = __builtin_bit_cast(uint32_t, p2);
   v[3] = __builtin_bit_cast(uint32_t, p3);
+}
+
+// The same as float16 pairs (v_cvt_scalef32_pk_f16_fp4; the code points are
+// exact in float16 too).
+__device__ __forceinline__ void unpack_mxfp4_f16(uint32_t w, uint32_t (&v)[4]) {
+  v[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0));
+  v[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 1));
+  v[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 2));
+  v[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 3));
 }
 
 // MXFP4 with its e8m0 scale folded in: v[h] = (code 2h, code 2h+1) * scale as

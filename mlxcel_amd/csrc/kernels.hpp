@@ -44,6 +44,8 @@ struct QmvArgs {
   const uint32_t* nseg_dev; // segments in the table
   const uint32_t* xrows;    // grouped row -> x row (flattened over x's batch)
   const uint32_t* orows;    // grouped row -> output row
+  int xt;                   // element type of x / scales / biases / out: 0 bfloat16, 1 float16
+                            // (float16: the row-streaming kernel's dense entry only)
   // Sorted gathers (rps == 1): nonzero = segments are runs of equal experts
   // among consecutive entries, at most `runs` entries each (row-streaming
   // kernel: 4; block-MFMA kernel: up to its 4 MS rows).

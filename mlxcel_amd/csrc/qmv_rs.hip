@@ -68,6 +68,32 @@ struct RsMultiArgs {
   uint16_t* out[kQmvMultiMax];
 };
 
+// 16-bit element type of activations, scales, biases and result: XT = 0
+// bfloat16, XT = 1 float16 (the reference's quantized_matmul in T = float16,
+// ops.cpp:4974-4992; same arithmetic: fp32 dot products of exact 16-bit
+// products, one rounding of the result).  Affine codes widen to the type's
+// "offset + q" pairs with one byte permute per pair: bfloat16 0x43nn =
+// 128 + q (q < 128), float16 0x64nn = 1024 + q (q < 256, so 8-bit codes take
+// the same route); the offset times sum(x) comes off with the bias.
+template <int XT>
+__device__ __forceinline__ float dotx(uint32_t a, uint32_t b, float c) {
+  if constexpr (XT == 0) return dot2(a, b, c);
+  else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
+  }
+}
+template <int XT>
+__device__ __forceinline__ float xt_to_f32(uint32_t h) {
+  if constexpr (XT == 0) return bf16_bits_to_f32(h);
+  else return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+template <int XT>
+__device__ __forceinline__ uint32_t f32_to_xt(float f) {
+  if constexpr (XT == 0) return f32_to_bf16_bits(f);
+  else return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
 // FMT: weight format; MR: activation rows (>= `count`);
 // R: weight rows per workgroup (power of two); CPW: 1 KiB chunks per wave and
 // row; UPW: quantization groups per scale load (1, 2 or 4: the widest load
@@ -79,7 +105,7 @@ struct RsMultiArgs {
 // One row tile: output rows [tile*R, tile*R + R) of the `count` activation
 // rows at x (row stride K) against the matrix Wm (N rows), written to Om
 // (row stride N).
-template <int FMT, int MR, int R, int CPW, int UPW>
+template <int FMT, int MR, int R, int CPW, int UPW, int XT = 0>
 __device__ __forceinline__ void rs_tile(const uint16_t* x, int count, const uint32_t* Wm, const void* Sm,
                                         const uint16_t* Bm, uint16_t* Om, int N, int K, int gs_shift, int tile) {
   constexpr bool AFF = FMT != MXFP4;
@@ -95,6 +121,9 @@ __device__ __forceinline__ void rs_tile(const uint16_t* x, int count, const uint
   constexpr int VQ = V >= 16 ? 1 : 16 / V;  // lanes per partial after it
   constexpr int SBE = 4;                    // scale loads per lane issued before the weights (at most)
   constexpr int ESZ = AFF ? 2 : 1;          // bytes per stored scale
+  // offset of the widened affine codes (bfloat16 8-bit codes convert exactly, no offset)
+  constexpr float OFS = XT ? 1024.0f : (FMT == AFF4 ? 128.0f : 0.0f);
+  constexpr uint32_t ONES = XT ? 0x3C003C00u : 0x3F803F80u;  // the pair (1, 1)
 
   extern __shared__ __align__(16) unsigned char smem[];
 
@@ -213,9 +242,9 @@ __device__ __forceinline__ void rs_tile(const uint16_t* x, int count, const uint
       for (int h = 0; h < UPW; h++) {
         const int idx = (j * gc + gl * UPW + h) * R + r;
         if constexpr (AFF) {
-          const float sc = bf16_bits_to_f32((sraw[i][h >> 1] >> (16 * (h & 1))) & 0xFFFFu);
-          const float bi = bf16_bits_to_f32((braw[i][h >> 1] >> (16 * (h & 1))) & 0xFFFFu);
-          reinterpret_cast<float2*>(wsl)[idx] = float2{sc, FMT == AFF4 ? __builtin_fmaf(-128.0f, sc, bi) : bi};
+          const float sc = xt_to_f32<XT>((sraw[i][h >> 1] >> (16 * (h & 1))) & 0xFFFFu);
+          const float bi = xt_to_f32<XT>((braw[i][h >> 1] >> (16 * (h & 1))) & 0xFFFFu);
+          reinterpret_cast<float2*>(wsl)[idx] = float2{sc, OFS != 0.0f ? __builtin_fmaf(-OFS, sc, bi) : bi};
         } else {
           reinterpret_cast<float*>(wsl)[idx] = e8m0_to_f32((sraw[i][0] >> (8 * h)) & 0xFFu);
         }
@@ -233,7 +262,7 @@ __device__ __forceinline__ void rs_tile(const uint16_t* x, int count, const uint
 #pragma unroll
         for (int v = 0; v < XV; v++)
 #pragma unroll
-          for (int e = 0; e < 4; e++) s = dot2(xv[m][j][v][e], 0x3F803F80u, s);  // pairs times (1, 1)
+          for (int e = 0; e < 4; e++) s = dotx<XT>(xv[m][j][v][e], ONES, s);  // pairs times (1, 1)
       }
       xs[m][j] = s;
       if constexpr (FMT == AFF4) {
@@ -272,7 +301,14 @@ __device__ __forceinline__ void rs_tile(const uint16_t* x, int count, const uint
       if (!live[j]) sc = bp = 0.f;  // lanes past the end of the row add exactly 0
       uint32_t pr[NP];
       const u32x4 w = wv[r][j];
-      if constexpr (FMT == AFF8) {
+      if constexpr (FMT == AFF8 && XT == 1) {
+        // byte pairs (b0, b1), (b2, b3) of each word as float16 1024 + q
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          pr[2 * q] = __builtin_amdgcn_perm(0x64646464u, w[q], 0x04010400u);
+          pr[2 * q + 1] = __builtin_amdgcn_perm(0x64646464u, w[q], 0x04030402u);
+        }
+      } else if constexpr (FMT == AFF8) {
         uint32_t t[4];
         unpack_aff8(w[0], w[1], t);
 #pragma unroll
@@ -284,7 +320,8 @@ __device__ __forceinline__ void rs_tile(const uint16_t* x, int count, const uint
 #pragma unroll
         for (int q = 0; q < 4; q++) {
           uint32_t t[4];
-          if constexpr (FMT == AFF4) unpack_aff4(w[q], t);
+          if constexpr (FMT == AFF4) unpack_aff4(w[q], t, XT ? 0x64646464u : 0x43434343u);
+          else if constexpr (XT == 1) unpack_mxfp4_f16(w[q], t);
           else unpack_mxfp4(w[q], t);
 #pragma unroll
           for (int e = 0; e < 4; e++) pr[4 * q + e] = t[e];
@@ -296,7 +333,7 @@ __device__ __forceinline__ void rs_tile(const uint16_t* x, int count, const uint
 #pragma unroll
         for (int p = 0; p < NP; p++) {
           // pair p covers lane-chunk K positions 2p, 2p+1 (AFF4: the permuted pair of word p/4)
-          d = dot2(pr[p], xv[m][j][p / 4][p % 4], d);
+          d = dotx<XT>(pr[p], xv[m][j][p / 4][p % 4], d);
         }
         float acc = y[r][m];
         if constexpr (AFF) acc = __builtin_fmaf(bp, xs[m][j], acc);
@@ -323,7 +360,7 @@ __device__ __forceinline__ void rs_tile(const uint16_t* x, int count, const uint
     for (int q = 0; q < NW * 4; q++) tot += red[q * V + idx];
     const int r = idx / MR, m = idx % MR;
     const int row = row0 + r;
-    if (row < N && m < count) Om[(int64_t)m * N + row] = (uint16_t)f32_to_bf16_bits(tot);
+    if (row < N && m < count) Om[(int64_t)m * N + row] = (uint16_t)f32_to_xt<XT>(tot);
   }
 }
 
@@ -374,10 +411,11 @@ __global__ __launch_bounds__(512) void qmv_rs_kernel(const QmvArgs a, int gs_shi
                                 Om + (int64_t)sidx * a.rps * N, N, a.K, gs_shift, tile);
 }
 
-// Dense entry: one 2-D matrix, `count` <= MR activation rows.
-template <int FMT, int MR, int R, int CPW, int UPW>
+// Dense entry: one 2-D matrix, `count` <= MR activation rows; XT: bfloat16
+// or float16 elements.
+template <int FMT, int MR, int R, int CPW, int UPW, int XT>
 __global__ __launch_bounds__(512) void qmv_rs_dense_kernel(const RsDenseArgs a) {
-  rs_tile<FMT, MR, R, CPW, UPW>(a.x, a.count, a.w, a.scales, a.biases, a.out, a.N, a.K, a.gs_shift, blockIdx.x);
+  rs_tile<FMT, MR, R, CPW, UPW, XT>(a.x, a.count, a.w, a.scales, a.biases, a.out, a.N, a.K, a.gs_shift, blockIdx.x);
 }
 
 // Several 2-D matrices of the same activations: matrix p owns the row tiles
@@ -416,6 +454,7 @@ enum RsEntry { RS_GENERAL, RS_DENSE, RS_MULTI };
 
 struct RsLaunch {
   RsEntry entry;
+  int xt;  // 0 bfloat16, 1 float16 (dense entry only)
   dim3 grid;
   const QmvArgs* a;
   int gs_shift;
@@ -429,8 +468,10 @@ hipError_t rs_launch_upw(const QmvRsPlan& p, const RsLaunch& L, hipStream_t stre
   const dim3 block((unsigned)(p.nw * 64));
 #define RS_CASE(MR_, R_, CPW_)                                                                                     \
   if (p.mr == MR_ && p.r == R_ && p.cpw == CPW_) {                                                                 \
-    if (L.entry == RS_DENSE)                                                                                       \
-      hipLaunchKernelGGL((qmv_rs_dense_kernel<FMT, MR_, R_, CPW_, UPW>), L.grid, block, p.lds, stream, L.dense);   \
+    if (L.entry == RS_DENSE && L.xt == 1)                                                                          \
+      hipLaunchKernelGGL((qmv_rs_dense_kernel<FMT, MR_, R_, CPW_, UPW, 1>), L.grid, block, p.lds, stream, L.dense); \
+    else if (L.entry == RS_DENSE)                                                                                  \
+      hipLaunchKernelGGL((qmv_rs_dense_kernel<FMT, MR_, R_, CPW_, UPW, 0>), L.grid, block, p.lds, stream, L.dense); \
     else if (L.entry == RS_MULTI)                                                                                  \
       hipLaunchKernelGGL((qmv_rs_multi_kernel<FMT, MR_, R_, CPW_, UPW>), L.grid, block, p.lds, stream, L.multi);   \
     else                                                                                                           \
@@ -558,6 +599,8 @@ hipError_t qmv_rs_launch(int fmt, int gs, const QmvArgs& a, int nseg, const QmvR
   } else {
     L.entry = RS_GENERAL;
   }
+  L.xt = a.xt;
+  if (a.xt != 0 && L.entry != RS_DENSE) return hipErrorInvalidValue;  // float16: dense entry only
   L.grid = dim3((unsigned)tiles, (unsigned)nseg, 1);
   switch (fmt) {
     case AFF4: return rs_launch_fmt<AFF4>(p, L, a.K, stream);

@@ -264,3 +264,42 @@ def test_dequantize_strided_scales():
     assert not st.is_contiguous()
     got = mq.dequantize(dev_u32(wqn), st, b, 64, 4)
     np.testing.assert_array_equal(got.float().cpu().numpy(), want.float().cpu().numpy())
+
+
+# ---- float16 decode on the row-streaming kernel --------------------------------
+# 1-4 rows of float16 x against 2-D weights with float16 scales/biases (affine
+# 4/8-bit) or e8m0 scales (mxfp4) run the row-streaming kernel's float16
+# instantiation (codes widened to float16 1024 + q pairs).
+
+@pytest.mark.parametrize("bits,gs", [(4, 32), (4, 64), (4, 128), (8, 32), (8, 64), (8, 128)])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("N,K", [(1000, 2304), (4096, 4096), (512, 14336)])
+def test_float16_decode_affine(bits, gs, M, N, K):
+    announce("f16_decode", bits, gs, M, N, K)
+    (x, wq, s, b), (xv, wqn, sv, bv) = case(M, N, K, bits, gs, "float16", "float16", True, 3000 + M + bits + gs)
+    y = mq.quantized_matmul(x, wq, s, b, True, gs, bits)
+    check(y, og.qmm(xv, wqn, sv, bv, True, gs, bits), "float16")
+
+
+@pytest.mark.parametrize("M", [1, 2, 4])
+def test_float16_decode_mxfp4(M):
+    announce("f16_decode_mxfp4", M)
+    rng = np.random.default_rng(3100 + M)
+    x, xv = dev(rng.standard_normal((M, 2880)), "float16")
+    codes = rng.integers(0, 16, size=(2888, 2880))
+    wqn = og.pack_codes(codes, 4)
+    sc = rng.integers(118, 127, size=(2888, 90)).astype(np.uint8)
+    y = mq.quantized_matmul(x, dev_u32(wqn), torch.from_numpy(sc).cuda(), None, True, 32, 4, "mxfp4")
+    check(y, og.qmm(xv, wqn, sc, None, True, 32, 4, "mxfp4"), "float16")
+
+
+def test_float16_decode_multi_matches_separate_calls():
+    # quantized_matmul_multi with float16 operands runs the projections one by
+    # one on the same kernel: bit for bit the separate calls
+    announce("f16_multi")
+    parts = [case(1, 512, 2048, 4, 64, "float16", "float16", True, 3200 + i)[0] for i in range(3)]
+    x = parts[0][0]
+    outs = mq.quantized_matmul_multi(x, [p[1] for p in parts], [p[2] for p in parts], [p[3] for p in parts], 64, 4)
+    for p, o in zip(parts, outs):
+        want = mq.quantized_matmul(x, p[1], p[2], p[3], True, 64, 4)
+        np.testing.assert_array_equal(o.float().cpu().numpy(), want.float().cpu().numpy())
