@@ -17,12 +17,13 @@ way (the practical bound at this size).
 Also reported (extra): the M in {1,2,4,8,16} x {4,8}-bit decode sweep, the
 qmm prefill configs, mxfp4 gather_qmm (gpt-oss-20b MoE shapes), the fused
 decode MoE (Qwen3-30B-A3B experts) against its gather_qmm chain, end-to-end
-decode of a Qwen3-8B-shaped model, the measured device copy ceiling, and the
+decode of a Qwen3-8B-shaped model, the general kernel (float16/float32,
+3-bit, transpose=false), the measured device copy ceiling, and the
 single-core CPU baseline (the oracle's restatement of MLX's CPU `_qmm_t`,
 overlays/cpu/mlx/backend/cpu/quantized.cpp:199-257).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
-                       [--extras copy,sweep,qmm,gather,moe,e2e]
+                       [--extras copy,sweep,qmm,gather,moe,e2e,general]
        python bench.py --traffic-probe   (under rocprofv3 --pmc: copy calibration + gate and gather launches)
 """
 from __future__ import annotations
@@ -289,6 +290,40 @@ def qmm_prefill(iters=20):
                                            "frac_mfma": round(tf_d / BF16_PEAK_TFLOPS, 3)},
                             "vs_dense": round(ms_d / ms, 3)})
             del ws, wts
+    return res
+
+
+def general_path(iters=10):
+    """The general kernel (qmm_gen.hip) and the float16 decode route at the
+    gate shape (N=14336, K=4096, g64): float16 / float32 activations and
+    scales, 3-bit codes, transpose=false; weights are random codes (the
+    arithmetic does not depend on their values)."""
+    N, K, gs = 14336, 4096, 64
+    res = []
+    cases = (("float16", 4, True), ("float32", 4, True), ("bfloat16", 3, True), ("bfloat16", 4, False))
+    for dtn, bits, tr in cases:
+        dt = getattr(torch, dtn)
+        rows, cols = (N, K) if tr else (K, N)
+        g = torch.Generator(device="cuda").manual_seed(90 + bits)
+        for M in (1, 2048):
+            # decode rotates enough weight copies to stream from HBM, not the MALL
+            nl = max(2, int(2.4 * MALL_BYTES / (N * K * bits // 8)) + 1) if M == 1 else 2
+            ws = []
+            for _ in range(nl):
+                wq = torch.randint(0, 2 ** 31 - 1, (rows, cols * bits // 32), device="cuda", generator=g,
+                                   dtype=torch.int64).to(torch.int32).view(torch.uint32)
+                s_ = (torch.rand(rows, cols // gs, device="cuda", generator=g) * 0.02).to(dt)
+                b_ = (torch.rand(rows, cols // gs, device="cuda", generator=g) * 0.02 - 0.01).to(dt)
+                ws.append((wq, s_, b_))
+            x = torch.randn(M, K, device="cuda", generator=g).to(dt)
+            out = torch.empty(M, N, dtype=dt, device="cuda")
+            gr = capture(lambda: [mq.quantized_matmul(x, *w, tr, gs, bits, out=out) for w in ws])
+            ms = timed_graphs([gr], max(2, iters), 1) / nl
+            del gr
+            res.append({"dtype": dtn, "bits": bits, "transpose": tr, "M": M, "us": round(ms * 1e3, 2),
+                        "weight_GBps": round(N * K * bits / 8 / (ms * 1e-3) / 1e9, 1),
+                        "TFLOPS": round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 1)})
+            del ws
     return res
 
 
@@ -687,8 +722,8 @@ def main():
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--extras", default="copy,sweep,qmm,gather,moe,e2e",
-                    help="comma-separated extra sections: copy, sweep, qmm, gather, moe, e2e")
+    ap.add_argument("--extras", default="copy,sweep,qmm,gather,moe,e2e,general",
+                    help="comma-separated extra sections: copy, sweep, qmm, gather, moe, e2e, general")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run 5 copies of 256 MiB and 5 gate launches, eager, for rocprofv3 --pmc")
@@ -753,6 +788,8 @@ def main():
             extra["fused_moe_decode"] = fused_moe()
         if "e2e" in want:
             extra["e2e_decode_qwen3_8b_shape"] = e2e_decode()
+        if "general" in want:
+            extra["general_path"] = general_path()
         line["extra"] = extra
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(gate)
