@@ -126,7 +126,7 @@ const char* mlxq_version(void);
  * transpose.  Shapes/dtypes exactly as mlx::core::quantized_matmul
  * (ops.cpp:4955-5008): out.shape = x.shape[:-1] + [N], out dtype =
  * promote(x, scales, biases) for affine and x.dtype for fp modes.
- * Implemented: both transposes; mode "affine" with bits 2, 3, 4, 5, 6 or 8
+ * Implemented: both transposes; mode "affine" with bits 1, 2, 3, 4, 5, 6 or 8
  * and group_size 32/64/128; mode "mxfp4"; bfloat16, float16 and float32
  * activations, scales and biases (computed in the promoted type, fp32
  * accumulation); w 2-D, or batched with batch dims that broadcast against
@@ -240,7 +240,7 @@ mlxq_status mlxq_gather_qmm_shape(const mlxq_array* x, const mlxq_array* w,
  * LUT[q] * from_fp8(s) (exact) (ops.cpp:5661-5695; e4m3 decoding as
  * rocm/quantized/convert_fp8.hip:68-90).
  * `dtype` < 0 selects the reference default (scales' dtype for affine,
- * bfloat16 for fp modes).  Affine: bits 2, 3, 4, 5, 6, 8 with scales/biases
+ * bfloat16 for fp modes).  Affine: bits 1-6 and 8 with scales/biases
  * of one type T in {bfloat16, float16, float32} and any of those outputs,
  * To(T(T(q*s) + b)) bit-exactly (ops.cpp:5494-5586 then astype).  mxfp4
  * also to float16/float32 (the scale 2^(s-127) formed in the output type,

@@ -666,8 +666,7 @@ void require_gen_support(const QmmSpec& sp, const mlxq_array* x, const mlxq_arra
     unsupported(std::string(tag) + ": mode '" + (sp.mode == NVFP4_M ? "nvfp4" : "mxfp8") + "' is not implemented");
   if (sp.mode == MXFP4_M && (sp.gs != 32 || sp.bits != 4))
     unsupported(std::string(tag) + ": mxfp4 needs group_size 32 and bits 4");
-  if (sp.mode == AFFINE && sp.bits != 2 && sp.bits != 3 && sp.bits != 4 && sp.bits != 5 && sp.bits != 6 &&
-      sp.bits != 8)
+  if (sp.mode == AFFINE && (sp.bits < 1 || sp.bits > 8 || sp.bits == 7))
     unsupported(std::string(tag) + ": affine bits " + std::to_string(sp.bits) + " is not implemented");
   if (sp.mode == AFFINE && sp.gs != 32 && sp.gs != 64 && sp.gs != 128)
     unsupported(std::string(tag) + ": group_size must be 32, 64 or 128");
@@ -1777,7 +1776,7 @@ mlxq_status mlxq_dequantize(const mlxq_array* w, const mlxq_array* scales, const
                           (mode != AFFINE || (scales->dtype == MLXQ_BFLOAT16 && biases->dtype == MLXQ_BFLOAT16));
     const bool dedicated = bf16_all && (mode != AFFINE || bits == 2 || bits == 4 || bits == 6 || bits == 8);
     if (!dedicated) {
-      if (mode == AFFINE && bits != 2 && bits != 3 && bits != 4 && bits != 5 && bits != 6 && bits != 8)
+      if (mode == AFFINE && (bits < 1 || bits > 8 || bits == 7))
         unsupported("dequantize: affine bits " + std::to_string(bits) + " is not implemented");
       if (mode == MXFP8_M || mode == NVFP4_M) unsupported("dequantize: only bfloat16 output is implemented for this mode");
       if (gen_type(out_type) < 0) unsupported("dequantize: output dtype " + std::string(dtype_name(out_type)) +

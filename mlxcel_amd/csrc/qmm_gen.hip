@@ -11,8 +11,8 @@
 // bits are read as a little-endian bit stream, quantized.cpp:107-137).
 //
 // Covered here: T in {bfloat16, float16, float32} (x and scales may each be
-// any of them; the cast to T is exact), affine codes of 2, 3, 4, 5, 6 and 8
-// bits with groups of 32, 64 or 128, mxfp4, both transposes, any rows per
+// any of them; the cast to T is exact), affine codes of 1, 2, 3, 4, 5, 6 and
+// 8 bits with groups of 32, 64 or 128, mxfp4, both transposes, any rows per
 // matrix, and the segment tables of gather_qmm.
 //
 // Design.  One workgroup computes a BM x 64 output tile of one segment over

@@ -70,7 +70,7 @@ def check(y, want64, dtype):
 
 
 @pytest.mark.parametrize("transpose", [True, False])
-@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 6, 8])
 @pytest.mark.parametrize("xt,st", [("float16", "float16"), ("float32", "float32"), ("bfloat16", "bfloat16"),
                                    ("bfloat16", "float16")])
 def test_quantized_matmul_types_and_widths(transpose, bits, xt, st):
@@ -224,7 +224,7 @@ def test_strided_operands_bitwise(kind):
 
 @pytest.mark.parametrize("ts", ["bfloat16", "float16", "float32"])
 @pytest.mark.parametrize("to", ["bfloat16", "float16", "float32"])
-@pytest.mark.parametrize("bits", [3, 4, 5])
+@pytest.mark.parametrize("bits", [1, 3, 4, 5])
 def test_dequantize_types_bitwise(ts, to, bits):
     announce("gen_dequant", ts, to, bits)
     rows, K, gs = 8, 256, 64

@@ -49,6 +49,7 @@ def test_six_bit_codes_hand_worked():
 
 
 @pytest.mark.parametrize("bits,byte,want", [
+    (1, 0xB4, [0, 0, 1, 0, 1, 1, 0, 1]),  # 1011 0100, low bit first
     (2, 0xB4, [0, 1, 3, 2]),        # 10 11 01 00, low pair first
     (4, 0xB4, [4, 11]),             # low nibble first
     (8, 0xB4, [180]),
@@ -58,7 +59,7 @@ def test_power_of_two_codes_hand_worked(bits, byte, want):
     assert got.tolist() == want
 
 
-@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 6, 8])
 def test_pack_unpack_round_trip(bits):
     rng = np.random.default_rng(bits)
     codes = rng.integers(0, 1 << bits, size=(3, 96))
