@@ -42,6 +42,7 @@ SOURCES = {
     "qmv_fr.hip": [],
     "qmv_b4.hip": [],
     "qmv_mid.hip": [],
+    "qmv_mr.hip": [],
     "qmm_group.hip": [],
     "qmm.hip": [],
     "qmm_gen.hip": [],

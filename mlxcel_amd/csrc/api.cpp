@@ -512,9 +512,10 @@ struct Knobs {
   int qmv_nw = 0, qmv_tk = 0, qmv_r = 0, b4_rg = 0, b4_cpw = 0;
   int qmm_min_rows = kQmmMinRows, qmm_tile = -1, qmm_ksplit = 0;
   int qmv_mid = 1, qmv_multi = 1;
+  int qmv_mr = 1;  // whole-row mid-size kernel where it applies (0: off)
   int gen_ks = 0;  // K splits of the general kernel (0: planner)
   int gather_sorted = 1, gather_group = -1, gather_runs = 1, gather_direct = 1;
-  std::string qmv_kernel;  // "", "rs", "b4", "mid", "fr", "mfma"
+  std::string qmv_kernel;  // "", "rs", "b4", "mid", "mr", "fr", "mfma"
 };
 
 int env_int(const char* name, int dflt) {
@@ -535,6 +536,7 @@ const Knobs* read_knobs() {
   k->qmm_ksplit = env_int("MLXQ_QMM_KSPLIT", 0);
   k->qmv_mid = env_int("MLXQ_QMV_MID", 1);
   k->qmv_multi = env_int("MLXQ_QMV_MULTI", 1);
+  k->qmv_mr = env_int("MLXQ_QMV_MR", 1);
   k->gen_ks = env_int("MLXQ_GEN_KS", 0);
   k->gather_sorted = env_int("MLXQ_GATHER_SORTED", 1);
   k->gather_group = env_int("MLXQ_GATHER_GROUP", -1);
@@ -732,7 +734,7 @@ Skinny skinny_choice(int rows, int fmt = mlxq::AFF4, int64_t K = 0) {
 bool use_mid(int rows, int fmt, int64_t K) {
   if (fmt == mlxq::MXFP4 || rows > 16) return false;
   const std::string& k = knobs().qmv_kernel;
-  if (k == "mid") return true;
+  if (k == "mid" || k == "mr") return true;
   if (!k.empty()) return false;
   if (knobs().qmv_mid == 0) return false;
   (void)K;
@@ -1036,9 +1038,43 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
   const int fmt = fmt_of(sp.mode, sp.bits);
   const int cap = mlxq::qmv_max_rows(fmt, sp.gs);
   View wv{w}, xv{x};
-  if (wv.ndim() == 2 && rows_total <= 16 && use_mid((int)rows_total, fmt, sp.K)) {
-    // 5-16 rows: activations staged once per 128 weight rows (qmv_mid.hip)
+  // 3-4 rows of 4-bit codes against a tall matrix: the whole-row mid-size
+  // kernel also beats the block-MFMA kernel (gate/up M=4: 11.8 us vs 12.6)
+  const bool mr_small = rows_total >= 3 && rows_total < kMidMinRows && fmt == mlxq::AFF4 && knobs().qmv_mr != 0 &&
+                        knobs().qmv_kernel.empty() && wv.ndim() == 2 &&
+                        mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows_total, device_info(current_device()).cus,
+                                          false).ok;
+  if (wv.ndim() == 2 && rows_total <= 16 && (mr_small || use_mid((int)rows_total, fmt, sp.K))) {
     const int dev = current_device();
+    int shift = 0;
+    while ((1 << shift) < sp.gs) shift++;
+    const std::string& forced = knobs().qmv_kernel;
+    // Matrices with ~one 64-row workgroup per CU: whole rows per wave, one
+    // launch (qmv_mr.hip).  It beats the split-K kernel below up to 8 rows
+    // and for 8-bit codes; 4-bit at 9-16 rows stays there (MI355X,
+    // Llama-3-8B gate/up, graph-timed: 4-bit M=8 11.8-12.0 us vs 12.4-12.5,
+    // 8-bit M=8 17.7 vs 20.7, 4-bit M=16 18.9 vs 15.8).
+    const bool mr_default = knobs().qmv_mr != 0 && forced.empty() && (fmt == mlxq::AFF8 || rows_total <= 8);
+    if (forced == "mr" || mr_default) {
+      const mlxq::QmvMrPlan rp = mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows_total, device_info(dev).cus,
+                                                   forced == "mr");
+      if (rp.ok) {
+        mlxq::QmvMrArgs m{};
+        m.x = a.x;
+        m.w = a.w;
+        m.scales = static_cast<const uint16_t*>(a.scales);
+        m.biases = a.biases;
+        m.out = a.out;
+        m.M = (int)rows_total;
+        m.N = (int)sp.N;
+        m.K = (int)sp.K;
+        m.gs_shift = shift;
+        hip_check(mlxq::qmv_mr_launch(fmt, m, rp, stream), "qmv_mr launch");
+        return;
+      }
+    }
+    // 5-16 rows: activations staged once per 128 weight rows, fp32 partials
+    // of the K ranges added by a second launch (qmv_mid.hip)
     const mlxq::QmvMidPlan mp = mlxq::qmv_mid_plan(fmt, sp.gs, sp.N, sp.K, (int)rows_total);
     if (mp.ok) {
       mlxq::QmvMidArgs m{};
@@ -1050,8 +1086,6 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
       m.M = (int)rows_total;
       m.N = (int)sp.N;
       m.K = (int)sp.K;
-      int shift = 0;
-      while ((1 << shift) < sp.gs) shift++;
       m.gs_shift = shift;
       m.ks = mp.ks;
       if (mp.ks > 1)

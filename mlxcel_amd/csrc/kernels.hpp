@@ -206,6 +206,30 @@ QmvMidPlan qmv_mid_plan(int fmt, int gs, int64_t N, int64_t K, int rows);
 // Launches the kernel and, with several K ranges, the fixed-order reduction.
 hipError_t qmv_mid_launch(int fmt, const QmvMidArgs& a, const QmvMidPlan& p, hipStream_t stream);
 
+// Mid-size decode over whole rows (qmv_mr.hip): 1-16 activation rows against
+// one affine 4/8-bit weight matrix with enough rows for ~one workgroup of 64
+// rows per CU; each wave finishes 16 outputs per activation row over all of K.
+struct QmvMrArgs {
+  const uint16_t* x;       // bf16 [M][K]
+  const uint32_t* w;       // packed codes [N][K*bits/32]
+  const uint16_t* scales;  // bf16 [N][K/gs]
+  const uint16_t* biases;  // bf16 [N][K/gs]
+  uint16_t* out;           // bf16 [M][N]
+  int M, N, K, gs_shift;
+};
+struct QmvMrPlan {
+  bool ok = false;
+  int s = 1;           // quantization groups per 4-chunk window
+  int na = 1;          // 16-row MFMA A tiles
+  int xr = 8;          // activation rows staged (8 or 16)
+  int rk = 1024;       // K positions per staged range
+  int row_blocks = 0;  // workgroups (64 weight rows each)
+  size_t lds = 0;
+};
+// force: plan even when the matrix has too few rows to fill the CUs
+QmvMrPlan qmv_mr_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int cus, bool force);
+hipError_t qmv_mr_launch(int fmt, const QmvMrArgs& a, const QmvMrPlan& p, hipStream_t stream);
+
 // Expert-sorted gather (qmm_group.hip), mxfp4, one activation row per index
 // entry: a workgroup per (128 weight rows, expert) finds the expert's rows in
 // the sorted indices and streams its weights once per 64 rows.
