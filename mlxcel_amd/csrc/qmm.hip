@@ -300,12 +300,17 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
   constexpr int BITS = FMT == AFF8 ? 8 : 4;
   constexpr int RS = BK;                     // LDS row stride (bf16): 128 bytes, swizzled
   constexpr int XL = BM * BK * 2 / 16 / NT;  // 16-byte activation loads per thread and K-step
-  constexpr int WT = BK * BITS / 8 / 16;     // threads per weight row and K-step (16 bytes each)
+  // weight piece per thread and load: 16 bytes, or 8 when a K-step of the
+  // tile's weights is less than 16 bytes per thread (256 x 128, 8 waves, 4-bit)
+  constexpr int PB = BN * BK * BITS / 8 / NT >= 16 ? 16 : 8;
+  constexpr int PW = PB / 4;                 // words per piece
+  constexpr int WT = BK * BITS / 8 / PB;     // threads per weight row and K-step
   constexpr int WROWS = NT / WT;             // weight rows per pass
   constexpr int WP = BN / WROWS;             // weight loads per thread and K-step
-  constexpr int VPL = 128 / BITS;            // values per 16-byte weight load
+  constexpr int VPL = PB * 8 / BITS;         // values per weight load
   constexpr int CHG = AFF ? 8 : 16;          // groups in a 16-byte scale chunk
   static_assert(WP >= 1 && WROWS * WP == BN && BN <= NT && XL >= 1, "tile shape");
+  static_assert(PB == 16 || (BITS == 4 && PB == 8), "8-byte pieces only for 4-bit codes");
 
   __shared__ __align__(16) uint16_t xs[2][BM * RS];
   __shared__ __align__(16) uint16_t wsm[2][BN * RS];
@@ -379,7 +384,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
 #pragma unroll
   for (int p = 0; p < WP; p++) {
     const int n = n0 + wrow + WROWS * p;
-    woff[p] = n < N ? (uint32_t)n * RB + (uint32_t)(wpc * 16) : kDeadOfs;
+    woff[p] = n < N ? (uint32_t)n * RB + (uint32_t)(wpc * PB) : kDeadOfs;
   }
 
   // scale chunks: thread t < BN loads the 16-byte chunk of row n0 + t
@@ -430,9 +435,16 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
   auto load_step = [&](int ks) {
     const int k0 = ks * BK;
 #pragma unroll
-    for (int p = 0; p < WP; p++)
-      wreg[p] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, woff[p] + (uint32_t)(k0 * BITS / 8), 0, 0));
+    for (int p = 0; p < WP; p++) {
+      if constexpr (PB == 16) {
+        wreg[p] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, woff[p] + (uint32_t)(k0 * BITS / 8), 0, 0));
+      } else {
+        const u32x2 h = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_raw_buffer_load_b64(wr, woff[p] + (uint32_t)(k0 * BITS / 8), 0, 0));
+        wreg[p] = u32x4{h[0], h[1], 0u, 0u};
+      }
+    }
 #pragma unroll
     for (int i = 0; i < XL; i++)
       xreg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff[i] + (uint32_t)k0 * 2u, 0, 0));
@@ -442,8 +454,9 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
   // MFMAs of one slice: part p stores the activation loads and dequantizes
   // the weight words that fall in the p-th share.
   constexpr int NPART = BK / 16;
-  constexpr int NWORD = WP * 4;  // weight words per thread and K-step
-  static_assert(BITS != 8 || WP % 2 == 0 || WP * 4 / NPART >= 2, "8-bit word pairs must fall in one part");
+  constexpr int NWORD = WP * PW;  // weight words per thread and K-step
+  // (8-bit: the part holding the even word of a pair writes both words; the
+  // registers hold the whole step until load_step(ks + 2), after the last part)
   auto store_part = [&](int buf, int p, int ks) {
 #pragma unroll
     for (int i = 0; i < XL; i++)
@@ -454,9 +467,9 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
 #pragma unroll
     for (int e = 0; e < NWORD; e++) {
       if (e * NPART / NWORD != p) continue;
-      const int pp = e / 4;  // which weight load
+      const int pp = e / PW;  // which weight load
       const int r = wrow + WROWS * pp;
-      const uint32_t w = wreg[pp][e % 4];
+      const uint32_t w = wreg[pp][e % PW];
       uint16_t* rowp = &wsm[buf][r * RS];
       const int r7 = swz(r);
       if constexpr (AFF) {
@@ -470,19 +483,19 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
                            pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<1>(lo), bi), __builtin_fmaf(sc, cvt_ubyte<1>(hi), bi)),
                            pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<2>(lo), bi), __builtin_fmaf(sc, cvt_ubyte<2>(hi), bi)),
                            pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<3>(lo), bi), __builtin_fmaf(sc, cvt_ubyte<3>(hi), bi))};
-          const int ch = wpc * 4 + (e % 4);  // logical 16-byte chunk (8 values)
+          const int ch = wpc * PW + (e % PW);  // logical 16-byte chunk (8 values)
           *reinterpret_cast<u32x4*>(rowp + ((ch ^ r7) << 3)) = o;
         } else {
           // two words (8 codes) per 16-byte chunk, written with the even word:
           // the same 16-byte LDS stores as the 4-bit path (8-byte stores of
           // one word each conflicted on 16% of the LDS cycles)
           if ((e & 1) == 0) {
-            const uint32_t w1 = wreg[pp][(e % 4) + 1];
+            const uint32_t w1 = wreg[pp][(e % PW) + 1];
             const u32x4 o = {pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<0>(w), bi), __builtin_fmaf(sc, cvt_ubyte<1>(w), bi)),
                              pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<2>(w), bi), __builtin_fmaf(sc, cvt_ubyte<3>(w), bi)),
                              pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<0>(w1), bi), __builtin_fmaf(sc, cvt_ubyte<1>(w1), bi)),
                              pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<2>(w1), bi), __builtin_fmaf(sc, cvt_ubyte<3>(w1), bi))};
-            const int ch = wpc * 2 + (e % 4) / 2;  // logical 16-byte chunk (8 values)
+            const int ch = wpc * (PW / 2) + (e % PW) / 2;  // logical 16-byte chunk (8 values)
             *reinterpret_cast<u32x4*>(rowp + ((ch ^ r7) << 3)) = o;
           }
         }
@@ -501,7 +514,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
           for (int h = 0; h < 4; h++)
             o[h] = pack_bf16x2(bf16_bits_to_f32(v[h] & 0xFFFFu) * sc, bf16_bits_to_f32(v[h] >> 16) * sc);
         }
-        const int ch = wpc * 4 + (e % 4);
+        const int ch = wpc * PW + (e % PW);
         *reinterpret_cast<u32x4*>(rowp + ((ch ^ r7) << 3)) = u32x4{o[0], o[1], o[2], o[3]};
       }
     }
@@ -653,11 +666,11 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
 namespace {
 // Tile codes: 0 = 256 x 128, 1 = 256 x 256, 2 = 128 x 128, 3 = 64 x 128
 // (16x16-MFMA kernel, grid (n, m, split)); 4 = 256 x 256 (8 waves), 5 = 256 x 128,
-// 6 = 128 x 128, 7 = 256 x 256 (4 waves) (32x32-MFMA tile kernel, 1-D
-// XCD-ordered grid).
-constexpr int kTiles = 8;
-const int kBM[kTiles] = {256, 256, 128, 64, 256, 256, 128, 256};
-const int kBN[kTiles] = {128, 256, 128, 128, 256, 128, 128, 256};
+// 6 = 128 x 128, 7 = 256 x 256 (4 waves), 8 = 256 x 128 (8 waves, 4 x 2)
+// (32x32-MFMA tile kernel, 1-D XCD-ordered grid).
+constexpr int kTiles = 9;
+const int kBM[kTiles] = {256, 256, 128, 64, 256, 256, 128, 256, 256};
+const int kBN[kTiles] = {128, 256, 128, 128, 256, 128, 128, 256, 128};
 bool is_tile_kernel(int tile) { return tile >= 4; }
 }  // namespace
 
@@ -675,9 +688,14 @@ QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus, 
     tile = tile_req;
   } else {
     // 256 x 256 (8 waves) when there are enough tiles or K is long enough
-    // for a K split to fill the CUs; else 128 x 128, two workgroups per CU
-    // (measured on MI355X at the Llama-3-8B prefill shapes)
-    tile = (M > 128 && (tiles_of(4) >= num_cus / 2 || K >= 8192)) ? 4 : 6;
+    // for a K split to fill the CUs; else 128 x 128, two workgroups per CU.
+    // Up to ~512 rows, 256 x 128 on 8 waves where it measured faster: long K
+    // (split, down projections: 88-89 us vs 91-93 at M=512) and 8-bit codes
+    // with ~one tile per CU (gate/up M=512: 83 us vs 94).  Measured on MI355X
+    // at the Llama-3-8B prefill shapes.
+    const bool mid_rows = M > 128 && M <= 768;
+    if (mid_rows && (K >= 8192 || (fmt == AFF8 && tiles_of(8) * 4 >= (int64_t)num_cus * 3))) tile = 8;
+    else tile = (M > 128 && (tiles_of(4) >= num_cus / 2 || K >= 8192)) ? 4 : 6;
   }
   p.tile = tile;
   p.rows_per_tile = kBM[tile];
@@ -714,6 +732,7 @@ void qmm_launch_fmt(const QmmArgs& a, const QmmPlan& p, hipStream_t stream) {
       case 4: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 256, 256, 2, 4>), grid, dim3(512), 0, stream, a); break;
       case 5: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 256, 128, 2, 2>), grid, dim3(256), 0, stream, a); break;
       case 7: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 256, 256, 2, 2>), grid, dim3(256), 0, stream, a); break;
+      case 8: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 256, 128, 4, 2>), grid, dim3(512), 0, stream, a); break;
       default: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 128, 128, 2, 2>), grid, dim3(256), 0, stream, a); break;
     }
     return;

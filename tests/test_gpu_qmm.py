@@ -22,21 +22,22 @@ def run(x, wq, s, b, gs, bits):
     return host_u16(y)
 
 
-@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 4, 5, 6, 7])
+@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 4, 5, 6, 7, 8])
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("gs", [32, 64, 128])
 @pytest.mark.parametrize("M,N,K", [(65, 200, 1024), (300, 136, 2048), (512, 384, 512)])
 def test_affine_qmm_vs_oracle(monkeypatch, tile, bits, gs, M, N, K):
     # every output-tile shape (MLXQ_QMM_TILE: 16x16-MFMA kernel 0 = 256x128,
     # 1 = 256x256, 2 = 128x128; 32x32-MFMA tile kernel 4 = 256x256,
-    # 5 = 256x128, 6 = 128x128, 7 = 256x256 on 4 waves; -1 = by shape)
+    # 5 = 256x128, 6 = 128x128, 7 = 256x256 on 4 waves, 8 = 256x128 on 8
+    # waves with 8-byte 4-bit weight pieces; -1 = by shape)
     setknob(monkeypatch, "MLXQ_QMM_TILE", str(tile))
     announce("qmm_affine", tile, bits, gs, M, N, K)
     x, wq, s, b = affine_case(M, N, K, gs, bits, 2100 + M + N + bits + gs)
     assert max_rel(run(x, wq, s, b, gs, bits), orc.qmm_t_affine(x, wq, s, b, gs, bits)) <= TOL
 
 
-@pytest.mark.parametrize("tile", [4, 5, 6, 7])
+@pytest.mark.parametrize("tile", [4, 5, 6, 7, 8])
 @pytest.mark.parametrize("bits,gs", [(4, 32), (4, 64), (8, 32), (8, 64)])
 def test_affine_qmm_unaligned_scale_rows(monkeypatch, tile, bits, gs):
     # K = 2880 (gpt-oss): K / gs groups per row = 90 or 45, so scale rows are
@@ -49,8 +50,8 @@ def test_affine_qmm_unaligned_scale_rows(monkeypatch, tile, bits, gs):
     assert max_rel(run(x, wq, s, b, gs, bits), orc.qmm_t_affine(x, wq, s, b, gs, bits)) <= TOL
 
 
-@pytest.mark.parametrize("tile,ksplit", [(-1, 0), (1, 3), (2, 5), (4, 3), (5, 5), (6, 2), (7, 3), (8, 3), (9, 5),
-                                         (9, 1)])
+@pytest.mark.parametrize("tile,ksplit", [(-1, 0), (1, 3), (2, 5), (4, 3), (5, 5), (6, 2), (7, 3), (8, 3), (8, 5),
+                                         (8, 1)])
 def test_affine_qmm_split_k_and_batch_fold(monkeypatch, tile, ksplit):
     # few output tiles and a long K: the K range is split across workgroups
     # (uneven splits included); x given as [2, 128, K] folds into 256 rows
@@ -67,7 +68,7 @@ def test_affine_qmm_split_k_and_batch_fold(monkeypatch, tile, ksplit):
     np.testing.assert_array_equal(got, again)
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 4, 5, 6, 7])
+@pytest.mark.parametrize("tile", [0, 1, 2, 4, 5, 6, 7, 8])
 def test_mxfp4_qmm_vs_oracle(monkeypatch, tile):
     setknob(monkeypatch, "MLXQ_QMM_TILE", str(tile))
     announce("qmm_mxfp4", tile)
