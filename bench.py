@@ -586,6 +586,25 @@ class QuantDecoder:
         self.pos.copy_(saved[1])
         return g
 
+    def projections_graph(self):
+        """Graph of one decode step's quantized projections alone (every
+        layer's q/k/v, o, gate/up and down, then the LM head) on fixed
+        activations of the step's shapes: the library's share of a step."""
+        c, B = self.c, self.B
+        xh = randn_bf16((B, c.hidden), 21)
+        xo = randn_bf16((B, c.nq * c.hd), 22)
+        xi = randn_bf16((B, c.inter), 23)
+
+        def run():
+            for L in self.layers:
+                self.qmm_n(xh, [L["q"], L["k"], L["v"]])
+                self.qmm(xo, L["o"])
+                self.qmm_n(xh, [L["g"], L["u"]])
+                self.qmm(xi, L["d"])
+            self.qmm(xh, self.lm)
+
+        return capture(run)
+
     def generate(self, prompt, steps, bucket=64):
         """Greedy decode `steps` tokens after `prompt`; returns (tokens [B, steps],
         prefill seconds, decode seconds).  Each step replays the graph of the
@@ -626,11 +645,16 @@ def e2e_decode(batches=(1, 16), prompt_len=512, steps=256, layers=36, separate_a
         prompt = torch.randint(0, model.c.vocab, (B, prompt_len), device="cuda", generator=g)
         model.generate(prompt[:, :64], 8)  # warm-up (kernels, allocator)
         toks, t_pre, t_dec = model.generate(prompt, steps)
+        # the same step's quantized projections alone, replayed back to back
+        lib_ms = timed_graphs([model.projections_graph()], 20, 3)
+        step_ms = t_dec / steps * 1e3
         res.append({"batch": B, "multi_projection": multi, "prompt": prompt_len, "decode_tokens": steps,
-                    "decode_tok_s": round(B * steps / t_dec, 1), "ms_per_step": round(t_dec / steps * 1e3, 3),
+                    "decode_tok_s": round(B * steps / t_dec, 1), "ms_per_step": round(step_ms, 3),
+                    "library_ms_per_step": round(lib_ms, 3), "library_share": round(lib_ms / step_ms, 3),
                     "prefill_tok_s": round(B * prompt_len / t_pre, 1),
                     "weight_GB": round(model.weight_bytes / 1e9, 3),
-                    "weight_stream_GBps": round(model.weight_bytes / (t_dec / steps) / 1e9, 1)})
+                    "weight_stream_GBps": round(model.weight_bytes / (t_dec / steps) / 1e9, 1),
+                    "library_weight_stream_GBps": round(model.weight_bytes / (lib_ms * 1e-3) / 1e9, 1)})
         del model
         torch.cuda.empty_cache()
     return res
