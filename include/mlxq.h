@@ -255,7 +255,10 @@ mlxq_status mlxq_dequantize(const mlxq_array* w, const mlxq_array* scales,
  * nvfp4 (without a global scale) follow the graph quantizer
  * (ops.cpp:5364-5431) as the ROCm backend evaluates it, to_fp8 included
  * (rocm/quantized/convert_fp8.hip:18-66).  `biases_out` is ignored for fp
- * modes.  Implemented for bfloat16 w; affine bits 2, 4, 6 and 8. */
+ * modes.  Affine: bfloat16, float16 or float32 w (scales and biases in w's
+ * type), bits 1-6 and 8 (8 codes per `bits` bytes, the little-endian bit
+ * stream of CPUQ:1283-1297); fp modes: bfloat16 w.  w row-contiguous and
+ * 16-byte aligned. */
 mlxq_status mlxq_quantize(const mlxq_array* w, int32_t group_size, int32_t bits,
                           const char* mode, mlxq_array* wq_out, mlxq_array* scales_out,
                           mlxq_array* biases_out, void* stream);

@@ -1920,19 +1920,19 @@ mlxq_status mlxq_quantize(const mlxq_array* w, int32_t group_size, int32_t bits,
     check_out(wq_out, qs, MLXQ_UINT32, tag);
     check_out(scales_out, ss, mode == AFFINE ? w->dtype : (int)MLXQ_UINT8, tag);
     if (mode == AFFINE) check_out(biases_out, ss, w->dtype, tag);
-    if (mode == AFFINE && bits != 2 && bits != 4 && bits != 6 && bits != 8)
-      unsupported("quantize: affine bits 2, 4, 6 and 8 are implemented");
-    if (w->dtype != MLXQ_BFLOAT16) unsupported("quantize: only bfloat16 weights are implemented");
+    if (mode == AFFINE && gen_type(w->dtype) < 0)
+      unsupported(std::string("quantize: ") + dtype_name(w->dtype) +
+                  " weights are not implemented (bfloat16, float16 and float32 are)");
+    if (mode != AFFINE && w->dtype != MLXQ_BFLOAT16)
+      unsupported("quantize: only bfloat16 weights are implemented for this mode");
     require_contiguous(w, "w");
     const int64_t K = wv.dim(-1);
     const int64_t rows = wv.size() / std::max<int64_t>(K, 1);
     if (rows == 0 || K == 0) return;
     hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
     if (mode == AFFINE) {
-      hip_check(mlxq::launch_affine_quantize(static_cast<const uint16_t*>(w->data),
-                                             static_cast<uint32_t*>(wq_out->data),
-                                             static_cast<uint16_t*>(scales_out->data),
-                                             static_cast<uint16_t*>(biases_out->data), rows, K, group_size, bits,
+      hip_check(mlxq::launch_affine_quantize(w->data, gen_type(w->dtype), static_cast<uint32_t*>(wq_out->data),
+                                             scales_out->data, biases_out->data, rows, K, group_size, bits,
                                              stream),
                 "quantize launch");
     } else if (mode == MXFP4_M) {

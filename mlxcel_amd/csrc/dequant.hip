@@ -171,24 +171,53 @@ hipError_t launch_mxfp4_dequantize(const uint32_t* w, const uint8_t* scales, uin
 }
 
 // ---- affine quantize --------------------------------------------------------
-// GS/8 consecutive lanes own one group; each lane converts 8 consecutive values.
+// GS/8 consecutive lanes own one group; each lane converts 8 consecutive
+// values.  TI: element type of the weights and of the scales / biases written
+// (GEN_BF16, GEN_F16, GEN_F32; MLX writes them in the weights' type).  The
+// arithmetic is the reference CPU quantizer's (quantized.cpp:1251-1303) in
+// float32, values widened exactly from TI.
 
-template <int BITS, int GS>
-__global__ __launch_bounds__(256) void affine_quant_kernel(const uint16_t* __restrict__ w,
-                                                           uint32_t* __restrict__ wq,
-                                                           uint16_t* __restrict__ scales,
-                                                           uint16_t* __restrict__ biases,
+template <int TI>
+__device__ __forceinline__ float widen16(uint32_t h) {
+  if constexpr (TI == GEN_F16) return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+  return bf16_bits_to_f32(h);
+}
+
+// static_cast<T>(v): round to nearest even
+template <int TI>
+__device__ __forceinline__ void store_typed(void* p, int64_t i, float v) {
+  if constexpr (TI == GEN_F32) reinterpret_cast<float*>(p)[i] = v;
+  else if constexpr (TI == GEN_F16) reinterpret_cast<_Float16*>(p)[i] = (_Float16)v;
+  else reinterpret_cast<uint16_t*>(p)[i] = (uint16_t)f32_to_bf16_bits(v);
+}
+
+template <int TI, int BITS, int GS>
+__global__ __launch_bounds__(256) void affine_quant_kernel(const void* __restrict__ w, uint32_t* __restrict__ wq,
+                                                           void* __restrict__ scales, void* __restrict__ biases,
                                                            int64_t n_pieces) {
   constexpr int L = GS / 8;  // lanes per group
   const int64_t piece = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // 8 values each
   const bool live = piece < n_pieces;
-  u32x4 v = {0u, 0u, 0u, 0u};
-  if (live) v = *reinterpret_cast<const u32x4*>(w + piece * 8);
   float vals[8];
+  if constexpr (TI == GEN_F32) {
+    u32x4 a = {0u, 0u, 0u, 0u}, b = {0u, 0u, 0u, 0u};
+    if (live) {
+      a = reinterpret_cast<const u32x4*>(w)[2 * piece];
+      b = reinterpret_cast<const u32x4*>(w)[2 * piece + 1];
+    }
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    vals[2 * i] = bf16_bits_to_f32(v[i] & 0xFFFFu);
-    vals[2 * i + 1] = bf16_bits_to_f32(v[i] >> 16);
+    for (int i = 0; i < 4; i++) {
+      vals[i] = __uint_as_float(a[i]);
+      vals[4 + i] = __uint_as_float(b[i]);
+    }
+  } else {
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (live) v = reinterpret_cast<const u32x4*>(w)[piece];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      vals[2 * i] = widen16<TI>(v[i] & 0xFFFFu);
+      vals[2 * i + 1] = widen16<TI>(v[i] >> 16);
+    }
   }
   // (a < b) ? b : a  /  (b < a) ? b : a  as std::max / std::min
   float w_max = -INFINITY, w_min = INFINITY;
@@ -206,19 +235,26 @@ __global__ __launch_bounds__(256) void affine_quant_kernel(const uint16_t* __res
   }
   const float n_bins = (float)((1 << BITS) - 1);
   const float eps = 1e-7f;
-  const bool mask = fabsf(w_min) > fabsf(w_max);
-  float scale = (w_max - w_min) / n_bins;
-  scale = (scale < eps) ? eps : scale;
-  scale = mask ? scale : -scale;
-  const float edge = mask ? w_min : w_max;
-  const float q0 = rintf(edge / scale);
-  float bias = 0.0f;
-  if (q0 != 0.0f) {
-    scale = edge / q0;
-    bias = edge;
+  float scale, bias;
+  if constexpr (BITS == 1) {
+    // code 0 -> w_min, code 1 -> w_max (quantized.cpp:1261-1264)
+    scale = w_max - w_min;
+    scale = (scale < eps) ? eps : scale;
+    bias = w_min;
+  } else {
+    const bool mask = fabsf(w_min) > fabsf(w_max);
+    scale = (w_max - w_min) / n_bins;
+    scale = (scale < eps) ? eps : scale;
+    scale = mask ? scale : -scale;
+    const float edge = mask ? w_min : w_max;
+    const float q0 = rintf(edge / scale);
+    bias = 0.0f;
+    if (q0 != 0.0f) {
+      scale = edge / q0;
+      bias = edge;
+    }
   }
-  // 8 codes of BITS bits, low bits first (8-bit: low 4 in `codes`, high 4 in
-  // `codes_hi`; 6-bit: bits 0-31 in `codes`, 32-47 in `codes_hi`)
+  // 8 codes of BITS bits, low bits first: BITS bytes of the row's stream
   uint64_t all = 0;
 #pragma unroll
   for (int i = 0; i < 8; i++) {
@@ -227,51 +263,58 @@ __global__ __launch_bounds__(256) void affine_quant_kernel(const uint16_t* __res
     q = (n_bins < q) ? n_bins : q;
     all |= (uint64_t)(uint32_t)q << (BITS * i);
   }
-  const uint32_t codes = (uint32_t)all, codes_hi = (uint32_t)(all >> 32);
-  if (BITS == 6) {
-    // two lanes (16 codes, 12 bytes: MLX's 3-byte packs of 4) per 3 words
-    const uint32_t olo = __shfl_xor(codes, 1), ohi = __shfl_xor(codes_hi, 1);
-    if (live && (piece & 1) == 0) {
-      uint32_t* d = wq + (piece >> 1) * 3;
-      d[0] = codes;
-      d[1] = codes_hi | (olo << 16);
-      d[2] = (olo >> 16) | (ohi << 16);
+  if (live) {
+    if constexpr (BITS == 4) {
+      wq[piece] = (uint32_t)all;
+    } else if constexpr (BITS == 8) {
+      *reinterpret_cast<u32x2*>(wq + piece * 2) = u32x2{(uint32_t)all, (uint32_t)(all >> 32)};
+    } else {
+      uint8_t* d = reinterpret_cast<uint8_t*>(wq) + piece * BITS;
+#pragma unroll
+      for (int b = 0; b < BITS; b++) d[b] = (uint8_t)(all >> (8 * b));
     }
-  } else if (BITS == 2) {
-    // two lanes (16 codes) per word
-    const uint32_t other = __shfl_xor(codes, 1);
-    if (live && (piece & 1) == 0) wq[piece >> 1] = codes | (other << 16);
-  } else if (BITS == 4) {
-    if (live) wq[piece] = codes;
-  } else {
-    if (live) *reinterpret_cast<u32x2*>(wq + piece * 2) = u32x2{codes, codes_hi};
-  }
-  if (live && (piece % L) == 0) {
-    scales[piece / L] = (uint16_t)f32_to_bf16_bits(scale);
-    biases[piece / L] = (uint16_t)f32_to_bf16_bits(bias);
+    if ((piece % L) == 0) {
+      store_typed<TI>(scales, piece / L, scale);
+      store_typed<TI>(biases, piece / L, bias);
+    }
   }
 }
 
-template <int BITS>
-static void launch_aq_bits(const uint16_t* w, uint32_t* wq, uint16_t* s, uint16_t* b, int64_t pieces,
-                           int gs, hipStream_t stream) {
+template <int TI, int BITS>
+static void launch_aq_bits(const void* w, uint32_t* wq, void* s, void* b, int64_t pieces, int gs,
+                           hipStream_t stream) {
   const dim3 grid((unsigned)((pieces + 255) / 256));
   if (gs == 32)
-    hipLaunchKernelGGL((affine_quant_kernel<BITS, 32>), grid, dim3(256), 0, stream, w, wq, s, b, pieces);
+    hipLaunchKernelGGL((affine_quant_kernel<TI, BITS, 32>), grid, dim3(256), 0, stream, w, wq, s, b, pieces);
   else if (gs == 64)
-    hipLaunchKernelGGL((affine_quant_kernel<BITS, 64>), grid, dim3(256), 0, stream, w, wq, s, b, pieces);
+    hipLaunchKernelGGL((affine_quant_kernel<TI, BITS, 64>), grid, dim3(256), 0, stream, w, wq, s, b, pieces);
   else
-    hipLaunchKernelGGL((affine_quant_kernel<BITS, 128>), grid, dim3(256), 0, stream, w, wq, s, b, pieces);
+    hipLaunchKernelGGL((affine_quant_kernel<TI, BITS, 128>), grid, dim3(256), 0, stream, w, wq, s, b, pieces);
 }
 
-hipError_t launch_affine_quantize(const uint16_t* w, uint32_t* wq, uint16_t* scales, uint16_t* biases,
-                                  int64_t rows, int64_t K, int gs, int bits, hipStream_t stream) {
+template <int TI>
+static void launch_aq_type(const void* w, uint32_t* wq, void* s, void* b, int64_t pieces, int gs, int bits,
+                           hipStream_t stream) {
+  switch (bits) {
+    case 1: launch_aq_bits<TI, 1>(w, wq, s, b, pieces, gs, stream); break;
+    case 2: launch_aq_bits<TI, 2>(w, wq, s, b, pieces, gs, stream); break;
+    case 3: launch_aq_bits<TI, 3>(w, wq, s, b, pieces, gs, stream); break;
+    case 4: launch_aq_bits<TI, 4>(w, wq, s, b, pieces, gs, stream); break;
+    case 5: launch_aq_bits<TI, 5>(w, wq, s, b, pieces, gs, stream); break;
+    case 6: launch_aq_bits<TI, 6>(w, wq, s, b, pieces, gs, stream); break;
+    default: launch_aq_bits<TI, 8>(w, wq, s, b, pieces, gs, stream); break;
+  }
+}
+
+hipError_t launch_affine_quantize(const void* w, int ti, uint32_t* wq, void* scales, void* biases, int64_t rows,
+                                  int64_t K, int gs, int bits, hipStream_t stream) {
   const int64_t pieces = rows * K / 8;
   if (pieces == 0) return hipSuccess;
-  if (bits == 2) launch_aq_bits<2>(w, wq, scales, biases, pieces, gs, stream);
-  else if (bits == 4) launch_aq_bits<4>(w, wq, scales, biases, pieces, gs, stream);
-  else if (bits == 6) launch_aq_bits<6>(w, wq, scales, biases, pieces, gs, stream);
-  else launch_aq_bits<8>(w, wq, scales, biases, pieces, gs, stream);
+  if ((bits < 1 || bits > 8 || bits == 7) || (gs != 32 && gs != 64 && gs != 128) || ti < 0 || ti > 2)
+    return hipErrorInvalidValue;
+  if (ti == GEN_F32) launch_aq_type<GEN_F32>(w, wq, scales, biases, pieces, gs, bits, stream);
+  else if (ti == GEN_F16) launch_aq_type<GEN_F16>(w, wq, scales, biases, pieces, gs, bits, stream);
+  else launch_aq_type<GEN_BF16>(w, wq, scales, biases, pieces, gs, bits, stream);
   return hipGetLastError();
 }
 

@@ -317,9 +317,10 @@ hipError_t launch_affine_dequantize(const uint32_t* w, const uint16_t* scales, c
                                     hipStream_t stream);
 hipError_t launch_mxfp4_dequantize(const uint32_t* w, const uint8_t* scales, uint16_t* out,
                                    int64_t rows, int64_t K, hipStream_t stream);
-hipError_t launch_affine_quantize(const uint16_t* w, uint32_t* wq, uint16_t* scales,
-                                  uint16_t* biases, int64_t rows, int64_t K, int gs, int bits,
-                                  hipStream_t stream);
+// affine quantize of bfloat16 / float16 / float32 weights (ti: GenType; the
+// scales and biases are written in the same type), bits 1-6 or 8
+hipError_t launch_affine_quantize(const void* w, int ti, uint32_t* wq, void* scales, void* biases, int64_t rows,
+                                  int64_t K, int gs, int bits, hipStream_t stream);
 // mxfp8 (e4m3 codes, e8m0 scales per 32) and nvfp4 (e2m1 codes, e4m3 scales per 16)
 enum FpMode : int { FP_MXFP8 = 0, FP_NVFP4 = 1 };
 hipError_t launch_fp_dequantize(int mode, const uint32_t* w, const uint8_t* scales, uint16_t* out, int64_t rows,

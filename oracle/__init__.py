@@ -44,6 +44,7 @@ def _declare(l: ctypes.CDLL) -> None:
         "oracle_f32_to_bf16_n": [_P, _P, _I64],
         "oracle_bf16_to_f32_n": [_P, _P, _I64],
         "oracle_affine_quantize": [_P, _I64, _I64, _I, _I, _P, _P, _P],
+        "oracle_affine_quantize_t": [_P, _I, _I64, _I64, _I, _I, _P, _P, _P],
         "oracle_affine_dequantize": [_P, _P, _P, _I64, _I64, _I, _I, _I, _P],
         "oracle_mxfp4_quantize": [_P, _I64, _I64, _P, _P],
         "oracle_mxfp4_dequantize": [_P, _P, _I64, _I64, _P],
@@ -64,6 +65,10 @@ def _declare(l: ctypes.CDLL) -> None:
         fn = getattr(l, name)
         fn.argtypes = args
         fn.restype = None if name.endswith("_n") else _I
+    l.oracle_f32_to_f16.argtypes = [ctypes.c_float]
+    l.oracle_f32_to_f16.restype = ctypes.c_uint16
+    l.oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
+    l.oracle_f16_to_f32.restype = ctypes.c_float
     l.oracle_e8m0_to_bf16.argtypes = [ctypes.c_uint8]
     l.oracle_e8m0_to_bf16.restype = ctypes.c_uint16
 
@@ -106,6 +111,32 @@ def affine_quantize(w_bf16: np.ndarray, group_size: int = 64, bits: int = 4):
     _check(lib().oracle_affine_quantize(_ptr(w), rows, K, group_size, bits, _ptr(wq), _ptr(s), _ptr(b)),
            "affine_quantize")
     return wq, s, b
+
+
+_QDT = {"bfloat16": (0, np.uint16), "float16": (1, np.float16), "float32": (2, np.float32)}
+
+
+def affine_quantize_t(w: np.ndarray, dtype: str, group_size: int = 64, bits: int = 4):
+    """Typed affine quantize: w holds bfloat16 bits (uint16), float16 or
+    float32 values per `dtype`; scales / biases come back in the same form."""
+    code, npdt = _QDT[dtype]
+    w = np.ascontiguousarray(w, dtype=npdt)
+    K = w.shape[-1]
+    rows = w.size // K
+    wq = np.empty(w.shape[:-1] + (K * bits // 32,), dtype=np.uint32)
+    s = np.empty(w.shape[:-1] + (K // group_size,), dtype=npdt)
+    b = np.empty_like(s)
+    _check(lib().oracle_affine_quantize_t(_ptr(w), code, rows, K, group_size, bits, _ptr(wq), _ptr(s), _ptr(b)),
+           "affine_quantize_t")
+    return wq, s, b
+
+
+def f32_to_f16_bits(v: float) -> int:
+    return int(lib().oracle_f32_to_f16(float(v)))
+
+
+def f16_bits_to_f32(h: int) -> float:
+    return float(lib().oracle_f16_to_f32(int(h)))
 
 
 def affine_dequantize(wq, scales, biases, group_size: int = 64, bits: int = 4, rounding: int = 2):

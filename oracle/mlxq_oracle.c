@@ -60,6 +60,36 @@ void oracle_bf16_to_f32_n(const uint16_t* in, float* out, int64_t n) {
   for (int64_t i = 0; i < n; i++) out[i] = oracle_bf16_to_f32(in[i]);
 }
 
+/* ---- float16 (IEEE binary16: 1 sign, 5 exponent, 10 mantissa bits) -------- */
+
+float oracle_f16_to_f32(uint16_t h) {
+  const int sign = h >> 15, e = (h >> 10) & 31, m = h & 1023;
+  float v;
+  if (e == 0) v = ldexpf((float)m, -24);                     /* zero, subnormal */
+  else if (e == 31) v = m ? NAN : INFINITY;
+  else v = ldexpf((float)(1024 + m), e - 25);
+  return sign ? -v : v;
+}
+
+/* round to nearest, ties to even; overflow to infinity; NaN -> 0x7E00 */
+uint16_t oracle_f32_to_f16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  const uint32_t a = u & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) return sign | 0x7E00u;
+  if (a >= 0x477FF000u) return sign | 0x7C00u;  /* >= 65520: rounds past 65504 */
+  if (a >= 0x38800000u) {                        /* >= 2^-14: normal */
+    uint32_t r = ((((a >> 23) - 112u) << 10) | ((a >> 13) & 1023u));
+    const uint32_t rem = a & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) r++;
+    return sign | (uint16_t)r;
+  }
+  float av;
+  memcpy(&av, &a, 4);
+  return sign | (uint16_t)rintf(av * 16777216.0f); /* subnormal: units of 2^-24 */
+}
+
 /* bf16 binary op as MLX evaluates it on the CPU: widen, operate in float,
  * round the float result to bf16. */
 static inline float bf(float f) { return oracle_bf16_to_f32(oracle_f32_to_bf16(f)); }
@@ -89,23 +119,41 @@ static inline uint32_t code_at(const uint32_t* row, int bits, int64_t i) {
 
 /* ---- affine quantize: CPUQ:1233-1305 ------------------------------------ */
 
-int oracle_affine_quantize(const uint16_t* w, int64_t rows, int64_t K, int group_size,
-                           int bits, uint32_t* wq, uint16_t* scales, uint16_t* biases) {
-  if (!affine_bits(bits) || !valid_gs(group_size) || K % group_size) return -1;
+/* element i of an array of dtype 0 = bfloat16, 1 = float16, 2 = float32, as
+ * float (exact for all three) */
+static inline float load_as_f32(const void* a, int dtype, int64_t i) {
+  if (dtype == 2) return ((const float*)a)[i];
+  const uint16_t h = ((const uint16_t*)a)[i];
+  return dtype == 1 ? oracle_f16_to_f32(h) : oracle_bf16_to_f32(h);
+}
+
+/* static_cast<T>(f) for the scale and bias outputs */
+static inline void store_from_f32(void* a, int dtype, int64_t i, float f) {
+  if (dtype == 2) ((float*)a)[i] = f;
+  else ((uint16_t*)a)[i] = dtype == 1 ? oracle_f32_to_f16(f) : oracle_f32_to_bf16(f);
+}
+
+/* Any width of 1-6 or 8 bits: the reference packs power-of-two widths
+ * 32/bits codes per uint32 (CPUQ:1283-1285) and 3/5/6 bits as 8, 8 and 4
+ * codes per 3, 5 and 3 bytes (CPUQ:1286-1297), low bits first; both are the
+ * one little-endian bit stream, written here as 8 codes per `bits` bytes. */
+int oracle_affine_quantize_t(const void* w, int dtype, int64_t rows, int64_t K, int group_size, int bits,
+                             uint32_t* wq, void* scales, void* biases) {
+  if (bits < 1 || bits > 8 || bits == 7 || !valid_gs(group_size) || K % group_size || dtype < 0 || dtype > 2)
+    return -1;
   const float n_bins = (float)((1 << bits) - 1);
   const float eps = 1e-7f;
-  const int el_per_int = bits == 6 ? 4 : 32 / bits;     /* codes per pack */
-  const int bytes_per_pack = bits == 6 ? 3 : 4;
-  /* packs per group (each pack a uint32, or 3 bytes at 6 bits) */
+  const int el_per_int = 8;                 /* codes per pack */
+  const int bytes_per_pack = bits;
   const int64_t int_per_group = (int64_t)group_size / el_per_int;
   const int64_t n_groups = rows * (K / group_size);
 
   for (int64_t i = 0; i < n_groups; ++i) {
-    const uint16_t* g = w + i * group_size;
+    const int64_t g = i * group_size;
     float w_min = INFINITY;
     float w_max = -w_min;
     for (int j = 0; j < group_size; ++j) {
-      float v = oracle_bf16_to_f32(g[j]);
+      float v = load_as_f32(w, dtype, g + j);
       w_max = std_max(w_max, v);
       w_min = std_min(w_min, v);
     }
@@ -129,17 +177,23 @@ int oracle_affine_quantize(const uint16_t* w, int64_t rows, int64_t K, int group
     for (int64_t j = 0; j < int_per_group; ++j) {
       uint64_t out_el = 0;
       for (int k = 0; k < el_per_int; ++k) {
-        float w_el = oracle_bf16_to_f32(g[j * el_per_int + k]);
+        float w_el = load_as_f32(w, dtype, g + j * el_per_int + k);
         w_el = rintf((w_el - bias) / scale);
         w_el = std_min(std_max(w_el, 0.0f), n_bins);
         out_el |= (uint64_t)w_el << (k * bits);
       }
       for (int b = 0; b < bytes_per_pack; ++b) out[j * bytes_per_pack + b] = (uint8_t)(out_el >> (8 * b));
     }
-    scales[i] = oracle_f32_to_bf16(scale);
-    biases[i] = oracle_f32_to_bf16(bias);
+    store_from_f32(scales, dtype, i, scale);
+    store_from_f32(biases, dtype, i, bias);
   }
   return 0;
+}
+
+int oracle_affine_quantize(const uint16_t* w, int64_t rows, int64_t K, int group_size,
+                           int bits, uint32_t* wq, uint16_t* scales, uint16_t* biases) {
+  if (!affine_bits(bits)) return -1;
+  return oracle_affine_quantize_t(w, 0, rows, K, group_size, bits, wq, scales, biases);
 }
 
 /* ---- affine dequantize: ROPS:5531-5573 (graph) and QAFF:164 (GPU) -------- */

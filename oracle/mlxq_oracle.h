@@ -24,12 +24,18 @@ extern "C" {
 /* float <-> bf16 with MLX's conversion (round to nearest even, NaN -> 0x7FC0). */
 uint16_t oracle_f32_to_bf16(float f);
 float oracle_bf16_to_f32(uint16_t h);
+uint16_t oracle_f32_to_f16(float f);
+float oracle_f16_to_f32(uint16_t h);
 void oracle_f32_to_bf16_n(const float* in, uint16_t* out, int64_t n);
 void oracle_bf16_to_f32_n(const uint16_t* in, float* out, int64_t n);
 
 /* Affine quantize, CPUQ:1233-1305 (`quantize<bfloat16_t, uint32_t>`).
  * w: [rows, K] bf16.  wq: [rows, K*bits/32] u32.  scales/biases: [rows, K/gs] bf16.
  * bits in {1, 2, 4, 8}; returns 0 on success, -1 on unsupported arguments. */
+/* MLX's CPU affine quantizer for dtype 0 = bfloat16, 1 = float16, 2 = float32
+ * weights (scales and biases written in the same dtype) and bits 1-6 or 8. */
+int oracle_affine_quantize_t(const void* w, int dtype, int64_t rows, int64_t K, int group_size, int bits,
+                             uint32_t* wq, void* scales, void* biases);
 int oracle_affine_quantize(const uint16_t* w, int64_t rows, int64_t K, int group_size,
                            int bits, uint32_t* wq, uint16_t* scales, uint16_t* biases);
 

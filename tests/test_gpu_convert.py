@@ -6,7 +6,9 @@
   quantized.cpp:1233-1305) and the mxfp4 graph quantizer (ops.cpp:5364-5431),
   plus the hand-derived ramp fixtures;
 * dequantize(slice) == slice(dequantize) (src/lib/mlxcel-core/src/ffi_tests.rs:5108-5170);
-* affine bits 2, 4, 6 (MLX's 3-byte packs of 4 codes) and 8;
+* affine bits 2, 4, 6 (MLX's 3-byte packs of 4 codes) and 8; quantize also
+  for float16 / float32 weights and bits 1, 3 and 5 against the oracle's
+  typed restatement (pinned in tests/test_oracle_quant_types.py);
 * mxfp8 and nvfp4 (e4m3 as the ROCm backend's to_fp8 / from_fp8 evaluate it,
   overlays/rocm/mlx/backend/rocm/quantized/convert_fp8.hip:18-90): quantize
   on wide-range data and the hand fixtures, dequantize over every code and
@@ -84,6 +86,66 @@ def test_affine_quantize_bitexact(bits, gs):
     np.testing.assert_array_equal(kw.cpu().numpy(), KAT[f"ramp_wq_b{bits}_g{gs}"])
     np.testing.assert_array_equal(host_u16(ks), KAT[f"ramp_s_b{bits}_g{gs}"])
     np.testing.assert_array_equal(host_u16(kb), KAT[f"ramp_b_b{bits}_g{gs}"])
+
+
+TORCH_DT = {"bfloat16": torch.bfloat16, "float16": torch.float16, "float32": torch.float32}
+
+
+def typed_weights(dtype, rows, K, seed):
+    """(numpy array in the oracle's form, the same values as a device tensor)"""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((rows, K)).astype(np.float32)
+    x *= (10.0 ** rng.uniform(-4, 2, (rows, 1))).astype(np.float32)
+    x[1] = np.abs(x[1])
+    x[2] = -np.abs(x[2])
+    x[3] = 0.375
+    x[4] = 0.0
+    t = torch.from_numpy(x).to(TORCH_DT[dtype])
+    if dtype == "bfloat16":
+        return t.view(torch.int16).numpy().astype(np.uint16), t.cuda()
+    return t.numpy(), t.cuda()
+
+
+def host_bytes(t):
+    return t.cpu().contiguous().view(torch.uint8).numpy()
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 6, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_affine_quantize_types_and_widths_bitexact(dtype, bits, gs):
+    # every weight type (scales and biases in that type) and width against
+    # the oracle's typed restatement of the MLX CPU quantizer, byte for byte
+    announce("quant_typed", dtype, bits, gs)
+    w, wd = typed_weights(dtype, 64, 512, 900 + 10 * bits + gs)
+    wq, s, b = mq.quantize(wd, gs, bits)
+    assert s.dtype == TORCH_DT[dtype] and b.dtype == TORCH_DT[dtype]
+    ewq, es, eb = orc.affine_quantize_t(w, dtype, gs, bits)
+    np.testing.assert_array_equal(wq.cpu().numpy(), ewq)
+    np.testing.assert_array_equal(host_bytes(s).reshape(-1), np.asarray(es).reshape(-1).view(np.uint8))
+    np.testing.assert_array_equal(host_bytes(b).reshape(-1), np.asarray(eb).reshape(-1).view(np.uint8))
+
+
+@pytest.mark.parametrize("dtype", ["float16", "float32"])
+@pytest.mark.parametrize("bits", [1, 3, 5])
+def test_affine_quantize_dequantize_round_trip(dtype, bits):
+    # dequantize(quantize(w)) on the GPU equals the MLX graph dequantize of
+    # the GPU's codes, bitwise, and each value lies within 1.5 steps of w (the
+    # edge snapping can clamp the far extreme by up to a step)
+    from oracle import generic as og
+    announce("quant_round_trip", dtype, bits)
+    gs = 64
+    w, wd = typed_weights(dtype, 16, 256, 950 + bits)
+    wq, s, b = mq.quantize(wd, gs, bits)
+    d = mq.dequantize(wq, s, b, gs, bits).float().cpu().numpy().astype(np.float64)
+    s64 = s.float().cpu().numpy().astype(np.float64)
+    b64 = b.float().cpu().numpy().astype(np.float64)
+    want = og.dequantize_graph(wq.cpu().numpy(), s64, b64, gs, bits, 256, dtype, dtype)
+    np.testing.assert_array_equal(d, want)
+    wf = wd.float().cpu().numpy().astype(np.float64)
+    step = np.repeat(np.abs(s64), gs, axis=1)
+    tol = 1.5 * step + 1e-3 * np.abs(wf) + 1e-30
+    assert (np.abs(d - wf) <= tol).all()
 
 
 HAND = sorted({k[len("hand_w_"):] for k in KAT.files if k.startswith("hand_w_")})
