@@ -513,6 +513,7 @@ struct Knobs {
   int qmm_min_rows = kQmmMinRows, qmm_tile = -1, qmm_ksplit = 0;
   int qmv_mid = 1, qmv_multi = 1;
   int qmv_mr = 1;  // whole-row mid-size kernel where it applies (0: off)
+  int mr_ring = 0;  // its weight ring depth in windows (0: planner)
   int gen_ks = 0;  // K splits of the general kernel (0: planner)
   int gather_sorted = 1, gather_group = -1, gather_runs = 1, gather_direct = 1;
   std::string qmv_kernel;  // "", "rs", "b4", "mid", "mr", "fr", "mfma"
@@ -537,6 +538,7 @@ const Knobs* read_knobs() {
   k->qmv_mid = env_int("MLXQ_QMV_MID", 1);
   k->qmv_multi = env_int("MLXQ_QMV_MULTI", 1);
   k->qmv_mr = env_int("MLXQ_QMV_MR", 1);
+  k->mr_ring = env_int("MLXQ_MR_RING", 0);
   k->gen_ks = env_int("MLXQ_GEN_KS", 0);
   k->gather_sorted = env_int("MLXQ_GATHER_SORTED", 1);
   k->gather_group = env_int("MLXQ_GATHER_GROUP", -1);
@@ -1039,25 +1041,25 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
   const int cap = mlxq::qmv_max_rows(fmt, sp.gs);
   View wv{w}, xv{x};
   // 3-4 rows of 4-bit codes against a tall matrix: the whole-row mid-size
-  // kernel also beats the block-MFMA kernel (gate/up M=4: 11.8 us vs 12.6)
+  // kernel also beats the block-MFMA kernel (gate/up M=4: 10.4 us vs 12.6;
+  // 8-bit keeps the row-streaming kernel: 15.3 us vs 16.3)
   const bool mr_small = rows_total >= 3 && rows_total < kMidMinRows && fmt == mlxq::AFF4 && knobs().qmv_mr != 0 &&
                         knobs().qmv_kernel.empty() && wv.ndim() == 2 &&
                         mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows_total, device_info(current_device()).cus,
-                                          false).ok;
+                                          false, 0).ok;
   if (wv.ndim() == 2 && rows_total <= 16 && (mr_small || use_mid((int)rows_total, fmt, sp.K))) {
     const int dev = current_device();
     int shift = 0;
     while ((1 << shift) < sp.gs) shift++;
     const std::string& forced = knobs().qmv_kernel;
     // Matrices with ~one 64-row workgroup per CU: whole rows per wave, one
-    // launch (qmv_mr.hip).  It beats the split-K kernel below up to 8 rows
-    // and for 8-bit codes; 4-bit at 9-16 rows stays there (MI355X,
-    // Llama-3-8B gate/up, graph-timed: 4-bit M=8 11.8-12.0 us vs 12.4-12.5,
-    // 8-bit M=8 17.7 vs 20.7, 4-bit M=16 18.9 vs 15.8).
-    const bool mr_default = knobs().qmv_mr != 0 && forced.empty() && (fmt == mlxq::AFF8 || rows_total <= 8);
+    // launch (qmv_mr.hip), faster than the split-K kernel below at every row
+    // count (MI355X, Llama-3-8B gate/up, graph-timed: 4-bit M=8 10.5 us vs
+    // 12.4, M=16 15.3 vs 15.6-16.7; 8-bit M=8 16.7 vs 20.8, M=16 17.4 vs 21.8).
+    const bool mr_default = knobs().qmv_mr != 0 && forced.empty();
     if (forced == "mr" || mr_default) {
       const mlxq::QmvMrPlan rp = mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows_total, device_info(dev).cus,
-                                                   forced == "mr");
+                                                   forced == "mr", knobs().mr_ring);
       if (rp.ok) {
         mlxq::QmvMrArgs m{};
         m.x = a.x;

@@ -223,11 +223,13 @@ struct QmvMrPlan {
   int na = 1;          // 16-row MFMA A tiles
   int xr = 8;          // activation rows staged (8 or 16)
   int rk = 1024;       // K positions per staged range
+  int ring = 8;        // windows of weight loads in flight (4, 8 or 16)
   int row_blocks = 0;  // workgroups (64 weight rows each)
   size_t lds = 0;
 };
-// force: plan even when the matrix has too few rows to fill the CUs
-QmvMrPlan qmv_mr_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int cus, bool force);
+// force: plan even when the matrix has too few rows to fill the CUs;
+// ring_req: 4, 8 or 16 forces the weight ring depth in windows (0: planner)
+QmvMrPlan qmv_mr_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int cus, bool force, int ring_req);
 hipError_t qmv_mr_launch(int fmt, const QmvMrArgs& a, const QmvMrPlan& p, hipStream_t stream);
 
 // Expert-sorted gather (qmm_group.hip), mxfp4, one activation row per index

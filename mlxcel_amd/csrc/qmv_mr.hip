@@ -17,8 +17,9 @@
 // 4-bit codes, 512 for 8-bit).  The four waves share one staged copy of each
 // range's activations, group sums and the 64 rows' scales, double-buffered in
 // LDS: while the waves multiply range r, the next range's activations and
-// scales are already in registers and a 16-window weight ring holds ranges
-// r + 1 and r + 2; one barrier per range.  Ranges go two per loop turn so
+// scales are already in registers and a ring of weight loads runs 4-16
+// windows ahead (8 by default: deeper rings measured slower, their
+// registers cost more than they hide); one barrier per range.  Ranges go two per loop turn so
 // every LDS and ring index is a compile-time constant (an odd last turn
 // multiplies zeros), and the loads of a range differ only in scalar offsets
 // and a scalar choice between a live and an empty buffer resource.  Used when the matrix has enough rows for
@@ -64,7 +65,7 @@ __host__ __device__ constexpr uint32_t mr_buf_bytes(int rk, int xr, int na, int 
 
 // FMT: AFF4 / AFF8; S: groups per window; NA: 16-row A tiles; XR: activation
 // rows staged (8 or 16, at least M).
-template <int FMT, int S, int NA, int XR>
+template <int FMT, int S, int NA, int XR, int RING>
 __global__ __launch_bounds__(MR_NT, 1) void qmv_mr_kernel(const QmvMrArgs a) {
   constexpr int CK = FMT == AFF8 ? 16 : 32;  // k per 16-byte code chunk
   constexpr int KW = 4 * CK;                 // k per window
@@ -182,7 +183,7 @@ __global__ __launch_bounds__(MR_NT, 1) void qmv_mr_kernel(const QmvMrArgs a) {
   };
 
   // weights: row row_wg + 16 wave + (lane & 15), chunk lane >> 4 of each
-  // window; a 16-window ring keeps two ranges of loads in flight
+  // window; a ring of RING windows keeps that many windows of loads in flight
   const int nl = lane & 15, g = lane >> 4;
   const int nrow = row_wg + wave * 16 + nl;
   const uint32_t woff = nrow < N ? (uint32_t)nrow * RB + (uint32_t)g * 16u : kDeadOfs;
@@ -192,11 +193,12 @@ __global__ __launch_bounds__(MR_NT, 1) void qmv_mr_kernel(const QmvMrArgs a) {
                                                                            range * (MR_WIN * 64), 0));
   };
 
-  // ---- prologue: range 0 staged, range 1 in registers, two ranges of weights
+  // ---- prologue: range 0 staged, range 1 in registers, RING windows of weights
+  static_assert(RING == 4 || RING == 8 || RING == 16, "the ring slots repeat every two ranges");
   issue_range(0);
-  u32x4 wbuf[2 * MR_WIN];
+  u32x4 wbuf[RING];
 #pragma unroll
-  for (int p = 0; p < 2 * MR_WIN; p++) wbuf[p] = w_load(p / MR_WIN, p % MR_WIN);
+  for (int p = 0; p < RING; p++) wbuf[p] = w_load(p / MR_WIN, p % MR_WIN);
   for (int i = tid; i < 2 * (XP * 2 / 16); i += MR_NT)
     *reinterpret_cast<u32x4*>(smem + (uint32_t)(i / (XP * 2 / 16)) * BUF + ZROW + (uint32_t)(i % (XP * 2 / 16)) * 16u) =
         u32x4{0u, 0u, 0u, 0u};
@@ -244,10 +246,11 @@ __global__ __launch_bounds__(MR_NT, 1) void qmv_mr_kernel(const QmvMrArgs a) {
 #pragma unroll
         for (int u = 0; u < NA; u++)
           xsv[u] = *reinterpret_cast<const f32x4*>(smem + bofs + XSO + (uint32_t)((w * 16 * NA + 16 * u + 4 * g) * 4));
-        // ring slot h * 8 + w: take this range's window w, refill it with
-        // the window two ranges on
-        const u32x4 wv = wbuf[h * MR_WIN + w];
-        wbuf[h * MR_WIN + w] = w_load(range + 2, w);
+        // ring slot: take this range's window w, refill it with the window
+        // RING windows on
+        const int rs = (h * MR_WIN + w) % RING;
+        const u32x4 wv = wbuf[rs];
+        wbuf[rs] = w_load(range + (w + RING) / MR_WIN, (w + RING) % MR_WIN);
         bf16x8 B[NQ];
         if constexpr (FMT == AFF4) {
 #pragma unroll
@@ -310,8 +313,16 @@ namespace {
 template <int FMT, int S, int NA>
 hipError_t mr_launch(const QmvMrPlan& p, const QmvMrArgs& a, hipStream_t stream) {
   const dim3 grid((unsigned)p.row_blocks), block((unsigned)MR_NT);
-  if (p.xr == 8) hipLaunchKernelGGL((qmv_mr_kernel<FMT, S, NA, 8>), grid, block, p.lds, stream, a);
-  else hipLaunchKernelGGL((qmv_mr_kernel<FMT, S, NA, 16>), grid, block, p.lds, stream, a);
+  if (p.ring == 4) {
+    if (p.xr == 8) hipLaunchKernelGGL((qmv_mr_kernel<FMT, S, NA, 8, 4>), grid, block, p.lds, stream, a);
+    else hipLaunchKernelGGL((qmv_mr_kernel<FMT, S, NA, 16, 4>), grid, block, p.lds, stream, a);
+  } else if (p.ring == 16) {
+    if (p.xr == 8) hipLaunchKernelGGL((qmv_mr_kernel<FMT, S, NA, 8, 16>), grid, block, p.lds, stream, a);
+    else hipLaunchKernelGGL((qmv_mr_kernel<FMT, S, NA, 16, 16>), grid, block, p.lds, stream, a);
+  } else {
+    if (p.xr == 8) hipLaunchKernelGGL((qmv_mr_kernel<FMT, S, NA, 8, 8>), grid, block, p.lds, stream, a);
+    else hipLaunchKernelGGL((qmv_mr_kernel<FMT, S, NA, 16, 8>), grid, block, p.lds, stream, a);
+  }
   return hipGetLastError();
 }
 
@@ -322,7 +333,7 @@ hipError_t mr_launch_s(const QmvMrPlan& p, const QmvMrArgs& a, hipStream_t strea
 
 }  // namespace
 
-QmvMrPlan qmv_mr_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int cus, bool force) {
+QmvMrPlan qmv_mr_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int cus, bool force, int ring_req) {
   QmvMrPlan p;
   if (fmt != AFF4 && fmt != AFF8) return p;
   if (rows < 1 || rows > 16 || (gs != 32 && gs != 64 && gs != 128) || N < 1 || K < 1) return p;
@@ -340,6 +351,10 @@ QmvMrPlan qmv_mr_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int cus, 
   // one launch needs ~one workgroup per CU; fewer rows leave CUs idle
   if (!force && (int64_t)p.row_blocks * 4 < (int64_t)cus * 3) return p;
   p.lds = 2u * mr_buf_bytes(p.rk, p.xr, p.na, kw / p.s);
+  // weight ring: 8 windows (one range), 4 with two A tiles, whose operands
+  // need the registers (MI355X, Llama-3-8B gate/up: 4-bit M=4 10.4 us with 8
+  // vs 11.1 with 4 and 11.6 with 16; M=16 15.3 with 4 vs 15.9 with 8)
+  p.ring = (ring_req == 4 || ring_req == 8 || ring_req == 16) ? ring_req : (p.na == 2 ? 4 : 8);
   // buffer offsets are 32-bit and 0x80000000 marks a dead lane
   const int64_t wbytes = N * K * (fmt == AFF8 ? 8 : 4) / 8;
   p.ok = p.lds <= 160 * 1024 && wbytes < ((int64_t)1 << 31) && N * G * 2 < ((int64_t)1 << 31) &&

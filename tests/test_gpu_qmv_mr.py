@@ -44,6 +44,20 @@ def test_mr_affine_every_variant(mr, bits, gs, M):
     assert max_rel(run(x, wq, s, b, gs, bits), orc.qmm_t_affine(x, wq, s, b, gs, bits)) <= TOL
 
 
+@pytest.mark.parametrize("ring", ["4", "16"])
+@pytest.mark.parametrize("bits,gs", [(4, 32), (4, 64), (8, 64), (8, 128)])
+@pytest.mark.parametrize("M", [2, 8, 12])
+def test_mr_weight_ring_depths(mr, monkeypatch, ring, bits, gs, M):
+    # the other ring depths (MLXQ_MR_RING; the default of 8 windows runs in
+    # every other test): refills cross into the next staged range at 4
+    # windows, and reach two ranges ahead at 16
+    setknob(monkeypatch, "MLXQ_MR_RING", ring)
+    N, K = 200, 3072
+    announce("mr_ring", ring, bits, gs, M)
+    x, wq, s, b = affine_case(M, N, K, gs, bits, 3900 + M + bits + gs)
+    assert max_rel(run(x, wq, s, b, gs, bits), orc.qmm_t_affine(x, wq, s, b, gs, bits)) <= TOL
+
+
 @pytest.mark.parametrize("bits,K", [(4, 1024), (4, 2048), (4, 5120), (8, 512), (8, 1024)])
 @pytest.mark.parametrize("M", [6, 16])
 def test_mr_range_counts(mr, bits, K, M):
