@@ -958,7 +958,7 @@ void run_gen(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const 
 bool try_rs_f16(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
                 const mlxq_array* biases, mlxq_array* out, int64_t rows, hipStream_t stream) {
   if (!sp.transpose || rows < 1 || rows > 4 || sp.K % 32 != 0 || sp.out_dtype != MLXQ_FLOAT16 ||
-      x->dtype != MLXQ_FLOAT16)
+      x->dtype != MLXQ_FLOAT16 || knobs().qmv_kernel == "mr" || knobs().qmv_kernel == "mid")
     return false;
   if (sp.mode == AFFINE) {
     if ((sp.bits != 4 && sp.bits != 8) || (sp.gs != 32 && sp.gs != 64 && sp.gs != 128)) return false;
@@ -987,6 +987,75 @@ bool try_rs_f16(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, con
   return true;
 }
 
+// float16 x / scales / biases / result, affine 4/8-bit codes (the mid-size
+// decode kernels' float16 instantiations)
+bool f16_affine(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* scales, const mlxq_array* biases) {
+  return sp.transpose && sp.mode == AFFINE && (sp.bits == 4 || sp.bits == 8) && x->dtype == MLXQ_FLOAT16 &&
+         sp.out_dtype == MLXQ_FLOAT16 && scales->dtype == MLXQ_FLOAT16 && biases && biases->dtype == MLXQ_FLOAT16;
+}
+
+// float16, 5-16 rows (3-4 for 4-bit codes; any row count when
+// MLXQ_QMV_KERNEL=mr) against a matrix with ~one 64-row block per CU: the
+// whole-row mid-size kernel (gate/up M=8 10.8 us vs 55 on the general kernel).
+bool try_mr_f16(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+                const mlxq_array* biases, mlxq_array* out, int64_t rows, hipStream_t stream) {
+  const bool forced = knobs().qmv_kernel == "mr";
+  if (!f16_affine(sp, x, scales, biases) || rows < 1 || rows > 16) return false;
+  const int64_t min_rows = sp.bits == 4 ? 3 : kMidMinRows;
+  if (!forced && (rows < min_rows || knobs().qmv_mr == 0 || !knobs().qmv_kernel.empty())) return false;
+  const int fmt = fmt_of(sp.mode, sp.bits);
+  const mlxq::QmvMrPlan rp = mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, device_info(current_device()).cus,
+                                               forced, knobs().mr_ring);
+  if (!rp.ok) return false;
+  mlxq::QmvMrArgs m{};
+  m.x = static_cast<const uint16_t*>(x->data);
+  m.w = static_cast<const uint32_t*>(w->data);
+  m.scales = static_cast<const uint16_t*>(scales->data);
+  m.biases = static_cast<const uint16_t*>(biases->data);
+  m.out = static_cast<uint16_t*>(out->data);
+  m.M = (int)rows;
+  m.N = (int)sp.N;
+  m.K = (int)sp.K;
+  int shift = 0;
+  while ((1 << shift) < sp.gs) shift++;
+  m.gs_shift = shift;
+  m.xt = 1;
+  hip_check(mlxq::qmv_mr_launch(fmt, m, rp, stream), "qmv_mr launch");
+  return true;
+}
+
+// float16, 5-16 rows (any row count when MLXQ_QMV_KERNEL=mid), other
+// matrices: the split-K mid-size kernel (down M=8: vs 84 us on the general
+// kernel).
+bool try_mid_f16(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+                 const mlxq_array* biases, mlxq_array* out, int64_t rows, hipStream_t stream, const ScratchSrc& ss) {
+  const bool forced = knobs().qmv_kernel == "mid";
+  if (!f16_affine(sp, x, scales, biases) || rows < 1 || rows > 16) return false;
+  if (!forced && (rows < kMidMinRows || knobs().qmv_mid == 0 || !knobs().qmv_kernel.empty())) return false;
+  const int fmt = fmt_of(sp.mode, sp.bits);
+  const mlxq::QmvMidPlan mp = mlxq::qmv_mid_plan(fmt, sp.gs, sp.N, sp.K, (int)rows);
+  if (!mp.ok) return false;
+  const int dev = current_device();
+  mlxq::QmvMidArgs m{};
+  m.x = static_cast<const uint16_t*>(x->data);
+  m.w = static_cast<const uint32_t*>(w->data);
+  m.scales = static_cast<const uint16_t*>(scales->data);
+  m.biases = static_cast<const uint16_t*>(biases->data);
+  m.out = static_cast<uint16_t*>(out->data);
+  m.M = (int)rows;
+  m.N = (int)sp.N;
+  m.K = (int)sp.K;
+  int shift = 0;
+  while ((1 << shift) < sp.gs) shift++;
+  m.gs_shift = shift;
+  m.ks = mp.ks;
+  m.xt = 1;
+  if (mp.ks > 1)
+    m.ws = reinterpret_cast<float*>(workspace(dev, stream, (size_t)mp.ks * rows * sp.N * sizeof(float), ss));
+  hip_check(mlxq::qmv_mid_launch(fmt, m, mp, stream), "qmv_mid launch");
+  return true;
+}
+
 // Enqueues one checked quantized_matmul call.
 void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
                           const mlxq_array* biases, mlxq_array* out, hipStream_t stream,
@@ -996,7 +1065,9 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
   if (sp.K == 0) unsupported("quantized_matmul: K == 0");
   if (!sp.fast) {
     View wv{w}, xv{x};
+    if (wv.ndim() == 2 && try_mr_f16(sp, x, w, scales, biases, out, rows_total, stream)) return;
     if (wv.ndim() == 2 && try_rs_f16(sp, x, w, scales, biases, out, rows_total, stream)) return;
+    if (wv.ndim() == 2 && try_mid_f16(sp, x, w, scales, biases, out, rows_total, stream, ss)) return;
     if (wv.ndim() == 2) {
       // every leading dim of x folds into rows
       run_gen(sp, x, w, scales, biases, out, rows_total, 1, 1, 1, nullptr, stream, ss);

@@ -59,6 +59,18 @@ __device__ __forceinline__ int seg_index(const uint32_t* idx, int stride, int si
 __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
+// the same product on the bit patterns of 16-bit operands of type XT
+// (0 bfloat16, 1 float16: v_mfma_f32_16x16x32_f16)
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+template <int XT>
+__device__ __forceinline__ f32x4 mfma16x16x32_xt(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (XT == 0)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+}
 
 // ---- unpack one 32-bit word of codes into an MFMA bf16 operand fragment ----
 //
@@ -169,6 +181,33 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
 }
+
+// 16-bit element type of activations, scales, biases and result: XT = 0
+// bfloat16, XT = 1 float16 (the reference's quantized_matmul in T = float16,
+// ops.cpp:4974-4992; same arithmetic: fp32 dot products of exact 16-bit
+// products, one rounding of the result).  Affine codes widen to the type's
+// "offset + q" pairs with one byte permute per pair: bfloat16 0x43nn =
+// 128 + q (q < 128), float16 0x64nn = 1024 + q (q < 256, so 8-bit codes take
+// the same route); the offset times sum(x) comes off with the bias.
+template <int XT>
+__device__ __forceinline__ float dotx(uint32_t a, uint32_t b, float c) {
+  if constexpr (XT == 0) return dot2(a, b, c);
+  else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
+  }
+}
+template <int XT>
+__device__ __forceinline__ float xt_to_f32(uint32_t h) {
+  if constexpr (XT == 0) return bf16_bits_to_f32(h);
+  else return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+template <int XT>
+__device__ __forceinline__ uint32_t f32_to_xt(float f) {
+  if constexpr (XT == 0) return f32_to_bf16_bits(f);
+  else return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {

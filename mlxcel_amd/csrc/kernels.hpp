@@ -187,6 +187,7 @@ struct QmvMidArgs {
   float* ws;               // fp32 partials [ks][M][N] (ks > 1)
   int M, N, K, gs_shift;
   int ks;                  // K ranges (gridDim.y)
+  int xt;                  // 16-bit type of x / scales / biases / out: 0 bfloat16, 1 float16
 };
 struct QmvMidLds {
   int xpitch = 0;  // bf16 per staged activation row
@@ -210,12 +211,13 @@ hipError_t qmv_mid_launch(int fmt, const QmvMidArgs& a, const QmvMidPlan& p, hip
 // one affine 4/8-bit weight matrix with enough rows for ~one workgroup of 64
 // rows per CU; each wave finishes 16 outputs per activation row over all of K.
 struct QmvMrArgs {
-  const uint16_t* x;       // bf16 [M][K]
+  const uint16_t* x;       // [M][K] of type xt
   const uint32_t* w;       // packed codes [N][K*bits/32]
-  const uint16_t* scales;  // bf16 [N][K/gs]
-  const uint16_t* biases;  // bf16 [N][K/gs]
-  uint16_t* out;           // bf16 [M][N]
+  const uint16_t* scales;  // [N][K/gs] of type xt
+  const uint16_t* biases;  // [N][K/gs] of type xt
+  uint16_t* out;           // [M][N] of type xt
   int M, N, K, gs_shift;
+  int xt;                  // 0 bfloat16, 1 float16
 };
 struct QmvMrPlan {
   bool ok = false;
@@ -311,7 +313,8 @@ QmmPlan qmm_plan_grouped(int fmt, int gs, int64_t N, int64_t K, int tile);
 QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus, int tile_req, int ksplit_req);
 hipError_t qmm_launch(int fmt, const QmmArgs& a, const QmmPlan& p, hipStream_t stream);
 // out[i] = bf16(sum over z < ks of ws[z * n + i]) (qmv.hip)
-hipError_t launch_splitk_reduce(const float* ws, uint16_t* out, int64_t n, int ks, hipStream_t stream);
+// out (16-bit type xt: 0 bfloat16, 1 float16) = sum over ks fp32 partials, in split order
+hipError_t launch_splitk_reduce(const float* ws, uint16_t* out, int64_t n, int ks, hipStream_t stream, int xt = 0);
 
 // Elementwise conversions (dequant.hip).
 hipError_t launch_affine_dequantize(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,

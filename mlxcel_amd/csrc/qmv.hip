@@ -402,17 +402,20 @@ __global__ __launch_bounds__(NW * 64) void qmv_kernel(const QmvArgs a) {
 
 // Second pass of a K split: out = bf16(sum over z of the fp32 partials), in a
 // fixed order (bitwise reproducible; no cross-workgroup fences needed).
+// XT: 16-bit result type (0 bfloat16, 1 float16)
+template <int XT>
 __global__ __launch_bounds__(256) void qmv_splitk_reduce(const float* __restrict__ ws, uint16_t* __restrict__ out,
                                                          int64_t n, int ks) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   float y = 0.f;
   for (int z = 0; z < ks; z++) y += ws[(int64_t)z * n + i];
-  out[i] = (uint16_t)f32_to_bf16_bits(y);
+  out[i] = (uint16_t)f32_to_xt<XT>(y);
 }
 
 // The same sum, 4 outputs per thread: 16-byte partial loads, four splits'
 // loads in flight before their adds (the split order of the sum is unchanged).
+template <int XT>
 __global__ __launch_bounds__(256) void qmv_splitk_reduce4(const float4* __restrict__ ws, uint2* __restrict__ out,
                                                           int64_t n4, int ks) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -438,18 +441,25 @@ __global__ __launch_bounds__(256) void qmv_splitk_reduce4(const float4* __restri
     y.z += v.z;
     y.w += v.w;
   }
-  out[i] = make_uint2(f32_to_bf16_bits(y.x) | (f32_to_bf16_bits(y.y) << 16),
-                      f32_to_bf16_bits(y.z) | (f32_to_bf16_bits(y.w) << 16));
+  out[i] = make_uint2(f32_to_xt<XT>(y.x) | (f32_to_xt<XT>(y.y) << 16),
+                      f32_to_xt<XT>(y.z) | (f32_to_xt<XT>(y.w) << 16));
 }
 
-hipError_t launch_splitk_reduce(const float* ws, uint16_t* out, int64_t n, int ks, hipStream_t stream) {
+template <int XT>
+static void splitk_reduce_xt(const float* ws, uint16_t* out, int64_t n, int ks, hipStream_t stream) {
   if (n % 4 == 0 && (reinterpret_cast<uintptr_t>(out) & 7) == 0 && (reinterpret_cast<uintptr_t>(ws) & 15) == 0) {
     const int64_t n4 = n / 4;
-    hipLaunchKernelGGL(qmv_splitk_reduce4, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream,
+    hipLaunchKernelGGL(qmv_splitk_reduce4<XT>, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream,
                        reinterpret_cast<const float4*>(ws), reinterpret_cast<uint2*>(out), n4, ks);
   } else {
-    hipLaunchKernelGGL(qmv_splitk_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, ws, out, n, ks);
+    hipLaunchKernelGGL(qmv_splitk_reduce<XT>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, ws, out, n,
+                       ks);
   }
+}
+
+hipError_t launch_splitk_reduce(const float* ws, uint16_t* out, int64_t n, int ks, hipStream_t stream, int xt) {
+  if (xt == 1) splitk_reduce_xt<1>(ws, out, n, ks, stream);
+  else splitk_reduce_xt<0>(ws, out, n, ks, stream);
   return hipGetLastError();
 }
 

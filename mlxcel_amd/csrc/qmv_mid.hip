@@ -1,11 +1,11 @@
 // qmv_mid.hip — decode kernel for 5 to 16 activation rows per weight matrix
-// (affine 4/8-bit) on gfx950.
+// (affine 4/8-bit, bfloat16 or float16) on gfx950.
 //
 // Same product as the other decode kernels (reference decode route: overlays/
 // rocm/mlx/backend/rocm/quantized/qmv_tiled_kernel.hip:29-128; CPU math
 // overlays/cpu/mlx/backend/cpu/quantized.cpp:199-257): y[m,n] = sum_g s[n,g] *
 // sum_{k in g} x[m,k] q[n,k] + b[n,g] * sum_{k in g} x[m,k], fp32
-// accumulation, one bf16 rounding on store.
+// accumulation, one rounding to the result type on store.
 //
 // Why a kernel of its own: at 16 activation rows the activations weigh 32
 // bytes per k against 8 bytes per k for 16 rows of 4-bit codes, so a kernel
@@ -84,7 +84,9 @@ __host__ __device__ inline QmvMidLds qmv_mid_lds(int fmt, int gs, int kr, int na
 // One A tile fits two waves per SIMD without spilling (the register bound
 // below makes the allocator pack the accumulators); more A tiles keep their
 // own allocation.
-template <int FMT, int S, int NA, int SW>
+// XT: 16-bit type of activations, scales, biases and result (0 bfloat16, 1
+// float16: codes widen to float16 1024 + q, products on the float16 MFMA).
+template <int FMT, int S, int NA, int SW, int XT>
 __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const QmvMidArgs a) {
   constexpr int CK = FMT == AFF8 ? 16 : 32;  // k per 16-byte code chunk
   constexpr int KW = 4 * CK;                 // k per window (4 chunks)
@@ -185,8 +187,9 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
       *reinterpret_cast<u32x4*>(xl + m * L.xpitch + 8 * c) = v;
     }
     float sum = 0.f;
+    constexpr uint32_t ONES = XT ? 0x3C003C00u : 0x3F803F80u;
 #pragma unroll
-    for (int e = 0; e < 4; e++) sum = dot2(xpre[i][e], 0x3F803F80u, sum);  // pairs times (1, 1); dead pieces are 0
+    for (int e = 0; e < 4; e++) sum = dotx<XT>(xpre[i][e], ONES, sum);  // pairs times (1, 1); dead pieces are 0
     sum = group_sum<PG>(sum);
     const int w = (8 * c) / KW, slot = ((8 * c) % KW) / XG;
     const int r = m * S + slot;
@@ -202,8 +205,11 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
       for (int h = 0; h < SW; h++) {
         const uint32_t sb = (spre[i][h >> 1] >> (16 * (h & 1))) & 0xFFFFu;
         const uint32_t bb = (bpre[i][h >> 1] >> (16 * (h & 1))) & 0xFFFFu;
-        const float s = bf16_bits_to_f32(sb), b = bf16_bits_to_f32(bb);
-        sl[r * spitch + gl + h] = float2{s, FMT == AFF4 ? __builtin_fmaf(-128.0f, s, b) : b};
+        const float s = xt_to_f32<XT>(sb), b = xt_to_f32<XT>(bb);
+        // the codes' offset (bfloat16 4-bit 128, float16 1024) times sum(x)
+        // comes off with the bias
+        constexpr float OFS = XT ? 1024.0f : (FMT == AFF4 ? 128.0f : 0.0f);
+        sl[r * spitch + gl + h] = float2{s, OFS != 0.0f ? __builtin_fmaf(-OFS, s, b) : b};
       }
     }
   }
@@ -241,13 +247,12 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
   {
 #pragma unroll
     for (int w = 0; w < MID_WIN; w++) {
-      bf16x8 A[NA][NQ];
+      u32x4 A[NA][NQ];
 #pragma unroll
       for (int t = 0; t < NA; t++)
 #pragma unroll
         for (int q = 0; q < NQ; q++)
-          A[t][q] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(smem + abase[t] + (uint32_t)w * wstep[t] +
-                                                                                (uint32_t)q * qstep[t]));
+          A[t][q] = *reinterpret_cast<const u32x4*>(smem + abase[t] + (uint32_t)w * wstep[t] + (uint32_t)q * qstep[t]);
       f32x4 xsv[NA];
 #pragma unroll
       for (int t = 0; t < NA; t++) xsv[t] = *reinterpret_cast<const f32x4*>(xsl + w * 16 * NA + 16 * t + 4 * g);
@@ -261,20 +266,28 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
           wbuf[w % MID_P][t] = __builtin_bit_cast(
               u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                          wr, woff[t] == kDeadOfs ? kDeadOfs : woff[t] + (uint32_t)(w + MID_P) * 64u, 0, 0));
-        bf16x8 B[NQ];
+        u32x4 B[NQ];
         if constexpr (FMT == AFF4) {
 #pragma unroll
           for (int q = 0; q < NQ; q++) {
             uint32_t pr[4];
-            unpack_aff4(wv[q], pr);
-            B[q] = as_bf16x8(pr);
+            unpack_aff4(wv[q], pr, XT ? 0x64646464u : 0x43434343u);
+            B[q] = u32x4{pr[0], pr[1], pr[2], pr[3]};
           }
+        } else if constexpr (XT == 1) {
+          // byte pairs (b0, b1), (b2, b3) of each word as float16 1024 + q
+#pragma unroll
+          for (int q = 0; q < 2; q++)
+            B[q] = u32x4{__builtin_amdgcn_perm(0x64646464u, wv[2 * q], 0x04010400u),
+                         __builtin_amdgcn_perm(0x64646464u, wv[2 * q], 0x04030402u),
+                         __builtin_amdgcn_perm(0x64646464u, wv[2 * q + 1], 0x04010400u),
+                         __builtin_amdgcn_perm(0x64646464u, wv[2 * q + 1], 0x04030402u)};
         } else {
           uint32_t pr[4];
           unpack_aff8(wv[0], wv[1], pr);
-          B[0] = as_bf16x8(pr);
+          B[0] = u32x4{pr[0], pr[1], pr[2], pr[3]};
           unpack_aff8(wv[2], wv[3], pr);
-          B[1] = as_bf16x8(pr);
+          B[1] = u32x4{pr[0], pr[1], pr[2], pr[3]};
         }
         // scale pairs (s, b') of this lane's weight row for the window's slots
         float2 sc[S];
@@ -285,7 +298,7 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
         for (int u = 0; u < NA; u++) {
           f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int q = 0; q < NQ; q++) d = mfma16x16x32(A[u][q], B[q], d);
+          for (int q = 0; q < NQ; q++) d = mfma16x16x32_xt<XT>(A[u][q], B[q], d);
 #pragma unroll
           for (int i = 0; i < 4; i++) {
             const int slot = (4 * g + i) % S;  // 16u is a multiple of S
@@ -309,7 +322,7 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
       for (int j = 0; j < YV; j++) {
         const int m = (16 * u + 4 * g) / S + j;
         if (m < M && n < N) {
-          if (a.ks == 1) a.out[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_bits(y[t][u][j]);
+          if (a.ks == 1) a.out[(int64_t)m * N + n] = (uint16_t)f32_to_xt<XT>(y[t][u][j]);
           else a.ws[((int64_t)sp * M + m) * N + n] = y[t][u][j];
         }
       }
@@ -320,12 +333,17 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
 
 namespace {
 
+template <int FMT, int S, int NA, int XT>
+hipError_t mid_launch_xt(const QmvMidPlan& p, const QmvMidArgs& a, hipStream_t stream) {
+  const dim3 grid((unsigned)p.row_blocks, (unsigned)p.ks, 1);
+  if (p.sw == 8) hipLaunchKernelGGL((qmv_mid_kernel<FMT, S, NA, 8, XT>), grid, dim3(MID_NT), p.lds, stream, a);
+  else hipLaunchKernelGGL((qmv_mid_kernel<FMT, S, NA, 2, XT>), grid, dim3(MID_NT), p.lds, stream, a);
+  return hipGetLastError();
+}
+
 template <int FMT, int S, int NA>
 hipError_t mid_launch_sna(const QmvMidPlan& p, const QmvMidArgs& a, hipStream_t stream) {
-  const dim3 grid((unsigned)p.row_blocks, (unsigned)p.ks, 1);
-  if (p.sw == 8) hipLaunchKernelGGL((qmv_mid_kernel<FMT, S, NA, 8>), grid, dim3(MID_NT), p.lds, stream, a);
-  else hipLaunchKernelGGL((qmv_mid_kernel<FMT, S, NA, 2>), grid, dim3(MID_NT), p.lds, stream, a);
-  return hipGetLastError();
+  return a.xt ? mid_launch_xt<FMT, S, NA, 1>(p, a, stream) : mid_launch_xt<FMT, S, NA, 0>(p, a, stream);
 }
 
 template <int FMT, int S>
@@ -380,7 +398,7 @@ hipError_t qmv_mid_launch(int fmt, const QmvMidArgs& a, const QmvMidPlan& p, hip
     e = p.s == 2 ? mid_launch_s<AFF8, 2>(p, a, stream) : mid_launch_s<AFF8, 1>(p, a, stream);
   }
   if (e != hipSuccess || p.ks == 1) return e;
-  return launch_splitk_reduce(a.ws, a.out, (int64_t)a.M * a.N, p.ks, stream);
+  return launch_splitk_reduce(a.ws, a.out, (int64_t)a.M * a.N, p.ks, stream, a.xt);
 }
 
 }  // namespace mlxq

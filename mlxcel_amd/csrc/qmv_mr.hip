@@ -1,5 +1,5 @@
 // qmv_mr.hip — decode kernel for 3 to 16 activation rows per weight matrix
-// (affine 4/8-bit, bfloat16) on gfx950 for matrices with many rows: each
+// (affine 4/8-bit, bfloat16 or float16) on gfx950 for matrices with many rows: each
 // wave owns 16 weight rows over the whole of K, so every output is finished
 // in one launch.
 //
@@ -64,8 +64,11 @@ __host__ __device__ constexpr uint32_t mr_buf_bytes(int rk, int xr, int na, int 
 }
 
 // FMT: AFF4 / AFF8; S: groups per window; NA: 16-row A tiles; XR: activation
-// rows staged (8 or 16, at least M).
-template <int FMT, int S, int NA, int XR, int RING>
+// rows staged (8 or 16, at least M); RING: windows of weight loads in flight;
+// XT: 16-bit type of activations, scales, biases and result (0 bfloat16, 1
+// float16: codes widen to float16 1024 + q for both widths, and the products
+// run on v_mfma_f32_16x16x32_f16).
+template <int FMT, int S, int NA, int XR, int RING, int XT>
 __global__ __launch_bounds__(MR_NT, 1) void qmv_mr_kernel(const QmvMrArgs a) {
   constexpr int CK = FMT == AFF8 ? 16 : 32;  // k per 16-byte code chunk
   constexpr int KW = 4 * CK;                 // k per window
@@ -160,8 +163,9 @@ __global__ __launch_bounds__(MR_NT, 1) void qmv_mr_kernel(const QmvMrArgs a) {
       const u32x4 v = FMT == AFF4 ? perm_aff4_v(xpre[i]) : xpre[i];
       *reinterpret_cast<u32x4*>(xl + m * XP + 8 * c) = v;
       float sum = 0.f;
+      constexpr uint32_t ONES = XT ? 0x3C003C00u : 0x3F803F80u;
 #pragma unroll
-      for (int e = 0; e < 4; e++) sum = dot2(xpre[i][e], 0x3F803F80u, sum);  // rows past M read 0
+      for (int e = 0; e < 4; e++) sum = dotx<XT>(xpre[i][e], ONES, sum);  // rows past M read 0
       sum = mr_group_sum<PG>(sum);
       const int w = (8 * c) / KW, slot = ((8 * c) % KW) / XG;
       const int r = m * S + slot;
@@ -174,9 +178,12 @@ __global__ __launch_bounds__(MR_NT, 1) void qmv_mr_kernel(const QmvMrArgs a) {
         const int r = u / (ngr / 4), gl = (u % (ngr / 4)) * 4;
 #pragma unroll
         for (int h = 0; h < 4; h++) {
-          const float s = bf16_bits_to_f32((spre[i][h >> 1] >> (16 * (h & 1))) & 0xFFFFu);
-          const float b = bf16_bits_to_f32((bpre[i][h >> 1] >> (16 * (h & 1))) & 0xFFFFu);
-          sl[r * SPITCH + gl + h] = float2{s, FMT == AFF4 ? __builtin_fmaf(-128.0f, s, b) : b};
+          const float s = xt_to_f32<XT>((spre[i][h >> 1] >> (16 * (h & 1))) & 0xFFFFu);
+          const float b = xt_to_f32<XT>((bpre[i][h >> 1] >> (16 * (h & 1))) & 0xFFFFu);
+          // the codes' offset (bfloat16 4-bit 128, float16 1024) times sum(x)
+          // comes off with the bias
+          constexpr float OFS = XT ? 1024.0f : (FMT == AFF4 ? 128.0f : 0.0f);
+          sl[r * SPITCH + gl + h] = float2{s, OFS != 0.0f ? __builtin_fmaf(-OFS, s, b) : b};
         }
       }
     }
@@ -235,13 +242,12 @@ __global__ __launch_bounds__(MR_NT, 1) void qmv_mr_kernel(const QmvMrArgs a) {
       const uint32_t bofs = (uint32_t)h * BUF;
 #pragma unroll
       for (int w = 0; w < MR_WIN; w++) {
-        bf16x8 A[NA][NQ];
+        u32x4 A[NA][NQ];
 #pragma unroll
         for (int u = 0; u < NA; u++)
 #pragma unroll
           for (int q = 0; q < NQ; q++)
-            A[u][q] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(
-                                                     smem + abase[u] + bofs + (uint32_t)(w * KW * 2 + q * 16)));
+            A[u][q] = *reinterpret_cast<const u32x4*>(smem + abase[u] + bofs + (uint32_t)(w * KW * 2 + q * 16));
         f32x4 xsv[NA];
 #pragma unroll
         for (int u = 0; u < NA; u++)
@@ -251,20 +257,28 @@ __global__ __launch_bounds__(MR_NT, 1) void qmv_mr_kernel(const QmvMrArgs a) {
         const int rs = (h * MR_WIN + w) % RING;
         const u32x4 wv = wbuf[rs];
         wbuf[rs] = w_load(range + (w + RING) / MR_WIN, (w + RING) % MR_WIN);
-        bf16x8 B[NQ];
+        u32x4 B[NQ];
         if constexpr (FMT == AFF4) {
 #pragma unroll
           for (int q = 0; q < NQ; q++) {
             uint32_t pr[4];
-            unpack_aff4(wv[q], pr);
-            B[q] = as_bf16x8(pr);
+            unpack_aff4(wv[q], pr, XT ? 0x64646464u : 0x43434343u);
+            B[q] = u32x4{pr[0], pr[1], pr[2], pr[3]};
           }
+        } else if constexpr (XT == 1) {
+          // byte pairs (b0, b1), (b2, b3) of each word as float16 1024 + q
+#pragma unroll
+          for (int q = 0; q < 2; q++)
+            B[q] = u32x4{__builtin_amdgcn_perm(0x64646464u, wv[2 * q], 0x04010400u),
+                         __builtin_amdgcn_perm(0x64646464u, wv[2 * q], 0x04030402u),
+                         __builtin_amdgcn_perm(0x64646464u, wv[2 * q + 1], 0x04010400u),
+                         __builtin_amdgcn_perm(0x64646464u, wv[2 * q + 1], 0x04030402u)};
         } else {
           uint32_t pr[4];
           unpack_aff8(wv[0], wv[1], pr);
-          B[0] = as_bf16x8(pr);
+          B[0] = u32x4{pr[0], pr[1], pr[2], pr[3]};
           unpack_aff8(wv[2], wv[3], pr);
-          B[1] = as_bf16x8(pr);
+          B[1] = u32x4{pr[0], pr[1], pr[2], pr[3]};
         }
         const int grp0 = (w * KW) >> gsh;  // first group of this window inside the range
         float2 sc[S];
@@ -275,7 +289,7 @@ __global__ __launch_bounds__(MR_NT, 1) void qmv_mr_kernel(const QmvMrArgs a) {
         for (int u = 0; u < NA; u++) {
           f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int q = 0; q < NQ; q++) d = mfma16x16x32(A[u][q], B[q], d);
+          for (int q = 0; q < NQ; q++) d = mfma16x16x32_xt<XT>(A[u][q], B[q], d);
 #pragma unroll
           for (int i = 0; i < 4; i++) {
             const int slot = (4 * g + i) % S;  // 16u is a multiple of S
@@ -301,7 +315,7 @@ __global__ __launch_bounds__(MR_NT, 1) void qmv_mr_kernel(const QmvMrArgs a) {
 #pragma unroll
       for (int j = 0; j < YV; j++) {
         const int m = (16 * u + 4 * g) / S + j;
-        if (m < M) a.out[(int64_t)m * N + nrow] = (uint16_t)f32_to_bf16_bits(y[u][j]);
+        if (m < M) a.out[(int64_t)m * N + nrow] = (uint16_t)f32_to_xt<XT>(y[u][j]);
       }
   }
 }
@@ -310,20 +324,25 @@ __global__ __launch_bounds__(MR_NT, 1) void qmv_mr_kernel(const QmvMrArgs a) {
 
 namespace {
 
-template <int FMT, int S, int NA>
-hipError_t mr_launch(const QmvMrPlan& p, const QmvMrArgs& a, hipStream_t stream) {
+template <int FMT, int S, int NA, int XT>
+hipError_t mr_launch_xt(const QmvMrPlan& p, const QmvMrArgs& a, hipStream_t stream) {
   const dim3 grid((unsigned)p.row_blocks), block((unsigned)MR_NT);
   if (p.ring == 4) {
-    if (p.xr == 8) hipLaunchKernelGGL((qmv_mr_kernel<FMT, S, NA, 8, 4>), grid, block, p.lds, stream, a);
-    else hipLaunchKernelGGL((qmv_mr_kernel<FMT, S, NA, 16, 4>), grid, block, p.lds, stream, a);
+    if (p.xr == 8) hipLaunchKernelGGL((qmv_mr_kernel<FMT, S, NA, 8, 4, XT>), grid, block, p.lds, stream, a);
+    else hipLaunchKernelGGL((qmv_mr_kernel<FMT, S, NA, 16, 4, XT>), grid, block, p.lds, stream, a);
   } else if (p.ring == 16) {
-    if (p.xr == 8) hipLaunchKernelGGL((qmv_mr_kernel<FMT, S, NA, 8, 16>), grid, block, p.lds, stream, a);
-    else hipLaunchKernelGGL((qmv_mr_kernel<FMT, S, NA, 16, 16>), grid, block, p.lds, stream, a);
+    if (p.xr == 8) hipLaunchKernelGGL((qmv_mr_kernel<FMT, S, NA, 8, 16, XT>), grid, block, p.lds, stream, a);
+    else hipLaunchKernelGGL((qmv_mr_kernel<FMT, S, NA, 16, 16, XT>), grid, block, p.lds, stream, a);
   } else {
-    if (p.xr == 8) hipLaunchKernelGGL((qmv_mr_kernel<FMT, S, NA, 8, 8>), grid, block, p.lds, stream, a);
-    else hipLaunchKernelGGL((qmv_mr_kernel<FMT, S, NA, 16, 8>), grid, block, p.lds, stream, a);
+    if (p.xr == 8) hipLaunchKernelGGL((qmv_mr_kernel<FMT, S, NA, 8, 8, XT>), grid, block, p.lds, stream, a);
+    else hipLaunchKernelGGL((qmv_mr_kernel<FMT, S, NA, 16, 8, XT>), grid, block, p.lds, stream, a);
   }
   return hipGetLastError();
+}
+
+template <int FMT, int S, int NA>
+hipError_t mr_launch(const QmvMrPlan& p, const QmvMrArgs& a, hipStream_t stream) {
+  return a.xt ? mr_launch_xt<FMT, S, NA, 1>(p, a, stream) : mr_launch_xt<FMT, S, NA, 0>(p, a, stream);
 }
 
 template <int FMT, int S>

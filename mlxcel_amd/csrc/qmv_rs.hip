@@ -68,32 +68,6 @@ struct RsMultiArgs {
   uint16_t* out[kQmvMultiMax];
 };
 
-// 16-bit element type of activations, scales, biases and result: XT = 0
-// bfloat16, XT = 1 float16 (the reference's quantized_matmul in T = float16,
-// ops.cpp:4974-4992; same arithmetic: fp32 dot products of exact 16-bit
-// products, one rounding of the result).  Affine codes widen to the type's
-// "offset + q" pairs with one byte permute per pair: bfloat16 0x43nn =
-// 128 + q (q < 128), float16 0x64nn = 1024 + q (q < 256, so 8-bit codes take
-// the same route); the offset times sum(x) comes off with the bias.
-template <int XT>
-__device__ __forceinline__ float dotx(uint32_t a, uint32_t b, float c) {
-  if constexpr (XT == 0) return dot2(a, b, c);
-  else {
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
-  }
-}
-template <int XT>
-__device__ __forceinline__ float xt_to_f32(uint32_t h) {
-  if constexpr (XT == 0) return bf16_bits_to_f32(h);
-  else return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
-}
-template <int XT>
-__device__ __forceinline__ uint32_t f32_to_xt(float f) {
-  if constexpr (XT == 0) return f32_to_bf16_bits(f);
-  else return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
-}
-
 // FMT: weight format; MR: activation rows (>= `count`);
 // R: weight rows per workgroup (power of two); CPW: 1 KiB chunks per wave and
 // row; UPW: quantization groups per scale load (1, 2 or 4: the widest load

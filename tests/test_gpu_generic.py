@@ -281,6 +281,53 @@ def test_float16_decode_affine(bits, gs, M, N, K):
     check(y, og.qmm(xv, wqn, sv, bv, True, gs, bits), "float16")
 
 
+@pytest.mark.parametrize("bits,gs", [(4, 32), (4, 64), (4, 128), (8, 32), (8, 64), (8, 128)])
+@pytest.mark.parametrize("M", [1, 3, 5, 8, 12, 16])
+def test_float16_whole_row_decode(monkeypatch, bits, gs, M):
+    # the whole-row mid-size kernel's float16 instantiation (MLXQ_QMV_KERNEL=mr
+    # forces it at any row count; 1024 + q code pairs, float16 MFMAs)
+    setknob(monkeypatch, "MLXQ_QMV_KERNEL", "mr")
+    announce("f16_mr", bits, gs, M)
+    (x, wq, s, b), (xv, wqn, sv, bv) = case(M, 200, 3072, bits, gs, "float16", "float16", True, 3300 + M + bits + gs)
+    y = mq.quantized_matmul(x, wq, s, b, True, gs, bits)
+    check(y, og.qmm(xv, wqn, sv, bv, True, gs, bits), "float16")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M", [5, 16])
+def test_float16_whole_row_decode_default_route(bits, M):
+    # 5-16 float16 rows against a matrix with ~one 64-row block per CU take
+    # the whole-row kernel by default (14336 rows: 224 blocks)
+    announce("f16_mr_default", bits, M)
+    (x, wq, s, b), (xv, wqn, sv, bv) = case(M, 14336, 4096, bits, 64, "float16", "float16", True, 3400 + M + bits)
+    y = mq.quantized_matmul(x, wq, s, b, True, 64, bits)
+    check(y, og.qmm(xv, wqn, sv, bv, True, 64, bits), "float16")
+
+
+@pytest.mark.parametrize("bits,gs", [(4, 32), (4, 64), (4, 128), (8, 32), (8, 64), (8, 128)])
+@pytest.mark.parametrize("M", [1, 5, 8, 12, 16])
+def test_float16_split_k_mid_decode(monkeypatch, bits, gs, M):
+    # the split-K mid-size kernel's float16 instantiation (MLXQ_QMV_KERNEL=mid
+    # forces it), K = 3072: three or six K ranges whose fp32 partials the
+    # reduction rounds to float16
+    setknob(monkeypatch, "MLXQ_QMV_KERNEL", "mid")
+    announce("f16_mid", bits, gs, M)
+    (x, wq, s, b), (xv, wqn, sv, bv) = case(M, 200, 3072, bits, gs, "float16", "float16", True, 3500 + M + bits + gs)
+    y = mq.quantized_matmul(x, wq, s, b, True, gs, bits)
+    check(y, og.qmm(xv, wqn, sv, bv, True, gs, bits), "float16")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M", [5, 16])
+def test_float16_mid_decode_default_route(bits, M):
+    # 5-16 float16 rows against the down shape (4096 rows: too few blocks for
+    # the whole-row kernel) take the split-K mid kernel by default
+    announce("f16_mid_default", bits, M)
+    (x, wq, s, b), (xv, wqn, sv, bv) = case(M, 4096, 14336, bits, 64, "float16", "float16", True, 3600 + M + bits)
+    y = mq.quantized_matmul(x, wq, s, b, True, 64, bits)
+    check(y, og.qmm(xv, wqn, sv, bv, True, 64, bits), "float16")
+
+
 @pytest.mark.parametrize("M", [1, 2, 4])
 def test_float16_decode_mxfp4(M):
     announce("f16_decode_mxfp4", M)
