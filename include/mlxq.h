@@ -134,9 +134,12 @@ const char* mlxq_version(void);
  * 16-byte aligned are first copied into a per-stream staging workspace, as
  * the reference copies them (rocm/quantized/qmm.hip:3557-3564), and a
  * strided `out` is written through it.  bfloat16 4/8-bit affine and mxfp4
- * with transpose=true run the specialised kernels; every other combination
- * runs the general kernel (float16 results also round the dequantized
- * weights to float16, as the reference's dequantize + GEMM route does). */
+ * with transpose=true run the specialised kernels, and so does float16
+ * (x, scales, biases and result) 4/8-bit affine with transpose=true (decode
+ * and prefill; its prefill dequantizes the weights to float16, as the
+ * reference's dequantize + GEMM route does); every other combination runs
+ * the general kernel (float16 results there also round the dequantized
+ * weights to float16). */
 mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w,
                                   const mlxq_array* scales, const mlxq_array* biases,
                                   bool transpose, int32_t group_size, int32_t bits,

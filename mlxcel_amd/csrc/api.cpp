@@ -1056,6 +1056,40 @@ bool try_mid_f16(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, co
   return true;
 }
 
+// float16 prefill (rows >= MLXQ_QMM_MIN_ROWS once the mid-size kernels have
+// declined): the 32x32-MFMA tile kernel's float16 instantiation; a requested
+// tile of the 16x16-MFMA kernel (bfloat16 only) falls back to the planner's.
+bool try_qmm_f16(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+                 const mlxq_array* biases, mlxq_array* out, int64_t rows, hipStream_t stream, const ScratchSrc& ss) {
+  if (!f16_affine(sp, x, scales, biases) || rows < knobs().qmm_min_rows) return false;
+  const int fmt = fmt_of(sp.mode, sp.bits);
+  const int dev = current_device();
+  const int tile_req = knobs().qmm_tile >= 4 ? knobs().qmm_tile : -1;
+  const mlxq::QmmPlan qp = mlxq::qmm_plan(fmt, sp.gs, rows, sp.N, sp.K, device_info(dev).cus, tile_req,
+                                          knobs().qmm_ksplit);
+  if (!qp.ok || qp.tile < 4) return false;
+  mlxq::QmmArgs q{};
+  q.x = static_cast<const uint16_t*>(x->data);
+  q.w = static_cast<const uint32_t*>(w->data);
+  q.scales = scales->data;
+  q.biases = static_cast<const uint16_t*>(biases->data);
+  q.out = static_cast<uint16_t*>(out->data);
+  q.M = (int)rows;
+  q.x_rows = (int)rows;
+  q.N = (int)sp.N;
+  q.K = (int)sp.K;
+  int shift = 0;
+  while ((1 << shift) < sp.gs) shift++;
+  q.gs_shift = shift;
+  q.ksplit = qp.ksplit;
+  q.ksteps_per_split = qp.ksteps_per_split;
+  q.xt = 1;
+  if (qp.ksplit > 1)
+    q.ws = reinterpret_cast<float*>(workspace(dev, stream, (size_t)qp.ksplit * rows * sp.N * sizeof(float), ss));
+  hip_check(mlxq::qmm_launch(fmt, q, qp, stream), "qmm launch");
+  return true;
+}
+
 // Enqueues one checked quantized_matmul call.
 void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
                           const mlxq_array* biases, mlxq_array* out, hipStream_t stream,
@@ -1068,6 +1102,7 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
     if (wv.ndim() == 2 && try_mr_f16(sp, x, w, scales, biases, out, rows_total, stream)) return;
     if (wv.ndim() == 2 && try_rs_f16(sp, x, w, scales, biases, out, rows_total, stream)) return;
     if (wv.ndim() == 2 && try_mid_f16(sp, x, w, scales, biases, out, rows_total, stream, ss)) return;
+    if (wv.ndim() == 2 && try_qmm_f16(sp, x, w, scales, biases, out, rows_total, stream, ss)) return;
     if (wv.ndim() == 2) {
       // every leading dim of x folds into rows
       run_gen(sp, x, w, scales, biases, out, rows_total, 1, 1, 1, nullptr, stream, ss);

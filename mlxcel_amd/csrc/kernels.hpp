@@ -294,6 +294,7 @@ struct QmmArgs {
   // Tile walk of the 32x32-MFMA kernel (qmm_tile_kernel): output tiles per
   // dimension and whether consecutive tiles advance along M (1) or N (0).
   int tiles_m, tiles_n, m_fast;
+  int xt;                  // 16-bit type of x / scales / biases / out: 0 bfloat16, 1 float16 (tile kernel, affine)
 };
 struct QmmPlan {
   bool ok = false;

@@ -39,6 +39,16 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 
+// The same for the 16-bit type XT (0 bfloat16, 1 float16), round to nearest even.
+template <int XT>
+__device__ __forceinline__ uint32_t pack_xt2(float lo, float hi) {
+  if constexpr (XT == 0) return pack_bf16x2(lo, hi);
+  else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, h2));
+  }
+}
+
 // Byte j of w as a float (v_cvt_f32_ubyte<j>).
 __device__ __forceinline__ float ubyte(uint32_t w, int j) { return (float)((w >> (8 * j)) & 0xFFu); }
 
@@ -286,12 +296,24 @@ __device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// on the bit patterns of 16-bit operands of type XT (1: v_mfma_f32_32x32x16_f16)
+template <int XT>
+__device__ __forceinline__ f32x16 mfma32x32x16_xt(bf16x8 a, bf16x8 b, f32x16 c) {
+  if constexpr (XT == 0) return mfma32x32x16(a, b, c);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+}
+
 // Interleave of one slice: after each MFMA, up to this many VALU
 // instructions (measured on MI355X: 6 keeps the dequantization under the
 // MFMAs at both tile sizes).
 constexpr int kValuPerMfma = 6;
 
-template <int FMT, int BM, int BN, int NWM, int NWN>
+// XT: 16-bit type of x, scales, biases and result (0 bfloat16, 1 float16:
+// weights dequantized to float16(s * q + b), products on the float16 MFMA;
+// affine only).
+template <int FMT, int BM, int BN, int NWM, int NWN, int XT>
 __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs a) {
   constexpr int NT = 64 * NWM * NWN;         // threads
   constexpr int TM = BM / NWM, TN = BN / NWN;  // wave tile
@@ -474,15 +496,15 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
       const int r7 = swz(r);
       if constexpr (AFF) {
         const uint32_t sb = tbl[gslot * BN + r];
-        const float sc = __uint_as_float(sb << 16);
-        const float bi = __uint_as_float(sb & 0xFFFF0000u);
+        const float sc = XT ? xt_to_f32<1>(sb & 0xFFFFu) : __uint_as_float(sb << 16);
+        const float bi = XT ? xt_to_f32<1>(sb >> 16) : __uint_as_float(sb & 0xFFFF0000u);
         if constexpr (BITS == 4) {
           // 8 codes: natural pair h = (nibble 2h, nibble 2h + 1) = (byte h of lo, byte h of hi)
           const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-          const u32x4 o = {pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<0>(lo), bi), __builtin_fmaf(sc, cvt_ubyte<0>(hi), bi)),
-                           pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<1>(lo), bi), __builtin_fmaf(sc, cvt_ubyte<1>(hi), bi)),
-                           pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<2>(lo), bi), __builtin_fmaf(sc, cvt_ubyte<2>(hi), bi)),
-                           pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<3>(lo), bi), __builtin_fmaf(sc, cvt_ubyte<3>(hi), bi))};
+          const u32x4 o = {pack_xt2<XT>(__builtin_fmaf(sc, cvt_ubyte<0>(lo), bi), __builtin_fmaf(sc, cvt_ubyte<0>(hi), bi)),
+                           pack_xt2<XT>(__builtin_fmaf(sc, cvt_ubyte<1>(lo), bi), __builtin_fmaf(sc, cvt_ubyte<1>(hi), bi)),
+                           pack_xt2<XT>(__builtin_fmaf(sc, cvt_ubyte<2>(lo), bi), __builtin_fmaf(sc, cvt_ubyte<2>(hi), bi)),
+                           pack_xt2<XT>(__builtin_fmaf(sc, cvt_ubyte<3>(lo), bi), __builtin_fmaf(sc, cvt_ubyte<3>(hi), bi))};
           const int ch = wpc * PW + (e % PW);  // logical 16-byte chunk (8 values)
           *reinterpret_cast<u32x4*>(rowp + ((ch ^ r7) << 3)) = o;
         } else {
@@ -491,10 +513,10 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
           // one word each conflicted on 16% of the LDS cycles)
           if ((e & 1) == 0) {
             const uint32_t w1 = wreg[pp][(e % PW) + 1];
-            const u32x4 o = {pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<0>(w), bi), __builtin_fmaf(sc, cvt_ubyte<1>(w), bi)),
-                             pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<2>(w), bi), __builtin_fmaf(sc, cvt_ubyte<3>(w), bi)),
-                             pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<0>(w1), bi), __builtin_fmaf(sc, cvt_ubyte<1>(w1), bi)),
-                             pack_bf16x2(__builtin_fmaf(sc, cvt_ubyte<2>(w1), bi), __builtin_fmaf(sc, cvt_ubyte<3>(w1), bi))};
+            const u32x4 o = {pack_xt2<XT>(__builtin_fmaf(sc, cvt_ubyte<0>(w), bi), __builtin_fmaf(sc, cvt_ubyte<1>(w), bi)),
+                             pack_xt2<XT>(__builtin_fmaf(sc, cvt_ubyte<2>(w), bi), __builtin_fmaf(sc, cvt_ubyte<3>(w), bi)),
+                             pack_xt2<XT>(__builtin_fmaf(sc, cvt_ubyte<0>(w1), bi), __builtin_fmaf(sc, cvt_ubyte<1>(w1), bi)),
+                             pack_xt2<XT>(__builtin_fmaf(sc, cvt_ubyte<2>(w1), bi), __builtin_fmaf(sc, cvt_ubyte<3>(w1), bi))};
             const int ch = wpc * (PW / 2) + (e % PW) / 2;  // logical 16-byte chunk (8 values)
             *reinterpret_cast<u32x4*>(rowp + ((ch ^ r7) << 3)) = o;
           }
@@ -606,7 +628,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
 #pragma unroll
         for (int i = 0; i < FM; i++)
 #pragma unroll
-          for (int j = 0; j < FN; j++) acc[i][j] = mfma32x32x16(af[cur][i], bv[cur][j], acc[i][j]);
+          for (int j = 0; j < FN; j++) acc[i][j] = mfma32x32x16_xt<XT>(af[cur][i], bv[cur][j], acc[i][j]);
         // step ks+1 goes to the other buffer in the first two slices, then
         // the registers take the loads of step ks+2
         if (s == 0) {
@@ -643,7 +665,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
     if (tr < rows && c < N) {
       const int64_t r = a.seg ? (int64_t)a.orows[r0 + tr] : (int64_t)(m0 + tr);
       if (split) a.ws[((int64_t)z * M + r) * N + c] = v;
-      else a.out[r * N + c] = (uint16_t)f32_to_bf16_bits(v);
+      else a.out[r * N + c] = (uint16_t)f32_to_xt<XT>(v);
     }
   };
 #pragma unroll
@@ -724,17 +746,28 @@ QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus, 
 }
 
 namespace {
+template <int FMT, int XT>
+void qmm_tile_launch(const QmmArgs& a, const QmmPlan& p, hipStream_t stream) {
+  const dim3 grid((unsigned)((int64_t)p.tiles_m * p.tiles_n * p.ksplit));
+  switch (p.tile) {
+    case 4: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 256, 256, 2, 4, XT>), grid, dim3(512), 0, stream, a); break;
+    case 5: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 256, 128, 2, 2, XT>), grid, dim3(256), 0, stream, a); break;
+    case 7: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 256, 256, 2, 2, XT>), grid, dim3(256), 0, stream, a); break;
+    case 8: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 256, 128, 4, 2, XT>), grid, dim3(512), 0, stream, a); break;
+    default: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 128, 128, 2, 2, XT>), grid, dim3(256), 0, stream, a); break;
+  }
+}
+
 template <int FMT>
 void qmm_launch_fmt(const QmmArgs& a, const QmmPlan& p, hipStream_t stream) {
   if (is_tile_kernel(p.tile)) {
-    const dim3 grid((unsigned)((int64_t)p.tiles_m * p.tiles_n * p.ksplit));
-    switch (p.tile) {
-      case 4: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 256, 256, 2, 4>), grid, dim3(512), 0, stream, a); break;
-      case 5: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 256, 128, 2, 2>), grid, dim3(256), 0, stream, a); break;
-      case 7: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 256, 256, 2, 2>), grid, dim3(256), 0, stream, a); break;
-      case 8: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 256, 128, 4, 2>), grid, dim3(512), 0, stream, a); break;
-      default: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 128, 128, 2, 2>), grid, dim3(256), 0, stream, a); break;
+    if constexpr (FMT != MXFP4) {
+      if (a.xt == 1) {
+        qmm_tile_launch<FMT, 1>(a, p, stream);
+        return;
+      }
     }
+    qmm_tile_launch<FMT, 0>(a, p, stream);
     return;
   }
   const dim3 grid((unsigned)p.tiles_n, (unsigned)p.tiles_m, (unsigned)p.ksplit);
@@ -765,6 +798,8 @@ QmmPlan qmm_plan_grouped(int fmt, int gs, int64_t N, int64_t K, int tile) {
 
 hipError_t qmm_launch(int fmt, const QmmArgs& a_in, const QmmPlan& p, hipStream_t stream) {
   if (!p.ok) return hipErrorInvalidValue;
+  // float16: affine codes on the 32x32-MFMA tile kernel only
+  if (a_in.xt != 0 && (fmt == MXFP4 || !is_tile_kernel(p.tile))) return hipErrorInvalidValue;
   QmmArgs a = a_in;
   a.tiles_m = p.tiles_m;
   a.tiles_n = p.tiles_n;
@@ -776,7 +811,7 @@ hipError_t qmm_launch(int fmt, const QmmArgs& a_in, const QmmPlan& p, hipStream_
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.ksplit == 1) return e;
-  return launch_splitk_reduce(a.ws, a.out, (int64_t)a.M * a.N, p.ksplit, stream);
+  return launch_splitk_reduce(a.ws, a.out, (int64_t)a.M * a.N, p.ksplit, stream, a.xt);
 }
 
 }  // namespace mlxq

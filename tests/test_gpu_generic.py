@@ -328,6 +328,30 @@ def test_float16_mid_decode_default_route(bits, M):
     check(y, og.qmm(xv, wqn, sv, bv, True, 64, bits), "float16")
 
 
+@pytest.mark.parametrize("tile", ["-1", "4", "5", "6", "7", "8"])
+@pytest.mark.parametrize("bits,gs", [(4, 32), (4, 64), (8, 64), (8, 128)])
+@pytest.mark.parametrize("M", [65, 300])
+def test_float16_prefill_tile_kernel(monkeypatch, tile, bits, gs, M):
+    # float16 prefill on the 32x32-MFMA tile kernel (every tile shape:
+    # MLXQ_QMM_TILE; -1 = the planner's), weights dequantized to float16
+    setknob(monkeypatch, "MLXQ_QMM_TILE", tile)
+    announce("f16_prefill", tile, bits, gs, M)
+    (x, wq, s, b), (xv, wqn, sv, bv) = case(M, 384, 1024, bits, gs, "float16", "float16", True, 3700 + M + bits + gs)
+    y = mq.quantized_matmul(x, wq, s, b, True, gs, bits)
+    check(y, og.qmm(xv, wqn, sv, bv, True, gs, bits), "float16")
+
+
+@pytest.mark.parametrize("tile,ksplit", [("8", "3"), ("4", "2"), ("6", "5")])
+def test_float16_prefill_split_k(monkeypatch, tile, ksplit):
+    # K split across workgroups: fp32 partials summed and rounded to float16
+    setknob(monkeypatch, "MLXQ_QMM_TILE", tile)
+    setknob(monkeypatch, "MLXQ_QMM_KSPLIT", ksplit)
+    announce("f16_prefill_splitk", tile, ksplit)
+    (x, wq, s, b), (xv, wqn, sv, bv) = case(256, 256, 8192, 4, 64, "float16", "float16", True, 3800)
+    y = mq.quantized_matmul(x, wq, s, b, True, 64, 4)
+    check(y, og.qmm(xv, wqn, sv, bv, True, 64, 4), "float16")
+
+
 @pytest.mark.parametrize("M", [1, 2, 4])
 def test_float16_decode_mxfp4(M):
     announce("f16_decode_mxfp4", M)
