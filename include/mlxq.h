@@ -213,10 +213,11 @@ mlxq_status mlxq_quantized_matmul_shape(const mlxq_array* x, const mlxq_array* w
  * the reference casts indices (ops.cpp:100), is non-decreasing in the flat
  * order of the broadcast batch; as in the reference's expert-run kernels
  * (rocm/quantized/qmm.hip:4705-4740, found by binary search) the result is
- * unspecified when the promise is false (the sorted mxfp4 route then leaves
- * some output rows unwritten: negative int32 values, for instance, are not
- * sorted after the cast).  Sorted and unsorted
- * routes differ only in summation order (same tolerance).  `global_scale` (nvfp4 only in the reference) must be
+ * unspecified when the promise is false (the sorted routes for one
+ * activation row per entry then leave some output rows unwritten: negative
+ * int32 values, for instance, are not sorted after the cast).  Sorted and
+ * unsorted routes differ only in summation order (same tolerance).
+ * `global_scale` (nvfp4 only in the reference) must be
  * NULL.  Index arrays may be any integer dtype and any strides
  * (broadcasting included).  Types, code widths, transposes and strides as
  * for mlxq_quantized_matmul; any rows per gathered matrix. */

@@ -515,7 +515,7 @@ struct Knobs {
   int qmv_mr = 1;  // whole-row mid-size kernel where it applies (0: off)
   int mr_ring = 0;  // its weight ring depth in windows (0: planner)
   int gen_ks = 0;  // K splits of the general kernel (0: planner)
-  int gather_sorted = 1, gather_group = -1, gather_runs = 1, gather_direct = 1;
+  int gather_sorted = 1, gather_group = -1, gather_runs = 2, gather_direct = 1;
   std::string qmv_kernel;  // "", "rs", "b4", "mid", "mr", "fr", "mfma"
 };
 
@@ -542,7 +542,7 @@ const Knobs* read_knobs() {
   k->gen_ks = env_int("MLXQ_GEN_KS", 0);
   k->gather_sorted = env_int("MLXQ_GATHER_SORTED", 1);
   k->gather_group = env_int("MLXQ_GATHER_GROUP", -1);
-  k->gather_runs = env_int("MLXQ_GATHER_RUNS", 1);
+  k->gather_runs = env_int("MLXQ_GATHER_RUNS", 2);
   k->gather_direct = env_int("MLXQ_GATHER_DIRECT", 1);
   const char* v = std::getenv("MLXQ_QMV_KERNEL");
   k->qmv_kernel = v ? v : "";
@@ -1707,18 +1707,23 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x_, const mlxq_array* w_, const ml
     }
 
     // Sorted gathers with one row per entry (the expert-sorted MoE decode of
-    // mlxcel's callers) run over runs of equal experts: each run streams its
-    // expert's weights once per 4 entries instead of once per entry.
-    // MLXQ_GATHER_RUNS=0 turns it off.
+    // mlxcel's callers): on the block-MFMA kernel, one workgroup row per
+    // expert finds the expert's entries by binary search and streams its
+    // weights once per 4 of them (MLXQ_GATHER_RUNS=2, the default; it relies
+    // on the order, as the reference's sorted route does).  Otherwise
+    // (MLXQ_GATHER_RUNS=1, or the row-streaming kernel) runs of equal
+    // consecutive experts, split at multiples of 4, correct for any order;
+    // MLXQ_GATHER_RUNS=0: one segment per entry.
     const int r_req = knobs().qmv_r;
     {
       const DirectIdx dl = direct_index(lhs_indices, dsh[0], g.idx_shape);
       const DirectIdx dr = direct_index(rhs_indices, dsh[1], g.idx_shape);
       if (sorted_indices && M == 1 && B >= 8 && dr.ok && dr.p && dl.ok && !dl.p && dl.div == 1 &&
           knobs().gather_runs != 0) {
-        // runs of up to 4 entries on the block-MFMA kernel (gpt-oss MoE shapes,
-        // T=16: 9% faster than one segment per entry; runs of 8 or 16 are
-        // slower), else the row-streaming kernel
+        // 4 entries at a time on the block-MFMA kernel (gpt-oss MoE shapes,
+        // T=16: runs of 4 were 9% faster than one segment per entry, runs of
+        // 8 or 16 slower; the row-streaming kernel with the expert search was
+        // 13% slower than the block-MFMA one), else on the row-streaming kernel
         const mlxq::QmvB4Plan bp = mlxq::qmv_b4_plan(fmt, sp.gs, sp.N, sp.K, 4, 0, 0);
         const mlxq::QmvRsPlan rp = bp.ok ? mlxq::QmvRsPlan{} : mlxq::qmv_rs_plan(fmt, sp.gs, sp.N, sp.K, 4, r_req);
         if (bp.ok || rp.ok) {
@@ -1743,7 +1748,11 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x_, const mlxq_array* w_, const ml
           a.out_rows = (int)B;
           a.rows_lds = 1;
           a.runs = 4;
-          if (bp.ok) {
+          if (bp.ok && knobs().gather_runs >= 2) {
+            // one workgroup row per expert, its entries found by binary search
+            a.runs = -1;
+            hip_check(mlxq::qmv_b4_launch(fmt, sp.gs, a, (int)E, bp, stream), "gather qmv launch");
+          } else if (bp.ok) {
             hip_check(mlxq::qmv_b4_launch(fmt, sp.gs, a, (int)B, bp, stream), "gather qmv launch");
           } else {
             hip_check(mlxq::qmv_rs_launch(fmt, sp.gs, a, (int)B, rp, stream), "gather qmv launch");

@@ -52,6 +52,71 @@ __device__ __forceinline__ int seg_index(const uint32_t* idx, int stride, int si
   return (int)min(idx[(int64_t)sidx * (stride > 1 ? stride : 1)], (uint32_t)(clamp - 1));
 }
 
+// First entry whose (clamped) expert is >= v in the sorted index array;
+// wave-uniform.  Each step samples 64 evenly spaced entries of [lo, hi).
+__device__ __forceinline__ int lower_bound_sorted(const uint32_t* idx, int stride, int n, int clamp, int v,
+                                                  int lane) {
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    const int span = hi - lo;
+    const int step = (span + 63) / 64;
+    const int pos = lo + lane * step;
+    const bool in = pos < hi;
+    const int val = in ? seg_index(idx, stride, pos, clamp, 0) : 0x7FFFFFFF;
+    const uint64_t below = __ballot(in && val < v);
+    const uint64_t inside = __ballot(in);
+    const int c = __popcll(below);
+    const int ns = __popcll(inside);
+    const int nlo = c > 0 ? lo + (c - 1) * step + 1 : lo;
+    const int nhi = c < ns ? lo + c * step : hi;
+    if (step == 1) return c < ns ? lo + c : hi;
+    lo = nlo;
+    hi = nhi;
+  }
+  return lo;
+}
+
+// [first entry whose expert is >= v, first entry whose expert is >= v + 1)
+// in the sorted index array, the two searches of lower_bound_sorted run in
+// lockstep so each step costs one load round; wave-uniform.
+__device__ __forceinline__ void sorted_run(const uint32_t* idx, int stride, int n, int clamp, int v, int lane,
+                                           int& first, int& end) {
+  int lo[2] = {0, 0}, hi[2] = {n, n}, res[2] = {n, n};
+  bool done[2] = {n <= 0, n <= 0};
+  while (!done[0] || !done[1]) {
+    int val[2], step[2];
+    bool in[2];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {  // both loads in flight before either ballot
+      step[s] = (hi[s] - lo[s] + 63) / 64;
+      const int pos = lo[s] + lane * step[s];
+      in[s] = !done[s] && pos < hi[s];
+      val[s] = in[s] ? seg_index(idx, stride, pos, clamp, 0) : 0x7FFFFFFF;
+    }
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+      if (done[s]) continue;
+      const uint64_t below = __ballot(in[s] && val[s] < v + s);
+      const int c = __popcll(below), ns = __popcll(__ballot(in[s]));
+      if (step[s] == 1) {
+        res[s] = c < ns ? lo[s] + c : hi[s];
+        done[s] = true;
+      } else {
+        const int nlo = c > 0 ? lo[s] + (c - 1) * step[s] + 1 : lo[s];
+        const int nhi = c < ns ? lo[s] + c * step[s] : hi[s];
+        lo[s] = nlo;
+        hi[s] = nhi;
+        if (lo[s] >= hi[s]) {
+          res[s] = lo[s];
+          done[s] = true;
+        }
+      }
+    }
+  }
+  first = n <= 0 ? 0 : res[0];
+  end = n <= 0 ? 0 : res[1];
+}
+
 // ---- MFMA ------------------------------------------------------------------
 // v_mfma_f32_16x16x32_bf16: D[16x16] += A[16x32] * B[32x16], fp32 accumulate.
 // Lane i holds A row (i % 16), B column (i % 16), both over the 8 k-slots

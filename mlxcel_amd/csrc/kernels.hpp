@@ -46,9 +46,11 @@ struct QmvArgs {
   const uint32_t* orows;    // grouped row -> output row
   int xt;                   // element type of x / scales / biases / out: 0 bfloat16, 1 float16
                             // (float16: the row-streaming kernel's dense entry only)
-  // Sorted gathers (rps == 1): nonzero = segments are runs of equal experts
+  // Sorted gathers (rps == 1): positive = segments are runs of equal experts
   // among consecutive entries, at most `runs` entries each (row-streaming
-  // kernel: 4; block-MFMA kernel: up to its 4 MS rows).
+  // kernel: 4; block-MFMA kernel: up to its 4 MS rows).  -1 (block-MFMA
+  // kernel, MS = 1): blockIdx.y is an expert, which finds its entries by
+  // binary search in the sorted indices and takes them 4 at a time.
   int runs;
 };
 

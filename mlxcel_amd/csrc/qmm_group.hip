@@ -46,30 +46,6 @@ constexpr int GQ_RING = 4;                   // blocks in the activation / weigh
 constexpr int GQ_XB = GQ_MC * GQ_KB * 2;     // activation bytes per block (16 KiB, 256 per row)
 constexpr int GQ_XI = GQ_XB / 1024 / GQ_NW;  // 1 KiB direct-to-LDS loads per wave and block (4)
 
-// First entry whose (clamped) expert is >= v in the sorted index array;
-// wave-uniform.  Each step samples 64 evenly spaced entries of [lo, hi).
-__device__ __forceinline__ int lower_bound_sorted(const uint32_t* idx, int stride, int n, int clamp, int v,
-                                                  int lane) {
-  int lo = 0, hi = n;
-  while (lo < hi) {
-    const int span = hi - lo;
-    const int step = (span + 63) / 64;
-    const int pos = lo + lane * step;
-    const bool in = pos < hi;
-    const int val = in ? seg_index(idx, stride, pos, clamp, 0) : 0x7FFFFFFF;
-    const uint64_t below = __ballot(in && val < v);
-    const uint64_t inside = __ballot(in);
-    const int c = __popcll(below);
-    const int ns = __popcll(inside);
-    const int nlo = c > 0 ? lo + (c - 1) * step + 1 : lo;
-    const int nhi = c < ns ? lo + c * step : hi;
-    if (step == 1) return c < ns ? lo + c : hi;
-    lo = nlo;
-    hi = nhi;
-  }
-  return lo;
-}
-
 }  // namespace
 
 __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGroupArgs a) {

@@ -58,42 +58,23 @@ __device__ __forceinline__ void mfma4_done(f32x4& d) { asm volatile("s_nop 7\n\t
 
 }  // namespace
 
-// FMT: weight format; MS: sets of 4 activation rows (1, 2 or 4); RG: groups
-// of 4 weight rows per workgroup; CPW: 16-piece K chunks per wave.
+// One pass: `count` activation rows starting at index entry / segment sidx
+// against the workgroup's 4 RG weight rows of `expert`.  `tid` is
+// threadIdx.x (see the expert-search kernel for why it is an argument).
 template <int FMT, int MS, int RG, int CPW>
-__global__ __launch_bounds__(512) void qmv_b4_kernel(const QmvArgs a, int gs_shift) {
+__device__ __forceinline__ void b4_pass(const QmvArgs& a, int gs_shift, float* red, int sidx, int count,
+                                        int expert, int tid) {
   constexpr bool AFF = FMT != MXFP4;
   constexpr int BITS = FMT == AFF8 ? 8 : 4;
   constexpr int KL = 128 / BITS;  // K values per 16-byte piece
   constexpr int XV = KL / 8;      // 16-byte activation loads per piece and row
   constexpr int NQ = KL / 4;      // MFMAs (4 k each) per piece and row set
   constexpr int V = MS * RG * 4;  // partial sums per lane
-
-  extern __shared__ __align__(16) float red[];  // [wave][row of 16 lanes][V][4 columns]
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
   const int NW = blockDim.x >> 6;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int b = lane >> 2;  // piece within the chunk
   const int j = lane & 3;   // weight row within a group / activation row within a set
-  const int sidx = blockIdx.y;
-
-  int count = min(a.rps, a.total_rows - sidx * a.rps);
-  if (count <= 0) return;
-  const int expert = seg_index(a.rhs, a.rhs_stride, sidx, a.E, a.w_expert_stride ? sidx : 0);
-  if (a.runs) {
-    // Expert runs of a sorted gather (one activation row per entry, 4 MS >=
-    // a.runs rows compiled): entry sidx starts a segment where the expert
-    // changes or at a multiple of a.runs, and the segment takes the following
-    // entries of the same expert up to the next multiple; other workgroups
-    // exit.
-    const int cap = a.runs;
-    if (sidx % cap != 0 && seg_index(a.rhs, a.rhs_stride, sidx - 1, a.E, 0) == expert) return;
-    count = 1;
-    while (count < cap && (sidx + count) % cap != 0 && sidx + count < a.total_rows &&
-           seg_index(a.rhs, a.rhs_stride, sidx + count, a.E, 0) == expert)
-      count++;
-  }
   const int xbatch = seg_index(a.lhs, a.lhs_stride, sidx, a.X, a.lhs_div > 1 ? sidx / a.lhs_div : sidx);
 
   const int N = a.N;
@@ -105,7 +86,8 @@ __global__ __launch_bounds__(512) void qmv_b4_kernel(const QmvArgs a, int gs_shi
   constexpr int ESZ = AFF ? 2 : 1;
 
   const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.w + (int64_t)expert * a.w_expert_stride, (uint32_t)N * RB);
-  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.x + (int64_t)xbatch * a.rps * K, (uint32_t)count * (uint32_t)K * 2u);
+  const __amdgpu_buffer_rsrc_t xr =
+      buffer_rsrc(a.x + (int64_t)xbatch * a.rps * K, (uint32_t)count * (uint32_t)K * 2u);
   const int64_t sb0 = (int64_t)expert * a.s_expert_stride;
   const __amdgpu_buffer_rsrc_t sr =
       buffer_rsrc(reinterpret_cast<const uint8_t*>(a.scales) + sb0 * ESZ, (uint32_t)(N * G * ESZ));
@@ -296,18 +278,70 @@ __global__ __launch_bounds__(512) void qmv_b4_kernel(const QmvArgs a, int gs_shi
   }
 }
 
+// FMT: weight format; MS: sets of 4 activation rows (1, 2 or 4); RG: groups
+// of 4 weight rows per workgroup; CPW: 16-piece K chunks per wave.
+template <int FMT, int MS, int RG, int CPW>
+__global__ __launch_bounds__(512) void qmv_b4_kernel(const QmvArgs a, int gs_shift) {
+  extern __shared__ __align__(16) float red[];  // [wave][row of 16 lanes][V][4 columns]
+  const int sidx = blockIdx.y;
+  int count = min(a.rps, a.total_rows - sidx * a.rps);
+  if (count <= 0) return;
+  const int expert = seg_index(a.rhs, a.rhs_stride, sidx, a.E, a.w_expert_stride ? sidx : 0);
+  if (a.runs) {
+    // Expert runs of a sorted gather (one activation row per entry, 4 MS >=
+    // a.runs rows compiled): entry sidx starts a segment where the expert
+    // changes or at a multiple of a.runs, and the segment takes the following
+    // entries of the same expert up to the next multiple; other workgroups
+    // exit.
+    const int cap = a.runs;
+    if (sidx % cap != 0 && seg_index(a.rhs, a.rhs_stride, sidx - 1, a.E, 0) == expert) return;
+    count = 1;
+    while (count < cap && (sidx + count) % cap != 0 && sidx + count < a.total_rows &&
+           seg_index(a.rhs, a.rhs_stride, sidx + count, a.E, 0) == expert)
+      count++;
+  }
+  b4_pass<FMT, MS, RG, CPW>(a, gs_shift, red, sidx, count, expert, threadIdx.x);
+}
+
+// Sorted gather with one activation row per entry, one workgroup row per
+// expert (blockIdx.y): the expert finds its entries [first, end) by binary
+// search in the sorted indices (as the reference's find_sorted_expert_run,
+// rocm/quantized/qmm.hip:4741-4915) and takes them 4 MS at a time, so its
+// weights stream once per 4 MS entries; experts without entries exit.  Every
+// per-lane value of a pass is derived from a thread index the compiler
+// cannot see through: hoisted out of the pass loop, the pass's addresses
+// would stay live across passes and cost a wave per SIMD.
+template <int FMT, int MS, int RG, int CPW>
+__global__ __launch_bounds__(512) void qmv_b4_search_kernel(const QmvArgs a, int gs_shift) {
+  extern __shared__ __align__(16) float red[];
+  const int expert = blockIdx.y;
+  int first, end;
+  sorted_run(a.rhs, a.rhs_stride, a.total_rows, a.E, expert, threadIdx.x & 63, first, end);
+  for (int s = first; s < end; s += 4 * MS) {  // workgroup-uniform
+    if (s > first) __syncthreads();  // the previous pass has read its reduction
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    b4_pass<FMT, MS, RG, CPW>(a, gs_shift, red, s, min(4 * MS, end - s), expert, tid);
+  }
+}
+
 // ---- host ------------------------------------------------------------------
 
 namespace {
 
-
+// a.runs < 0 (expert search, grid.y = experts): the search kernel, compiled
+// for one set of 4 activation rows per pass
 template <int FMT, int MS>
 hipError_t b4_launch_ms(const QmvB4Plan& p, const QmvArgs& a, int gs_shift, dim3 grid, hipStream_t stream) {
   const dim3 block((unsigned)(p.nw * 64));
-#define B4_CASE(RG_, CPW_)                                                                             \
-  if (p.rg == RG_ && p.cpw == CPW_) {                                                                  \
-    hipLaunchKernelGGL((qmv_b4_kernel<FMT, MS, RG_, CPW_>), grid, block, p.lds, stream, a, gs_shift); \
-    return hipGetLastError();                                                                          \
+  if (MS != 1 && a.runs < 0) return hipErrorInvalidValue;
+#define B4_CASE(RG_, CPW_)                                                                                      \
+  if (p.rg == RG_ && p.cpw == CPW_) {                                                                           \
+    if (MS == 1 && a.runs < 0)                                                                                  \
+      hipLaunchKernelGGL((qmv_b4_search_kernel<FMT, 1, RG_, CPW_>), grid, block, p.lds, stream, a, gs_shift); \
+    else                                                                                                        \
+      hipLaunchKernelGGL((qmv_b4_kernel<FMT, MS, RG_, CPW_>), grid, block, p.lds, stream, a, gs_shift);        \
+    return hipGetLastError();                                                                                   \
   }
   B4_CASE(1, 1)
   B4_CASE(2, 1)

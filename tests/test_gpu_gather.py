@@ -213,10 +213,11 @@ def test_direct_indices_match_index_prep(monkeypatch, dtype, case):
 @pytest.mark.parametrize("pattern", ["random_sorted", "one_expert", "pairs", "alternating", "unsorted"])
 @pytest.mark.parametrize("dtype", [torch.int32, torch.int64])
 def test_sorted_runs(monkeypatch, pattern, dtype):
-    # the run path of sorted gathers: equal consecutive experts form segments
-    # of up to 4 entries; every pattern must give the per-entry result
-    # (oracle), with runs longer than 4, runs across multiples of 4, a ragged
-    # tail (B = 37), and input that is not actually sorted
+    # the run path of sorted gathers (MLXQ_GATHER_RUNS=1): equal consecutive
+    # experts form segments of up to 4 entries; every pattern must give the
+    # per-entry result (oracle), with runs longer than 4, runs across
+    # multiples of 4, a ragged tail (B = 37), and input that is not actually
+    # sorted (the run path does not rely on the order)
     announce("gather_sorted_runs", pattern, dtype)
     E, N, K, B = 8, 264, 2048, 37
     rng = np.random.default_rng(970)
@@ -225,6 +226,7 @@ def test_sorted_runs(monkeypatch, pattern, dtype):
     # the reference's sorted route does, and "pairs" (wrapping at E),
     # "alternating" and "unsorted" are not sorted
     setknob(monkeypatch, "MLXQ_GATHER_SORTED", "0")
+    setknob(monkeypatch, "MLXQ_GATHER_RUNS", "1")
     if pattern == "random_sorted":
         rhs = np.sort(rng.integers(0, E, B))
     elif pattern == "one_expert":
@@ -259,6 +261,57 @@ def test_sorted_runs_affine():
                                  torch.from_numpy(rhs).cuda(), True, 64, 4, sorted_indices=True))
     want = orc.gather_qmm_t(x, wq, s, b, np.arange(B, dtype=np.uint32), rhs.astype(np.uint32))
     assert max_rel(got, want) <= TOL
+
+
+@pytest.mark.parametrize("fmt", ["mxfp4", "affine4", "affine8"])
+@pytest.mark.parametrize("pattern", ["random_sorted", "one_expert", "skewed", "clamped_tail", "few_entries",
+                                     "long"])
+def test_sorted_expert_search(monkeypatch, fmt, pattern):
+    # the expert-search form of the sorted run path (the default,
+    # MLXQ_GATHER_RUNS=2, block-MFMA kernel): one workgroup row per expert
+    # finds its entries by binary search and takes them 4 at a time.  Experts without entries, one expert holding all 37
+    # entries (10 passes), a skewed spread, out-of-range ids at the end
+    # (clamped to the last expert, which keeps the order) and fewer entries
+    # than experts, and 300 entries (searches of several steps); bitwise the
+    # runs-of-4 result, within tolerance of the oracle
+    announce("gather_sorted_expert_search", fmt, pattern)
+    E, N, K, B = 8, 264, 2048, 37
+    rng = np.random.default_rng(976)
+    if pattern == "random_sorted":
+        rhs = np.sort(rng.integers(0, E, B))
+    elif pattern == "one_expert":
+        rhs = np.full(B, 5)
+    elif pattern == "skewed":
+        rhs = np.sort(np.minimum(rng.geometric(0.3, B) - 1, E - 1))
+    elif pattern == "clamped_tail":
+        rhs = np.sort(rng.integers(0, E, B))
+        rhs[-5:] = 1000
+    elif pattern == "few_entries":
+        E, B = 24, 9
+        rhs = np.sort(rng.choice(E, B, replace=False))
+    else:
+        B = 300
+        rhs = np.sort(rng.integers(0, E, B))
+    x = orc.normal_bf16((B, 1, K), 1.0, 977)
+    R = torch.from_numpy(rhs.astype(np.int64)).cuda()
+    if fmt == "mxfp4":
+        wq, sc = mx_experts(E, N, K, 978)
+        args, s, b, gs, bits, mode = (dev_u32(wq), dev_u8(sc), None), sc, None, 32, 4, "mxfp4"
+    else:
+        bits = 4 if fmt == "affine4" else 8
+        wq, s, b = affine_experts(E, N, K, 979, bits=bits)
+        args, sc, gs, mode = (dev_u32(wq), dev_bf16(s), dev_bf16(b)), s, 64, "affine"
+    X = dev_bf16(x)
+    setknob(monkeypatch, "MLXQ_GATHER_SORTED", "0")
+    setknob(monkeypatch, "MLXQ_GATHER_GROUP", "0")
+    setknob(monkeypatch, "MLXQ_GATHER_RUNS", "2")
+    got = host_u16(mq.gather_qmm(X, *args, None, R, True, gs, bits, mode, sorted_indices=True))
+    want = orc.gather_qmm_t(x, wq, sc, b, np.arange(B, dtype=np.uint32),
+                            np.minimum(rhs, E - 1).astype(np.uint32), gs, bits, mode=mode)
+    assert max_rel(got, want) <= TOL
+    setknob(monkeypatch, "MLXQ_GATHER_RUNS", "1")
+    runs = host_u16(mq.gather_qmm(X, *args, None, R, True, gs, bits, mode, sorted_indices=True))
+    np.testing.assert_array_equal(got, runs)
 
 
 @pytest.mark.parametrize("pattern", ["uniform", "one_expert", "skewed", "clamped_tail"])
