@@ -712,11 +712,15 @@ QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus, 
     // 256 x 256 (8 waves) when there are enough tiles or K is long enough
     // for a K split to fill the CUs; else 128 x 128, two workgroups per CU.
     // Up to ~512 rows, 256 x 128 on 8 waves where it measured faster: long K
-    // (split, down projections: 88-89 us vs 91-93 at M=512) and 8-bit codes
-    // with ~one tile per CU (gate/up M=512: 83 us vs 94).  Measured on MI355X
-    // at the Llama-3-8B prefill shapes.
+    // (split, down projections: 88-89 us vs 91-93 at M=512), 8-bit codes
+    // with ~one tile per CU (gate/up M=512: 83 us vs 94) and 4-bit codes
+    // with 0.75-1 tile per CU (gate/up M=384-512: 83-85 us vs 95, steady
+    // state; at M=768, 1.3 tiles per CU, 162 vs 127).  Measured on MI355X at
+    // the Llama-3-8B prefill shapes.
     const bool mid_rows = M > 128 && M <= 768;
-    if (mid_rows && (K >= 8192 || (fmt == AFF8 && tiles_of(8) * 4 >= (int64_t)num_cus * 3))) tile = 8;
+    const int64_t t8 = tiles_of(8);
+    const bool one_round8 = t8 * 4 >= (int64_t)num_cus * 3 && (fmt == AFF8 || (fmt == AFF4 && t8 <= num_cus));
+    if (mid_rows && (K >= 8192 || one_round8)) tile = 8;
     else tile = (M > 128 && (tiles_of(4) >= num_cus / 2 || K >= 8192)) ? 4 : 6;
   }
   p.tile = tile;
