@@ -334,8 +334,14 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
   static_assert(WP >= 1 && WROWS * WP == BN && BN <= NT && XL >= 1, "tile shape");
   static_assert(PB == 16 || (BITS == 4 && PB == 8), "8-byte pieces only for 4-bit codes");
 
-  __shared__ __align__(16) uint16_t xs[2][BM * RS];
-  __shared__ __align__(16) uint16_t wsm[2][BN * RS];
+  // double-buffered activation and dequantized-weight tiles; after the last
+  // K-step the same bytes stage the output tile
+  constexpr int XS_BYTES = 2 * BM * RS * 2, WS_BYTES = 2 * BN * RS * 2;
+  __shared__ __align__(16) unsigned char stage[XS_BYTES + WS_BYTES];
+  uint16_t(*xs)[BM * RS] = reinterpret_cast<uint16_t(*)[BM * RS]>(stage);
+  uint16_t(*wsm)[BN * RS] = reinterpret_cast<uint16_t(*)[BN * RS]>(stage + XS_BYTES);
+  static_assert(BM * BN * 2 <= XS_BYTES + WS_BYTES && TM * BN * 4 <= XS_BYTES + WS_BYTES,
+                "the output tile (16-bit) and a wave row of it (fp32) fit in the staging buffers");
   // per-chunk (scale, bias) table: affine u32 (bf16 scale | bf16 bias << 16)
   // [slot][group][row]; mxfp4 e8m0 bytes [slot][group][row]
   __shared__ __align__(16) uint32_t tbl[2 * 8 * BN];
@@ -628,7 +634,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
 #pragma unroll
         for (int i = 0; i < FM; i++)
 #pragma unroll
-          for (int j = 0; j < FN; j++) acc[i][j] = mfma32x32x16_xt<XT>(af[cur][i], bv[cur][j], acc[i][j]);
+          for (int j = 0; j < FN; j++) acc[i][j] = mfma32x32x16_xt<XT>(bv[cur][j], af[cur][i], acc[i][j]);
         // step ks+1 goes to the other buffer in the first two slices, then
         // the registers take the loads of step ks+2
         if (s == 0) {
@@ -659,28 +665,81 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
     }
   }
 
-  // ---- epilogue: lane holds column (lane % 32) and rows 8 (q / 4) + 4 (lane / 32) + q % 4
+  // ---- epilogue ---------------------------------------------------------------
+  // The products ran as (weights, activations), so block (i, j) of a lane
+  // holds activation row m = wm TM + 32 i + (lane % 32) and weight columns
+  // n = wn TN + 32 j + 8 t + 4 (lane / 32) + r at acc[i][j][4 t + r]: four
+  // consecutive columns.  The tile goes through the (now free) staging LDS,
+  // 16-byte chunk c of a row at c ^ (row % chunks per row), and leaves as
+  // 16-byte row pieces (per-element stores of the accumulators took ~8%
+  // longer at M = 2048).  fp32 split-K partials go one wave row at a time.
   const bool split = a.ksplit > 1;
-  auto put = [&](int tr, int c, float v) {
-    if (tr < rows && c < N) {
-      const int64_t r = a.seg ? (int64_t)a.orows[r0 + tr] : (int64_t)(m0 + tr);
-      if (split) a.ws[((int64_t)z * M + r) * N + c] = v;
-      else a.out[r * N + c] = (uint16_t)f32_to_xt<XT>(v);
-    }
-  };
+  auto out_row = [&](int tr) -> int64_t { return a.seg ? (int64_t)a.orows[r0 + tr] : (int64_t)(m0 + tr); };
+  if (!split) {
+    constexpr int CPR = BN / 8;  // 16-byte chunks per row (8 values)
+    uint16_t* ot = reinterpret_cast<uint16_t*>(stage);
 #pragma unroll
-  for (int i = 0; i < FM; i++)
+    for (int i = 0; i < FM; i++)
 #pragma unroll
-    for (int j = 0; j < FN; j++) {
-      const int tr0 = wm * TM + i * 32 + 4 * (lane >> 5);
-      const int c = n0 + wn * TN + j * 32 + fr;
-      const f32x16 v = acc[i][j];
-      // element indices spelled out: a loop index here can leave the array in scratch
-#define QMM_PUT4(Q) put(tr0 + 2 * (Q), c, v[Q]); put(tr0 + 2 * (Q) + 1, c, v[(Q) + 1]); \
-                    put(tr0 + 2 * (Q) + 2, c, v[(Q) + 2]); put(tr0 + 2 * (Q) + 3, c, v[(Q) + 3]);
-      QMM_PUT4(0) QMM_PUT4(4) QMM_PUT4(8) QMM_PUT4(12)
-#undef QMM_PUT4
+      for (int j = 0; j < FN; j++) {
+        const int m = wm * TM + i * 32 + fr;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const int c = (wn * TN + j * 32 + 8 * q) >> 3;
+          const u32x2 pr = {pack_xt2<XT>(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
+                            pack_xt2<XT>(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3])};
+          *reinterpret_cast<u32x2*>(ot + m * BN + ((c ^ (m & (CPR - 1))) << 3) + 4 * (lane >> 5)) = pr;
+        }
+      }
+    __syncthreads();
+    const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0;
+    for (int idx = t; idx < BM * CPR; idx += NT) {
+      const int m = idx / CPR, c = idx - m * CPR;
+      const int n = n0 + 8 * c;
+      if (m >= rows || n >= N) continue;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(ot + m * BN + ((c ^ (m & (CPR - 1))) << 3));
+      uint16_t* dst = a.out + out_row(m) * N + n;
+      if (vec) {
+        *reinterpret_cast<u32x4*>(dst) = v;
+      } else {
+        for (int e = 0; e < 8 && n + e < N; e++) dst[e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+      }
     }
+  } else {
+    constexpr int CPR = BN / 4;  // 16-byte chunks per row (4 fp32)
+    float* ot = reinterpret_cast<float*>(stage);
+    const bool vec = (N & 3) == 0;
+    for (int p = 0; p < NWM; p++) {  // one wave row of the tile per pass
+      if (p > 0) __syncthreads();    // the previous pass has been read
+      if (wm == p) {
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+          for (int j = 0; j < FN; j++) {
+            const int mm = i * 32 + fr;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+              const int c = ((wn * TN + j * 32 + 8 * q) >> 2) + (lane >> 5);
+              const f32x4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+              *reinterpret_cast<f32x4*>(ot + mm * BN + ((c ^ (mm & (CPR - 1))) << 2)) = v;
+            }
+          }
+      }
+      __syncthreads();
+      for (int idx = t; idx < TM * CPR; idx += NT) {
+        const int mm = idx / CPR, c = idx - mm * CPR;
+        const int m = p * TM + mm, n = n0 + 4 * c;
+        if (m >= rows || n >= N) continue;
+        const f32x4 v = *reinterpret_cast<const f32x4*>(ot + mm * BN + ((c ^ (mm & (CPR - 1))) << 2));
+        float* dst = a.ws + ((int64_t)z * M + out_row(m)) * N + n;
+        if (vec) {
+          *reinterpret_cast<f32x4*>(dst) = v;
+        } else {
+          for (int e = 0; e < 4 && n + e < N; e++) dst[e] = v[e];
+        }
+      }
+    }
+  }
 }
 
 // ---- host ------------------------------------------------------------------
