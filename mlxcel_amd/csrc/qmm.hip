@@ -776,9 +776,12 @@ QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus, 
     // with 0.75-1 tile per CU (gate/up M=384-512: 83-85 us vs 95, steady
     // state; at M=768, 1.3 tiles per CU, 162 vs 127).  Measured on MI355X at
     // the Llama-3-8B prefill shapes.
+    // At 129-256 rows (less than one 256 x 128 tile per CU) the same tile
+    // with a K split measured best too (gate/up M=256: 51.8 us vs 62 on 128 x
+    // 128).
     const bool mid_rows = M > 128 && M <= 768;
     const int64_t t8 = tiles_of(8);
-    const bool one_round8 = t8 * 4 >= (int64_t)num_cus * 3 && (fmt == AFF8 || (fmt == AFF4 && t8 <= num_cus));
+    const bool one_round8 = (fmt == AFF8 && t8 * 4 >= (int64_t)num_cus * 3) || (fmt != MXFP4 && t8 <= num_cus);
     if (mid_rows && (K >= 8192 || one_round8)) tile = 8;
     else tile = (M > 128 && (tiles_of(4) >= num_cus / 2 || K >= 8192)) ? 4 : 6;
   }
@@ -791,10 +794,11 @@ QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus, 
   if (ksplit_req > 0) {
     ks = ksplit_req;
   } else {
-    // split K while the grid covers less than the CUs (two workgroups per CU
-    // for few rows, where each tile is cheap) and each split keeps >= 8 K-steps
+    // split K while the grid covers less than the CUs (up to two workgroups
+    // per CU for few rows, where each tile is cheap) and each split keeps >= 8
+    // K-steps (gate/up M=32-128: 448 workgroups 31-38 us, 896 37-50 us)
     if (M <= 128) {
-      while (tiles * ks < 2 * num_cus && nks / (ks * 2) >= 8) ks *= 2;
+      while (tiles * ks * 2 <= 2 * num_cus && nks / (ks * 2) >= 8) ks *= 2;
     } else {
       while (tiles * ks * 2 <= num_cus && nks / (ks * 2) >= 8) ks *= 2;
     }
