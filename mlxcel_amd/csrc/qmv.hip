@@ -413,33 +413,31 @@ __global__ __launch_bounds__(256) void qmv_splitk_reduce(const float* __restrict
   out[i] = (uint16_t)f32_to_xt<XT>(y);
 }
 
-// The same sum, 4 outputs per thread: 16-byte partial loads, four splits'
-// loads in flight before their adds (the split order of the sum is unchanged).
+// The same sum, 4 outputs per thread: 16-byte partial loads, up to 16
+// splits' loads in flight before their adds (one memory round trip for the
+// mid-size decode kernel's 14 K ranges instead of four; the split order of
+// the sum is unchanged).
 template <int XT>
 __global__ __launch_bounds__(256) void qmv_splitk_reduce4(const float4* __restrict__ ws, uint2* __restrict__ out,
                                                           int64_t n4, int ks) {
+  constexpr int ZB = 16;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n4) return;
   float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
-  int z = 0;
-  for (; z + 4 <= ks; z += 4) {
-    float4 v[4];
+  for (int z = 0; z < ks; z += ZB) {  // uniform
+    float4 v[ZB];
 #pragma unroll
-    for (int u = 0; u < 4; u++) v[u] = ws[(int64_t)(z + u) * n4 + i];
+    for (int u = 0; u < ZB; u++)
+      if (z + u < ks) v[u] = ws[(int64_t)(z + u) * n4 + i];
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-      y.x += v[u].x;
-      y.y += v[u].y;
-      y.z += v[u].z;
-      y.w += v[u].w;
+    for (int u = 0; u < ZB; u++) {
+      if (z + u < ks) {
+        y.x += v[u].x;
+        y.y += v[u].y;
+        y.z += v[u].z;
+        y.w += v[u].w;
+      }
     }
-  }
-  for (; z < ks; z++) {
-    const float4 v = ws[(int64_t)z * n4 + i];
-    y.x += v.x;
-    y.y += v.y;
-    y.z += v.z;
-    y.w += v.w;
   }
   out[i] = make_uint2(f32_to_xt<XT>(y.x) | (f32_to_xt<XT>(y.y) << 16),
                       f32_to_xt<XT>(y.z) | (f32_to_xt<XT>(y.w) << 16));
