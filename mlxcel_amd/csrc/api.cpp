@@ -1748,8 +1748,10 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x_, const mlxq_array* w_, const ml
           a.out_rows = (int)B;
           a.rows_lds = 1;
           a.runs = 4;
-          if (bp.ok && knobs().gather_runs >= 2) {
+          if (bp.ok && knobs().gather_runs >= 2 && E <= B) {
             // one workgroup row per expert, its entries found by binary search
+            // (with more experts than entries most rows would only search
+            // and exit: runs then)
             a.runs = -1;
             hip_check(mlxq::qmv_b4_launch(fmt, sp.gs, a, (int)E, bp, stream), "gather qmv launch");
           } else if (bp.ok) {

@@ -271,9 +271,9 @@ def test_sorted_expert_search(monkeypatch, fmt, pattern):
     # MLXQ_GATHER_RUNS=2, block-MFMA kernel): one workgroup row per expert
     # finds its entries by binary search and takes them 4 at a time.  Experts without entries, one expert holding all 37
     # entries (10 passes), a skewed spread, out-of-range ids at the end
-    # (clamped to the last expert, which keeps the order) and fewer entries
-    # than experts, and 300 entries (searches of several steps); bitwise the
-    # runs-of-4 result, within tolerance of the oracle
+    # (clamped to the last expert, which keeps the order), as many entries as
+    # experts on a third of them, and 300 entries (searches of several
+    # steps); bitwise the runs-of-4 result, within tolerance of the oracle
     announce("gather_sorted_expert_search", fmt, pattern)
     E, N, K, B = 8, 264, 2048, 37
     rng = np.random.default_rng(976)
@@ -287,8 +287,8 @@ def test_sorted_expert_search(monkeypatch, fmt, pattern):
         rhs = np.sort(rng.integers(0, E, B))
         rhs[-5:] = 1000
     elif pattern == "few_entries":
-        E, B = 24, 9
-        rhs = np.sort(rng.choice(E, B, replace=False))
+        E, B = 12, 12  # as many entries as experts (the search's limit), most on a few experts
+        rhs = np.sort(rng.choice(4, B) * 3)
     else:
         B = 300
         rhs = np.sort(rng.integers(0, E, B))
