@@ -485,13 +485,26 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
   constexpr int NWORD = WP * PW;  // weight words per thread and K-step
   // (8-bit: the part holding the even word of a pair writes both words; the
   // registers hold the whole step until load_step(ks + 2), after the last part)
-  auto store_part = [&](int buf, int p, int ks) {
+  // Table word (affine: scale | bias << 16; mxfp4: the e8m0 byte) of each
+  // weight row this thread dequantizes, for this thread's group of step ks
+  // (one per 16-byte piece: VPL <= group size).  Read once per step, before
+  // the step's fragment reads are issued: LDS reads complete in order, so a
+  // table read issued behind them would wait for all of them.
+  uint32_t sbw[WP];
+  auto table_read = [&](int ks) {
+    const int g = ((ks * BK + wpc * VPL) >> gs_shift);
+    const int gslot = ((g / CHG) & 1) * CHG + g % CHG;
+#pragma unroll
+    for (int pp = 0; pp < WP; pp++) {
+      const int r = wrow + WROWS * pp;
+      if constexpr (AFF) sbw[pp] = tbl[gslot * BN + r];
+      else sbw[pp] = reinterpret_cast<const uint8_t*>(tbl)[gslot * BN + r];
+    }
+  };
+  auto store_part = [&](int buf, int p) {
 #pragma unroll
     for (int i = 0; i < XL; i++)
       if (i * NPART / XL == p) *reinterpret_cast<u32x4*>(&xs[buf][xdst(i)]) = xreg[i];
-    // this thread's group of step ks (one per 16-byte piece: VPL <= group size)
-    const int g = ((ks * BK + wpc * VPL) >> gs_shift);
-    const int gslot = ((g / CHG) & 1) * CHG + g % CHG;
 #pragma unroll
     for (int e = 0; e < NWORD; e++) {
       if (e * NPART / NWORD != p) continue;
@@ -501,7 +514,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
       uint16_t* rowp = &wsm[buf][r * RS];
       const int r7 = swz(r);
       if constexpr (AFF) {
-        const uint32_t sb = tbl[gslot * BN + r];
+        const uint32_t sb = sbw[pp];
         const float sc = XT ? xt_to_f32<1>(sb & 0xFFFFu) : __uint_as_float(sb << 16);
         const float bi = XT ? xt_to_f32<1>(sb >> 16) : __uint_as_float(sb & 0xFFFF0000u);
         if constexpr (BITS == 4) {
@@ -530,7 +543,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
       } else {
         // fp4 code points times a normal power of two are exact in bf16 (one
         // scaled conversion per pair); 2^-127 and NaN take the explicit product
-        const uint32_t sb = reinterpret_cast<const uint8_t*>(tbl)[gslot * BN + r];
+        const uint32_t sb = sbw[pp];
         const float sc = e8m0_to_f32(sb);
         uint32_t o[4];
         if (sb - 1u < 254u) {
@@ -593,8 +606,9 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
     }
     load_step(ks0);
     __syncthreads();
+    table_read(ks0);
 #pragma unroll
-    for (int p = 0; p < NPART; p++) store_part(0, p, ks0);
+    for (int p = 0; p < NPART; p++) store_part(0, p);
     load_step(ks0 + 1);
     __syncthreads();
     bf16x8 af[2][FM], bv[2][FN];
@@ -607,6 +621,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
       // step's barriers), loads for step ks+3 issued a step ahead
       if ((ks + 2) % SPC == 0 && ks + 2 < ks1) chunk_write((ks + 2) / SPC);
       if ((ks + 3) % SPC == 0 && ks + 3 < ks1) chunk_load((ks + 3) / SPC);
+      table_read(ks + 1);
       const int buf = (ks - ks0) & 1;
       const uint16_t* xb = xs[buf];
       const uint16_t* wb = wsm[buf];
@@ -638,11 +653,11 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
         // step ks+1 goes to the other buffer in the first two slices, then
         // the registers take the loads of step ks+2
         if (s == 0) {
-          store_part(buf ^ 1, 0, ks + 1);
-          store_part(buf ^ 1, 1, ks + 1);
+          store_part(buf ^ 1, 0);
+          store_part(buf ^ 1, 1);
         } else if (s == 1) {
-          store_part(buf ^ 1, 2, ks + 1);
-          store_part(buf ^ 1, 3, ks + 1);
+          store_part(buf ^ 1, 2);
+          store_part(buf ^ 1, 3);
           load_step(ks + 2);
         }
         // interleave within the slice: one MFMA, then a share of the VALU,
