@@ -8,19 +8,19 @@
 // dequantizer's rounding, affine_quantize.hip:164) or fp4(q) * 2^(e-127)
 // (mxfp4, exact), fp32 accumulation, one bf16 rounding on store.
 //
-// Tiling (MI355X-first):
-//  * workgroup = 4 waves (2 x 2) computing a 256 x 128 tile of y; each wave
-//    owns 128 x 64 = 8 x 4 tiles of v_mfma_f32_16x16x32_bf16 (128 fp32
-//    accumulators per lane);
-//  * K advances 64 at a time through double-buffered LDS: activation tile
-//    [256][64 + 8] and dequantized weight tile [128][64 + 8] bf16 (the 8-element
-//    pad puts the 16 rows a fragment read touches on distinct banks);
-//  * the next K-step's global loads are issued before the current step's
-//    MFMAs, so HBM/L2 latency hides behind the matrix cores; one barrier per
-//    K-step;
-//  * when the grid would leave CUs idle (short M), K is split across
-//    workgroups and fp32 partials are summed by a second kernel in a fixed
-//    order (bitwise reproducible).
+// Two kernels:
+//  * qmm_tile_kernel (dense prefill, and grouped gathers at tiles 4-8): tiles
+//    of 128 x 128 to 256 x 256 on 4 or 8 waves of v_mfma_f32_32x32x16_bf16
+//    (or _f16), K in steps of 64 through double-buffered, XOR-swizzled LDS;
+//    described above the kernel;
+//  * qmm_kernel (grouped gathers at tiles 0-3): 4 waves (2 x 2) of
+//    v_mfma_f32_16x16x32_bf16 over padded LDS rows [BM][64 + 8] and
+//    [BN][64 + 8] (the 8-element pad puts the 16 rows a fragment read
+//    touches on distinct banks), the next K-step's loads issued before the
+//    current step's MFMAs, one barrier per K-step.
+// When the grid would leave CUs idle (short M), K is split across
+// workgroups and the fp32 partials are summed by a second kernel in a fixed
+// order (bitwise reproducible).
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -267,19 +267,20 @@ __global__ __launch_bounds__(NT) void qmm_kernel(const QmmArgs a) {
 
 // ---- 32x32-MFMA tile kernel -------------------------------------------------
 //
-// y[BM x BN tile] with 4 waves in a 2 x 2 grid; a wave owns (BM/2) x (BN/2)
-// output elements as (BM/64) x (BN/64) v_mfma_f32_32x32x16_bf16 tiles (the
-// 256 x 256 tile keeps 256 fp32 accumulators per lane, in AGPRs).
+// y[BM x BN tile] with NWM x NWN waves (2 x 2, 2 x 4 or 4 x 2); a wave owns
+// (BM/NWM) x (BN/NWN) output elements as v_mfma_f32_32x32x16_bf16 tiles of
+// 32 x 32 (128 fp32 accumulators per lane at 128 x 64 per wave).
 //
 // Per 64-wide K-step, activations [BM][64] and dequantized weights [BN][64]
 // (bf16) sit in double-buffered LDS.  Rows are 128 bytes with the 16-byte
 // chunk c of row r stored at c ^ swz(r), swz(r) = (r ^ (r >> 3)) & 7, so the
 // 16 rows that one LDS cycle of a fragment read touches (same chunk) hit
 // distinct banks; with c ^ (r & 7) rows r and r + 8 collided (37% of the LDS
-// cycles were bank conflicts by SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE).  One K-step, one barrier: while the MFMAs of step ks run
-// from buffer ks&1, the wave dequantizes step ks+1 from registers into the
-// other buffer and then issues the global loads of step ks+2, a whole K-step
-// ahead of their first use.
+// cycles were bank conflicts by SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE).
+// While the MFMAs of step ks run from buffer ks&1, the wave dequantizes step
+// ks+1 from registers into the other buffer and then issues the global loads
+// of step ks+2, a whole K-step ahead of their first use; two barriers per
+// K-step (the loop below says which each one publishes).
 //
 // Memory requests are what the L1/TA sees per instruction, so every load is
 // shaped to touch few lines: activations as 8 lanes x 16 B per 128-byte row
