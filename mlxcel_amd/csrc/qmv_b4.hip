@@ -28,6 +28,10 @@
 // (bitwise reproducible).  Bounds-checked buffer loads return 0 past the end
 // of an operand, which covers ragged N, partial chunks and missing
 // activation rows without branches.
+// gather_qmm runs the same pass (b4_pass) per index entry, per expert
+// segment, per run of a sorted index list, or, in qmv_b4_search_kernel, per
+// expert (grid.y) over the entries a binary search of the sorted indices
+// finds for it.
 #include "common.hpp"
 #include "kernels.hpp"
 
