@@ -76,46 +76,6 @@ __device__ __forceinline__ int lower_bound_sorted(const uint32_t* idx, int strid
   return lo;
 }
 
-// [first entry whose expert is >= v, first entry whose expert is >= v + 1)
-// in the sorted index array, the two searches of lower_bound_sorted run in
-// lockstep so each step costs one load round; wave-uniform.
-__device__ __forceinline__ void sorted_run(const uint32_t* idx, int stride, int n, int clamp, int v, int lane,
-                                           int& first, int& end) {
-  int lo[2] = {0, 0}, hi[2] = {n, n}, res[2] = {n, n};
-  bool done[2] = {n <= 0, n <= 0};
-  while (!done[0] || !done[1]) {
-    int val[2], step[2];
-    bool in[2];
-#pragma unroll
-    for (int s = 0; s < 2; s++) {  // both loads in flight before either ballot
-      step[s] = (hi[s] - lo[s] + 63) / 64;
-      const int pos = lo[s] + lane * step[s];
-      in[s] = !done[s] && pos < hi[s];
-      val[s] = in[s] ? seg_index(idx, stride, pos, clamp, 0) : 0x7FFFFFFF;
-    }
-#pragma unroll
-    for (int s = 0; s < 2; s++) {
-      if (done[s]) continue;
-      const uint64_t below = __ballot(in[s] && val[s] < v + s);
-      const int c = __popcll(below), ns = __popcll(__ballot(in[s]));
-      if (step[s] == 1) {
-        res[s] = c < ns ? lo[s] + c : hi[s];
-        done[s] = true;
-      } else {
-        const int nlo = c > 0 ? lo[s] + (c - 1) * step[s] + 1 : lo[s];
-        const int nhi = c < ns ? lo[s] + c * step[s] : hi[s];
-        lo[s] = nlo;
-        hi[s] = nhi;
-        if (lo[s] >= hi[s]) {
-          res[s] = lo[s];
-          done[s] = true;
-        }
-      }
-    }
-  }
-  first = n <= 0 ? 0 : res[0];
-  end = n <= 0 ? 0 : res[1];
-}
 
 // ---- MFMA ------------------------------------------------------------------
 // v_mfma_f32_16x16x32_bf16: D[16x16] += A[16x32] * B[32x16], fp32 accumulate.
@@ -241,6 +201,81 @@ constexpr uint32_t kDeadOfs = 0x80000000u;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
+
+// [first entry whose expert is >= v, first entry whose expert is >= v + 1)
+// in the sorted index array, the two searches of lower_bound_sorted run in
+// lockstep so each step costs one load round; wave-uniform.  The entries are
+// read with bounds-checked buffer loads (no branch around a load, so the
+// wave waits for them only where it compares).  `issued` runs once, right
+// after the first round's loads are issued and before the wave waits for
+// them: vector loads complete in order, so loads it issues stay in flight
+// while the first round is consumed.
+struct NoHook {
+  __device__ void operator()() const {}
+};
+template <class Hook = NoHook>
+__device__ __forceinline__ void sorted_run(const uint32_t* idx, int stride, int n, int clamp, int v, int lane,
+                                           int& first, int& end, Hook&& issued = Hook{}) {
+  if (n <= 0) {
+    first = end = 0;
+    return;
+  }
+  const int st = stride > 1 ? stride : 1;
+  // n * st * 4 < 2^31: the callers' index arrays hold at most a few million entries
+  const __amdgpu_buffer_rsrc_t ir = buffer_rsrc(idx, (uint32_t)((int64_t)n * st * 4));
+  int lo[2] = {0, 0}, hi[2] = {n, n}, res[2] = {n, n};
+  bool done[2] = {false, false};
+  uint32_t raw[2];
+  int step[2];
+  bool in[2];
+  // Lanes past the range read 0 (dead offset) and are masked out of the
+  // ballots by `in`; the value itself is used unconditionally, so no branch
+  // (and no wait) forms around the load.
+  auto load_round = [&]() {
+#pragma unroll
+    for (int s = 0; s < 2; s++) {  // both loads in flight before either ballot
+      step[s] = (hi[s] - lo[s] + 63) / 64;
+      const int pos = lo[s] + lane * step[s];
+      in[s] = !done[s] && pos < hi[s];
+      raw[s] = __builtin_amdgcn_raw_buffer_load_b32(ir, in[s] ? (uint32_t)pos * (uint32_t)(st * 4) : kDeadOfs, 0, 0);
+    }
+  };
+  auto consume = [&](int s) {
+    const int val = (int)min(raw[s], (uint32_t)(clamp - 1));  // first use of the load
+    const uint64_t below = __ballot(in[s] && val < v + s);
+    const int c = __popcll(below), ns = __popcll(__ballot(in[s]));
+    if (step[s] == 1) {
+      res[s] = c < ns ? lo[s] + c : hi[s];
+      done[s] = true;
+    } else {
+      const int nlo = c > 0 ? lo[s] + (c - 1) * step[s] + 1 : lo[s];
+      const int nhi = c < ns ? lo[s] + c * step[s] : hi[s];
+      lo[s] = nlo;
+      hi[s] = nhi;
+      if (lo[s] >= hi[s]) {
+        res[s] = lo[s];
+        done[s] = true;
+      }
+    }
+  };
+  // first round peeled (both searches live), so the hook's loads sit between
+  // its loads and its comparisons in straight-line code
+  load_round();
+  __builtin_amdgcn_sched_barrier(0);
+  issued();
+  __builtin_amdgcn_sched_barrier(0);
+  consume(0);
+  consume(1);
+  while (!done[0] || !done[1]) {
+    load_round();
+#pragma unroll
+    for (int s = 0; s < 2; s++)
+      if (!done[s]) consume(s);
+  }
+  first = res[0];
+  end = res[1];
+}
+
 
 // c + a.lo * b.lo + a.hi * b.hi over bf16 pairs, fp32 accumulate
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {

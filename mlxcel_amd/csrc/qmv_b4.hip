@@ -62,12 +62,76 @@ __device__ __forceinline__ void mfma4_done(f32x4& d) { asm volatile("s_nop 7\n\t
 
 }  // namespace
 
+// A lane's weight pieces and their scale (and bias) codes for one pass.
+template <int RG, int CPW>
+struct B4Weights {
+  u32x4 wv[CPW][RG];
+  uint32_t sraw[CPW][RG], braw[CPW][RG];
+};
+
+// Issues the scale, bias and weight loads of the workgroup's 4 RG weight rows
+// of `expert` (lane pieces as in b4_pass); they do not depend on which
+// activation rows the pass takes.
+template <int FMT, int RG, int CPW>
+__device__ __forceinline__ void b4_load_weights(const QmvArgs& a, int gs_shift, int expert, int tid,
+                                                B4Weights<RG, CPW>& W) {
+  constexpr bool AFF = FMT != MXFP4;
+  constexpr int BITS = FMT == AFF8 ? 8 : 4;
+  constexpr int KL = 128 / BITS;
+  const int NW = blockDim.x >> 6;
+  const int lane = tid & 63, wave = tid >> 6, b = lane >> 2, j = lane & 3;
+  const int N = a.N, K = a.K;
+  const int row0 = blockIdx.x * (4 * RG);
+  const int nlc = K / KL;
+  const uint32_t RB = (uint32_t)nlc * 16u;
+  const int G = K >> gs_shift;
+  constexpr int ESZ = AFF ? 2 : 1;
+  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.w + (int64_t)expert * a.w_expert_stride, (uint32_t)N * RB);
+  const int64_t sb0 = (int64_t)expert * a.s_expert_stride;
+  const __amdgpu_buffer_rsrc_t sr =
+      buffer_rsrc(reinterpret_cast<const uint8_t*>(a.scales) + sb0 * ESZ, (uint32_t)(N * G * ESZ));
+  const __amdgpu_buffer_rsrc_t br =
+      buffer_rsrc(AFF ? (const void*)(a.biases + sb0) : a.scales, (uint32_t)(AFF ? N * G * 2 : 0));
+#pragma unroll
+  for (int c = 0; c < CPW; c++) {
+    const int pc = (wave + NW * c) * 16 + b;
+    const bool live = pc < nlc;
+#pragma unroll
+    for (int g = 0; g < RG; g++) {
+      const int n = row0 + 4 * g + j;
+      const uint32_t og = (uint32_t)(n * G + ((pc * KL) >> gs_shift));  // in groups
+      const uint32_t ob = (live && n < N) ? og * (uint32_t)ESZ : kDeadOfs;
+      if constexpr (AFF) {
+        W.sraw[c][g] = __builtin_amdgcn_raw_buffer_load_b16(sr, ob, 0, 0);
+        W.braw[c][g] = __builtin_amdgcn_raw_buffer_load_b16(br, ob, 0, 0);
+      } else {
+        W.sraw[c][g] = __builtin_amdgcn_raw_buffer_load_b8(sr, ob, 0, 0);
+        W.braw[c][g] = 0u;
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < CPW; c++) {
+    const int pc = (wave + NW * c) * 16 + b;
+    const bool live = pc < nlc;
+#pragma unroll
+    for (int g = 0; g < RG; g++) {
+      const int n = row0 + 4 * g + j;
+      const uint32_t o = (live && n < N) ? (uint32_t)n * RB + (uint32_t)pc * 16u : kDeadOfs;
+      // default cache policy: measured faster than the streaming hint here
+      W.wv[c][g] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, o, 0, 0));
+    }
+  }
+}
+
 // One pass: `count` activation rows starting at index entry / segment sidx
 // against the workgroup's 4 RG weight rows of `expert`.  `tid` is
 // threadIdx.x (see the expert-search kernel for why it is an argument).
-template <int FMT, int MS, int RG, int CPW>
+// PRE: W already holds (or has in flight) this pass's weights, loaded by
+// b4_load_weights; otherwise the pass loads them after its activations.
+template <int FMT, int MS, int RG, int CPW, bool PRE = false>
 __device__ __forceinline__ void b4_pass(const QmvArgs& a, int gs_shift, float* red, int sidx, int count,
-                                        int expert, int tid) {
+                                        int expert, int tid, B4Weights<RG, CPW>& W) {
   constexpr bool AFF = FMT != MXFP4;
   constexpr int BITS = FMT == AFF8 ? 8 : 4;
   constexpr int KL = 128 / BITS;  // K values per 16-byte piece
@@ -89,14 +153,8 @@ __device__ __forceinline__ void b4_pass(const QmvArgs& a, int gs_shift, float* r
   const int G = K >> gs_shift;
   constexpr int ESZ = AFF ? 2 : 1;
 
-  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.w + (int64_t)expert * a.w_expert_stride, (uint32_t)N * RB);
   const __amdgpu_buffer_rsrc_t xr =
       buffer_rsrc(a.x + (int64_t)xbatch * a.rps * K, (uint32_t)count * (uint32_t)K * 2u);
-  const int64_t sb0 = (int64_t)expert * a.s_expert_stride;
-  const __amdgpu_buffer_rsrc_t sr =
-      buffer_rsrc(reinterpret_cast<const uint8_t*>(a.scales) + sb0 * ESZ, (uint32_t)(N * G * ESZ));
-  const __amdgpu_buffer_rsrc_t br =
-      buffer_rsrc(AFF ? (const void*)(a.biases + sb0) : a.scales, (uint32_t)(AFF ? N * G * 2 : 0));
 
   // pieces of this lane: chunk (wave + NW c), piece b
   int pc[CPW];
@@ -118,32 +176,7 @@ __device__ __forceinline__ void b4_pass(const QmvArgs& a, int gs_shift, float* r
         const uint32_t o = live[c] ? (uint32_t)((4 * s + j) * K + pc[c] * KL) * 2u + (uint32_t)v * 16u : kDeadOfs;
         xv[c][s][v] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, o, 0, 0));
       }
-  uint32_t sraw[CPW][RG], braw[CPW][RG];
-#pragma unroll
-  for (int c = 0; c < CPW; c++)
-#pragma unroll
-    for (int g = 0; g < RG; g++) {
-      const int n = row0 + 4 * g + j;
-      const uint32_t og = (uint32_t)(n * G + ((pc[c] * KL) >> gs_shift));  // in groups
-      const uint32_t ob = (live[c] && n < N) ? og * (uint32_t)ESZ : kDeadOfs;
-      if constexpr (AFF) {
-        sraw[c][g] = __builtin_amdgcn_raw_buffer_load_b16(sr, ob, 0, 0);
-        braw[c][g] = __builtin_amdgcn_raw_buffer_load_b16(br, ob, 0, 0);
-      } else {
-        sraw[c][g] = __builtin_amdgcn_raw_buffer_load_b8(sr, ob, 0, 0);
-        braw[c][g] = 0u;
-      }
-    }
-  u32x4 wv[CPW][RG];
-#pragma unroll
-  for (int c = 0; c < CPW; c++)
-#pragma unroll
-    for (int g = 0; g < RG; g++) {
-      const int n = row0 + 4 * g + j;
-      const uint32_t o = (live[c] && n < N) ? (uint32_t)n * RB + (uint32_t)pc[c] * 16u : kDeadOfs;
-      // default cache policy: measured faster than the streaming hint here
-      wv[c][g] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, o, 0, 0));
-    }
+  if constexpr (!PRE) b4_load_weights<FMT, RG, CPW>(a, gs_shift, expert, tid, W);
   __builtin_amdgcn_sched_barrier(0);  // keep the arithmetic below the loads
 
   // ---- 2. activation operands and sums ---------------------------------------
@@ -181,7 +214,7 @@ __device__ __forceinline__ void b4_pass(const QmvArgs& a, int gs_shift, float* r
 #pragma unroll
     for (int g = 0; g < RG; g++) {
       uint32_t pr[KL / 2];  // bf16 pairs of this piece (AFF4 in "128 + q" pair order)
-      const u32x4 w = wv[c][g];
+      const u32x4 w = W.wv[c][g];
       if constexpr (FMT == AFF4) {
 #pragma unroll
         for (int q = 0; q < 4; q++) {
@@ -204,7 +237,7 @@ __device__ __forceinline__ void b4_pass(const QmvArgs& a, int gs_shift, float* r
         // (e8m0 0 and 255) are applied to D in fp32 instead, as MLX applies
         // the scale to the group sum: the products stay out of bf16's
         // subnormal range.
-        const uint32_t sb = sraw[c][g];
+        const uint32_t sb = W.sraw[c][g];
         if (sb - 1u < 254u) {
 #pragma unroll
           for (int q = 0; q < 4; q++) unpack_mxfp4_scaled(w[q], e8m0_to_f32(sb), &pr[4 * q]);
@@ -215,12 +248,12 @@ __device__ __forceinline__ void b4_pass(const QmvArgs& a, int gs_shift, float* r
       }
       float sc = 0.f, bp = 0.f;
       if constexpr (AFF) {
-        sc = bf16_bits_to_f32(sraw[c][g] & 0xFFFFu);
-        const float bi = bf16_bits_to_f32(braw[c][g] & 0xFFFFu);
+        sc = bf16_bits_to_f32(W.sraw[c][g] & 0xFFFFu);
+        const float bi = bf16_bits_to_f32(W.braw[c][g] & 0xFFFFu);
         bp = FMT == AFF4 ? __builtin_fmaf(-128.0f, sc, bi) : bi;
         if (!live[c] || row0 + 4 * g + j >= N) sc = bp = 0.f;  // dead pieces add exactly 0
       } else {
-        const uint32_t sb = sraw[c][g];
+        const uint32_t sb = W.sraw[c][g];
         sc = sb - 1u < 254u ? 1.0f : e8m0_to_f32(sb);  // scale still to apply to D
       }
       // The MS accumulator chains advance together (quad q of every row set
@@ -304,28 +337,37 @@ __global__ __launch_bounds__(512) void qmv_b4_kernel(const QmvArgs a, int gs_shi
            seg_index(a.rhs, a.rhs_stride, sidx + count, a.E, 0) == expert)
       count++;
   }
-  b4_pass<FMT, MS, RG, CPW>(a, gs_shift, red, sidx, count, expert, threadIdx.x);
+  B4Weights<RG, CPW> W;
+  b4_pass<FMT, MS, RG, CPW>(a, gs_shift, red, sidx, count, expert, threadIdx.x, W);
 }
 
 // Sorted gather with one activation row per entry, one workgroup row per
 // expert (blockIdx.y): the expert finds its entries [first, end) by binary
 // search in the sorted indices (as the reference's find_sorted_expert_run,
 // rocm/quantized/qmm.hip:4741-4915) and takes them 4 MS at a time, so its
-// weights stream once per 4 MS entries; experts without entries exit.  Every
-// per-lane value of a pass is derived from a thread index the compiler
-// cannot see through: hoisted out of the pass loop, the pass's addresses
-// would stay live across passes and cost a wave per SIMD.
+// weights stream once per 4 MS entries; experts without entries exit.  The
+// first pass's weights do not depend on the search: they are issued right
+// behind the search's first loads, so their stream overlaps the search and
+// the activation loads (for an expert without entries they are read for
+// nothing).  Every per-lane value of a later pass is derived from a thread
+// index the compiler cannot see through: hoisted out of the pass loop, the
+// pass's addresses would stay live across passes and cost a wave per SIMD.
 template <int FMT, int MS, int RG, int CPW>
 __global__ __launch_bounds__(512) void qmv_b4_search_kernel(const QmvArgs a, int gs_shift) {
   extern __shared__ __align__(16) float red[];
   const int expert = blockIdx.y;
   int first, end;
-  sorted_run(a.rhs, a.rhs_stride, a.total_rows, a.E, expert, threadIdx.x & 63, first, end);
-  for (int s = first; s < end; s += 4 * MS) {  // workgroup-uniform
-    if (s > first) __syncthreads();  // the previous pass has read its reduction
+  B4Weights<RG, CPW> W;
+  sorted_run(a.rhs, a.rhs_stride, a.total_rows, a.E, expert, threadIdx.x & 63, first, end,
+             [&]() { b4_load_weights<FMT, RG, CPW>(a, gs_shift, expert, threadIdx.x, W); });
+  if (first >= end) return;
+  b4_pass<FMT, MS, RG, CPW, true>(a, gs_shift, red, first, min(4 * MS, end - first), expert, threadIdx.x, W);
+  for (int s = first + 4 * MS; s < end; s += 4 * MS) {  // workgroup-uniform
+    __syncthreads();  // the previous pass has read its reduction
     int tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
-    b4_pass<FMT, MS, RG, CPW>(a, gs_shift, red, s, min(4 * MS, end - s), expert, tid);
+    B4Weights<RG, CPW> Wn;
+    b4_pass<FMT, MS, RG, CPW>(a, gs_shift, red, s, min(4 * MS, end - s), expert, tid, Wn);
   }
 }
 
