@@ -23,7 +23,7 @@ single-core CPU baseline (the oracle's restatement of MLX's CPU `_qmm_t`,
 overlays/cpu/mlx/backend/cpu/quantized.cpp:199-257).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
-                       [--extras copy,sweep,qmm,gather,moe,e2e,general]
+                       [--extras copy,c1,sweep,qmm,gather,moe,e2e,general]
        python bench.py --traffic-probe   (under rocprofv3 --pmc: copy calibration + gate and gather launches)
 """
 from __future__ import annotations
@@ -48,6 +48,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0  # dense
 MALL_BYTES = 256 << 20
 SETTLE_MS = 60.0  # untimed replays before each prefill measurement (see timed)
+GATE_REPLAYS = 12  # replays of the 8-launch gate graph behind `roofline` (>= 96 launches)
 # HBM bytes per gate launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on
 # `bench.py --traffic-probe`, each counter scaled by what it reads for a
 # device copy of exactly 256 MiB (FETCH_SIZE x 1.999799, WRITE_SIZE x 1.0):
@@ -188,8 +189,11 @@ def headline(steps, warmup, layers=8):
     # the replay stream (rocprofv3's kernel trace of the same command gives the
     # kernel bodies alone; the two agree within ~2%)
     gate_graph = capture(lambda: [mq.quantized_matmul(x, *mlp[l][0], True, 64, 4, out=out_g) for l in range(layers)])
-    reps = max(1, steps // layers)
-    gate_us = timed_graphs([gate_graph], reps, max(1, warmup // layers)) * 1e3 / layers
+    # a fixed >= 96 launches (>= 12 replays of the 8-launch graph) whatever
+    # --steps is, after ~60 ms of untimed replays, so the figure does not
+    # depend on the driver's step count
+    reps = max(GATE_REPLAYS, steps // layers)
+    gate_us = timed_graphs([gate_graph], reps, max(2, warmup // layers), SETTLE_MS) * 1e3 / layers
     # the same steps with gate and up as one quantized_matmul_multi launch
     # (two launches per step instead of three; same bytes)
     def multi_step(l):
@@ -199,7 +203,7 @@ def headline(steps, warmup, layers=8):
         mq.quantized_matmul(h, *down, True, 64, 4, out=out_d)
 
     multi_graph = capture(lambda: [multi_step(l) for l in range(layers)])
-    multi_ms = timed_graphs([multi_graph], reps, max(1, warmup // layers)) / layers
+    multi_ms = timed_graphs([multi_graph], reps, max(2, warmup // layers), SETTLE_MS) / layers
     multi_value = 3 * per_launch / (multi_ms * 1e-3) / 1e9
     return value, ms, ms * 1e3 / 3, per_launch, gate_us, mlp[0][0], multi_value, multi_ms
 
@@ -275,32 +279,72 @@ def qmv_sweep(iters=200):
 def qmm_prefill(iters=20):
     """Prefill GEMM: M in {512, 2048}, 4/8-bit, the
     Llama-3-8B gate/up and down shapes; TFLOPS = 2 M N K / time.  Beside
-    each, torch's bf16 GEMM (hipBLASLt) on the dequantized weights of the same
-    shape, timed the same way in the same run (`dense_bf16`): the library
-    GEMM the reference's prefill route calls after dequantizing."""
+    each, timed the same way in the same run:
+    - `ref_route`: the reference's CDNA prefill route on this device, the
+      quantized weights dequantized to bf16 (this library's bit-exact
+      `dequantize`, the role of affine_dequantize_packed_kernel,
+      rocm/quantized/qmm.hip:1376-1617) then torch's bf16 GEMM (hipBLASLt)
+      x @ W^T, both in one graph per weight copy;
+    - `dense_bf16`: the GEMM alone on already-dequantized [K, N] weights."""
     res = []
     for bits in (4, 8):
         for (N, K, name) in ((14336, 4096, "gate_up"), (4096, 14336, "down")):
             ws = [make_affine(N, K, bits, 64, 80 + c) for c in range(3)]
             # [K, N] contiguous bf16 copies of the dequantized weights
             wts = [mq.dequantize(*w, 64, bits).t().contiguous() for w in ws]
+            wdq = torch.empty(N, K, dtype=torch.bfloat16, device="cuda")  # the route's dequantized matrix
+
+            def ref_route(w, x, out):
+                mq.dequantize(*w, 64, bits, out=wdq)
+                torch.nn.functional.linear(x, wdq, out=out)
+
             for M in (512, 2048):
                 x = randn_bf16((M, K), 13)
                 out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
                 g = capture(lambda: [mq.quantized_matmul(x, *w, True, 64, bits, out=out) for w in ws])
                 ms = timed_graphs([g], max(1, iters // len(ws)), 1, SETTLE_MS) / len(ws)
                 del g
+                gr = capture(lambda: [ref_route(w, x, out) for w in ws])
+                ms_r = timed_graphs([gr], max(1, iters // len(ws)), 1, SETTLE_MS) / len(ws)
+                del gr
                 gd = capture(lambda: [torch.mm(x, wt, out=out) for wt in wts])
                 ms_d = timed_graphs([gd], max(1, iters // len(wts)), 1, SETTLE_MS) / len(wts)
                 del gd
-                tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-                tf_d = 2.0 * M * N * K / (ms_d * 1e-3) / 1e12
+                fl = 2.0 * M * N * K
+                tf, tf_r, tf_d = (fl / (t * 1e-3) / 1e12 for t in (ms, ms_r, ms_d))
                 res.append({"bits": bits, "shape": name, "M": M, "N": N, "K": K, "us": round(ms * 1e3, 1),
                             "TFLOPS": round(tf, 1), "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 3),
+                            "ref_route": {"us": round(ms_r * 1e3, 1), "TFLOPS": round(tf_r, 1),
+                                          "frac_mfma": round(tf_r / BF16_PEAK_TFLOPS, 3)},
+                            "vs_ref_route": round(ms_r / ms, 3),
                             "dense_bf16": {"us": round(ms_d * 1e3, 1), "TFLOPS": round(tf_d, 1),
                                            "frac_mfma": round(tf_d / BF16_PEAK_TFLOPS, 3)},
                             "vs_dense": round(ms_d / ms, 3)})
-            del ws, wts
+            del ws, wts, wdq
+    return res
+
+
+def c1_qmv(iters=400, cpu_budget_s=5.0, with_cpu=True):
+    """one 4-bit g64 qmv, N = K = 4096, M = 1 (the
+    reference's CPU-runnable case), on the GPU (weights rotated over enough
+    copies to overflow the MALL, one graph) and with the single-core oracle
+    `_qmm_t` on the host (a bounded sample of calls)."""
+    N = K = 4096
+    b = qmv_bytes(1, N, K, 4, 64)
+    assert b == 9_453_568
+    copies = max(2, math.ceil(2.4 * MALL_BYTES / qmv_bytes(0, N, K, 4, 64)))
+    ws = [make_affine(N, K, 4, 64, 150 + c) for c in range(copies)]
+    x = randn_bf16((1, K), 151)
+    out = torch.empty(1, N, dtype=torch.bfloat16, device="cuda")
+    g = capture(lambda: [mq.quantized_matmul(x, *w, True, 64, 4, out=out) for w in ws])
+    ms = timed_graphs([g], max(4, iters // copies), 2, SETTLE_MS) / copies
+    del g
+    res = {"workload": "C1: x [1,4096] bf16, w [4096,512] u32 (4-bit g64), transpose=true",
+           "bytes": b, "us": round(ms * 1e3, 3), "GBps": round(b / (ms * 1e-3) / 1e9, 1),
+           "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
+    if with_cpu:
+        res["cpu"] = cpu_time(ws[0], x, N, K, cpu_budget_s)
+    del ws
     return res
 
 
@@ -671,15 +715,37 @@ def e2e_decode(batches=(1, 16), prompt_len=512, steps=256, layers=36, separate_a
     return res
 
 
-def cpu_baseline(gate, budget_s=10.0):
-    """Single-core oracle `_qmm_t` on the gate projection (same bytes as the GPU launch)."""
+def host_facts():
+    """The host the CPU baseline runs on: logical CPUs (and those this
+    process may use), the CPU model, and how the oracle was compiled."""
     import oracle as orc
 
-    wq, s, b = gate
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count()
+    return {"nproc": os.cpu_count(), "nproc_usable": usable, "cpu_model": model, **orc.build_info()}
+
+
+def cpu_time(w, x, N, K, budget_s):
+    """Seconds per call of the single-core oracle `_qmm_t` (the restatement of
+    MLX's CPU path, overlays/cpu/mlx/backend/cpu/quantized.cpp:199-257) on
+    the weights `w` and activation row `x`, over calls filling `budget_s`."""
+    import oracle as orc
+
+    wq, s, b = w
     wq_h = wq.cpu().numpy()
     s_h = s.cpu().view(torch.int16).numpy().astype(np.uint16)
     b_h = b.cpu().view(torch.int16).numpy().astype(np.uint16)
-    x_h = orc.normal_bf16((1, 4096), 1.0, 99)
+    x_h = x.cpu().view(torch.int16).numpy().astype(np.uint16).reshape(1, K)
     orc.qmm_t_affine(x_h, wq_h, s_h, b_h, 64, 4)  # warm
     n, t0 = 0, time.perf_counter()
     while True:
@@ -689,10 +755,18 @@ def cpu_baseline(gate, budget_s=10.0):
         if el >= budget_s:
             break
     per = el / n
-    gbs = qmv_bytes(1, 14336, 4096, 4, 64) / per / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{n} calls of the gate projection (N=14336, K=4096, 4-bit g64, M=1), "
-                      f"{per * 1e3:.1f} ms/call, oracle restatement of MLX CPU _qmm_t (scalar, 1 thread)"}
+    return {"GBps": round(qmv_bytes(1, N, K, 4, 64) / per / 1e9, 3), "ms_per_call": round(per * 1e3, 2),
+            "calls": n, "cores": 1}
+
+
+def cpu_baseline(gate, budget_s=10.0):
+    """Single-core oracle `_qmm_t` on the gate projection (same bytes as the GPU launch)."""
+    x = randn_bf16((1, 4096), 99)
+    t = cpu_time(gate, x, 14336, 4096, budget_s)
+    return {"value": t["GBps"], "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{t['calls']} calls of the gate projection (N=14336, K=4096, 4-bit g64, M=1), "
+                      f"{t['ms_per_call']:.1f} ms/call, oracle restatement of MLX CPU _qmm_t (scalar, 1 thread)",
+            **host_facts()}
 
 
 def traffic_probe():
@@ -757,8 +831,8 @@ def main():
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--extras", default="copy,sweep,qmm,gather,moe,e2e,general",
-                    help="comma-separated extra sections: copy, sweep, qmm, gather, moe, e2e, general")
+    ap.add_argument("--extras", default="copy,c1,sweep,qmm,gather,moe,e2e,general",
+                    help="comma-separated extra sections: copy, c1, sweep, qmm, gather, moe, e2e, general")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run 5 copies of 256 MiB and 5 gate launches, eager, for rocprofv3 --pmc")
@@ -813,6 +887,8 @@ def main():
                                                     "launch (2 launches per step instead of 3)"}}
         if "copy" in want:
             extra["copy_ceiling_GBps"] = round(copy_ceiling(), 1)
+        if "c1" in want:
+            extra["c1_qmv_4096"] = c1_qmv(with_cpu=not args.no_cpu)
         if "sweep" in want:
             extra["qmv_sweep"] = qmv_sweep()
         if "qmm" in want:

@@ -97,7 +97,11 @@ typedef struct mlxq_array {
  * MLXQ_ENOMEM instead of allocating.  Callers that capture either run each
  * call shape once before the capture or reserve the workspace up front. */
 
-/* Grows `stream`'s workspace on the current device to at least `bytes`.  No
+/* Grows `stream`'s workspace on the current device to at least `bytes`, both
+ * the kernel scratch and the staging buffer that holds row-contiguous copies
+ * of strided or misaligned operands (each at least `bytes`), so a capture of
+ * calls needing at most that much of either allocates nothing.  Also resolves
+ * the device address of mlxq_quantized_matmul_noalloc's fixed scratch.  No
  * counterpart in the reference (MLX allocates inside each eval). */
 mlxq_status mlxq_workspace_reserve(size_t bytes, void* stream);
 
@@ -139,7 +143,10 @@ const char* mlxq_version(void);
  * and prefill; its prefill dequantizes the weights to float16, as the
  * reference's dequantize + GEMM route does); every other combination runs
  * the general kernel (float16 results there also round the dequantized
- * weights to float16). */
+ * weights to float16).  Operands of 2 GiB and more: with 2-D weights, x and
+ * the result run as row chunks below 2 GiB on the same kernels; a weight
+ * matrix (or its scales) of 2 GiB or more runs on the general kernel.
+ * Batched weights take any rows per batch. */
 mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w,
                                   const mlxq_array* scales, const mlxq_array* biases,
                                   bool transpose, int32_t group_size, int32_t bits,
@@ -220,7 +227,9 @@ mlxq_status mlxq_quantized_matmul_shape(const mlxq_array* x, const mlxq_array* w
  * `global_scale` (nvfp4 only in the reference) must be
  * NULL.  Index arrays may be any integer dtype and any strides
  * (broadcasting included).  Types, code widths, transposes and strides as
- * for mlxq_quantized_matmul; any rows per gathered matrix. */
+ * for mlxq_quantized_matmul; any rows per gathered matrix.  Any number of
+ * index entries: more than 65528 run as chunks of 65528 entries over flat
+ * copies of the indices in the stream's workspace. */
 mlxq_status mlxq_gather_qmm(const mlxq_array* x, const mlxq_array* w,
                             const mlxq_array* scales, const mlxq_array* biases,
                             const mlxq_array* lhs_indices, const mlxq_array* rhs_indices,

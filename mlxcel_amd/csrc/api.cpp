@@ -274,7 +274,24 @@ struct QmmSpec {
   Shape out_shape;
   bool transpose = true;
   bool fast = true;  // the specialised kernels take the call (else qmm_gen.hip)
+  bool small_w = true;  // each weight matrix and its scales below 2 GiB (buffer-resource kernels)
 };
+
+// The specialised kernels address each operand (or one weight matrix of it)
+// through a buffer resource with 32-bit byte offsets, and lanes without work
+// read at offset 2^31 (common.hpp kDeadOfs), so every such operand stays
+// below 2 GiB.  Larger ones take other routes: 2-D-weight calls run as row
+// chunks below the limit, gathers as chunks of index entries, and weight
+// matrices of 2 GiB or more the general kernel (64-bit indexing).
+constexpr int64_t kBufMax = (int64_t)1 << 31;
+
+// Index entries per gather launch (a grid dimension holds at most 65535); a
+// multiple of 8, so every chunk's output starts 16-byte aligned.
+constexpr int64_t kGatherChunk = 65528;
+
+// Elements of one dequantize / quantize call: the conversion kernels index in
+// 64 bits and take >= 8 elements per thread, and a launch covers < 2^32 threads.
+constexpr int64_t kElemMax = (int64_t)1 << 34;
 
 QmmSpec spec_quantized_matmul(const mlxq_array* xa, const mlxq_array* wa, const mlxq_array* sa,
                               const mlxq_array* ba, bool transpose, int32_t gs, int32_t bits,
@@ -432,7 +449,8 @@ struct Workspace {
   size_t retired_bytes = 0;
 };
 // key: (device, stream, slot); slot 0 holds kernel scratch, slot 1 the
-// row-contiguous copies of strided operands
+// row-contiguous copies of strided operands, slot 2 the flat index lists of
+// gathers run in chunks
 std::map<std::tuple<int, hipStream_t, int>, Workspace> g_ws;
 
 int current_device() {
@@ -684,9 +702,13 @@ void require_gen_support(const QmmSpec& sp, const mlxq_array* x, const mlxq_arra
 }
 
 // Route of a validated call: sets sp.fast, or refuses what no kernel covers.
-void choose_route(QmmSpec& sp, const mlxq_array* x, const mlxq_array* scales, const mlxq_array* biases,
-                  const char* tag) {
-  sp.fast = fast_route(sp, x, scales, biases) && sp.K <= ((int64_t)1 << 30) && sp.N <= ((int64_t)1 << 30);
+void choose_route(QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+                  const mlxq_array* biases, const char* tag) {
+  View wv{w}, sv{scales};
+  const int s_esz = std::max(dtype_size(scales->dtype), biases ? dtype_size(biases->dtype) : 0);
+  sp.small_w = wv.dim(-2) * wv.dim(-1) * 4 < kBufMax && sv.dim(-2) * sv.dim(-1) * s_esz < kBufMax;
+  sp.fast = fast_route(sp, x, scales, biases) && sp.small_w && sp.K <= ((int64_t)1 << 30) &&
+            sp.N <= ((int64_t)1 << 30);
   if (!sp.fast) require_gen_support(sp, x, scales, biases, tag);
 }
 
@@ -808,7 +830,7 @@ QmmSpec check_quantized_matmul(const mlxq_array* x, const mlxq_array* w, const m
                                const char* mode, const mlxq_array* out, const char* tag) {
   QmmSpec sp = spec_quantized_matmul(x, w, scales, biases, transpose, group_size, bits, mode);
   check_out(out, sp.out_shape, sp.out_dtype, tag);
-  choose_route(sp, x, scales, biases, tag);
+  choose_route(sp, x, w, scales, biases, tag);
   return sp;
 }
 
@@ -950,6 +972,49 @@ void run_gen(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const 
   a.out_elems = out_elems;
   hip_check(mlxq::qmm_gen_launch(a, p, tc, sp.transpose, nseg, stream), "qmm_gen launch");
   if (p.ks > 1) hip_check(mlxq::launch_gen_reduce(a.ws, out->data, out_elems, p.ks, tc, stream), "reduce launch");
+}
+
+// Batched weights on the general kernel: the default indices of gather_qmm
+// over the broadcast batch shape (x batches and weight matrices broadcast
+// against it), any rows per batch.
+void run_gen_batched(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+                     const mlxq_array* biases, mlxq_array* out, hipStream_t stream, const ScratchSrc& ss) {
+  View wv{w}, xv{x};
+  if (xv.ndim() <= 2) unsupported("quantized_matmul: batched w needs batched x");
+  const Shape ob(sp.out_shape.begin(), sp.out_shape.end() - 2);
+  if ((int)ob.size() > MLXQ_MAX_DIMS) unsupported("quantized_matmul: batch rank too large");
+  mlxq::IdxPrepArgs ip{};
+  ip.bnd = (int)ob.size();
+  int64_t B = 1;
+  for (int d = 0; d < ip.bnd; d++) {
+    ip.bshape[d] = ob[d];
+    B *= ob[d];
+  }
+  ip.B = B;
+  const Shape dx = default_index_shape(xv), dw = default_index_shape(wv);
+  bstrides_for(nullptr, dx, ob, ip.bstrides[0]);
+  bstrides_for(nullptr, dw, ob, ip.bstrides[1]);
+  ip.dtype[0] = ip.dtype[1] = MLXQ_UINT32;
+  int64_t X = 1, E = 1;
+  for (auto d : dx) X *= d;
+  for (auto d : dw) E *= d;
+  ip.clamp[0] = std::max<int64_t>(X, 1);
+  ip.clamp[1] = std::max<int64_t>(E, 1);
+  run_gen(sp, x, w, scales, biases, out, xv.dim(-2), B, X, E, &ip, stream, ss);
+}
+
+// Rows [r0, r0 + rc) of a row-contiguous operand with `cols` elements per
+// row, as a 2-D view.
+mlxq_array rows_view(const mlxq_array* a, int64_t r0, int64_t rc, int64_t cols) {
+  mlxq_array v{};
+  v.data = static_cast<char*>(a->data) + r0 * cols * dtype_size(a->dtype);
+  v.dtype = a->dtype;
+  v.ndim = 2;
+  v.shape[0] = rc;
+  v.shape[1] = cols;
+  v.strides[0] = cols;
+  v.strides[1] = 1;
+  return v;
 }
 
 // float16 decode (1-4 rows, 2-D weights): the row-streaming kernel's float16
@@ -1097,40 +1162,42 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
   const int64_t rows_total = View{out}.size() / std::max<int64_t>(sp.N, 1);
   if (rows_total == 0 || sp.N == 0) return;
   if (sp.K == 0) unsupported("quantized_matmul: K == 0");
+  if (View{w}.ndim() == 2) {
+    // Rows of x and out are independent: activations or results of 2 GiB
+    // and more run as row chunks below the limit, each on the same kernels
+    // (operands are row-contiguous here, after staging).
+    const int64_t per_row = std::max(sp.K * dtype_size(x->dtype), sp.N * dtype_size(out->dtype));
+    if (per_row >= kBufMax) unsupported("quantized_matmul: one row of x or of the result reaches 2 GiB");
+    if (rows_total * per_row >= kBufMax) {
+      // equal chunks (a small last one would plan differently, e.g. split K),
+      // multiples of 256 rows where possible, so chunk starts stay 16-byte aligned
+      const int64_t max_rows = (kBufMax - 1) / per_row;
+      const int64_t n = (rows_total + max_rows - 1) / max_rows;
+      int64_t chunk = (rows_total + n - 1) / n;
+      if (((chunk + 255) & ~(int64_t)255) <= max_rows) chunk = (chunk + 255) & ~(int64_t)255;
+      else if (max_rows >= 256) chunk = max_rows & ~(int64_t)255;
+      else chunk = max_rows;
+      for (int64_t r0 = 0; r0 < rows_total; r0 += chunk) {
+        const int64_t rc = std::min(chunk, rows_total - r0);
+        mlxq_array xc = rows_view(x, r0, rc, sp.K), oc = rows_view(out, r0, rc, sp.N);
+        run_quantized_matmul(sp, &xc, w, scales, biases, &oc, stream, ss);
+      }
+      return;
+    }
+  }
   if (!sp.fast) {
-    View wv{w}, xv{x};
-    if (wv.ndim() == 2 && try_mr_f16(sp, x, w, scales, biases, out, rows_total, stream)) return;
-    if (wv.ndim() == 2 && try_rs_f16(sp, x, w, scales, biases, out, rows_total, stream)) return;
-    if (wv.ndim() == 2 && try_mid_f16(sp, x, w, scales, biases, out, rows_total, stream, ss)) return;
-    if (wv.ndim() == 2 && try_qmm_f16(sp, x, w, scales, biases, out, rows_total, stream, ss)) return;
+    View wv{w};
+    const bool dense = wv.ndim() == 2 && sp.small_w;  // the float16 routes use buffer resources too
+    if (dense && try_mr_f16(sp, x, w, scales, biases, out, rows_total, stream)) return;
+    if (dense && try_rs_f16(sp, x, w, scales, biases, out, rows_total, stream)) return;
+    if (dense && try_mid_f16(sp, x, w, scales, biases, out, rows_total, stream, ss)) return;
+    if (dense && try_qmm_f16(sp, x, w, scales, biases, out, rows_total, stream, ss)) return;
     if (wv.ndim() == 2) {
       // every leading dim of x folds into rows
       run_gen(sp, x, w, scales, biases, out, rows_total, 1, 1, 1, nullptr, stream, ss);
       return;
     }
-    // batched weights: the default indices of gather_qmm over the broadcast
-    // batch shape (x batches and weight matrices broadcast against it)
-    if (xv.ndim() <= 2) unsupported("quantized_matmul: batched w needs batched x");
-    const Shape ob(sp.out_shape.begin(), sp.out_shape.end() - 2);
-    if ((int)ob.size() > MLXQ_MAX_DIMS) unsupported("quantized_matmul: batch rank too large");
-    mlxq::IdxPrepArgs ip{};
-    ip.bnd = (int)ob.size();
-    int64_t B = 1;
-    for (int d = 0; d < ip.bnd; d++) {
-      ip.bshape[d] = ob[d];
-      B *= ob[d];
-    }
-    ip.B = B;
-    const Shape dx = default_index_shape(xv), dw = default_index_shape(wv);
-    bstrides_for(nullptr, dx, ob, ip.bstrides[0]);
-    bstrides_for(nullptr, dw, ob, ip.bstrides[1]);
-    ip.dtype[0] = ip.dtype[1] = MLXQ_UINT32;
-    int64_t X = 1, E = 1;
-    for (auto d : dx) X *= d;
-    for (auto d : dw) E *= d;
-    ip.clamp[0] = std::max<int64_t>(X, 1);
-    ip.clamp[1] = std::max<int64_t>(E, 1);
-    run_gen(sp, x, w, scales, biases, out, xv.dim(-2), B, X, E, &ip, stream, ss);
+    run_gen_batched(sp, x, w, scales, biases, out, stream, ss);
     return;
   }
 
@@ -1256,10 +1323,14 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
     Shape wb(wsh.begin(), wsh.end() - 2);
     Shape ob(sp.out_shape.begin(), sp.out_shape.end() - 2);
     Shape xb = xv.ndim() > 2 ? Shape(xsh.begin(), xsh.end() - 2) : Shape{};
-    if (xv.ndim() <= 2 || wb != ob || xb != ob)
-      unsupported("quantized_matmul: batched w needs x with the same batch shape (use gather_qmm to broadcast)");
+    // Batches that broadcast, or more rows per batch than the decode kernels
+    // stage (the reference takes any M: qmm.hip:3606-3620, 2362-2766), run
+    // on the general kernel over the default gather indices.
+    if (xv.ndim() <= 2 || wb != ob || xb != ob || xv.dim(-2) > cap) {
+      run_gen_batched(sp, x, w, scales, biases, out, stream, ss);
+      return;
+    }
     const int64_t M = xv.dim(-2);
-    if (M > cap) unsupported("quantized_matmul: batched w with more than " + std::to_string(cap) + " rows per batch");
     int64_t nb = 1;
     for (auto d : wb) nb *= d;
     a.E = (int)nb;
@@ -1270,6 +1341,402 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
     a.total_rows = (int)rows_total;
     run_qmv(sp, a, (int)nb, (int)M, stream, ss);
   }
+}
+
+const char* mode_name(Mode m) {
+  return m == AFFINE ? "affine" : (m == MXFP4_M ? "mxfp4" : (m == MXFP8_M ? "mxfp8" : "nvfp4"));
+}
+
+// A row-contiguous operand as [batch, rows, cols] (its leading dims folded).
+mlxq_array as3(const mlxq_array* a, int64_t batch) {
+  mlxq_array v = *a;
+  View av{a};
+  v.ndim = 3;
+  v.shape[0] = batch;
+  v.shape[1] = av.dim(-2);
+  v.shape[2] = av.dim(-1);
+  v.strides[2] = 1;
+  v.strides[1] = v.shape[2];
+  v.strides[0] = v.shape[1] * v.shape[2];
+  return v;
+}
+
+// A contiguous 1-D uint32 array of n entries.
+mlxq_array u32_view(uint32_t* p, int64_t n) {
+  mlxq_array v{};
+  v.data = p;
+  v.dtype = MLXQ_UINT32;
+  v.ndim = 1;
+  v.shape[0] = n;
+  v.strides[0] = 1;
+  return v;
+}
+
+void gather_run(GatherSpec& g, const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+                const mlxq_array* biases, const mlxq_array* lhs_indices, const mlxq_array* rhs_indices,
+                bool sorted_indices, mlxq_array* out, hipStream_t stream);
+
+// A gather with more index entries than one launch covers (the reference's
+// dispatch has no cap, qmm.hip:6590; nor its CPU gather, quantized.cpp:764-813):
+// the flat uint32 indices of every entry (clamped by index_prep) go to the
+// stream's workspace slot 2, then the entries run in chunks of kGatherChunk,
+// each a gather with contiguous index arrays over the same x and w.  A chunk
+// of a sorted rhs is sorted, and where the default lhs maps entry b to x batch
+// b the chunk keeps the default over the matching slice of x, so the sorted
+// routes stay open.  The chunks' own scratch lives in slots 0 and 1.
+void gather_chunked(const GatherSpec& g, const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+                    const mlxq_array* biases, const mlxq_array* lhs_indices, bool sorted_indices,
+                    mlxq_array* out, hipStream_t stream, mlxq::IdxPrepArgs ip, int64_t B, int64_t X, int64_t E) {
+  const QmmSpec& sp = g.q;
+  View xv{x};
+  const int64_t M = xv.dim(-2);
+  if (B >= ((int64_t)1 << 30)) unsupported("gather_qmm: more than 2^30 index entries");
+  uint32_t* flat = static_cast<uint32_t*>(
+      workspace(current_device(), stream, (size_t)B * 2 * sizeof(uint32_t), ScratchSrc{}, 2));
+  ip.out[0] = flat;
+  ip.out[1] = flat + B;
+  hip_check(mlxq::launch_index_prep(ip, stream), "index_prep launch");
+  const bool lhs_default = !lhs_indices && default_index_shape(xv) == g.idx_shape;
+  const mlxq_array x3 = as3(x, X), w3 = as3(w, E), s3 = as3(scales, E);
+  const mlxq_array b3 = biases ? as3(biases, E) : mlxq_array{};
+  const int64_t xrow = M * sp.K * dtype_size(x->dtype), orow = M * sp.N * dtype_size(out->dtype);
+  for (int64_t c0 = 0; c0 < B; c0 += kGatherChunk) {
+    const int64_t cb = std::min(kGatherChunk, B - c0);
+    mlxq_array li = u32_view(flat + c0, cb), ri = u32_view(flat + B + c0, cb);
+    mlxq_array xc = x3;
+    if (lhs_default) {
+      xc.data = static_cast<char*>(x->data) + c0 * xrow;
+      xc.shape[0] = cb;
+    }
+    mlxq_array oc = as3(out, cb);
+    oc.shape[1] = M;
+    oc.shape[2] = sp.N;
+    oc.strides[2] = 1;
+    oc.strides[1] = sp.N;
+    oc.strides[0] = M * sp.N;
+    oc.data = static_cast<char*>(out->data) + c0 * orow;
+    const mlxq_array* lc = lhs_default ? nullptr : &li;
+    GatherSpec gc = spec_gather(&xc, &w3, &s3, biases ? &b3 : nullptr, lc, &ri, sp.transpose, sp.gs, sp.bits,
+                                mode_name(sp.mode), nullptr);
+    choose_route(gc.q, &xc, &w3, &s3, biases ? &b3 : nullptr, "gather_qmm");
+    gather_run(gc, &xc, &w3, &s3, biases ? &b3 : nullptr, lc, &ri, sorted_indices, &oc, stream);
+  }
+}
+
+// One gather_qmm call on staged (row-contiguous, 16-byte aligned) operands.
+void gather_run(GatherSpec& g, const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+                const mlxq_array* biases, const mlxq_array* lhs_indices, const mlxq_array* rhs_indices,
+                bool sorted_indices, mlxq_array* out, hipStream_t stream) {
+  QmmSpec& sp = g.q;
+  View xv{x}, wv{w}, sv{scales};
+  const int64_t M = xv.dim(-2);
+  int64_t B = 1;
+  for (auto d : g.idx_shape) B *= d;
+  if (B == 0 || M == 0 || sp.N == 0) return;
+  if ((int)g.idx_shape.size() > MLXQ_MAX_DIMS) unsupported("gather_qmm: index rank too large");
+  const int64_t X = xv.size() / std::max<int64_t>(M * sp.K, 1);
+  const int64_t E = wv.size() / std::max<int64_t>(wv.dim(-2) * wv.dim(-1), 1);
+
+  // flat uint32 lhs/rhs over the broadcast index shape, in the workspace tail
+  mlxq::IdxPrepArgs ip{};
+  ip.bnd = (int)g.idx_shape.size();
+  for (int d = 0; d < ip.bnd; d++) ip.bshape[d] = g.idx_shape[d];
+  ip.B = B;
+  const mlxq_array* idx[2] = {lhs_indices, rhs_indices};
+  const Shape dsh[2] = {default_index_shape(xv), default_index_shape(wv)};
+  for (int s = 0; s < 2; s++) {
+    ip.data[s] = idx[s] ? idx[s]->data : nullptr;
+    ip.dtype[s] = idx[s] ? idx[s]->dtype : MLXQ_UINT32;
+    bstrides_for(idx[s], dsh[s], g.idx_shape, ip.bstrides[s]);
+  }
+  ip.clamp[0] = std::max<int64_t>(X, 1);
+  ip.clamp[1] = std::max<int64_t>(E, 1);
+  if (B > kGatherChunk) {
+    gather_chunked(g, x, w, scales, biases, lhs_indices, sorted_indices, out, stream, ip, B, X, E);
+    return;
+  }
+
+  if (!sp.fast) {
+    run_gen(sp, x, w, scales, biases, out, M, B, X, E, &ip, stream, ScratchSrc{});
+    return;
+  }
+  const int fmt = fmt_of(sp.mode, sp.bits);
+  const int cap = mlxq::qmv_max_rows(fmt, sp.gs);
+  if (M > cap) {
+    // more rows per gathered matrix than the decode kernels stage: the
+    // general kernel tiles any row count
+    run_gen(sp, x, w, scales, biases, out, M, B, X, E, &ip, stream, ScratchSrc{});
+    return;
+  }
+
+  const int dev = current_device();
+  const DevInfo di = device_info(dev);
+
+  // Expert-sorted mxfp4 gathers with one row per entry and >= 4 rows per
+  // expert on average (mlxcel's sorted MoE path, gpt_oss.rs:317-345): one
+  // kernel streams each expert's weights once per 64 of its rows, finding
+  // the rows by binary search in the sorted indices (qmm_group.hip); fewer
+  // rows per expert run as segments of up to 4 entries (below).  Like the reference's sorted route, it
+  // relies on sorted_indices being true.  MLXQ_GATHER_SORTED=0 turns it off.
+  if (sorted_indices && M == 1 && fmt == mlxq::MXFP4 && B >= 32 && B >= 4 * E &&
+      knobs().gather_sorted != 0) {
+    const DirectIdx dl = direct_index(lhs_indices, dsh[0], g.idx_shape);
+    const DirectIdx dr = direct_index(rhs_indices, dsh[1], g.idx_shape);
+    const mlxq::QmmGroupPlan gp = mlxq::qmm_group_plan(fmt, sp.N, sp.K, E, B);
+    if (gp.ok && dr.ok && dr.p && dl.ok && !dl.p && dl.div == 1) {
+      mlxq::QmmGroupArgs q{};
+      q.x = static_cast<const uint16_t*>(x->data);
+      q.w = static_cast<const uint32_t*>(w->data);
+      q.scales = static_cast<const uint8_t*>(scales->data);
+      q.out = static_cast<uint16_t*>(out->data);
+      q.rhs = dr.p;
+      q.rhs_stride = dr.stride;
+      q.N = (int)sp.N;
+      q.K = (int)sp.K;
+      q.E = (int)E;
+      q.B = (int)B;
+      hip_check(mlxq::qmm_group_launch(q, gp, stream), "gather group launch");
+      return;
+    }
+  }
+
+  // Many rows per expert (MoE prefill, large batches): group rows by expert
+  // on the device, then one GEMM tile reads each expert's weights once per
+  // tile of rows (qmm.hip), instead of once per index entry.  Auto when the
+  // entries average >= 8 rows per touched expert; MLXQ_GATHER_GROUP=0|1
+  // forces the choice (A/B switch for tests).
+  const int grp_env = knobs().gather_group;
+  const int64_t rows = B * M;
+  const bool want_group = grp_env == 1 || (grp_env != 0 && rows >= 8 * std::min<int64_t>(E, B));
+  if (E <= mlxq::kGroupMaxExperts && want_group) {
+    const int64_t per_expert = rows / std::max<int64_t>(1, std::min<int64_t>(E, B));
+    const mlxq::QmmPlan qp =
+        mlxq::qmm_plan_grouped(fmt, sp.gs, sp.N, sp.K, per_expert <= 64 ? 3 : (per_expert <= 128 ? 2 : 0));
+    const bool use_qmm = qp.ok && X * M * sp.K * 2 < ((int64_t)1 << 31);
+    // K not a multiple of 64: the MFMA skinny kernel over the same grouping
+    const int cap_rows = use_qmm ? qp.rows_per_tile : (int)std::min<int64_t>(cap, rows);
+    const int64_t maxseg = rows / cap_rows + std::min<int64_t>(E, B) + 1;
+    if (maxseg > 65535) unsupported("gather_qmm: too many expert segments for one launch");
+    mlxq::QmvPlan p;
+    if (!use_qmm) {
+      int nw, pf;
+      qmv_shape_choice(sp.N, sp.K, nw, pf);
+      p = mlxq::qmv_plan(fmt, sp.gs, sp.N, sp.K, cap_rows, (int)maxseg, di.cus, nw, pf);
+      if (p.lds > mlxq::kQmvLdsMax) unsupported("gather_qmm: activation tile does not fit in LDS");
+    }
+    auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    const size_t o_x = al((size_t)B * 2 * sizeof(uint32_t));
+    const size_t o_o = o_x + al((size_t)rows * sizeof(uint32_t));
+    const size_t o_seg = o_o + al((size_t)rows * sizeof(uint32_t));
+    const size_t o_n = o_seg + al((size_t)maxseg * 3 * sizeof(uint32_t));
+    const size_t o_part = o_n + 256;
+    const size_t part = (!use_qmm && p.ks > 1) ? (size_t)p.ks * rows * sp.N * sizeof(float) : 0;
+    char* base = static_cast<char*>(workspace(dev, stream, o_part + part));
+    uint32_t* flat = reinterpret_cast<uint32_t*>(base);
+    ip.out[0] = flat;
+    ip.out[1] = flat + B;
+    hip_check(mlxq::launch_index_prep(ip, stream), "index_prep launch");
+    mlxq::GroupArgs ga{};
+    ga.lhs = flat;
+    ga.rhs = flat + B;
+    ga.B = (int)B;
+    ga.M = (int)M;
+    ga.E = (int)E;
+    ga.cap = cap_rows;
+    ga.xrows = reinterpret_cast<uint32_t*>(base + o_x);
+    ga.orows = reinterpret_cast<uint32_t*>(base + o_o);
+    ga.seg = reinterpret_cast<uint32_t*>(base + o_seg);
+    ga.nseg = reinterpret_cast<uint32_t*>(base + o_n);
+    hip_check(mlxq::launch_group_by_expert(ga, stream), "group launch");
+    if (use_qmm) {
+      mlxq::QmmArgs q{};
+      q.x = static_cast<const uint16_t*>(x->data);
+      q.w = static_cast<const uint32_t*>(w->data);
+      q.scales = scales->data;
+      q.biases = biases ? static_cast<const uint16_t*>(biases->data) : nullptr;
+      q.out = static_cast<uint16_t*>(out->data);
+      q.M = (int)rows;
+      q.x_rows = (int)(X * M);
+      q.N = (int)sp.N;
+      q.K = (int)sp.K;
+      int shift = 0;
+      while ((1 << shift) < sp.gs) shift++;
+      q.gs_shift = shift;
+      q.ksplit = 1;
+      q.ksteps_per_split = qp.ksteps_per_split;
+      q.seg = ga.seg;
+      q.nseg_dev = ga.nseg;
+      q.xrows = ga.xrows;
+      q.orows = ga.orows;
+      q.w_expert_stride = wv.dim(-2) * wv.dim(-1);
+      q.s_expert_stride = sv.dim(-2) * sv.dim(-1);
+      mlxq::QmmPlan gp = qp;
+      gp.tiles_m = (int)maxseg;
+      hip_check(mlxq::qmm_launch(fmt, q, gp, stream), "gather qmm launch");
+      return;
+    }
+    mlxq::QmvArgs a{};
+    a.x = static_cast<const uint16_t*>(x->data);
+    a.w = static_cast<const uint32_t*>(w->data);
+    a.scales = scales->data;
+    a.biases = biases ? static_cast<const uint16_t*>(biases->data) : nullptr;
+    a.out = static_cast<uint16_t*>(out->data);
+    a.N = (int)sp.N;
+    a.K = (int)sp.K;
+    a.E = (int)E;
+    a.X = (int)X;
+    a.w_expert_stride = wv.dim(-2) * wv.dim(-1);
+    a.s_expert_stride = sv.dim(-2) * sv.dim(-1);
+    a.rps = cap_rows;
+    a.total_rows = (int)rows;
+    a.out_rows = (int)rows;
+    a.rows_lds = cap_rows;
+    a.ks = p.ks;
+    a.kst_per_wg = p.kst_per_wg;
+    if (p.ks > 1) a.ws = reinterpret_cast<float*>(base + o_part);
+    a.seg = ga.seg;
+    a.nseg_dev = ga.nseg;
+    a.xrows = ga.xrows;
+    a.orows = ga.orows;
+    hip_check(mlxq::qmv_launch(fmt, sp.gs, a, (int)maxseg, p, stream), "gather qmv launch");
+    return;
+  }
+
+  // Sorted gathers with one row per entry (the expert-sorted MoE decode of
+  // mlxcel's callers): on the block-MFMA kernel, one workgroup row per
+  // expert finds the expert's entries by binary search and streams its
+  // weights once per 4 of them (MLXQ_GATHER_RUNS=2, the default; it relies
+  // on the order, as the reference's sorted route does).  Otherwise
+  // (MLXQ_GATHER_RUNS=1, or the row-streaming kernel) runs of equal
+  // consecutive experts, split at multiples of 4, correct for any order;
+  // MLXQ_GATHER_RUNS=0: one segment per entry.
+  const int r_req = knobs().qmv_r;
+  {
+    const DirectIdx dl = direct_index(lhs_indices, dsh[0], g.idx_shape);
+    const DirectIdx dr = direct_index(rhs_indices, dsh[1], g.idx_shape);
+    if (sorted_indices && M == 1 && B >= 8 && dr.ok && dr.p && dl.ok && !dl.p && dl.div == 1 &&
+        knobs().gather_runs != 0) {
+      // 4 entries at a time on the block-MFMA kernel (gpt-oss MoE shapes,
+      // T=16: runs of 4 were 9% faster than one segment per entry, runs of
+      // 8 or 16 slower; the row-streaming kernel with the expert search was
+      // 13% slower than the block-MFMA one), else on the row-streaming kernel
+      const mlxq::QmvB4Plan bp = mlxq::qmv_b4_plan(fmt, sp.gs, sp.N, sp.K, 4, 0, 0);
+      const mlxq::QmvRsPlan rp = bp.ok ? mlxq::QmvRsPlan{} : mlxq::qmv_rs_plan(fmt, sp.gs, sp.N, sp.K, 4, r_req);
+      if (bp.ok || rp.ok) {
+        mlxq::QmvArgs a{};
+        a.x = static_cast<const uint16_t*>(x->data);
+        a.w = static_cast<const uint32_t*>(w->data);
+        a.scales = scales->data;
+        a.biases = biases ? static_cast<const uint16_t*>(biases->data) : nullptr;
+        a.out = static_cast<uint16_t*>(out->data);
+        a.rhs = dr.p;
+        a.rhs_stride = dr.stride;
+        a.lhs_stride = 1;
+        a.lhs_div = 1;
+        a.N = (int)sp.N;
+        a.K = (int)sp.K;
+        a.E = (int)E;
+        a.X = (int)X;
+        a.w_expert_stride = wv.dim(-2) * wv.dim(-1);
+        a.s_expert_stride = sv.dim(-2) * sv.dim(-1);
+        a.rps = 1;
+        a.total_rows = (int)B;
+        a.out_rows = (int)B;
+        a.rows_lds = 1;
+        a.runs = 4;
+        if (bp.ok && knobs().gather_runs >= 2 && E <= B) {
+          // one workgroup row per expert, its entries found by binary search
+          // (with more experts than entries most rows would only search
+          // and exit: runs then)
+          a.runs = -1;
+          hip_check(mlxq::qmv_b4_launch(fmt, sp.gs, a, (int)E, bp, stream), "gather qmv launch");
+        } else if (bp.ok) {
+          hip_check(mlxq::qmv_b4_launch(fmt, sp.gs, a, (int)B, bp, stream), "gather qmv launch");
+        } else {
+          hip_check(mlxq::qmv_rs_launch(fmt, sp.gs, a, (int)B, rp, stream), "gather qmv launch");
+        }
+        return;
+      }
+    }
+  }
+
+  const Skinny kind = skinny_choice((int)M, fmt, sp.K);
+  const mlxq::QmvFrPlan fp =
+      kind == Skinny::FR ? mlxq::qmv_fr_plan(fmt, sp.gs, sp.N, sp.K, (int)M, r_req) : mlxq::QmvFrPlan{};
+  const mlxq::QmvB4Plan bp =
+      kind == Skinny::B4 ? mlxq::qmv_b4_plan(fmt, sp.gs, sp.N, sp.K, (int)M, knobs().b4_rg,
+                                             knobs().b4_cpw)
+                         : mlxq::QmvB4Plan{};
+  const mlxq::QmvRsPlan rp =
+      (kind == Skinny::RS || (kind == Skinny::FR && !fp.ok) || (kind == Skinny::B4 && !bp.ok && M <= 4))
+          ? mlxq::qmv_rs_plan(fmt, sp.gs, sp.N, sp.K, (int)M, r_req)
+          : mlxq::QmvRsPlan{};
+  const bool use_rs = fp.ok || rp.ok || bp.ok;
+  int nw, pf;
+  qmv_shape_choice(sp.N, sp.K, nw, pf);
+  mlxq::QmvPlan p;
+  if (!use_rs) {
+    p = mlxq::qmv_plan(fmt, sp.gs, sp.N, sp.K, (int)M, (int)B, di.cus, nw, pf);
+    if (p.lds > mlxq::kQmvLdsMax) unsupported("gather_qmm: activation tile does not fit in LDS");
+  }
+  // indices the kernels can read in place skip the index_prep launch
+  const DirectIdx dl = direct_index(lhs_indices, dsh[0], g.idx_shape);
+  const DirectIdx dr = direct_index(rhs_indices, dsh[1], g.idx_shape);
+  const bool direct = dl.ok && dr.ok && dr.div == 1 && knobs().gather_direct != 0;
+  const size_t idx_bytes = direct ? 0 : ((size_t)B * 2 * sizeof(uint32_t) + 255) & ~(size_t)255;
+  const size_t part_bytes = p.ks > 1 ? (size_t)p.ks * B * M * sp.N * sizeof(float) : 0;
+  char* wsb = nullptr;
+  if (idx_bytes + part_bytes > 0) wsb = static_cast<char*>(workspace(dev, stream, idx_bytes + part_bytes));
+  const uint32_t* lhs_p = dl.p;
+  const uint32_t* rhs_p = dr.p;
+  int lhs_stride = dl.stride, rhs_stride = dr.stride, lhs_div = dl.div;
+  if (!direct) {
+    uint32_t* flat = reinterpret_cast<uint32_t*>(wsb);
+    ip.out[0] = flat;
+    ip.out[1] = flat + B;
+    hip_check(mlxq::launch_index_prep(ip, stream), "index_prep launch");
+    lhs_p = flat;
+    rhs_p = flat + B;
+    lhs_stride = rhs_stride = lhs_div = 1;
+  }
+
+  mlxq::QmvArgs a{};
+  a.x = static_cast<const uint16_t*>(x->data);
+  a.w = static_cast<const uint32_t*>(w->data);
+  a.scales = scales->data;
+  a.biases = biases ? static_cast<const uint16_t*>(biases->data) : nullptr;
+  a.out = static_cast<uint16_t*>(out->data);
+  a.lhs = lhs_p;
+  a.rhs = rhs_p;
+  a.lhs_stride = lhs_stride;
+  a.rhs_stride = rhs_stride;
+  a.lhs_div = lhs_div;
+  a.N = (int)sp.N;
+  a.K = (int)sp.K;
+  a.E = (int)E;
+  a.X = (int)X;
+  a.w_expert_stride = wv.dim(-2) * wv.dim(-1);
+  a.s_expert_stride = sv.dim(-2) * sv.dim(-1);
+  a.rps = (int)M;
+  a.total_rows = (int)(B * M);
+  a.out_rows = (int)(B * M);
+  a.rows_lds = (int)M;
+  if (fp.ok) {
+    hip_check(mlxq::qmv_fr_launch(fmt, sp.gs, a, (int)B, fp, stream), "gather qmv launch");
+    return;
+  }
+  if (bp.ok) {
+    hip_check(mlxq::qmv_b4_launch(fmt, sp.gs, a, (int)B, bp, stream), "gather qmv launch");
+    return;
+  }
+  if (rp.ok) {
+    hip_check(mlxq::qmv_rs_launch(fmt, sp.gs, a, (int)B, rp, stream), "gather qmv launch");
+    return;
+  }
+  a.ks = p.ks;
+  a.kst_per_wg = p.kst_per_wg;
+  if (p.ks > 1) a.ws = reinterpret_cast<float*>(wsb + idx_bytes);
+  hip_check(mlxq::qmv_launch(fmt, sp.gs, a, (int)B, p, stream), "gather qmv launch");
 }
 
 }  // namespace
@@ -1329,11 +1796,18 @@ mlxq_status mlxq_workspace_reserve(size_t bytes, void* stream_) {
   return guarded([&] {
     hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
     const int dev = current_device();
+    // the no-allocation entry point's scratch address, resolved here too so a
+    // caller that reserves before a capture never resolves it under capture
+    void* fixed = nullptr;
+    hip_check(mlxq::static_scratch(dev, &fixed), "hipGetSymbolAddress(scratch)");
     std::lock_guard<std::mutex> lk(g_mu);
-    Workspace& w = g_ws[{dev, stream, 0}];
-    if (w.bytes >= bytes) return;
-    if (stream_capturing(stream)) unsupported("mlxq_workspace_reserve: the stream is being captured");
-    grow_workspace(w, bytes);
+    // kernel scratch (slot 0) and the staging copies of strided operands (slot 1)
+    for (int slot = 0; slot < 2; slot++) {
+      Workspace& w = g_ws[{dev, stream, slot}];
+      if (w.bytes >= bytes) continue;
+      if (stream_capturing(stream)) unsupported("mlxq_workspace_reserve: the stream is being captured");
+      grow_workspace(w, bytes);
+    }
   });
 }
 
@@ -1525,7 +1999,7 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x_, const mlxq_array* w_, const ml
                                mode, global_scale);
     QmmSpec& sp = g.q;
     check_out(out_, sp.out_shape, sp.out_dtype, tag);
-    choose_route(sp, x_, scales_, biases_, tag);
+    choose_route(sp, x_, w_, scales_, biases_, tag);
     if (global_scale) unsupported("gather_qmm: global_scale (nvfp4) is not implemented");
     hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
     Staged st = stage_operands(x_, w_, scales_, biases_, out_, stream, true, tag);
@@ -1534,314 +2008,7 @@ mlxq_status mlxq_gather_qmm(const mlxq_array* x_, const mlxq_array* w_, const ml
     const mlxq_array* scales = st.in[2];
     const mlxq_array* biases = st.in[3];
     mlxq_array* out = st.out;
-    [&] {
-    View xv{x}, wv{w}, sv{scales};
-    const int64_t M = xv.dim(-2);
-    int64_t B = 1;
-    for (auto d : g.idx_shape) B *= d;
-    if (B == 0 || M == 0 || sp.N == 0) return;
-    if ((int)g.idx_shape.size() > MLXQ_MAX_DIMS) unsupported("gather_qmm: index rank too large");
-    if (B > 65535) unsupported("gather_qmm: more than 65535 index entries");
-    const int64_t X = xv.size() / std::max<int64_t>(M * sp.K, 1);
-    const int64_t E = wv.size() / std::max<int64_t>(wv.dim(-2) * wv.dim(-1), 1);
-
-    // flat uint32 lhs/rhs over the broadcast index shape, in the workspace tail
-    mlxq::IdxPrepArgs ip{};
-    ip.bnd = (int)g.idx_shape.size();
-    for (int d = 0; d < ip.bnd; d++) ip.bshape[d] = g.idx_shape[d];
-    ip.B = B;
-    const mlxq_array* idx[2] = {lhs_indices, rhs_indices};
-    const Shape dsh[2] = {default_index_shape(xv), default_index_shape(wv)};
-    for (int s = 0; s < 2; s++) {
-      ip.data[s] = idx[s] ? idx[s]->data : nullptr;
-      ip.dtype[s] = idx[s] ? idx[s]->dtype : MLXQ_UINT32;
-      bstrides_for(idx[s], dsh[s], g.idx_shape, ip.bstrides[s]);
-    }
-    ip.clamp[0] = std::max<int64_t>(X, 1);
-    ip.clamp[1] = std::max<int64_t>(E, 1);
-
-    if (!sp.fast) {
-      run_gen(sp, x, w, scales, biases, out, M, B, X, E, &ip, stream, ScratchSrc{});
-      return;
-    }
-    const int fmt = fmt_of(sp.mode, sp.bits);
-    const int cap = mlxq::qmv_max_rows(fmt, sp.gs);
-    if (M > cap) {
-      // more rows per gathered matrix than the decode kernels stage: the
-      // general kernel tiles any row count
-      run_gen(sp, x, w, scales, biases, out, M, B, X, E, &ip, stream, ScratchSrc{});
-      return;
-    }
-
-    const int dev = current_device();
-    const DevInfo di = device_info(dev);
-
-    // Expert-sorted mxfp4 gathers with one row per entry and >= 4 rows per
-    // expert on average (mlxcel's sorted MoE path, gpt_oss.rs:317-345): one
-    // kernel streams each expert's weights once per 64 of its rows, finding
-    // the rows by binary search in the sorted indices (qmm_group.hip); fewer
-    // rows per expert run as segments of up to 4 entries (below).  Like the reference's sorted route, it
-    // relies on sorted_indices being true.  MLXQ_GATHER_SORTED=0 turns it off.
-    if (sorted_indices && M == 1 && fmt == mlxq::MXFP4 && B >= 32 && B >= 4 * E &&
-        knobs().gather_sorted != 0) {
-      const DirectIdx dl = direct_index(lhs_indices, dsh[0], g.idx_shape);
-      const DirectIdx dr = direct_index(rhs_indices, dsh[1], g.idx_shape);
-      const mlxq::QmmGroupPlan gp = mlxq::qmm_group_plan(fmt, sp.N, sp.K, E, B);
-      if (gp.ok && dr.ok && dr.p && dl.ok && !dl.p && dl.div == 1) {
-        mlxq::QmmGroupArgs q{};
-        q.x = static_cast<const uint16_t*>(x->data);
-        q.w = static_cast<const uint32_t*>(w->data);
-        q.scales = static_cast<const uint8_t*>(scales->data);
-        q.out = static_cast<uint16_t*>(out->data);
-        q.rhs = dr.p;
-        q.rhs_stride = dr.stride;
-        q.N = (int)sp.N;
-        q.K = (int)sp.K;
-        q.E = (int)E;
-        q.B = (int)B;
-        hip_check(mlxq::qmm_group_launch(q, gp, stream), "gather group launch");
-        return;
-      }
-    }
-
-    // Many rows per expert (MoE prefill, large batches): group rows by expert
-    // on the device, then one GEMM tile reads each expert's weights once per
-    // tile of rows (qmm.hip), instead of once per index entry.  Auto when the
-    // entries average >= 8 rows per touched expert; MLXQ_GATHER_GROUP=0|1
-    // forces the choice (A/B switch for tests).
-    const int grp_env = knobs().gather_group;
-    const int64_t rows = B * M;
-    const bool want_group = grp_env == 1 || (grp_env != 0 && rows >= 8 * std::min<int64_t>(E, B));
-    if (E <= mlxq::kGroupMaxExperts && want_group) {
-      const int64_t per_expert = rows / std::max<int64_t>(1, std::min<int64_t>(E, B));
-      const mlxq::QmmPlan qp =
-          mlxq::qmm_plan_grouped(fmt, sp.gs, sp.N, sp.K, per_expert <= 64 ? 3 : (per_expert <= 128 ? 2 : 0));
-      const bool use_qmm = qp.ok && X * M * sp.K * 2 < ((int64_t)1 << 31);
-      // K not a multiple of 64: the MFMA skinny kernel over the same grouping
-      const int cap_rows = use_qmm ? qp.rows_per_tile : (int)std::min<int64_t>(cap, rows);
-      const int64_t maxseg = rows / cap_rows + std::min<int64_t>(E, B) + 1;
-      if (maxseg > 65535) unsupported("gather_qmm: too many expert segments for one launch");
-      mlxq::QmvPlan p;
-      if (!use_qmm) {
-        int nw, pf;
-        qmv_shape_choice(sp.N, sp.K, nw, pf);
-        p = mlxq::qmv_plan(fmt, sp.gs, sp.N, sp.K, cap_rows, (int)maxseg, di.cus, nw, pf);
-        if (p.lds > mlxq::kQmvLdsMax) unsupported("gather_qmm: activation tile does not fit in LDS");
-      }
-      auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
-      const size_t o_x = al((size_t)B * 2 * sizeof(uint32_t));
-      const size_t o_o = o_x + al((size_t)rows * sizeof(uint32_t));
-      const size_t o_seg = o_o + al((size_t)rows * sizeof(uint32_t));
-      const size_t o_n = o_seg + al((size_t)maxseg * 3 * sizeof(uint32_t));
-      const size_t o_part = o_n + 256;
-      const size_t part = (!use_qmm && p.ks > 1) ? (size_t)p.ks * rows * sp.N * sizeof(float) : 0;
-      char* base = static_cast<char*>(workspace(dev, stream, o_part + part));
-      uint32_t* flat = reinterpret_cast<uint32_t*>(base);
-      ip.out[0] = flat;
-      ip.out[1] = flat + B;
-      hip_check(mlxq::launch_index_prep(ip, stream), "index_prep launch");
-      mlxq::GroupArgs ga{};
-      ga.lhs = flat;
-      ga.rhs = flat + B;
-      ga.B = (int)B;
-      ga.M = (int)M;
-      ga.E = (int)E;
-      ga.cap = cap_rows;
-      ga.xrows = reinterpret_cast<uint32_t*>(base + o_x);
-      ga.orows = reinterpret_cast<uint32_t*>(base + o_o);
-      ga.seg = reinterpret_cast<uint32_t*>(base + o_seg);
-      ga.nseg = reinterpret_cast<uint32_t*>(base + o_n);
-      hip_check(mlxq::launch_group_by_expert(ga, stream), "group launch");
-      if (use_qmm) {
-        mlxq::QmmArgs q{};
-        q.x = static_cast<const uint16_t*>(x->data);
-        q.w = static_cast<const uint32_t*>(w->data);
-        q.scales = scales->data;
-        q.biases = biases ? static_cast<const uint16_t*>(biases->data) : nullptr;
-        q.out = static_cast<uint16_t*>(out->data);
-        q.M = (int)rows;
-        q.x_rows = (int)(X * M);
-        q.N = (int)sp.N;
-        q.K = (int)sp.K;
-        int shift = 0;
-        while ((1 << shift) < sp.gs) shift++;
-        q.gs_shift = shift;
-        q.ksplit = 1;
-        q.ksteps_per_split = qp.ksteps_per_split;
-        q.seg = ga.seg;
-        q.nseg_dev = ga.nseg;
-        q.xrows = ga.xrows;
-        q.orows = ga.orows;
-        q.w_expert_stride = wv.dim(-2) * wv.dim(-1);
-        q.s_expert_stride = sv.dim(-2) * sv.dim(-1);
-        mlxq::QmmPlan gp = qp;
-        gp.tiles_m = (int)maxseg;
-        hip_check(mlxq::qmm_launch(fmt, q, gp, stream), "gather qmm launch");
-        return;
-      }
-      mlxq::QmvArgs a{};
-      a.x = static_cast<const uint16_t*>(x->data);
-      a.w = static_cast<const uint32_t*>(w->data);
-      a.scales = scales->data;
-      a.biases = biases ? static_cast<const uint16_t*>(biases->data) : nullptr;
-      a.out = static_cast<uint16_t*>(out->data);
-      a.N = (int)sp.N;
-      a.K = (int)sp.K;
-      a.E = (int)E;
-      a.X = (int)X;
-      a.w_expert_stride = wv.dim(-2) * wv.dim(-1);
-      a.s_expert_stride = sv.dim(-2) * sv.dim(-1);
-      a.rps = cap_rows;
-      a.total_rows = (int)rows;
-      a.out_rows = (int)rows;
-      a.rows_lds = cap_rows;
-      a.ks = p.ks;
-      a.kst_per_wg = p.kst_per_wg;
-      if (p.ks > 1) a.ws = reinterpret_cast<float*>(base + o_part);
-      a.seg = ga.seg;
-      a.nseg_dev = ga.nseg;
-      a.xrows = ga.xrows;
-      a.orows = ga.orows;
-      hip_check(mlxq::qmv_launch(fmt, sp.gs, a, (int)maxseg, p, stream), "gather qmv launch");
-      return;
-    }
-
-    // Sorted gathers with one row per entry (the expert-sorted MoE decode of
-    // mlxcel's callers): on the block-MFMA kernel, one workgroup row per
-    // expert finds the expert's entries by binary search and streams its
-    // weights once per 4 of them (MLXQ_GATHER_RUNS=2, the default; it relies
-    // on the order, as the reference's sorted route does).  Otherwise
-    // (MLXQ_GATHER_RUNS=1, or the row-streaming kernel) runs of equal
-    // consecutive experts, split at multiples of 4, correct for any order;
-    // MLXQ_GATHER_RUNS=0: one segment per entry.
-    const int r_req = knobs().qmv_r;
-    {
-      const DirectIdx dl = direct_index(lhs_indices, dsh[0], g.idx_shape);
-      const DirectIdx dr = direct_index(rhs_indices, dsh[1], g.idx_shape);
-      if (sorted_indices && M == 1 && B >= 8 && dr.ok && dr.p && dl.ok && !dl.p && dl.div == 1 &&
-          knobs().gather_runs != 0) {
-        // 4 entries at a time on the block-MFMA kernel (gpt-oss MoE shapes,
-        // T=16: runs of 4 were 9% faster than one segment per entry, runs of
-        // 8 or 16 slower; the row-streaming kernel with the expert search was
-        // 13% slower than the block-MFMA one), else on the row-streaming kernel
-        const mlxq::QmvB4Plan bp = mlxq::qmv_b4_plan(fmt, sp.gs, sp.N, sp.K, 4, 0, 0);
-        const mlxq::QmvRsPlan rp = bp.ok ? mlxq::QmvRsPlan{} : mlxq::qmv_rs_plan(fmt, sp.gs, sp.N, sp.K, 4, r_req);
-        if (bp.ok || rp.ok) {
-          mlxq::QmvArgs a{};
-          a.x = static_cast<const uint16_t*>(x->data);
-          a.w = static_cast<const uint32_t*>(w->data);
-          a.scales = scales->data;
-          a.biases = biases ? static_cast<const uint16_t*>(biases->data) : nullptr;
-          a.out = static_cast<uint16_t*>(out->data);
-          a.rhs = dr.p;
-          a.rhs_stride = dr.stride;
-          a.lhs_stride = 1;
-          a.lhs_div = 1;
-          a.N = (int)sp.N;
-          a.K = (int)sp.K;
-          a.E = (int)E;
-          a.X = (int)X;
-          a.w_expert_stride = wv.dim(-2) * wv.dim(-1);
-          a.s_expert_stride = sv.dim(-2) * sv.dim(-1);
-          a.rps = 1;
-          a.total_rows = (int)B;
-          a.out_rows = (int)B;
-          a.rows_lds = 1;
-          a.runs = 4;
-          if (bp.ok && knobs().gather_runs >= 2 && E <= B) {
-            // one workgroup row per expert, its entries found by binary search
-            // (with more experts than entries most rows would only search
-            // and exit: runs then)
-            a.runs = -1;
-            hip_check(mlxq::qmv_b4_launch(fmt, sp.gs, a, (int)E, bp, stream), "gather qmv launch");
-          } else if (bp.ok) {
-            hip_check(mlxq::qmv_b4_launch(fmt, sp.gs, a, (int)B, bp, stream), "gather qmv launch");
-          } else {
-            hip_check(mlxq::qmv_rs_launch(fmt, sp.gs, a, (int)B, rp, stream), "gather qmv launch");
-          }
-          return;
-        }
-      }
-    }
-
-    const Skinny kind = skinny_choice((int)M, fmt, sp.K);
-    const mlxq::QmvFrPlan fp =
-        kind == Skinny::FR ? mlxq::qmv_fr_plan(fmt, sp.gs, sp.N, sp.K, (int)M, r_req) : mlxq::QmvFrPlan{};
-    const mlxq::QmvB4Plan bp =
-        kind == Skinny::B4 ? mlxq::qmv_b4_plan(fmt, sp.gs, sp.N, sp.K, (int)M, knobs().b4_rg,
-                                               knobs().b4_cpw)
-                           : mlxq::QmvB4Plan{};
-    const mlxq::QmvRsPlan rp =
-        (kind == Skinny::RS || (kind == Skinny::FR && !fp.ok) || (kind == Skinny::B4 && !bp.ok && M <= 4))
-            ? mlxq::qmv_rs_plan(fmt, sp.gs, sp.N, sp.K, (int)M, r_req)
-            : mlxq::QmvRsPlan{};
-    const bool use_rs = fp.ok || rp.ok || bp.ok;
-    int nw, pf;
-    qmv_shape_choice(sp.N, sp.K, nw, pf);
-    mlxq::QmvPlan p;
-    if (!use_rs) {
-      p = mlxq::qmv_plan(fmt, sp.gs, sp.N, sp.K, (int)M, (int)B, di.cus, nw, pf);
-      if (p.lds > mlxq::kQmvLdsMax) unsupported("gather_qmm: activation tile does not fit in LDS");
-    }
-    // indices the kernels can read in place skip the index_prep launch
-    const DirectIdx dl = direct_index(lhs_indices, dsh[0], g.idx_shape);
-    const DirectIdx dr = direct_index(rhs_indices, dsh[1], g.idx_shape);
-    const bool direct = dl.ok && dr.ok && dr.div == 1 && knobs().gather_direct != 0;
-    const size_t idx_bytes = direct ? 0 : ((size_t)B * 2 * sizeof(uint32_t) + 255) & ~(size_t)255;
-    const size_t part_bytes = p.ks > 1 ? (size_t)p.ks * B * M * sp.N * sizeof(float) : 0;
-    char* wsb = nullptr;
-    if (idx_bytes + part_bytes > 0) wsb = static_cast<char*>(workspace(dev, stream, idx_bytes + part_bytes));
-    const uint32_t* lhs_p = dl.p;
-    const uint32_t* rhs_p = dr.p;
-    int lhs_stride = dl.stride, rhs_stride = dr.stride, lhs_div = dl.div;
-    if (!direct) {
-      uint32_t* flat = reinterpret_cast<uint32_t*>(wsb);
-      ip.out[0] = flat;
-      ip.out[1] = flat + B;
-      hip_check(mlxq::launch_index_prep(ip, stream), "index_prep launch");
-      lhs_p = flat;
-      rhs_p = flat + B;
-      lhs_stride = rhs_stride = lhs_div = 1;
-    }
-
-    mlxq::QmvArgs a{};
-    a.x = static_cast<const uint16_t*>(x->data);
-    a.w = static_cast<const uint32_t*>(w->data);
-    a.scales = scales->data;
-    a.biases = biases ? static_cast<const uint16_t*>(biases->data) : nullptr;
-    a.out = static_cast<uint16_t*>(out->data);
-    a.lhs = lhs_p;
-    a.rhs = rhs_p;
-    a.lhs_stride = lhs_stride;
-    a.rhs_stride = rhs_stride;
-    a.lhs_div = lhs_div;
-    a.N = (int)sp.N;
-    a.K = (int)sp.K;
-    a.E = (int)E;
-    a.X = (int)X;
-    a.w_expert_stride = wv.dim(-2) * wv.dim(-1);
-    a.s_expert_stride = sv.dim(-2) * sv.dim(-1);
-    a.rps = (int)M;
-    a.total_rows = (int)(B * M);
-    a.out_rows = (int)(B * M);
-    a.rows_lds = (int)M;
-    if (fp.ok) {
-      hip_check(mlxq::qmv_fr_launch(fmt, sp.gs, a, (int)B, fp, stream), "gather qmv launch");
-      return;
-    }
-    if (bp.ok) {
-      hip_check(mlxq::qmv_b4_launch(fmt, sp.gs, a, (int)B, bp, stream), "gather qmv launch");
-      return;
-    }
-    if (rp.ok) {
-      hip_check(mlxq::qmv_rs_launch(fmt, sp.gs, a, (int)B, rp, stream), "gather qmv launch");
-      return;
-    }
-    a.ks = p.ks;
-    a.kst_per_wg = p.kst_per_wg;
-    if (p.ks > 1) a.ws = reinterpret_cast<float*>(wsb + idx_bytes);
-    hip_check(mlxq::qmv_launch(fmt, sp.gs, a, (int)B, p, stream), "gather qmv launch");
-    }();
+    gather_run(g, x, w, scales, biases, lhs_indices, rhs_indices, sorted_indices, out, stream);
     st.finish();
   });
 }
@@ -1949,6 +2116,8 @@ mlxq_status mlxq_dequantize(const mlxq_array* w, const mlxq_array* scales, const
     const int64_t rows = View{out}.size() / std::max<int64_t>(K, 1);
     if (rows == 0 || K == 0) return;
     if (K % group_size) unsupported("dequantize: K must be a multiple of group_size");
+    // 64-bit element indices; one launch grid covers at most 2^32 threads of >= 8 elements
+    if (rows * K >= kElemMax) unsupported("dequantize: 2^34 elements or more");
     if (!dedicated) {
       hip_check(mlxq::launch_gen_dequantize(mode == MXFP4_M ? mlxq::GEN_MXFP4 : mlxq::GEN_AFFINE,
                                             static_cast<const uint32_t*>(w->data), scales->data,
@@ -2048,6 +2217,7 @@ mlxq_status mlxq_quantize(const mlxq_array* w, int32_t group_size, int32_t bits,
     const int64_t K = wv.dim(-1);
     const int64_t rows = wv.size() / std::max<int64_t>(K, 1);
     if (rows == 0 || K == 0) return;
+    if (rows * K >= kElemMax) unsupported("quantize: 2^34 elements or more");
     hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
     if (mode == AFFINE) {
       hip_check(mlxq::launch_affine_quantize(w->data, gen_type(w->dtype), static_cast<uint32_t*>(wq_out->data),

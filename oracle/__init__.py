@@ -24,6 +24,21 @@ def build() -> None:
     subprocess.run(["make", "-s", "-C", _HERE, "-B", "liboracle.so"], check=True)
 
 
+def build_info() -> dict:
+    """Compiler and flags liboracle.so is built with (the Makefile's CC and
+    CFLAGS), for reports that time the oracle."""
+    cflags = ""
+    for line in open(os.path.join(_HERE, "Makefile")):
+        if line.startswith("CFLAGS"):
+            cflags = line.split("=", 1)[1].strip()
+    cc = os.environ.get("CC", "gcc")
+    try:
+        ver = subprocess.run([cc, "--version"], capture_output=True, text=True).stdout.splitlines()[0]
+    except Exception:
+        ver = cc
+    return {"compiler": ver, "cflags": cflags}
+
+
 def lib() -> ctypes.CDLL:
     global _lib
     if _lib is None:

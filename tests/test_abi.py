@@ -294,3 +294,31 @@ def test_quantized_linear_and_dense_gemm_predicate(lib):
     st = lib.mlxq_quantized_linear(ctypes.byref(bad), ctypes.byref(w), ctypes.byref(s), ctypes.byref(s), None, 64, 4,
                                    b"affine", ctypes.byref(out), None)
     assert st == _lib.EINVAL
+
+
+def test_sizes_no_launch_covers_are_refused_before_device_work(lib):
+    # what the splits cannot bring below one launch's limits is refused with
+    # MLXQ_EUNSUPPORTED (the caller falls back) before any device call
+    # one activation row of 2 GiB (2^30 bf16): no row chunk fits a buffer resource
+    K = 1 << 30
+    x, w, s = arr([1, K], BF), arr([1, K // 8], U32), arr([1, K // 64], BF)
+    out = arr([1, 1], BF)
+    st = lib.mlxq_quantized_matmul(ctypes.byref(x), ctypes.byref(w), ctypes.byref(s), ctypes.byref(s), True, 64, 4,
+                                   b"affine", ctypes.byref(out), None)
+    assert st == _lib.EUNSUPPORTED and "reaches 2 GiB" in _lib.last_error()
+    # 2^30 gather entries (the chunked gather's flat index lists stay below 2^30)
+    B = 1 << 30
+    xg, wg, sg, rhs = arr([B, 1, 64], BF), arr([4, 64, 8], U32), arr([4, 64, 1], BF), arr([B], U32)
+    outg = arr([B, 1, 64], BF)
+    st = lib.mlxq_gather_qmm(ctypes.byref(xg), ctypes.byref(wg), ctypes.byref(sg), ctypes.byref(sg), None,
+                             ctypes.byref(rhs), True, 64, 4, False, b"affine", None, ctypes.byref(outg), None)
+    assert st == _lib.EUNSUPPORTED and "2^30 index entries" in _lib.last_error()
+    # conversions of 2^34 elements (beyond one launch grid)
+    rows, Kd = 1 << 20, 1 << 14
+    wd, sd, od = arr([rows, Kd // 8], U32), arr([rows, Kd // 64], BF), arr([rows, Kd], BF)
+    st = lib.mlxq_dequantize(ctypes.byref(wd), ctypes.byref(sd), ctypes.byref(sd), 64, 4, b"affine", -1,
+                             ctypes.byref(od), None)
+    assert st == _lib.EUNSUPPORTED and "2^34" in _lib.last_error()
+    st = lib.mlxq_quantize(ctypes.byref(od), 64, 4, b"affine", ctypes.byref(wd), ctypes.byref(sd), ctypes.byref(sd),
+                           None)
+    assert st == _lib.EUNSUPPORTED and "2^34" in _lib.last_error()

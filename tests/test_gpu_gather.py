@@ -345,3 +345,27 @@ def test_sorted_grouped_mxfp4(pattern, dtype):
     assert max_rel(got, want) <= TOL
     again = host_u16(mq.gather_qmm(X, W, S, None, None, R, True, 32, 4, "mxfp4", sorted_indices=True))
     np.testing.assert_array_equal(got, again)
+
+
+@pytest.mark.parametrize("K", [96, 128, 256, 4096])
+def test_sorted_grouped_mxfp4_k(monkeypatch, K):
+    # the expert-grouped kernel's ring at other reduction lengths: K below
+    # 384 (fewer 128-k blocks than the ring's 3-ahead prologue: the blocks
+    # past the last issue dead loads and skip their MFMAs), K = 96 (one
+    # partial block), K = 128 / 256 / 4096 (multiples of 128: no tail window)
+    announce("gather_sorted_grouped_k", K)
+    E, N, B = 8, 256, 256
+    rhs = np.sort(np.random.default_rng(990 + K).integers(0, E, B))
+    wq, sc = mx_experts(E, N, K, 991 + K)
+    x = orc.normal_bf16((B, 1, K), 1.0, 992 + K)
+    X, W, S = dev_bf16(x), dev_u32(wq), dev_u8(sc)
+    R = torch.from_numpy(rhs.astype(np.int32)).cuda()
+    got = host_u16(mq.gather_qmm(X, W, S, None, None, R, True, 32, 4, "mxfp4", sorted_indices=True))
+    want = orc.gather_qmm_t(x, wq, sc, None, np.arange(B, dtype=np.uint32), rhs.astype(np.uint32), mode="mxfp4")
+    assert max_rel(got, want) <= TOL
+    # the same entries on the routes that do not rely on the order agree
+    # within tolerance (a different fp32 summation order)
+    setknob(monkeypatch, "MLXQ_GATHER_SORTED", "0")
+    setknob(monkeypatch, "MLXQ_GATHER_RUNS", "0")
+    per_entry = host_u16(mq.gather_qmm(X, W, S, None, None, R, True, 32, 4, "mxfp4", sorted_indices=True))
+    assert max_rel(per_entry, got) <= TOL

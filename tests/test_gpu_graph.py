@@ -168,3 +168,30 @@ def test_replay_after_the_workspace_grew():
     replay_and_check(g, out, eager, lambda: junk.mul_(1.5))
     want_big = host_u16(mq.quantized_matmul(X2, W2, S2, B2, True, 64, 4))
     np.testing.assert_array_equal(host_u16(big), want_big)
+
+
+def test_capture_with_strided_x_after_a_reserve():
+    # a strided activation is copied into the stream's staging buffer first;
+    # mlxq_workspace_reserve grows that buffer too, so a capture right after
+    # a reserve (no eager warm-up on the stream) allocates nothing
+    announce("graph_strided_reserve")
+    M, N, K = 256, 256, 8192  # prefill with split K: scratch and staging both used
+    x, wq, s, b = affine_case(M, N, K, 64, 4, 1280)
+    W, S, B = dev_u32(wq), dev_bf16(s), dev_bf16(b)
+    wide = torch.zeros(M, 2 * K, dtype=torch.bfloat16, device="cuda")
+    wide[:, ::2] = dev_bf16(x)
+    X = wide[:, ::2]  # stride 2 along K: needs the staging copy
+    assert not X.is_contiguous()
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    eager = host_u16(mq.quantized_matmul(X.contiguous(), W, S, B, True, 64, 4))
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        mq.workspace_reserve(64 << 20)
+    torch.cuda.synchronize()
+    held = mq.get_cache_memory()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        mq.quantized_matmul(X, W, S, B, True, 64, 4, out=out)
+    assert mq.get_cache_memory() == held
+    junk = torch.randn(1 << 20, device="cuda")
+    replay_and_check(g, out, eager, lambda: junk.mul_(0.25))

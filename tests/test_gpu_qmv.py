@@ -38,7 +38,7 @@ def test_affine_small_shapes(bits, gs, M):
 
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("N,K", [(4096, 4096), (14336, 4096), (4096, 14336)])
-@pytest.mark.parametrize("M", [1, 4, 8])
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
 def test_affine_llama_shapes(bits, N, K, M):
     announce("affine_llama", bits, N, K, M)
     x, wq, s, b = affine_case(M, N, K, 64, bits, 7000 + N + K + M + bits)

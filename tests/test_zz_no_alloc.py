@@ -3,9 +3,15 @@ mlxq_quantized_matmul, called through the C-ABI.  Its output must be the
 existing entry point's, bit for bit (same kernels, same plan), on two calls in
 a row (the second smaller, so stale scratch contents from the first would
 show), for routes that use scratch (5-16-row decode partials, split-K
-prefill) and one that does not; it must not grow any workspace; and a call
-needing more scratch than the fixed array returns MLXQ_ENOMEM."""
+prefill) and one that does not; it must not grow any workspace; a call
+needing more scratch than the fixed array returns MLXQ_ENOMEM; and a fresh
+process whose first library call is a noalloc call under HIP-graph capture
+(the scratch address resolved while the stream captures) replays it with new
+activations bitwise equal to the eager entry point."""
 import ctypes
+import os
+import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -73,3 +79,50 @@ def test_noalloc_rejects_calls_beyond_its_scratch(monkeypatch):
     assert "scratch" in _lib.last_error()
     st.synchronize()
     assert float(out.float().abs().max()) == 0.0  # nothing ran
+
+
+# Run in a fresh process, so the captured call is the first call into the
+# library there: the device address of the fixed scratch is resolved while
+# the stream is being captured.
+CAPTURE_FIRST = r"""
+import ctypes, sys
+import numpy as np, torch
+sys.path.insert(0, sys.argv[1]); sys.path.insert(0, sys.argv[1] + "/tests")
+import mlxcel_amd as mq
+from mlxcel_amd import _lib
+from mlxcel_amd.ops import _arr, _ref
+from helpers import affine_case, dev_bf16, dev_u32, host_u16
+M, N, K = 16, 4096, 8192  # 5-16-row decode kernel with K-range partials in the scratch
+x, wq, s, b = affine_case(M, N, K, 64, 4, 3200)
+X, W, S, B = dev_bf16(x), dev_u32(wq), dev_bf16(s), dev_bf16(b)
+out = torch.zeros(M, N, dtype=torch.bfloat16, device="cuda")
+lib = _lib.load()
+args = [_arr(t) for t in (X, W, S, B, out)]
+st = torch.cuda.Stream()
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g, stream=st):
+    rc = lib.mlxq_quantized_matmul_noalloc(*[_ref(a) for a in args[:4]], True, 64, 4, b"affine", _ref(args[4]),
+                                           ctypes.c_void_p(st.cuda_stream))
+assert rc == _lib.OK, _lib.last_error()
+assert mq.get_cache_memory() == 0  # nothing allocated by the library in this process
+for rep in range(3):
+    x2, _, _, _ = affine_case(M, N, K, 64, 4, 3300 + rep)  # new activations, same buffer
+    X.copy_(dev_bf16(x2))
+    out.zero_()
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    want = host_u16(mq.quantized_matmul(X, W, S, B, True, 64, 4))
+    np.testing.assert_array_equal(host_u16(out), want, err_msg=f"replay {rep}")
+print("capture-first noalloc: 3 replays bitwise equal", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_capture_in_a_fresh_process():
+    announce("noalloc_capture_first (subprocess)")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", CAPTURE_FIRST, root], capture_output=True, text=True, timeout=300)
+    print(r.stdout[-2000:], r.stderr[-4000:], flush=True)
+    assert r.returncode == 0, r.stderr[-4000:]
+    assert "3 replays bitwise equal" in r.stdout
