@@ -244,6 +244,33 @@ def read_ceiling(nbytes=33_067_008, reps=40):
             "workgroups": wgs, "threads": thr}
 
 
+def n_sweep(iters=240):
+    """The M=1 gate-shape qmv (K=4096, 4-bit g64) over N, beside the plain
+    streaming read of the same bytes (read_ceiling), both graph-timed on
+    rotated copies: a least-squares line time = fixed + bytes / rate for
+    each, so the fixed cost per launch and the streaming rate separate."""
+    K = 4096
+    rows = []
+    for N in (2048, 4096, 7168, 14336, 28672, 57344):
+        b = qmv_bytes(1, N, K, 4, 64)
+        copies = max(2, math.ceil(2.4 * MALL_BYTES / qmv_bytes(0, N, K, 4, 64)))
+        ws = [make_affine(N, K, 4, 64, 300 + c) for c in range(copies)]
+        x = randn_bf16((1, K), 301)
+        out = torch.empty(1, N, dtype=torch.bfloat16, device="cuda")
+        g = capture(lambda: [mq.quantized_matmul(x, *w, True, 64, 4, out=out) for w in ws])
+        us = timed_graphs([g], max(4, iters // copies), 2, SETTLE_MS) * 1e3 / copies
+        del g, ws
+        rd = read_ceiling(b)
+        rows.append({"N": N, "bytes": b, "qmv_us": round(us, 3), "read_us": rd["us"]})
+    fit = {}
+    for key in ("qmv_us", "read_us"):
+        xs = np.array([r["bytes"] for r in rows], np.float64)
+        ys = np.array([r[key] for r in rows], np.float64)
+        slope, icpt = np.polyfit(xs, ys, 1)
+        fit[key] = {"fixed_us": round(float(icpt), 3), "rate_GBps": round(float(1e-3 / slope), 1)}
+    return {"rows": rows, "fit": fit}
+
+
 def copy_ceiling():
     n = 1 << 30
     src = torch.empty(n, dtype=torch.uint8, device="cuda")
@@ -832,7 +859,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--extras", default="copy,c1,sweep,qmm,gather,moe,e2e,general",
-                    help="comma-separated extra sections: copy, c1, sweep, qmm, gather, moe, e2e, general")
+                    help="comma-separated extra sections: copy, c1, sweep, qmm, gather, moe, e2e, general "
+                         "(and nsweep, not in the default set)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run 5 copies of 256 MiB and 5 gate launches, eager, for rocprofv3 --pmc")
@@ -889,6 +917,8 @@ def main():
             extra["copy_ceiling_GBps"] = round(copy_ceiling(), 1)
         if "c1" in want:
             extra["c1_qmv_4096"] = c1_qmv(with_cpu=not args.no_cpu)
+        if "nsweep" in want:
+            extra["qmv_n_sweep"] = n_sweep()
         if "sweep" in want:
             extra["qmv_sweep"] = qmv_sweep()
         if "qmm" in want:
