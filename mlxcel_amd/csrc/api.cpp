@@ -1155,6 +1155,157 @@ bool try_qmm_f16(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, co
   return true;
 }
 
+// Route of a dense (2-D weight) bfloat16 call of `rows` activation rows on
+// the mid-size decode kernels, or DR_OTHER (row streaming, block MFMA,
+// prefill GEMM):
+// - 3-4 rows of 4-bit codes against a tall matrix: the whole-row kernel also
+//   beats the block-MFMA kernel (gate/up M=4: 10.4 us vs 12.6; 8-bit keeps
+//   the row-streaming kernel: 15.3 us vs 16.3);
+// - 5-16 rows: matrices with ~one 64-row workgroup per CU take the whole-row
+//   kernel, one launch (qmv_mr.hip), faster than the split-K kernel at every
+//   row count (MI355X, Llama-3-8B gate/up, graph-timed: 4-bit M=8 10.5 us vs
+//   12.4, M=16 15.3 vs 15.6-16.7; 8-bit M=8 16.7 vs 20.8, M=16 17.4 vs 21.8);
+//   other matrices the split-K kernel (activations staged once per 128
+//   weight rows, fp32 partials of the K ranges added by a second launch,
+//   qmv_mid.hip).
+enum DenseKind { DR_OTHER, DR_MR, DR_MID };
+struct DenseRoute {
+  DenseKind kind = DR_OTHER;
+  mlxq::QmvMrPlan mr;
+  mlxq::QmvMidPlan mid;
+};
+
+DenseRoute dense_route(const QmmSpec& sp, int64_t rows, int cus) {
+  DenseRoute r;
+  const int fmt = fmt_of(sp.mode, sp.bits);
+  if (rows < 1 || rows > 16) return r;
+  const bool mr_small = rows >= 3 && rows < kMidMinRows && fmt == mlxq::AFF4 && knobs().qmv_mr != 0 &&
+                        knobs().qmv_kernel.empty() &&
+                        mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, false, 0).ok;
+  if (!mr_small && !use_mid((int)rows, fmt, sp.K)) return r;
+  const std::string& forced = knobs().qmv_kernel;
+  if (forced == "mr" || (knobs().qmv_mr != 0 && forced.empty())) {
+    r.mr = mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, forced == "mr", knobs().mr_ring);
+    if (r.mr.ok) {
+      r.kind = DR_MR;
+      return r;
+    }
+  }
+  r.mid = mlxq::qmv_mid_plan(fmt, sp.gs, sp.N, sp.K, (int)rows);
+  if (r.mid.ok) r.kind = DR_MID;
+  return r;
+}
+
+int gs_shift_of(int gs) {
+  int shift = 0;
+  while ((1 << shift) < gs) shift++;
+  return shift;
+}
+
+mlxq::QmvMrArgs mr_args(const QmmSpec& sp, const uint16_t* x, int64_t rows, const uint32_t* w, const void* scales,
+                        const uint16_t* biases, uint16_t* out) {
+  mlxq::QmvMrArgs m{};
+  m.x = x;
+  m.w = w;
+  m.scales = static_cast<const uint16_t*>(scales);
+  m.biases = biases;
+  m.out = out;
+  m.M = (int)rows;
+  m.N = (int)sp.N;
+  m.K = (int)sp.K;
+  m.gs_shift = gs_shift_of(sp.gs);
+  return m;
+}
+
+mlxq::QmvMidArgs mid_args(const QmmSpec& sp, const uint16_t* x, int64_t rows, const uint32_t* w,
+                          const void* scales, const uint16_t* biases, uint16_t* out, int ks) {
+  mlxq::QmvMidArgs m{};
+  m.x = x;
+  m.w = w;
+  m.scales = static_cast<const uint16_t*>(scales);
+  m.biases = biases;
+  m.out = out;
+  m.M = (int)rows;
+  m.N = (int)sp.N;
+  m.K = (int)sp.K;
+  m.gs_shift = gs_shift_of(sp.gs);
+  m.ks = ks;
+  return m;
+}
+
+// Several projections of one activation block (quantized_matmul_multi) on
+// the whole-row or split-K mid-size kernel as one launch (the split-K
+// partials of all matrices summed by one reduction launch).  False: the
+// projections take different kernels or plans (the caller runs them one by
+// one).
+bool try_multi_mid(const std::vector<QmmSpec>& sp, int n, const mlxq_array* x, const mlxq_array* const* w,
+                   const mlxq_array* const* scales, const mlxq_array* const* biases, mlxq_array* const* out,
+                   int64_t rows, hipStream_t stream) {
+  const int dev = current_device();
+  const int cus = device_info(dev).cus;
+  const int fmt = fmt_of(sp[0].mode, sp[0].bits);
+  if (sp[0].mode != AFFINE) return false;
+  std::vector<DenseRoute> r;
+  for (int i = 0; i < n; i++) {
+    if (sp[i].N == 0 || sp[i].K != sp[0].K || sp[i].gs != sp[0].gs) return false;
+    r.push_back(dense_route(sp[i], rows, cus));
+    if (r[i].kind == DR_OTHER || r[i].kind != r[0].kind) return false;
+    if (r[i].kind == DR_MR) {
+      const mlxq::QmvMrPlan &a = r[i].mr, &b = r[0].mr;
+      if (a.s != b.s || a.na != b.na || a.xr != b.xr || a.rk != b.rk || a.ring != b.ring || a.lds != b.lds)
+        return false;
+    } else {
+      const mlxq::QmvMidPlan &a = r[i].mid, &b = r[0].mid;
+      if (a.s != b.s || a.na != b.na || a.kr != b.kr || a.ks != b.ks || a.sw != b.sw || a.lds != b.lds) return false;
+    }
+  }
+  mlxq::QmvMatTable t{};
+  t.n = n;
+  int64_t blocks = 0, ntot = 0;
+  for (int i = 0; i < n; i++) {
+    blocks += r[i].kind == DR_MR ? r[i].mr.row_blocks : r[i].mid.row_blocks;
+    t.blk_end[i] = (int)blocks;
+    t.N[i] = (int)sp[i].N;
+    t.noff[i] = (int)ntot;
+    ntot += sp[i].N;
+    t.w[i] = static_cast<const uint32_t*>(w[i]->data);
+    t.scales[i] = static_cast<const uint16_t*>(scales[i]->data);
+    t.biases[i] = static_cast<const uint16_t*>(biases[i]->data);
+    t.out[i] = static_cast<uint16_t*>(out[i]->data);
+  }
+  for (int i = n; i < mlxq::kQmvMultiMax; i++) {  // unused entries repeat the last one
+    t.blk_end[i] = t.blk_end[n - 1];
+    t.N[i] = t.N[n - 1];
+    t.noff[i] = t.noff[n - 1];
+    t.w[i] = t.w[n - 1];
+    t.scales[i] = t.scales[n - 1];
+    t.biases[i] = t.biases[n - 1];
+    t.out[i] = t.out[n - 1];
+  }
+  if (blocks > 65535 || ntot >= ((int64_t)1 << 30)) return false;
+  t.ntot = (int)ntot;
+  const uint16_t* xd = static_cast<const uint16_t*>(x->data);
+  if (r[0].kind == DR_MR) {
+    mlxq::QmvMrArgs m = mr_args(sp[0], xd, rows, t.w[0], t.scales[0], t.biases[0], t.out[0]);
+    m.mt = t;
+    mlxq::QmvMrPlan p = r[0].mr;
+    p.row_blocks = (int)blocks;
+    hip_check(mlxq::qmv_mr_launch(fmt, m, p, stream), "qmv_mr launch");
+    return true;
+  }
+  mlxq::QmvMidPlan p = r[0].mid;
+  p.row_blocks = (int)blocks;
+  mlxq::QmvMidArgs m = mid_args(sp[0], xd, rows, t.w[0], t.scales[0], t.biases[0], t.out[0], p.ks);
+  m.mt = t;
+  if (p.ks > 1) {
+    const size_t part = (size_t)p.ks * rows * ntot * sizeof(float);
+    if ((int64_t)part >= kBufMax) return false;
+    m.ws = reinterpret_cast<float*>(workspace(dev, stream, part));
+  }
+  hip_check(mlxq::qmv_mid_launch(fmt, m, p, stream), "qmv_mid launch");
+  return true;
+}
+
 // Enqueues one checked quantized_matmul call.
 void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
                           const mlxq_array* biases, mlxq_array* out, hipStream_t stream,
@@ -1213,59 +1364,19 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
   const int fmt = fmt_of(sp.mode, sp.bits);
   const int cap = mlxq::qmv_max_rows(fmt, sp.gs);
   View wv{w}, xv{x};
-  // 3-4 rows of 4-bit codes against a tall matrix: the whole-row mid-size
-  // kernel also beats the block-MFMA kernel (gate/up M=4: 10.4 us vs 12.6;
-  // 8-bit keeps the row-streaming kernel: 15.3 us vs 16.3)
-  const bool mr_small = rows_total >= 3 && rows_total < kMidMinRows && fmt == mlxq::AFF4 && knobs().qmv_mr != 0 &&
-                        knobs().qmv_kernel.empty() && wv.ndim() == 2 &&
-                        mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows_total, device_info(current_device()).cus,
-                                          false, 0).ok;
-  if (wv.ndim() == 2 && rows_total <= 16 && (mr_small || use_mid((int)rows_total, fmt, sp.K))) {
-    const int dev = current_device();
-    int shift = 0;
-    while ((1 << shift) < sp.gs) shift++;
-    const std::string& forced = knobs().qmv_kernel;
-    // Matrices with ~one 64-row workgroup per CU: whole rows per wave, one
-    // launch (qmv_mr.hip), faster than the split-K kernel below at every row
-    // count (MI355X, Llama-3-8B gate/up, graph-timed: 4-bit M=8 10.5 us vs
-    // 12.4, M=16 15.3 vs 15.6-16.7; 8-bit M=8 16.7 vs 20.8, M=16 17.4 vs 21.8).
-    const bool mr_default = knobs().qmv_mr != 0 && forced.empty();
-    if (forced == "mr" || mr_default) {
-      const mlxq::QmvMrPlan rp = mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows_total, device_info(dev).cus,
-                                                   forced == "mr", knobs().mr_ring);
-      if (rp.ok) {
-        mlxq::QmvMrArgs m{};
-        m.x = a.x;
-        m.w = a.w;
-        m.scales = static_cast<const uint16_t*>(a.scales);
-        m.biases = a.biases;
-        m.out = a.out;
-        m.M = (int)rows_total;
-        m.N = (int)sp.N;
-        m.K = (int)sp.K;
-        m.gs_shift = shift;
-        hip_check(mlxq::qmv_mr_launch(fmt, m, rp, stream), "qmv_mr launch");
-        return;
-      }
+  if (wv.ndim() == 2) {
+    const DenseRoute dr = dense_route(sp, rows_total, device_info(current_device()).cus);
+    if (dr.kind == DR_MR) {
+      mlxq::QmvMrArgs m = mr_args(sp, a.x, rows_total, a.w, a.scales, a.biases, a.out);
+      hip_check(mlxq::qmv_mr_launch(fmt, m, dr.mr, stream), "qmv_mr launch");
+      return;
     }
-    // 5-16 rows: activations staged once per 128 weight rows, fp32 partials
-    // of the K ranges added by a second launch (qmv_mid.hip)
-    const mlxq::QmvMidPlan mp = mlxq::qmv_mid_plan(fmt, sp.gs, sp.N, sp.K, (int)rows_total);
-    if (mp.ok) {
-      mlxq::QmvMidArgs m{};
-      m.x = a.x;
-      m.w = a.w;
-      m.scales = static_cast<const uint16_t*>(a.scales);
-      m.biases = a.biases;
-      m.out = a.out;
-      m.M = (int)rows_total;
-      m.N = (int)sp.N;
-      m.K = (int)sp.K;
-      m.gs_shift = shift;
-      m.ks = mp.ks;
-      if (mp.ks > 1)
-        m.ws = reinterpret_cast<float*>(workspace(dev, stream, (size_t)mp.ks * rows_total * sp.N * sizeof(float), ss));
-      hip_check(mlxq::qmv_mid_launch(fmt, m, mp, stream), "qmv_mid launch");
+    if (dr.kind == DR_MID) {
+      mlxq::QmvMidArgs m = mid_args(sp, a.x, rows_total, a.w, a.scales, a.biases, a.out, dr.mid.ks);
+      if (dr.mid.ks > 1)
+        m.ws = reinterpret_cast<float*>(
+            workspace(current_device(), stream, (size_t)dr.mid.ks * rows_total * sp.N * sizeof(float), ss));
+      hip_check(mlxq::qmv_mid_launch(fmt, m, dr.mid, stream), "qmv_mid launch");
       return;
     }
   }
@@ -1927,7 +2038,9 @@ mlxq_status mlxq_quantized_matmul_multi(const mlxq_array* x, int32_t n, const ml
     mlxq::QmvMulti mp{};
     mp.n = n;
     for (int i = 0; i < n && fused; i++) {
-      if (sp[i].N == 0) fused = false;
+      // a projection that alone would take a mid-size kernel is not fused here
+      if (sp[i].N == 0 || dense_route(sp[i], rows, device_info(current_device()).cus).kind != DR_OTHER)
+        fused = false;
       const mlxq::QmvRsPlan p =
           mlxq::qmv_rs_plan(fmt, sp[i].gs, sp[i].N, sp[i].K, (int)rows, knobs().qmv_r);
       if (!p.ok || (i > 0 && (p.mr != plan.mr || p.r != plan.r || p.cpw != plan.cpw || p.nw != plan.nw ||
@@ -1942,6 +2055,12 @@ mlxq_status mlxq_quantized_matmul_multi(const mlxq_array* x, int32_t n, const ml
       mp.out[i] = static_cast<uint16_t*>(out[i]->data);
     }
     if (!fused) {
+      // 3-16 rows on the mid-size kernels: one launch when every projection
+      // alone takes the same kernel with the same plan (only the row blocks
+      // differ), so each output is the separate call's, bit for bit
+      if (plain && n > 1 && knobs().qmv_multi != 0 && sp[0].K > 0 && rows >= 1 &&
+          try_multi_mid(sp, n, x, w, scales, biases, out, rows, stream))
+        return;
       for (int i = 0; i < n; i++) {
         Staged st = stage_operands(x, w[i], scales[i], biases ? biases[i] : nullptr, out[i], stream, true, tag);
         run_quantized_matmul(sp[i], st.in[0], st.in[1], st.in[2], st.in[3], st.out, stream);

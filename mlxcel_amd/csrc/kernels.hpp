@@ -180,6 +180,56 @@ hipError_t qmv_b4_launch(int fmt, int gs, const QmvArgs& a, int nseg, const QmvB
 // Mid-size decode (qmv_mid.hip): 1-16 activation rows against one affine
 // 4/8-bit weight matrix; workgroups of 128 weight rows x one K range of 8
 // windows; fp32 partials of several K ranges are added by launch_splitk_reduce.
+//
+// Several 2-D matrices of one activation block in one launch (q/k/v,
+// gate/up; the mid-size and whole-row kernels): matrix p owns the row blocks
+// [blk_end[p-1], blk_end[p]) of the grid's x dimension and, in the split-K
+// partials, the columns [noff[p], noff[p] + N[p]) of a [ks][M][ntot] array.
+// n <= 1: the kernel's own w / scales / biases / out / N fields alone.
+struct QmvMatTable {
+  int n;
+  int ntot;  // sum of N over the matrices (the partials' row length)
+  int blk_end[kQmvMultiMax];
+  int N[kQmvMultiMax];
+  int noff[kQmvMultiMax];
+  const uint32_t* w[kQmvMultiMax];
+  const uint16_t* scales[kQmvMultiMax];
+  const uint16_t* biases[kQmvMultiMax];
+  uint16_t* out[kQmvMultiMax];
+};
+// The matrix that row block `blk` of a launch belongs to (uniform): its
+// operands, N, first column in the partials and the block's index inside it.
+// Every table entry is read and selected, so the argument loads form one
+// round.
+struct QmvMat {
+  const uint32_t* w;
+  const uint16_t* scales;
+  const uint16_t* biases;
+  uint16_t* out;
+  int N, noff, blk;
+};
+__device__ __forceinline__ QmvMat pick_matrix(const QmvMatTable& t, const uint32_t* w, const uint16_t* scales,
+                                              const uint16_t* biases, uint16_t* out, int N, int blk) {
+  QmvMat m{w, scales, biases, out, N, 0, blk};
+  if (t.n > 1) {
+    int p = 0;
+#pragma unroll
+    for (int i = 0; i < kQmvMultiMax - 1; i++) p += (i < t.n - 1 && blk >= t.blk_end[i]) ? 1 : 0;
+#pragma unroll
+    for (int i = 0; i < kQmvMultiMax; i++) {
+      const bool on = p == i;
+      m.w = on ? t.w[i] : m.w;
+      m.scales = on ? t.scales[i] : m.scales;
+      m.biases = on ? t.biases[i] : m.biases;
+      m.out = on ? t.out[i] : m.out;
+      m.N = on ? t.N[i] : m.N;
+      m.noff = on ? t.noff[i] : m.noff;
+      m.blk = on ? blk - (i > 0 ? t.blk_end[i - 1] : 0) : m.blk;
+    }
+  }
+  return m;
+}
+
 struct QmvMidArgs {
   const uint16_t* x;       // bf16 [M][K]
   const uint32_t* w;       // packed codes [N][K*bits/32]
@@ -190,6 +240,7 @@ struct QmvMidArgs {
   int M, N, K, gs_shift;
   int ks;                  // K ranges (gridDim.y)
   int xt;                  // 16-bit type of x / scales / biases / out: 0 bfloat16, 1 float16
+  QmvMatTable mt;          // several matrices (mt.n > 1)
 };
 struct QmvMidLds {
   int xpitch = 0;  // bf16 per staged activation row
@@ -220,6 +271,7 @@ struct QmvMrArgs {
   uint16_t* out;           // [M][N] of type xt
   int M, N, K, gs_shift;
   int xt;                  // 0 bfloat16, 1 float16
+  QmvMatTable mt;          // several matrices (mt.n > 1)
 };
 struct QmvMrPlan {
   bool ok = false;
@@ -318,6 +370,10 @@ hipError_t qmm_launch(int fmt, const QmmArgs& a, const QmmPlan& p, hipStream_t s
 // out[i] = bf16(sum over z < ks of ws[z * n + i]) (qmv.hip)
 // out (16-bit type xt: 0 bfloat16, 1 float16) = sum over ks fp32 partials, in split order
 hipError_t launch_splitk_reduce(const float* ws, uint16_t* out, int64_t n, int ks, hipStream_t stream, int xt = 0);
+// The same sum over the partials [ks][M][t.ntot] of several matrices, each
+// column written to its matrix's output (the split order as above).
+hipError_t launch_splitk_reduce_multi(const float* ws, const QmvMatTable& t, int M, int ks, hipStream_t stream,
+                                      int xt = 0);
 
 // Elementwise conversions (dequant.hip).
 hipError_t launch_affine_dequantize(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,

@@ -461,6 +461,78 @@ hipError_t launch_splitk_reduce(const float* ws, uint16_t* out, int64_t n, int k
   return hipGetLastError();
 }
 
+// The sum over the partials [ks][M][t.ntot] of several matrices: thread i
+// takes VEC consecutive columns of one row (a matrix's columns start at a
+// multiple of VEC), finds their matrix and writes its output; the same split
+// order as qmv_splitk_reduce4, so the bits are those of one reduction per
+// matrix.
+template <int XT, int VEC>
+__global__ __launch_bounds__(256) void qmv_splitk_reduce_multi(const float* __restrict__ ws, const QmvMatTable t,
+                                                              int M, int ks) {
+  constexpr int ZB = 16;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int cq = t.ntot / VEC;
+  if (i >= (int64_t)M * cq) return;
+  const int m = (int)(i / cq), c = (int)(i % cq) * VEC;
+  int p = 0;
+#pragma unroll
+  for (int j = 0; j < kQmvMultiMax - 1; j++) p += (j < t.n - 1 && c >= t.noff[j + 1]) ? 1 : 0;
+  const int64_t MN = (int64_t)M * t.ntot;
+  const float* src = ws + (int64_t)m * t.ntot + c;
+  float y[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; e++) y[e] = 0.f;
+  for (int z = 0; z < ks; z += ZB) {  // uniform
+    float v[ZB][VEC];
+#pragma unroll
+    for (int u = 0; u < ZB; u++) {
+      if (z + u < ks) {
+        if constexpr (VEC == 4) {
+          const float4 q = *reinterpret_cast<const float4*>(src + (int64_t)(z + u) * MN);
+          v[u][0] = q.x;
+          v[u][1] = q.y;
+          v[u][2] = q.z;
+          v[u][3] = q.w;
+        } else {
+          v[u][0] = src[(int64_t)(z + u) * MN];
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < ZB; u++)
+      if (z + u < ks)
+#pragma unroll
+        for (int e = 0; e < VEC; e++) y[e] += v[u][e];
+  }
+  uint16_t* dst = t.out[0];
+  int Np = t.N[0], off = 0;
+#pragma unroll
+  for (int j = 1; j < kQmvMultiMax; j++) {
+    const bool on = p == j;
+    dst = on ? t.out[j] : dst;
+    Np = on ? t.N[j] : Np;
+    off = on ? t.noff[j] : off;
+  }
+#pragma unroll
+  for (int e = 0; e < VEC; e++) dst[(int64_t)m * Np + (c - off) + e] = (uint16_t)f32_to_xt<XT>(y[e]);
+}
+
+hipError_t launch_splitk_reduce_multi(const float* ws, const QmvMatTable& t, int M, int ks, hipStream_t stream,
+                                      int xt) {
+  bool vec = (reinterpret_cast<uintptr_t>(ws) & 15) == 0 && t.ntot % 4 == 0;
+  for (int j = 0; j < t.n; j++) vec = vec && t.N[j] % 4 == 0 && t.noff[j] % 4 == 0;
+  const int64_t n = (int64_t)M * t.ntot / (vec ? 4 : 1);
+  const dim3 grid((unsigned)((n + 255) / 256)), block(256);
+  if (vec) {
+    if (xt == 1) hipLaunchKernelGGL((qmv_splitk_reduce_multi<1, 4>), grid, block, 0, stream, ws, t, M, ks);
+    else hipLaunchKernelGGL((qmv_splitk_reduce_multi<0, 4>), grid, block, 0, stream, ws, t, M, ks);
+  } else {
+    if (xt == 1) hipLaunchKernelGGL((qmv_splitk_reduce_multi<1, 1>), grid, block, 0, stream, ws, t, M, ks);
+    else hipLaunchKernelGGL((qmv_splitk_reduce_multi<0, 1>), grid, block, 0, stream, ws, t, M, ks);
+  }
+  return hipGetLastError();
+}
+
 // ---- gather index preparation ----------------------------------------------
 
 __device__ __forceinline__ int64_t load_index(const void* p, int dtype, int64_t loc) {

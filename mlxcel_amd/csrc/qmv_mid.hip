@@ -102,11 +102,12 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const QmvMat mat = pick_matrix(a.mt, a.w, a.scales, a.biases, a.out, a.N, blockIdx.x);
   const int M = a.M;
-  const int N = a.N;
+  const int N = mat.N;
   const int K = a.K;
   constexpr int kr = KR;
-  const int rb = blockIdx.x;
+  const int rb = mat.blk;
   const int sp = blockIdx.y;
   const int k0 = sp * kr;
   constexpr int nwin = MID_WIN;  // every split is a full K range (K % KR == 0)
@@ -117,10 +118,10 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
   const QmvMidLds L = qmv_mid_lds(FMT, 1 << a.gs_shift, kr, NA);
 
   const uint32_t RB = (uint32_t)(K / CK) * 16u;  // bytes per weight row
-  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.w, (uint32_t)N * RB);
+  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(mat.w, (uint32_t)N * RB);
   const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.x, (uint32_t)M * (uint32_t)K * 2u);
-  const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(a.scales, (uint32_t)N * (uint32_t)G * 2u);
-  const __amdgpu_buffer_rsrc_t br = buffer_rsrc(a.biases, (uint32_t)N * (uint32_t)G * 2u);
+  const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(mat.scales, (uint32_t)N * (uint32_t)G * 2u);
+  const __amdgpu_buffer_rsrc_t br = buffer_rsrc(mat.biases, (uint32_t)N * (uint32_t)G * 2u);
 
   // ---- 1. loads: activation range, the block's scales, then the first
   // windows of weights (the staged data is consumed first; loads retire in
@@ -313,6 +314,7 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
   }
 
   // ---- 4. store: bf16 (one K range) or this range's fp32 partials ----------
+  const int ntot = a.mt.n > 1 ? a.mt.ntot : N;  // partials' row length
 #pragma unroll
   for (int t = 0; t < MID_T; t++) {
     const int n = row_wg + wave * (MID_T * 16) + t * 16 + nl;
@@ -322,8 +324,8 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
       for (int j = 0; j < YV; j++) {
         const int m = (16 * u + 4 * g) / S + j;
         if (m < M && n < N) {
-          if (a.ks == 1) a.out[(int64_t)m * N + n] = (uint16_t)f32_to_xt<XT>(y[t][u][j]);
-          else a.ws[((int64_t)sp * M + m) * N + n] = y[t][u][j];
+          if (a.ks == 1) mat.out[(int64_t)m * N + n] = (uint16_t)f32_to_xt<XT>(y[t][u][j]);
+          else a.ws[((int64_t)sp * M + m) * ntot + mat.noff + n] = y[t][u][j];
         }
       }
   }
@@ -398,6 +400,7 @@ hipError_t qmv_mid_launch(int fmt, const QmvMidArgs& a, const QmvMidPlan& p, hip
     e = p.s == 2 ? mid_launch_s<AFF8, 2>(p, a, stream) : mid_launch_s<AFF8, 1>(p, a, stream);
   }
   if (e != hipSuccess || p.ks == 1) return e;
+  if (a.mt.n > 1) return launch_splitk_reduce_multi(a.ws, a.mt, a.M, p.ks, stream, a.xt);
   return launch_splitk_reduce(a.ws, a.out, (int64_t)a.M * a.N, p.ks, stream, a.xt);
 }
 

@@ -97,24 +97,25 @@ __global__ __launch_bounds__(MR_NT, 1) void qmv_mr_kernel(const QmvMrArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int M = a.M, N = a.N, K = a.K;
+  const QmvMat mat = pick_matrix(a.mt, a.w, a.scales, a.biases, a.out, a.N, blockIdx.x);
+  const int M = a.M, N = mat.N, K = a.K;
   const int gsh = a.gs_shift;
   const int G = K >> gsh;
   const int ngr = RK >> gsh;  // groups per range
-  const int row_wg = blockIdx.x * MR_RW;
+  const int row_wg = mat.blk * MR_RW;
   const int nranges = K / RK;
 
   const uint32_t RB = (uint32_t)(K / CK) * 16u;  // bytes per weight row
   // live resources and dead ones (no records: every load returns 0), chosen
   // per range with scalar selects; range offsets go in the scalar offset
-  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.w, (uint32_t)N * RB);
+  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(mat.w, (uint32_t)N * RB);
   const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.x, (uint32_t)M * (uint32_t)K * 2u);
-  const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(a.scales, (uint32_t)N * (uint32_t)G * 2u);
-  const __amdgpu_buffer_rsrc_t br = buffer_rsrc(a.biases, (uint32_t)N * (uint32_t)G * 2u);
-  const __amdgpu_buffer_rsrc_t w0 = buffer_rsrc(a.w, 0u);
+  const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(mat.scales, (uint32_t)N * (uint32_t)G * 2u);
+  const __amdgpu_buffer_rsrc_t br = buffer_rsrc(mat.biases, (uint32_t)N * (uint32_t)G * 2u);
+  const __amdgpu_buffer_rsrc_t w0 = buffer_rsrc(mat.w, 0u);
   const __amdgpu_buffer_rsrc_t x0 = buffer_rsrc(a.x, 0u);
-  const __amdgpu_buffer_rsrc_t s0 = buffer_rsrc(a.scales, 0u);
-  const __amdgpu_buffer_rsrc_t b0 = buffer_rsrc(a.biases, 0u);
+  const __amdgpu_buffer_rsrc_t s0 = buffer_rsrc(mat.scales, 0u);
+  const __amdgpu_buffer_rsrc_t b0 = buffer_rsrc(mat.biases, 0u);
 
   // Per-thread load offsets inside a range.  Activation piece i: p = tid +
   // 256 i, row p / PCS, piece p % PCS.  Scale unit i: u = tid + 256 i, row
@@ -315,7 +316,7 @@ __global__ __launch_bounds__(MR_NT, 1) void qmv_mr_kernel(const QmvMrArgs a) {
 #pragma unroll
       for (int j = 0; j < YV; j++) {
         const int m = (16 * u + 4 * g) / S + j;
-        if (m < M) a.out[(int64_t)m * N + nrow] = (uint16_t)f32_to_xt<XT>(y[u][j]);
+        if (m < M) mat.out[(int64_t)m * N + nrow] = (uint16_t)f32_to_xt<XT>(y[u][j]);
       }
   }
 }

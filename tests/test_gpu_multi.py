@@ -2,8 +2,10 @@
 activation: q/k/v, gate/up): every output is bit for bit the separate
 mlxq_quantized_matmul call's, and within max|y - y_ref| / max|y_ref| <= 1e-2
 of the oracle.  Decode rows (1-2, and 3-4 over long rows) take the single
-row-streaming launch over all projections; other row counts, and forced
-kernels, run the calls one after another and must give the same bytes.
+row-streaming launch over all projections; 3-16 rows where every projection
+takes the same mid-size kernel take one launch of it (and one reduction of
+the split-K partials); other row counts, and forced kernels, run the calls
+one after another and must give the same bytes.
 """
 import numpy as np
 import pytest
@@ -140,3 +142,61 @@ def test_argument_errors():
         mq.quantized_matmul_multi(xd, [dev[0][0], bad], [d[1] for d in dev], [d[2] for d in dev], 64, 4)
     with pytest.raises(ValueError):  # more than four projections
         mq.quantized_matmul_multi(xd, [dev[0][0]] * 5, [dev[0][1]] * 5, [dev[0][2]] * 5, 64, 4)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M", [5, 8, 16])
+def test_qkv_mid_one_launch(bits, M):
+    # 5-16 rows: q/k/v of the Qwen3-8B shape each take the split-K mid-size
+    # kernel alone, so the three run as one launch and one reduction
+    announce("multi_qkv_mid", bits, M)
+    K = 4096
+    x = orc.normal_bf16((M, K), 1.0, 1900 + M)
+    check(x, affine_sets([4096, 1024, 1024], K, bits, 64, 1910 + bits), 64, bits)
+
+
+@pytest.mark.parametrize("M", [3, 4, 8, 16])
+def test_gate_up_whole_row_one_launch(M):
+    # 3-16 rows: gate/up (12288 rows each) each take the whole-row kernel
+    # alone, so the two run as one launch
+    announce("multi_gate_up_mr", M)
+    K = 4096
+    x = orc.normal_bf16((M, K), 1.0, 1920 + M)
+    check(x, affine_sets([12288, 12288], K, 4, 64, 1930), 64, 4)
+
+
+@pytest.mark.parametrize("gs", [32, 128])
+def test_mid_one_launch_ragged(gs):
+    # ragged widths (partial 128-row blocks, widths not a multiple of 4: the
+    # reduction's scalar path), K with several splits
+    announce("multi_mid_ragged", gs)
+    K = 8192
+    x = orc.normal_bf16((12, K), 1.0, 1940 + gs)
+    check(x, affine_sets([1030, 77, 513], K, 4, gs, 1950 + gs), gs, 4)
+
+
+def test_mid_one_launch_graph_replays():
+    announce("multi_mid_graph")
+    K, M = 4096, 8
+    sets = affine_sets([4096, 1024, 1024], K, 4, 64, 1960)
+    dev = [(dev_u32(w), dev_bf16(s), dev_bf16(b)) for w, s, b in sets]
+    xs = [orc.normal_bf16((M, K), 1.0, 1961 + i) for i in range(3)]
+    xd = dev_bf16(xs[0])
+    outs = [torch.empty(M, N, dtype=torch.bfloat16, device="cuda") for N in (4096, 1024, 1024)]
+    args = ([d[0] for d in dev], [d[1] for d in dev], [d[2] for d in dev], 64, 4)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        mq.quantized_matmul_multi(xd, *args, out=outs)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        mq.quantized_matmul_multi(xd, *args, out=outs)
+    torch.cuda.synchronize()
+    for i in (0, 1, 2, 1):
+        xd.copy_(dev_bf16(xs[i]))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, (w, s, b) in zip(outs, dev):
+            np.testing.assert_array_equal(host_u16(o), host_u16(mq.quantized_matmul(xd, w, s, b)))
