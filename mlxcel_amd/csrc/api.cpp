@@ -534,6 +534,7 @@ struct Knobs {
   int mr_ring = 0;  // its weight ring depth in windows (0: planner)
   int gen_ks = 0;  // K splits of the general kernel (0: planner)
   int gather_sorted = 1, gather_group = -1, gather_runs = 2, gather_direct = 1;
+  int red_vec = 0;  // outputs per thread of the mid-size kernel's split-K reduction (0: default)
   std::string qmv_kernel;  // "", "rs", "b4", "mid", "mr", "fr", "mfma"
 };
 
@@ -562,6 +563,7 @@ const Knobs* read_knobs() {
   k->gather_group = env_int("MLXQ_GATHER_GROUP", -1);
   k->gather_runs = env_int("MLXQ_GATHER_RUNS", 2);
   k->gather_direct = env_int("MLXQ_GATHER_DIRECT", 1);
+  k->red_vec = env_int("MLXQ_REDUCE_VEC", 0);
   const char* v = std::getenv("MLXQ_QMV_KERNEL");
   k->qmv_kernel = v ? v : "";
   return k;
@@ -1115,6 +1117,7 @@ bool try_mid_f16(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, co
   m.gs_shift = shift;
   m.ks = mp.ks;
   m.xt = 1;
+  m.red_vec = knobs().red_vec;
   if (mp.ks > 1)
     m.ws = reinterpret_cast<float*>(workspace(dev, stream, (size_t)mp.ks * rows * sp.N * sizeof(float), ss));
   hip_check(mlxq::qmv_mid_launch(fmt, m, mp, stream), "qmv_mid launch");
@@ -1230,6 +1233,7 @@ mlxq::QmvMidArgs mid_args(const QmmSpec& sp, const uint16_t* x, int64_t rows, co
   m.K = (int)sp.K;
   m.gs_shift = gs_shift_of(sp.gs);
   m.ks = ks;
+  m.red_vec = knobs().red_vec;
   return m;
 }
 

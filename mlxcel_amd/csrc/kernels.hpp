@@ -241,6 +241,7 @@ struct QmvMidArgs {
   int ks;                  // K ranges (gridDim.y)
   int xt;                  // 16-bit type of x / scales / biases / out: 0 bfloat16, 1 float16
   QmvMatTable mt;          // several matrices (mt.n > 1)
+  int red_vec;             // outputs per thread of the split-K reduction (1, 2, 4; 0: default)
 };
 struct QmvMidLds {
   int xpitch = 0;  // bf16 per staged activation row
@@ -373,7 +374,7 @@ hipError_t launch_splitk_reduce(const float* ws, uint16_t* out, int64_t n, int k
 // The same sum over the partials [ks][M][t.ntot] of several matrices, each
 // column written to its matrix's output (the split order as above).
 hipError_t launch_splitk_reduce_multi(const float* ws, const QmvMatTable& t, int M, int ks, hipStream_t stream,
-                                      int xt = 0);
+                                      int xt = 0, int vec = 0);
 
 // Elementwise conversions (dequant.hip).
 hipError_t launch_affine_dequantize(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,

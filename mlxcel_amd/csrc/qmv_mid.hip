@@ -400,8 +400,15 @@ hipError_t qmv_mid_launch(int fmt, const QmvMidArgs& a, const QmvMidPlan& p, hip
     e = p.s == 2 ? mid_launch_s<AFF8, 2>(p, a, stream) : mid_launch_s<AFF8, 1>(p, a, stream);
   }
   if (e != hipSuccess || p.ks == 1) return e;
-  if (a.mt.n > 1) return launch_splitk_reduce_multi(a.ws, a.mt, a.M, p.ks, stream, a.xt);
-  return launch_splitk_reduce(a.ws, a.out, (int64_t)a.M * a.N, p.ks, stream, a.xt);
+  QmvMatTable t = a.mt;
+  if (t.n <= 1) {
+    t.n = 1;
+    t.ntot = a.N;
+    t.N[0] = a.N;
+    t.noff[0] = 0;
+    t.out[0] = a.out;
+  }
+  return launch_splitk_reduce_multi(a.ws, t, a.M, p.ks, stream, a.xt, a.red_vec);
 }
 
 }  // namespace mlxq
