@@ -51,11 +51,11 @@ SETTLE_MS = 60.0  # untimed replays before each prefill measurement (see timed)
 GATE_REPLAYS = 12  # replays of the 8-launch gate graph behind `roofline` (>= 96 launches)
 # HBM bytes per gate launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on
 # `bench.py --traffic-probe`, each counter scaled by what it reads for a
-# device copy of exactly 256 MiB (FETCH_SIZE x 1.999799, WRITE_SIZE x 1.0):
-# 16198.5 KiB fetched + 56 KiB written per launch of qmv_rs_dense_kernel
-# (profiles/qmv_rs_gate_m1_traffic.txt), 1.0049 x the algorithmic bytes.
-# Re-measure when the kernel changes.
-TRAFFIC_GATE = 33_228_536
+# device copy of exactly 256 MiB (FETCH_SIZE x 1.999800, WRITE_SIZE x 1.0):
+# 16207.6 KiB fetched + 56 KiB written per launch of qmv_rs_dense_kernel
+# (profiles/qmv_rs_gate_m1_traffic.txt, build 827e1df), 1.0054 x the
+# algorithmic bytes.  Re-measure when qmv_rs.hip or common.hpp changes.
+TRAFFIC_GATE = 33_247_110
 
 
 def qmv_bytes(M, N, K, bits, gs):
