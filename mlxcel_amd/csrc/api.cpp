@@ -535,6 +535,7 @@ struct Knobs {
   int gen_ks = 0;  // K splits of the general kernel (0: planner)
   int gather_sorted = 1, gather_group = -1, gather_runs = 2, gather_direct = 1;
   int red_vec = 0;  // outputs per thread of the mid-size kernel's split-K reduction (0: default)
+  int qmm_mix = 1;  // prefill: two-launch plan for a part-full last round of tiles (0: off)
   std::string qmv_kernel;  // "", "rs", "b4", "mid", "mr", "fr", "mfma"
 };
 
@@ -564,6 +565,7 @@ const Knobs* read_knobs() {
   k->gather_runs = env_int("MLXQ_GATHER_RUNS", 2);
   k->gather_direct = env_int("MLXQ_GATHER_DIRECT", 1);
   k->red_vec = env_int("MLXQ_REDUCE_VEC", 0);
+  k->qmm_mix = env_int("MLXQ_QMM_MIX", 1);
   const char* v = std::getenv("MLXQ_QMV_KERNEL");
   k->qmv_kernel = v ? v : "";
   return k;
@@ -1134,7 +1136,7 @@ bool try_qmm_f16(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, co
   const int dev = current_device();
   const int tile_req = knobs().qmm_tile >= 4 ? knobs().qmm_tile : -1;
   const mlxq::QmmPlan qp = mlxq::qmm_plan(fmt, sp.gs, rows, sp.N, sp.K, device_info(dev).cus, tile_req,
-                                          knobs().qmm_ksplit);
+                                          knobs().qmm_ksplit, knobs().qmm_mix);
   if (!qp.ok || qp.tile < 4) return false;
   mlxq::QmmArgs q{};
   q.x = static_cast<const uint16_t*>(x->data);
@@ -1389,7 +1391,7 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
     const int dev = current_device();
     // MLXQ_QMM_TILE / MLXQ_QMM_KSPLIT: A/B overrides of the tile shape and K split
     const mlxq::QmmPlan qp = mlxq::qmm_plan(fmt, sp.gs, rows_total, sp.N, sp.K, device_info(dev).cus,
-                                            knobs().qmm_tile, knobs().qmm_ksplit);
+                                            knobs().qmm_tile, knobs().qmm_ksplit, knobs().qmm_mix);
     if (qp.ok) {
       mlxq::QmmArgs q{};
       q.x = a.x;

@@ -350,6 +350,7 @@ struct QmmArgs {
   // dimension and whether consecutive tiles advance along M (1) or N (0).
   int tiles_m, tiles_n, m_fast;
   int xt;                  // 16-bit type of x / scales / biases / out: 0 bfloat16, 1 float16 (tile kernel, affine)
+  int ldo;                 // row stride of out in elements (0: N); tile kernel without a K split
 };
 struct QmmPlan {
   bool ok = false;
@@ -360,13 +361,19 @@ struct QmmPlan {
   int rows_per_tile = 256;
   int tiles_n = 1, tiles_m = 1, ksplit = 1, ksteps_per_split = 1;
   int m_fast = 0;  // tile kernel: consecutive workgroups walk along M
+  // Two launches (tile2 >= 0): output columns [0, n_first) on `tile` in
+  // whole rounds of the CUs, then [n_first, N) on the narrower tile2
+  // (tiles_n2 tiles along N) in one round.  tiles_n is the first launch's.
+  int tile2 = -1, n_first = 0, tiles_n2 = 0;
 };
 // rows of x per output tile of a tile code (0 if unknown)
 int qmm_tile_rows(int tile);
 // Grouped gather: tiles along N for `tile`; tiles_m = segments is set by the caller.
 QmmPlan qmm_plan_grouped(int fmt, int gs, int64_t N, int64_t K, int tile);
 // tile_req / ksplit_req < 0 (or 0 for ksplit) choose by shape.
-QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus, int tile_req, int ksplit_req);
+// mix: allow the two-launch plan (tile2) when neither tile nor split is requested.
+QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus, int tile_req, int ksplit_req,
+                 int mix = 1);
 hipError_t qmm_launch(int fmt, const QmmArgs& a, const QmmPlan& p, hipStream_t stream);
 // out[i] = bf16(sum over z < ks of ws[z * n + i]) (qmv.hip)
 // out (16-bit type xt: 0 bfloat16, 1 float16) = sum over ks fp32 partials, in split order

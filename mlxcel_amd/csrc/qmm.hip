@@ -708,13 +708,14 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
         }
       }
     __syncthreads();
-    const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0;
+    const int64_t ldo = a.ldo > 0 ? a.ldo : N;  // output row stride (a column block of a wider result)
+    const bool vec = ((N | ldo) & 7) == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0;
     for (int idx = t; idx < BM * CPR; idx += NT) {
       const int m = idx / CPR, c = idx - m * CPR;
       const int n = n0 + 8 * c;
       if (m >= rows || n >= N) continue;
       const u32x4 v = *reinterpret_cast<const u32x4*>(ot + m * BN + ((c ^ (m & (CPR - 1))) << 3));
-      uint16_t* dst = a.out + out_row(m) * N + n;
+      uint16_t* dst = a.out + out_row(m) * ldo + n;
       if (vec) {
         *reinterpret_cast<u32x4*>(dst) = v;
       } else {
@@ -773,7 +774,8 @@ bool is_tile_kernel(int tile) { return tile >= 4; }
 
 int qmm_tile_rows(int tile) { return tile >= 0 && tile < kTiles ? kBM[tile] : 0; }
 
-QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus, int tile_req, int ksplit_req) {
+QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus, int tile_req, int ksplit_req,
+                 int mix) {
   QmmPlan p;
   const int bits = fmt == AFF8 ? 8 : 4;
   if (K % BK != 0 || K % gs != 0 || M <= 0 || N <= 0) return p;
@@ -825,20 +827,65 @@ QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus, 
   // along the dimension whose operand is the smaller of the two to re-read
   p.m_fast = M * K * 2 <= N * K * bits / 8 ? 1 : 0;
   p.ok = tiles * p.ksplit < ((int64_t)1 << 31);
+  // Part-full last round: more 256 x 256 tiles than CUs, and the columns
+  // past the whole rounds fit one round of 256 x 128 tiles.  Whole columns
+  // of 256 x 256 tiles fill the full rounds, the rest runs as that one round
+  // of the narrower tile, about 0.65 of a 256 x 256 tile's time (MI355X,
+  // gate/up K=4096: M=1280-1536 x N=14336 202 us vs 233, M=2048 x N=12288
+  // 214 vs 234).  A 256 x 192 tail for M=2048 x N=14336 measured slower
+  // than the second 256 x 256 round (246 vs 240), so none is planned there.
+  if (mix && tile_req < 0 && ksplit_req <= 0 && p.tile == 4 && p.ksplit == 1 && tiles > num_cus) {
+    const int64_t nb = (tiles / num_cus) * num_cus / p.tiles_m;  // 256-wide column tiles in whole rounds
+    const int64_t n1 = nb * kBN[4];
+    const int64_t tn2 = (N - n1 + kBN[8] - 1) / kBN[8];
+    if (n1 > 0 && n1 < N && tn2 * p.tiles_m <= num_cus) {
+      p.tile2 = 8;
+      p.n_first = (int)n1;
+      p.tiles_n2 = (int)tn2;
+      p.tiles_n = (int)nb;
+    }
+  }
   return p;
 }
 
 namespace {
 template <int FMT, int XT>
-void qmm_tile_launch(const QmmArgs& a, const QmmPlan& p, hipStream_t stream) {
-  const dim3 grid((unsigned)((int64_t)p.tiles_m * p.tiles_n * p.ksplit));
-  switch (p.tile) {
+void qmm_tile_launch1(const QmmArgs& a, int tile, int ksplit, hipStream_t stream) {
+  const dim3 grid((unsigned)((int64_t)a.tiles_m * a.tiles_n * ksplit));
+  switch (tile) {
     case 4: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 256, 256, 2, 4, XT>), grid, dim3(512), 0, stream, a); break;
     case 5: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 256, 128, 2, 2, XT>), grid, dim3(256), 0, stream, a); break;
     case 7: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 256, 256, 2, 2, XT>), grid, dim3(256), 0, stream, a); break;
     case 8: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 256, 128, 4, 2, XT>), grid, dim3(512), 0, stream, a); break;
     default: hipLaunchKernelGGL((qmm_tile_kernel<FMT, 128, 128, 2, 2, XT>), grid, dim3(256), 0, stream, a); break;
   }
+}
+
+template <int FMT, int XT>
+void qmm_tile_launch(const QmmArgs& a, const QmmPlan& p, hipStream_t stream) {
+  if (p.tile2 < 0) {
+    qmm_tile_launch1<FMT, XT>(a, p.tile, p.ksplit, stream);
+    return;
+  }
+  // columns [0, n_first) on p.tile, then [n_first, N) on p.tile2: the second
+  // launch sees the weight rows, scale rows and result columns from n_first
+  // on, with the result's full row stride
+  QmmArgs a1 = a;
+  a1.N = p.n_first;
+  a1.ldo = a.N;
+  qmm_tile_launch1<FMT, XT>(a1, p.tile, 1, stream);
+  constexpr int BITS = FMT == AFF8 ? 8 : 4;
+  const int64_t n1 = p.n_first;
+  const int64_t groups = (int64_t)a.K >> a.gs_shift;
+  QmmArgs a2 = a;
+  a2.w = a.w + n1 * ((int64_t)a.K * BITS / 32);
+  a2.scales = reinterpret_cast<const uint8_t*>(a.scales) + n1 * groups * (FMT != MXFP4 ? 2 : 1);
+  a2.biases = a.biases ? a.biases + n1 * groups : a.biases;
+  a2.out = a.out + n1;
+  a2.N = a.N - p.n_first;
+  a2.ldo = a.N;
+  a2.tiles_n = p.tiles_n2;
+  qmm_tile_launch1<FMT, XT>(a2, p.tile2, 1, stream);
 }
 
 template <int FMT>

@@ -102,3 +102,36 @@ def test_llama_prefill_shapes_vs_dequant_fp32(monkeypatch, tile, bits, M, N, K):
     ref = x.float() @ wd.t()
     err = float((y - ref).abs().max() / ref.abs().max())
     assert err <= TOL, err
+
+
+@pytest.mark.parametrize("mode", ["affine4", "affine8", "mxfp4", "float16"])
+@pytest.mark.parametrize("M,N", [(2048, 12288), (1536, 12288), (1280, 14336), (1999, 12200)])
+def test_two_launch_tail_round_bitwise(monkeypatch, mode, M, N):
+    # More 256 x 256 tiles than CUs (256 on MI355X) with a part-full last
+    # round: whole tile columns in full rounds, the columns left as one round
+    # of 256 x 128 tiles (1999 x 12200: ragged last row and column tiles).
+    # Each output is the same MFMA sequence either way, so the result is
+    # bitwise the single-launch plan's (MLXQ_QMM_MIX=0); the whole result is
+    # checked against a float32 product of the bit-exact dequantized weights.
+    K = 1024
+    announce("qmm_mix", mode, M, N)
+    g = torch.Generator(device="cuda").manual_seed(2600 + M)
+    dt = torch.float16 if mode == "float16" else torch.bfloat16
+    w = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(dt)
+    x = torch.randn(M, K, device="cuda", generator=g).to(dt)
+    if mode == "mxfp4":
+        wq, s = mq.quantize(w, 32, 4, "mxfp4")
+        args, gs, bits, md = (wq, s, None), 32, 4, "mxfp4"
+    else:
+        bits = 8 if mode == "affine8" else 4
+        wq, s, b = mq.quantize(w, 64, bits)
+        args, gs, md = (wq, s, b), 64, "affine"
+    mixed = mq.quantized_matmul(x, *args, True, gs, bits, md)
+    setknob(monkeypatch, "MLXQ_QMM_MIX", "0")
+    single = mq.quantized_matmul(x, *args, True, gs, bits, md)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host_u16(mixed), host_u16(single))
+    wd = mq.dequantize(*args, gs, bits, md).float()
+    ref = x.float() @ wd.t()
+    err = float((mixed.float() - ref).abs().max() / ref.abs().max())
+    assert err <= TOL, err
