@@ -72,11 +72,13 @@ def _compile(name: str, extra: list[str]) -> str:
 
 def _verify_group_ring_waits() -> None:
     """qmm_group.hip waits for its LDS ring with a hand-counted
-    `s_waitcnt vmcnt(16)`: 2 younger blocks of 8 vector-memory instructions
-    each (4 direct-to-LDS activation loads, 2 weight and 2 scale loads per
-    wave).  If the compiler ever emitted a different number per block the
-    wait would be wrong, so check the kernel's AMD assembly (built here): 3
-    blocks before the first wait, then exactly 8 loads after each of the 4
+    `s_waitcnt vmcnt(2 n)`: 2 younger blocks of n vector-memory instructions
+    each per wave (4 direct-to-LDS activation loads and 2 weight loads, plus 2
+    scale loads in the instantiation without the LDS scale table: n = 8, else
+    n = 6).  If the compiler ever emitted a different number per block the
+    wait would be wrong, so check each instantiation's AMD assembly (built
+    here): 3 blocks before the first wait (and, with the scale table, its one
+    staging load ahead of them), then exactly n loads after each of the 4
     waits of a ring turn."""
     src = os.path.join(CSRC, "qmm_group.hip")
     asm = os.path.join(BUILD, "qmm_group.device.s")
@@ -85,19 +87,29 @@ def _verify_group_ring_waits() -> None:
     if r.returncode != 0:
         raise RuntimeError(f"hipcc -S failed for qmm_group.hip:\n{r.stderr}")
     lines = open(asm).read().splitlines()
-    start = next(i for i, l in enumerate(lines) if l.startswith("_ZN4mlxq22qmm_group_mxfp4_kernel"))
-    end = next(i for i in range(start, len(lines)) if "s_endpgm" in lines[i])
-    body = [l.strip() for l in lines[start:end]]
-    marks = [i for i, l in enumerate(body) if l.startswith("s_waitcnt vmcnt(16)")]
-    if len(marks) != 4:
-        raise RuntimeError(f"qmm_group ring check: expected 4 ring waits, found {len(marks)}")
-    loads = lambda a, b: sum(1 for l in body[a:b] if l.startswith("buffer_load"))
-    bounds = marks + [next(i for i in range(marks[-1], len(body)) if body[i].startswith("s_waitcnt vmcnt(0)"))]
-    per = [loads(bounds[k] + 1, bounds[k + 1]) for k in range(4)]
-    pro = loads(0, marks[0])
-    if per != [8, 8, 8, 8] or pro != 24:
-        raise RuntimeError(f"qmm_group ring check: loads per ring step {per}, prologue {pro} "
-                           "(the kernel's vmcnt(16) assumes 8 per step and 24 before the first wait)")
+    prefix = "_ZN4mlxq22qmm_group_mxfp4_kernelILi"
+    starts = [i for i, l in enumerate(lines) if l.startswith(prefix) and l.split(";")[0].rstrip().endswith(":")]
+    seen = set()
+    for start in starts:
+        scl = int(lines[start][len(prefix):].split("E", 1)[0])
+        n = 8 if scl == 0 else 6
+        end = next(i for i in range(start, len(lines)) if "s_endpgm" in lines[i])
+        body = [l.strip() for l in lines[start:end]]
+        wait = f"s_waitcnt vmcnt({2 * n})"
+        marks = [i for i, l in enumerate(body) if l == wait and body[i + 1].startswith("s_barrier")]
+        if len(marks) != 4:
+            raise RuntimeError(f"qmm_group<{scl}> ring check: expected 4 ring waits, found {len(marks)}")
+        loads = lambda a, b: sum(1 for l in body[a:b] if l.startswith("buffer_load"))
+        bounds = marks + [next(i for i in range(marks[-1], len(body)) if body[i].startswith("s_waitcnt vmcnt(0)"))]
+        per = [loads(bounds[k] + 1, bounds[k + 1]) for k in range(4)]
+        pro = loads(0, marks[0])
+        want_pro = 3 * n + (0 if scl == 0 else 1)
+        if per != [n] * 4 or pro != want_pro:
+            raise RuntimeError(f"qmm_group<{scl}> ring check: loads per ring step {per}, prologue {pro} "
+                               f"(the kernel's vmcnt({2 * n}) assumes {n} per step and {want_pro} before the first wait)")
+        seen.add(scl)
+    if seen != {0, 4, 16}:
+        raise RuntimeError(f"qmm_group ring check: instantiations {sorted(seen)}, expected [0, 4, 16]")
 
 
 def build(verbose: bool = True) -> str:

@@ -536,6 +536,8 @@ struct Knobs {
   int gather_sorted = 1, gather_group = -1, gather_runs = 2, gather_direct = 1;
   int red_vec = 0;  // outputs per thread of the mid-size kernel's split-K reduction (0: default)
   int qmm_mix = 1;  // prefill: two-launch plan for a part-full last round of tiles (0: off)
+  int mid_win = 0;  // mid-size kernel: windows per workgroup (4 or 8; 0: planner)
+  int gather_scale_table = 1;  // grouped sorted gather: scales staged in LDS where they fit (0: per block)
   std::string qmv_kernel;  // "", "rs", "b4", "mid", "mr", "fr", "mfma"
 };
 
@@ -566,6 +568,8 @@ const Knobs* read_knobs() {
   k->gather_direct = env_int("MLXQ_GATHER_DIRECT", 1);
   k->red_vec = env_int("MLXQ_REDUCE_VEC", 0);
   k->qmm_mix = env_int("MLXQ_QMM_MIX", 1);
+  k->mid_win = env_int("MLXQ_QMV_MID_WIN", 0);
+  k->gather_scale_table = env_int("MLXQ_GATHER_SCALE_TABLE", 1);
   const char* v = std::getenv("MLXQ_QMV_KERNEL");
   k->qmv_kernel = v ? v : "";
   return k;
@@ -1102,7 +1106,8 @@ bool try_mid_f16(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, co
   if (!f16_affine(sp, x, scales, biases) || rows < 1 || rows > 16) return false;
   if (!forced && (rows < kMidMinRows || knobs().qmv_mid == 0 || !knobs().qmv_kernel.empty())) return false;
   const int fmt = fmt_of(sp.mode, sp.bits);
-  const mlxq::QmvMidPlan mp = mlxq::qmv_mid_plan(fmt, sp.gs, sp.N, sp.K, (int)rows);
+  const mlxq::QmvMidPlan mp =
+      mlxq::qmv_mid_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, device_info(current_device()).cus, knobs().mid_win);
   if (!mp.ok) return false;
   const int dev = current_device();
   mlxq::QmvMidArgs m{};
@@ -1196,7 +1201,7 @@ DenseRoute dense_route(const QmmSpec& sp, int64_t rows, int cus) {
       return r;
     }
   }
-  r.mid = mlxq::qmv_mid_plan(fmt, sp.gs, sp.N, sp.K, (int)rows);
+  r.mid = mlxq::qmv_mid_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, knobs().mid_win);
   if (r.mid.ok) r.kind = DR_MID;
   return r;
 }
@@ -1599,7 +1604,8 @@ void gather_run(GatherSpec& g, const mlxq_array* x, const mlxq_array* w, const m
       knobs().gather_sorted != 0) {
     const DirectIdx dl = direct_index(lhs_indices, dsh[0], g.idx_shape);
     const DirectIdx dr = direct_index(rhs_indices, dsh[1], g.idx_shape);
-    const mlxq::QmmGroupPlan gp = mlxq::qmm_group_plan(fmt, sp.N, sp.K, E, B);
+    mlxq::QmmGroupPlan gp = mlxq::qmm_group_plan(fmt, sp.N, sp.K, E, B);
+    if (knobs().gather_scale_table == 0) gp.scale_table = false;
     if (gp.ok && dr.ok && dr.p && dl.ok && !dl.p && dl.div == 1) {
       mlxq::QmmGroupArgs q{};
       q.x = static_cast<const uint16_t*>(x->data);

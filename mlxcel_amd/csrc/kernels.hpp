@@ -257,7 +257,9 @@ struct QmvMidPlan {
   int sw = 8;          // scale groups per staging load
   size_t lds = 0;
 };
-QmvMidPlan qmv_mid_plan(int fmt, int gs, int64_t N, int64_t K, int rows);
+// cus: the device's CUs (the K range halves when the full one leaves CUs
+// idle); win_req 4 or 8 forces the windows per workgroup.
+QmvMidPlan qmv_mid_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int cus = 0, int win_req = 0);
 // Launches the kernel and, with several K ranges, the fixed-order reduction.
 hipError_t qmv_mid_launch(int fmt, const QmvMidArgs& a, const QmvMidPlan& p, hipStream_t stream);
 
@@ -304,6 +306,7 @@ struct QmmGroupArgs {
 struct QmmGroupPlan {
   bool ok = false;
   int row_blocks = 0;  // workgroups along N (128 weight rows each)
+  bool scale_table = false;  // K / 32 scale bytes per row fit the kernel's LDS table
 };
 QmmGroupPlan qmm_group_plan(int fmt, int64_t N, int64_t K, int64_t E, int64_t B);
 hipError_t qmm_group_launch(const QmmGroupArgs& a, const QmmGroupPlan& p, hipStream_t stream);

@@ -29,6 +29,14 @@
 // distinct banks), and its weights and scales into one of 4 register slots;
 // both run 3 blocks ahead of the block being multiplied, with no registers
 // spent on activations in flight.
+//
+// Scales: the workgroup's 128 scale rows are one contiguous range of the
+// expert's e8m0 bytes; where they fit (K <= 4096) and are aligned, a few
+// wide direct-to-LDS loads bring them into an LDS table once, ahead of the
+// ring, and each block reads its byte from there.  Otherwise every block
+// loads each lane's scale byte with the weights (one 64-lane byte load per
+// tile and block, 16 scattered rows: on MI355X 13% of the T=256 gate/up
+// gather's time at K=2880).
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -45,13 +53,18 @@ constexpr int GQ_NT = 64 * GQ_NW;
 constexpr int GQ_RING = 4;                   // blocks in the activation / weight rings
 constexpr int GQ_XB = GQ_MC * GQ_KB * 2;     // activation bytes per block (16 KiB, 256 per row)
 constexpr int GQ_XI = GQ_XB / 1024 / GQ_NW;  // 1 KiB direct-to-LDS loads per wave and block (4)
+constexpr int GQ_STB = GQ_ROWS * 128;       // LDS scale table: 128 rows of up to 128 e8m0 bytes (K <= 4096)
 
 }  // namespace
 
+// SCL: 0, scale bytes loaded per block; 4 or 16, the scale table staged in
+// LDS by direct loads of that many bytes per lane.
+template <int SCL>
 __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGroupArgs a) {
   // the ring as four LDS objects, so the compiler's wait analysis sees that
   // a buffer being refilled is not the one being read
   __shared__ __align__(16) unsigned char xl0[GQ_XB], xl1[GQ_XB], xl2[GQ_XB], xl3[GQ_XB];
+  __shared__ __align__(16) unsigned char stb[SCL ? GQ_STB : 16];
   static_assert(GQ_RING == 4, "four ring buffers");
   auto ring = [&](int slot) -> unsigned char* { return slot == 0 ? xl0 : slot == 1 ? xl1 : slot == 2 ? xl2 : xl3; };
 
@@ -103,11 +116,35 @@ __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGrou
     const uint32_t o = (srow[t] != kDeadOfs && c < nchunk) ? srow[t] + (uint32_t)c : kDeadOfs;
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(sr, o, 0, 0);
   };
+  // Scale table (SCL != 0): table row r = weight row nb0 + r, nchunk bytes
+  // each, read straight from the range that starts at row nb0; loads past
+  // the expert's scales read 0.  Issued before the ring, so the ring's first
+  // wait covers them.
+  if constexpr (SCL != 0) {
+    const int tb = min(GQ_ROWS, N - nb0) * nchunk;  // bytes of this row block's scale rows
+    constexpr int PER = 64 * SCL;                   // bytes per wave load
+    for (int i = wave; i * PER < tb; i += GQ_NW) {
+      auto* dst = (__attribute__((address_space(3))) void*)(stb + i * PER);
+      const uint32_t o = (uint32_t)(nb0 * nchunk + i * PER + lane * SCL);
+      if constexpr (SCL == 16) __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, dst, 16, o, 0, 0, 0);
+      else __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, dst, 4, o, 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  bool slive[GQ_T];
+#pragma unroll
+  for (int t = 0; t < GQ_T; t++) slive[t] = srow[t] != kDeadOfs;
+  // the scale byte of tile t, chunk c (SCL != 0): rows past N and chunks
+  // past the row are 0 (a finite 2^-127), never another row's byte
+  auto sread = [&](int c, int t) -> uint32_t {
+    const int r = wave * (GQ_T * 16) + t * 16 + nl;
+    return (slive[t] && c < nchunk) ? (uint32_t)stb[r * nchunk + c] : 0u;
+  };
   // LDS layout of a block: row r at r * 256 bytes, its logical 16-byte chunk
   // c at position c ^ (r & 15).  Wave load j of wave w fills rows
   // 4 (w GQ_XI + j) .. +3: lane L writes row rr = 4 (w GQ_XI + j) + L / 16,
   // position L % 16, so it fetches logical chunk (L % 16) ^ (rr & 15).
-  constexpr int GQ_VMEM = GQ_XI + 2 * GQ_T;  // vector-memory instructions per block and wave
+  constexpr int GQ_VMEM = GQ_XI + (SCL ? 1 : 2) * GQ_T;  // vector-memory instructions per block and wave
 
   for (int r0 = lo; r0 < hi; r0 += GQ_MC) {
     const int cnt = min(GQ_MC, hi - r0);
@@ -140,7 +177,7 @@ __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGrou
 #pragma unroll
       for (int t = 0; t < GQ_T; t++) {
         wn[slot][t] = wload(b, t);
-        sn[slot][t] = sload(b, t);
+        if constexpr (SCL == 0) sn[slot][t] = sload(b, t);
       }
     };
 
@@ -173,9 +210,15 @@ __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGrou
         // no LDS read moves across either; a plain barrier, because the
         // workgroup fences of __syncthreads would also wait for the ring's
         // younger activation loads)
-        // (mlxcel_amd/build.py checks the emitted assembly for exactly 8 loads per block)
-        static_assert(GQ_VMEM * (GQ_RING - 2) == 16, "the wait below counts 2 blocks of 8 instructions");
-        asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+        // (mlxcel_amd/build.py checks the emitted assembly for exactly 8, or 6,
+        // loads per block)
+        if constexpr (SCL == 0) {
+          static_assert(SCL != 0 || GQ_VMEM * (GQ_RING - 2) == 16, "the wait below counts 2 blocks of 8");
+          asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+        } else {
+          static_assert(SCL == 0 || GQ_VMEM * (GQ_RING - 2) == 12, "the wait below counts 2 blocks of 6");
+          asm volatile("s_waitcnt vmcnt(12)\n\ts_barrier" ::: "memory");
+        }
         issue(b + GQ_RING - 1, (d + GQ_RING - 1) % GQ_RING, wn, sn);
         if (b >= nblk) continue;  // workgroup-uniform
         const unsigned char* xb = ring(d);
@@ -183,7 +226,7 @@ __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGrou
         bf16x8 B[GQ_T][4];
 #pragma unroll
         for (int t = 0; t < GQ_T; t++) {
-          const float sc = e8m0_to_f32(sn[d][t]);
+          const float sc = e8m0_to_f32(SCL ? sread(b * 4 + g, t) : sn[d][t]);
 #pragma unroll
           for (int q = 0; q < 4; q++) {
             uint32_t pr[4];
@@ -235,6 +278,7 @@ QmmGroupPlan qmm_group_plan(int fmt, int64_t N, int64_t K, int64_t E, int64_t B)
   QmmGroupPlan p;
   if (fmt != MXFP4 || N < 1 || K < 32 || K % 32 != 0 || E < 1 || B < 1) return p;
   p.row_blocks = (int)((N + GQ_ROWS - 1) / GQ_ROWS);
+  p.scale_table = K / 32 <= GQ_STB / GQ_ROWS;
   // buffer offsets are 32-bit and 0x80000000 marks a dead lane
   p.ok = N * (K / 2) < ((int64_t)1 << 31) && (int64_t)GQ_MC * K * 2 < ((int64_t)1 << 31) && E <= 65535 &&
          p.row_blocks <= 65535 && B * K * 2 < ((int64_t)1 << 40);
@@ -243,8 +287,17 @@ QmmGroupPlan qmm_group_plan(int fmt, int64_t N, int64_t K, int64_t E, int64_t B)
 
 hipError_t qmm_group_launch(const QmmGroupArgs& a, const QmmGroupPlan& p, hipStream_t stream) {
   if (!p.ok) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(qmm_group_mxfp4_kernel, dim3((unsigned)p.row_blocks, (unsigned)a.E), dim3(GQ_NT), 0, stream,
-                     a);
+  const dim3 grid((unsigned)p.row_blocks, (unsigned)a.E);
+  // the LDS scale table's direct loads need their source aligned to the
+  // load width: the scales' base and every expert's N * K / 32 bytes
+  const uintptr_t sb = reinterpret_cast<uintptr_t>(a.scales);
+  const int64_t eb = (int64_t)a.N * (a.K / 32);
+  if (p.scale_table && sb % 16 == 0 && eb % 16 == 0)
+    hipLaunchKernelGGL(qmm_group_mxfp4_kernel<16>, grid, dim3(GQ_NT), 0, stream, a);
+  else if (p.scale_table && sb % 4 == 0 && eb % 4 == 0)
+    hipLaunchKernelGGL(qmm_group_mxfp4_kernel<4>, grid, dim3(GQ_NT), 0, stream, a);
+  else
+    hipLaunchKernelGGL(qmm_group_mxfp4_kernel<0>, grid, dim3(GQ_NT), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -27,7 +27,9 @@
 // per pair.
 //
 // Each workgroup covers a K range of 8 windows (1024 k for 4-bit, 512 for
-// 8-bit); every wave keeps 4 windows of weight loads in flight per tile.  K ranges
+// 8-bit), or of 4 where 8 would give fewer workgroups than CUs (o and q/k/v
+// of an 8B model at 4096 x 4096); every wave keeps 4 windows of weight loads
+// in flight per tile.  K ranges
 // of one row block write fp32 partials that a second kernel adds in a fixed
 // order (bitwise reproducible).  (A last-workgroup-adds-them variant needs a
 // device-scope release/acquire per workgroup, which on MI355X writes back and
@@ -42,7 +44,7 @@ namespace {
 constexpr int MID_NW = 4;                      // waves per workgroup
 constexpr int MID_T = 2;                       // 16-row tiles per wave
 constexpr int MID_ROWS = MID_NW * MID_T * 16;  // weight rows per workgroup
-constexpr int MID_WIN = 8;                     // windows per workgroup
+constexpr int MID_WIN = 8;                     // windows per workgroup (4 when that fills the CUs)
 constexpr int MID_P = 4;                       // windows of weight loads in flight per tile
 constexpr int MID_NT = 64 * MID_NW;            // threads per workgroup
 
@@ -86,14 +88,15 @@ __host__ __device__ inline QmvMidLds qmv_mid_lds(int fmt, int gs, int kr, int na
 // own allocation.
 // XT: 16-bit type of activations, scales, biases and result (0 bfloat16, 1
 // float16: codes widen to float16 1024 + q, products on the float16 MFMA).
-template <int FMT, int S, int NA, int SW, int XT>
+// W: windows per workgroup (8, or 4).
+template <int FMT, int S, int NA, int SW, int XT, int W>
 __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const QmvMidArgs a) {
   constexpr int CK = FMT == AFF8 ? 16 : 32;  // k per 16-byte code chunk
   constexpr int KW = 4 * CK;                 // k per window (4 chunks)
   constexpr int NQ = CK / 8;                 // MFMAs per window, tile and A tile
   constexpr int XG = KW / S;                 // k per group slot of a window
   constexpr int YV = 4 / S;                  // activation rows per lane and A tile after the fold
-  constexpr int KR = MID_WIN * KW;           // k per workgroup
+  constexpr int KR = W * KW;                 // k per workgroup
   constexpr int XPMAX = 16 * KR / 8 / MID_NT;  // activation pieces per thread, upper bound
   constexpr int SPMAX = SW == 8 ? 2 : 4;     // scale loads per thread and operand, upper bound (checked on the host)
 
@@ -110,7 +113,7 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
   const int rb = mat.blk;
   const int sp = blockIdx.y;
   const int k0 = sp * kr;
-  constexpr int nwin = MID_WIN;  // every split is a full K range (K % KR == 0)
+  constexpr int nwin = W;  // every split is a full K range (K % KR == 0)
   const int G = K >> a.gs_shift;
   const int ngr = kr >> a.gs_shift;  // groups per K range
   const int spitch = ngr + 2;        // scale pairs per staged row
@@ -247,7 +250,7 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
 
   {
 #pragma unroll
-    for (int w = 0; w < MID_WIN; w++) {
+    for (int w = 0; w < W; w++) {
       u32x4 A[NA][NQ];
 #pragma unroll
       for (int t = 0; t < NA; t++)
@@ -263,7 +266,7 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
       for (int t = 0; t < MID_T; t++) {
         // ring slot w % MID_P: take window w, refill it with window w + MID_P
         const u32x4 wv = wbuf[w % MID_P][t];
-        if (w + MID_P < MID_WIN)
+        if (w + MID_P < W)
           wbuf[w % MID_P][t] = __builtin_bit_cast(
               u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                          wr, woff[t] == kDeadOfs ? kDeadOfs : woff[t] + (uint32_t)(w + MID_P) * 64u, 0, 0));
@@ -335,12 +338,18 @@ __global__ __launch_bounds__(MID_NT, NA == 1 ? 2 : 1) void qmv_mid_kernel(const 
 
 namespace {
 
+template <int FMT, int S, int NA, int XT, int W>
+hipError_t mid_launch_w(const QmvMidPlan& p, const QmvMidArgs& a, hipStream_t stream) {
+  const dim3 grid((unsigned)p.row_blocks, (unsigned)p.ks, 1);
+  if (p.sw == 8) hipLaunchKernelGGL((qmv_mid_kernel<FMT, S, NA, 8, XT, W>), grid, dim3(MID_NT), p.lds, stream, a);
+  else hipLaunchKernelGGL((qmv_mid_kernel<FMT, S, NA, 2, XT, W>), grid, dim3(MID_NT), p.lds, stream, a);
+  return hipGetLastError();
+}
+
 template <int FMT, int S, int NA, int XT>
 hipError_t mid_launch_xt(const QmvMidPlan& p, const QmvMidArgs& a, hipStream_t stream) {
-  const dim3 grid((unsigned)p.row_blocks, (unsigned)p.ks, 1);
-  if (p.sw == 8) hipLaunchKernelGGL((qmv_mid_kernel<FMT, S, NA, 8, XT>), grid, dim3(MID_NT), p.lds, stream, a);
-  else hipLaunchKernelGGL((qmv_mid_kernel<FMT, S, NA, 2, XT>), grid, dim3(MID_NT), p.lds, stream, a);
-  return hipGetLastError();
+  constexpr int kw = FMT == AFF8 ? 64 : 128;
+  return p.kr == 4 * kw ? mid_launch_w<FMT, S, NA, XT, 4>(p, a, stream) : mid_launch_w<FMT, S, NA, XT, 8>(p, a, stream);
 }
 
 template <int FMT, int S, int NA>
@@ -359,7 +368,7 @@ hipError_t mid_launch_s(const QmvMidPlan& p, const QmvMidArgs& a, hipStream_t st
 
 }  // namespace
 
-QmvMidPlan qmv_mid_plan(int fmt, int gs, int64_t N, int64_t K, int rows) {
+QmvMidPlan qmv_mid_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int cus, int win_req) {
   QmvMidPlan p;
   if (fmt != AFF4 && fmt != AFF8) return p;
   if (rows < 1 || rows > 16 || (gs != 32 && gs != 64 && gs != 128) || N < 1 || K < 1) return p;
@@ -372,6 +381,10 @@ QmvMidPlan qmv_mid_plan(int fmt, int gs, int64_t N, int64_t K, int rows) {
   p.row_blocks = (int)((N + MID_ROWS - 1) / MID_ROWS);
   p.kr = MID_WIN * kw;  // K per workgroup (a multiple of every group size)
   if (K % p.kr != 0) return p;
+  // half the K range where the full one leaves CUs without a workgroup
+  // (MI355X, 4096 x 4096 4-bit g64 at 16 rows: 256 workgroups instead of 128)
+  const bool half = win_req == 4 || (win_req != 8 && p.row_blocks * (K / p.kr) < cus);
+  if (half) p.kr = 4 * kw;
   p.ks = (int)(K / p.kr);
   const int64_t G = K / gs;
   const int ngr = p.kr / gs;

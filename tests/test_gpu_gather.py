@@ -369,3 +369,28 @@ def test_sorted_grouped_mxfp4_k(monkeypatch, K):
     setknob(monkeypatch, "MLXQ_GATHER_RUNS", "0")
     per_entry = host_u16(mq.gather_qmm(X, W, S, None, None, R, True, 32, 4, "mxfp4", sorted_indices=True))
     assert max_rel(per_entry, got) <= TOL
+
+
+@pytest.mark.parametrize("N,K", [(256, 2880), (100, 2880), (516, 96), (130, 96), (256, 4160)])
+def test_sorted_grouped_scale_table(monkeypatch, N, K):
+    # the expert-grouped kernel's scale sources: an LDS table staged with
+    # 16-byte direct loads (256 x 2880: every expert's 256 * 90 scale bytes a
+    # multiple of 16), with 4-byte loads (100 x 2880: 9000 bytes; 516 x 96),
+    # and per-block byte loads where the table does not apply (130 x 96: 390
+    # bytes per expert, not 4-aligned; K = 4160: 130 bytes per row, past the
+    # 128-byte table rows).  Each is bitwise the per-block loads' result
+    # (MLXQ_GATHER_SCALE_TABLE=0) and within tolerance of the oracle; a
+    # partial last 128-row block reads 0 for rows past N.
+    announce("gather_sorted_grouped_scales", N, K)
+    E, B = 8, 512
+    rhs = np.sort(np.random.default_rng(1990 + N + K).integers(0, E, B))
+    wq, sc = mx_experts(E, N, K, 1991 + N + K)
+    x = orc.normal_bf16((B, 1, K), 1.0, 1992 + N + K)
+    X, W, S = dev_bf16(x), dev_u32(wq), dev_u8(sc)
+    R = torch.from_numpy(rhs.astype(np.int32)).cuda()
+    got = host_u16(mq.gather_qmm(X, W, S, None, None, R, True, 32, 4, "mxfp4", sorted_indices=True))
+    want = orc.gather_qmm_t(x, wq, sc, None, np.arange(B, dtype=np.uint32), rhs.astype(np.uint32), mode="mxfp4")
+    assert max_rel(got, want) <= TOL
+    setknob(monkeypatch, "MLXQ_GATHER_SCALE_TABLE", "0")
+    per_block = host_u16(mq.gather_qmm(X, W, S, None, None, R, True, 32, 4, "mxfp4", sorted_indices=True))
+    np.testing.assert_array_equal(got, per_block)
