@@ -257,8 +257,8 @@ struct QmvMidPlan {
   int sw = 8;          // scale groups per staging load
   size_t lds = 0;
 };
-// cus: the device's CUs (the K range halves when the full one leaves CUs
-// idle); win_req 4 or 8 forces the windows per workgroup.
+// win_req 4 halves the K range per workgroup (8 windows otherwise); cus is
+// kept for plans that weigh the grid against the CUs.
 QmvMidPlan qmv_mid_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int cus = 0, int win_req = 0);
 // Launches the kernel and, with several K ranges, the fixed-order reduction.
 hipError_t qmv_mid_launch(int fmt, const QmvMidArgs& a, const QmvMidPlan& p, hipStream_t stream);

@@ -27,8 +27,7 @@
 // per pair.
 //
 // Each workgroup covers a K range of 8 windows (1024 k for 4-bit, 512 for
-// 8-bit), or of 4 where 8 would give fewer workgroups than CUs (o and q/k/v
-// of an 8B model at 4096 x 4096); every wave keeps 4 windows of weight loads
+// 8-bit; 4 windows on request); every wave keeps 4 windows of weight loads
 // in flight per tile.  K ranges
 // of one row block write fp32 partials that a second kernel adds in a fixed
 // order (bitwise reproducible).  (A last-workgroup-adds-them variant needs a
@@ -44,7 +43,7 @@ namespace {
 constexpr int MID_NW = 4;                      // waves per workgroup
 constexpr int MID_T = 2;                       // 16-row tiles per wave
 constexpr int MID_ROWS = MID_NW * MID_T * 16;  // weight rows per workgroup
-constexpr int MID_WIN = 8;                     // windows per workgroup (4 when that fills the CUs)
+constexpr int MID_WIN = 8;                     // windows per workgroup (4 on request)
 constexpr int MID_P = 4;                       // windows of weight loads in flight per tile
 constexpr int MID_NT = 64 * MID_NW;            // threads per workgroup
 
@@ -381,10 +380,13 @@ QmvMidPlan qmv_mid_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int cus
   p.row_blocks = (int)((N + MID_ROWS - 1) / MID_ROWS);
   p.kr = MID_WIN * kw;  // K per workgroup (a multiple of every group size)
   if (K % p.kr != 0) return p;
-  // half the K range where the full one leaves CUs without a workgroup
-  // (MI355X, 4096 x 4096 4-bit g64 at 16 rows: 256 workgroups instead of 128)
-  const bool half = win_req == 4 || (win_req != 8 && p.row_blocks * (K / p.kr) < cus);
-  if (half) p.kr = 4 * kw;
+  // Half the K range on request only.  MI355X, Qwen3-8B shapes, 4-bit g64,
+  // 16 rows (kernel + reduction): o 4096 x 4096 10.3 -> 9.4 us (256
+  // workgroups instead of 128), down 4096 x 12288 17.0 -> 16.1, but q/k/v in
+  // one launch 11.4 -> 13.0 (384 instead of 192); a q/k/v launch must give
+  // the bits of its single calls, and q has o's shape, so one rule for both.
+  (void)cus;
+  if (win_req == 4) p.kr = 4 * kw;
   p.ks = (int)(K / p.kr);
   const int64_t G = K / gs;
   const int ngr = p.kr / gs;
