@@ -121,3 +121,24 @@ def test_mid_unsupported_shapes_fall_back(mid):
     announce("mid_fallback")
     x, wq, s, b = affine_case(8, 96, 2880, 64, 4, 2600)
     assert max_rel(run(x, wq, s, b, 64, 4), orc.qmm_t_affine(x, wq, s, b, 64, 4)) <= TOL
+
+
+@pytest.mark.parametrize("bits,gs", [(4, 32), (4, 64), (4, 128), (8, 64), (8, 128)])
+@pytest.mark.parametrize("M", [5, 16])
+def test_mid_half_k_range(mid, monkeypatch, bits, gs, M):
+    # MLXQ_QMV_MID_WIN=4: K ranges of 4 windows (512 k for 4-bit, 256 for
+    # 8-bit; 8-bit g128 then has one group per two ranges' worth of windows
+    # staged two at a time), against the oracle, and a q/k/v launch bitwise
+    # equal to its single calls at the same setting
+    setknob(monkeypatch, "MLXQ_QMV_MID_WIN", "4")
+    announce("mid_half_k", bits, gs, M)
+    K = 2048
+    x, wq, s, b = affine_case(M, 200, K, gs, bits, 2700 + M + bits + gs)
+    assert max_rel(run(x, wq, s, b, gs, bits), orc.qmm_t_affine(x, wq, s, b, gs, bits)) <= TOL
+    setknob(monkeypatch, "MLXQ_QMV_KERNEL", "")
+    sets = [orc.affine_quantize(orc.normal_bf16((n, K), 0.02, 2710 + n), gs, bits) for n in (512, 128, 128)]
+    xd = dev_bf16(x)
+    dev = [(dev_u32(w), dev_bf16(sc), dev_bf16(bi)) for w, sc, bi in sets]
+    multi = mq.quantized_matmul_multi(xd, [d[0] for d in dev], [d[1] for d in dev], [d[2] for d in dev], gs, bits)
+    for m, d in zip(multi, dev):
+        np.testing.assert_array_equal(host_u16(m), host_u16(mq.quantized_matmul(xd, *d, True, gs, bits)))
