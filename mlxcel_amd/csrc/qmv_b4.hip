@@ -236,15 +236,13 @@ __device__ __forceinline__ void b4_pass(const QmvArgs& a, int gs_shift, float* r
         // times 2^k are exact in bf16) and the fold adds D.  2^-127 and NaN
         // (e8m0 0 and 255) are applied to D in fp32 instead, as MLX applies
         // the scale to the group sum: the products stay out of bf16's
-        // subnormal range.
+        // subnormal range.  One conversion either way (scale 1 for those two
+        // codes): a per-lane branch between two conversions compiled to
+        // exec-masked blocks that kept the scheduler from overlapping pieces.
         const uint32_t sb = W.sraw[c][g];
-        if (sb - 1u < 254u) {
+        const float cs = sb - 1u < 254u ? e8m0_to_f32(sb) : 1.0f;
 #pragma unroll
-          for (int q = 0; q < 4; q++) unpack_mxfp4_scaled(w[q], e8m0_to_f32(sb), &pr[4 * q]);
-        } else {
-#pragma unroll
-          for (int q = 0; q < 4; q++) unpack_mxfp4(w[q], *reinterpret_cast<uint32_t(*)[4]>(&pr[4 * q]));
-        }
+        for (int q = 0; q < 4; q++) unpack_mxfp4_scaled(w[q], cs, &pr[4 * q]);
       }
       float sc = 0.f, bp = 0.f;
       if constexpr (AFF) {
