@@ -1270,6 +1270,29 @@ bool try_multi_mid(const std::vector<QmmSpec>& sp, int n, const mlxq_array* x, c
       if (a.s != b.s || a.na != b.na || a.kr != b.kr || a.ks != b.ks || a.sw != b.sw || a.lds != b.lds) return false;
     }
   }
+  // The whole-row kernel runs one 64-row block per CU at a time: where the
+  // projections' blocks together need more than one round of the CUs
+  // (gate + up, 2 x 12288 rows: 384 blocks), the split-K mid-size kernel
+  // takes the launch instead, if it covers every projection alike (MI355X,
+  // Qwen3-8B gate + up, 4-bit g64: 16 rows 27.8 -> 24.6 us, 8 rows 19.2 ->
+  // 18.3).  Each output then has the mid-size kernel's bits (those of single
+  // calls with MLXQ_QMV_MR=0), within tolerance of the single calls'.
+  if (r[0].kind == DR_MR && knobs().qmv_kernel.empty() && use_mid((int)rows, fmt, sp[0].K)) {
+    int64_t mr_blocks = 0;
+    for (int i = 0; i < n; i++) mr_blocks += r[i].mr.row_blocks;
+    if (mr_blocks > cus) {
+      std::vector<DenseRoute> m(r);
+      bool ok = true;
+      for (int i = 0; i < n && ok; i++) {
+        m[i].kind = DR_MID;
+        m[i].mid = mlxq::qmv_mid_plan(fmt, sp[i].gs, sp[i].N, sp[i].K, (int)rows, cus, knobs().mid_win);
+        const mlxq::QmvMidPlan &a = m[i].mid, &b0 = m[0].mid;
+        ok = a.ok && a.s == b0.s && a.na == b0.na && a.kr == b0.kr && a.ks == b0.ks && a.sw == b0.sw &&
+             a.lds == b0.lds;
+      }
+      if (ok) r = m;
+    }
+  }
   mlxq::QmvMatTable t{};
   t.n = n;
   int64_t blocks = 0, ntot = 0;

@@ -5,7 +5,9 @@ of the oracle.  Decode rows (1-2, and 3-4 over long rows) take the single
 row-streaming launch over all projections; 3-16 rows where every projection
 takes the same mid-size kernel take one launch of it (and one reduction of
 the split-K partials); other row counts, and forced kernels, run the calls
-one after another and must give the same bytes.
+one after another and must give the same bytes.  Where the projections'
+whole-row blocks together need more than one round of the CUs, the one
+launch runs the mid-size kernel and matches single calls on that kernel.
 """
 import numpy as np
 import pytest
@@ -155,14 +157,34 @@ def test_qkv_mid_one_launch(bits, M):
     check(x, affine_sets([4096, 1024, 1024], K, bits, 64, 1910 + bits), 64, bits)
 
 
-@pytest.mark.parametrize("M", [3, 4, 8, 16])
+@pytest.mark.parametrize("M", [3, 4])
 def test_gate_up_whole_row_one_launch(M):
-    # 3-16 rows: gate/up (12288 rows each) each take the whole-row kernel
-    # alone, so the two run as one launch
+    # 3-4 rows: gate/up (12288 rows each) each take the whole-row kernel
+    # alone, so the two run as one launch of it
     announce("multi_gate_up_mr", M)
     K = 4096
     x = orc.normal_bf16((M, K), 1.0, 1920 + M)
     check(x, affine_sets([12288, 12288], K, 4, 64, 1930), 64, 4)
+
+
+@pytest.mark.parametrize("M", [5, 8, 16])
+def test_gate_up_past_one_round_takes_mid(monkeypatch, M):
+    # 5-16 rows: gate and up alone each take the whole-row kernel (192
+    # 64-row blocks, one round of the CUs), but together 384 blocks: the one
+    # launch runs the split-K mid-size kernel instead, so each output is
+    # bitwise a single call's on that kernel (MLXQ_QMV_MR=0) and within
+    # tolerance of the oracle and of the whole-row single calls
+    announce("multi_gate_up_mid", M)
+    K = 4096
+    x = orc.normal_bf16((M, K), 1.0, 1940 + M)
+    sets = affine_sets([12288, 12288], K, 4, 64, 1950)
+    multi, single_mr = run_both(x, sets, 64, 4)
+    setknob(monkeypatch, "MLXQ_QMV_MR", "0")
+    _, single_mid = run_both(x, sets, 64, 4)
+    for i in range(2):
+        np.testing.assert_array_equal(multi[i], single_mid[i], err_msg=f"projection {i}")
+        assert max_rel(multi[i], single_mr[i]) <= TOL
+        assert max_rel(multi[i], orc.qmm_t_affine(x, *sets[i], 64, 4)) <= TOL
 
 
 @pytest.mark.parametrize("gs", [32, 128])
