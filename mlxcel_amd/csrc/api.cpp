@@ -1196,7 +1196,12 @@ DenseRoute dense_route(const QmmSpec& sp, int64_t rows, int cus) {
   const std::string& forced = knobs().qmv_kernel;
   if (forced == "mr" || (knobs().qmv_mr != 0 && forced.empty())) {
     r.mr = mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, forced == "mr", knobs().mr_ring);
-    if (r.mr.ok) {
+    // The whole-row kernel holds one 64-row block per CU at a time: past one
+    // round of the CUs the split-K mid-size kernel is faster where it applies
+    // (MI355X, 4-bit g64 K=4096: 151936 rows, 2374 blocks, 16 rows 133 ->
+    // 124 us, 8 rows 88.7 -> 85.6; 12288 rows, 192 blocks, stays whole-row)
+    if (r.mr.ok && !(forced.empty() && r.mr.row_blocks > cus && use_mid((int)rows, fmt, sp.K) &&
+                     mlxq::qmv_mid_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, knobs().mid_win).ok)) {
       r.kind = DR_MR;
       return r;
     }
