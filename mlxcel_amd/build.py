@@ -73,9 +73,9 @@ def _compile(name: str, extra: list[str]) -> str:
 def _verify_group_ring_waits() -> None:
     """qmm_group.hip waits for its LDS ring with a hand-counted
     `s_waitcnt vmcnt(2 n)`: 2 younger blocks of n vector-memory instructions
-    each per wave (4 direct-to-LDS activation loads and 2 weight loads, plus 2
-    scale loads in the instantiation without the LDS scale table: n = 8, else
-    n = 6).  If the compiler ever emitted a different number per block the
+    each per wave (3 or 4 direct-to-LDS activation loads, one weight load per
+    tile of the wave (3 or 2) and, without the LDS scale table, one scale load
+    per tile: n = 6 with the table, 8 without).  If the compiler ever emitted a different number per block the
     wait would be wrong, so check each instantiation's AMD assembly (built
     here): 3 blocks before the first wait (and, with the scale table, its one
     staging load ahead of them), then exactly n loads after each of the 4
@@ -91,25 +91,28 @@ def _verify_group_ring_waits() -> None:
     starts = [i for i, l in enumerate(lines) if l.startswith(prefix) and l.split(";")[0].rstrip().endswith(":")]
     seen = set()
     for start in starts:
-        scl = int(lines[start][len(prefix):].split("E", 1)[0])
-        n = 8 if scl == 0 else 6
+        # _ZN4mlxq22qmm_group_mxfp4_kernelILi<SCL>ELi<tiles>EEEv...
+        args = lines[start][len(prefix):].split("EEEv", 1)[0]
+        scl, tiles = (int(v) for v in args.split("ELi"))
+        xi = 4 if tiles == 2 else 3
+        n = xi + tiles * (2 if scl == 0 else 1)
         end = next(i for i in range(start, len(lines)) if "s_endpgm" in lines[i])
         body = [l.strip() for l in lines[start:end]]
         wait = f"s_waitcnt vmcnt({2 * n})"
         marks = [i for i, l in enumerate(body) if l == wait and body[i + 1].startswith("s_barrier")]
         if len(marks) != 4:
-            raise RuntimeError(f"qmm_group<{scl}> ring check: expected 4 ring waits, found {len(marks)}")
+            raise RuntimeError(f"qmm_group<{scl},{tiles}> ring check: expected 4 ring waits, found {len(marks)}")
         loads = lambda a, b: sum(1 for l in body[a:b] if l.startswith("buffer_load"))
         bounds = marks + [next(i for i in range(marks[-1], len(body)) if body[i].startswith("s_waitcnt vmcnt(0)"))]
         per = [loads(bounds[k] + 1, bounds[k + 1]) for k in range(4)]
         pro = loads(0, marks[0])
         want_pro = 3 * n + (0 if scl == 0 else 1)
         if per != [n] * 4 or pro != want_pro:
-            raise RuntimeError(f"qmm_group<{scl}> ring check: loads per ring step {per}, prologue {pro} "
+            raise RuntimeError(f"qmm_group<{scl},{tiles}> ring check: loads per ring step {per}, prologue {pro} "
                                f"(the kernel's vmcnt({2 * n}) assumes {n} per step and {want_pro} before the first wait)")
-        seen.add(scl)
-    if seen != {0, 4, 16}:
-        raise RuntimeError(f"qmm_group ring check: instantiations {sorted(seen)}, expected [0, 4, 16]")
+        seen.add((scl, tiles))
+    if seen != {(0, 2), (4, 2), (16, 2), (4, 3), (16, 3)}:
+        raise RuntimeError(f"qmm_group ring check: instantiations {sorted(seen)}")
 
 
 def build(verbose: bool = True) -> str:

@@ -538,6 +538,7 @@ struct Knobs {
   int qmm_mix = 1;  // prefill: two-launch plan for a part-full last round of tiles (0: off)
   int mid_win = 0;  // mid-size kernel: windows per workgroup (4 or 8; 0: planner)
   int gather_scale_table = 1;  // grouped sorted gather: scales staged in LDS where they fit (0: per block)
+  int gather_tiles = 0;  // grouped sorted gather: 2 or 3 weight tiles per wave (0: planner)
   std::string qmv_kernel;  // "", "rs", "b4", "mid", "mr", "fr", "mfma"
 };
 
@@ -570,6 +571,7 @@ const Knobs* read_knobs() {
   k->qmm_mix = env_int("MLXQ_QMM_MIX", 1);
   k->mid_win = env_int("MLXQ_QMV_MID_WIN", 0);
   k->gather_scale_table = env_int("MLXQ_GATHER_SCALE_TABLE", 1);
+  k->gather_tiles = env_int("MLXQ_GATHER_TILES", 0);
   const char* v = std::getenv("MLXQ_QMV_KERNEL");
   k->qmv_kernel = v ? v : "";
   return k;
@@ -1632,7 +1634,8 @@ void gather_run(GatherSpec& g, const mlxq_array* x, const mlxq_array* w, const m
       knobs().gather_sorted != 0) {
     const DirectIdx dl = direct_index(lhs_indices, dsh[0], g.idx_shape);
     const DirectIdx dr = direct_index(rhs_indices, dsh[1], g.idx_shape);
-    mlxq::QmmGroupPlan gp = mlxq::qmm_group_plan(fmt, sp.N, sp.K, E, B);
+    mlxq::QmmGroupPlan gp =
+        mlxq::qmm_group_plan(fmt, sp.N, sp.K, E, B, device_info(current_device()).cus, knobs().gather_tiles);
     if (knobs().gather_scale_table == 0) gp.scale_table = false;
     if (gp.ok && dr.ok && dr.p && dl.ok && !dl.p && dl.div == 1) {
       mlxq::QmmGroupArgs q{};

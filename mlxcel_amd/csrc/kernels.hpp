@@ -305,10 +305,12 @@ struct QmmGroupArgs {
 };
 struct QmmGroupPlan {
   bool ok = false;
-  int row_blocks = 0;  // workgroups along N (128 weight rows each)
+  int tiles = 2;       // 16-row weight tiles per wave: workgroups of 64 * tiles rows
+  int row_blocks = 0;  // workgroups along N
   bool scale_table = false;  // K / 32 scale bytes per row fit the kernel's LDS table
 };
-QmmGroupPlan qmm_group_plan(int fmt, int64_t N, int64_t K, int64_t E, int64_t B);
+// cus: the device's CUs; tiles_req 2 or 3 forces the workgroup rows (0: planner).
+QmmGroupPlan qmm_group_plan(int fmt, int64_t N, int64_t K, int64_t E, int64_t B, int cus, int tiles_req = 0);
 hipError_t qmm_group_launch(const QmmGroupArgs& a, const QmmGroupPlan& p, hipStream_t stream);
 
 // Full-row decode kernel (qmv_fr.hip) for 1 or 2 activation rows per weight

@@ -45,26 +45,33 @@ namespace mlxq {
 namespace {
 
 constexpr int GQ_NW = 4;                     // waves per workgroup
-constexpr int GQ_T = 2;                      // 16-row weight tiles per wave
-constexpr int GQ_ROWS = GQ_NW * GQ_T * 16;   // weight rows per workgroup (128)
-constexpr int GQ_MC = 64;                    // activation rows per chunk (4 A tiles)
+constexpr int GQ_MCMAX = 64;                 // activation rows per chunk, at most
 constexpr int GQ_KB = 128;                   // k per block (one 4-group window)
 constexpr int GQ_NT = 64 * GQ_NW;
 constexpr int GQ_RING = 4;                   // blocks in the activation / weight rings
-constexpr int GQ_XB = GQ_MC * GQ_KB * 2;     // activation bytes per block (16 KiB, 256 per row)
-constexpr int GQ_XI = GQ_XB / 1024 / GQ_NW;  // 1 KiB direct-to-LDS loads per wave and block (4)
-constexpr int GQ_STB = GQ_ROWS * 128;       // LDS scale table: 128 rows of up to 128 e8m0 bytes (K <= 4096)
+constexpr int GQ_STB = 128;                  // LDS scale table: up to 128 e8m0 bytes per row (K <= 4096)
 
 }  // namespace
 
 // SCL: 0, scale bytes loaded per block; 4 or 16, the scale table staged in
-// LDS by direct loads of that many bytes per lane.
-template <int SCL>
+// LDS by direct loads of that many bytes per lane.  GT: 16-row weight tiles
+// per wave: 2 (128 weight rows, chunks of 64 activation rows), or 3 (192
+// rows, chunks of 48, with the scale table only: for a launch that needs one
+// round of the CUs' workgroup slots where 128-row blocks need two).
+template <int SCL, int GT>
 __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGroupArgs a) {
+  static_assert(GT == 2 || (GT == 3 && SCL != 0), "192-row workgroups take scales from the table");
+  constexpr int GQ_T = GT;                       // 16-row weight tiles per wave
+  constexpr int GQ_ROWS = GQ_NW * GQ_T * 16;     // weight rows per workgroup
+  constexpr int GQ_MC = GT == 3 ? 48 : 64;       // activation rows per chunk
+  constexpr int GQ_AT = GQ_MC / 16;              // A tiles per chunk
+  constexpr int GQ_XB = GQ_MC * GQ_KB * 2;       // activation bytes per block (256 per row)
+  constexpr int GQ_XI = GQ_XB / 1024 / GQ_NW;    // 1 KiB direct-to-LDS loads per wave and block (4 or 3)
+  static_assert(GQ_XI * 1024 * GQ_NW == GQ_XB, "whole 1 KiB wave loads");
   // the ring as four LDS objects, so the compiler's wait analysis sees that
   // a buffer being refilled is not the one being read
   __shared__ __align__(16) unsigned char xl0[GQ_XB], xl1[GQ_XB], xl2[GQ_XB], xl3[GQ_XB];
-  __shared__ __align__(16) unsigned char stb[SCL ? GQ_STB : 16];
+  __shared__ __align__(16) unsigned char stb[SCL ? GQ_ROWS * GQ_STB : 16];
   static_assert(GQ_RING == 4, "four ring buffers");
   auto ring = [&](int slot) -> unsigned char* { return slot == 0 ? xl0 : slot == 1 ? xl1 : slot == 2 ? xl2 : xl3; };
 
@@ -181,9 +188,9 @@ __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGrou
       }
     };
 
-    f32x4 acc[4][GQ_T];
+    f32x4 acc[GQ_AT][GQ_T];
 #pragma unroll
-    for (int u = 0; u < 4; u++)
+    for (int u = 0; u < GQ_AT; u++)
 #pragma unroll
       for (int t = 0; t < GQ_T; t++) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -235,7 +242,7 @@ __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGrou
           }
         }
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < GQ_AT; u++) {
           if (u < nat) {
             // A: activation row 16u + nl, logical chunk 4g + q at position (4g + q) ^ nl
             const unsigned char* row = xb + (16 * u + nl) * 256;
@@ -258,7 +265,7 @@ __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGrou
 
     // ---- store: D row 4 g + i of A tile u is activation row 16u + 4g + i ------
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
+    for (int u = 0; u < GQ_AT; u++) {
       if (u < nat) {
 #pragma unroll
         for (int t = 0; t < GQ_T; t++) {
@@ -274,30 +281,46 @@ __global__ __launch_bounds__(GQ_NT, 2) void qmm_group_mxfp4_kernel(const QmmGrou
   }
 }
 
-QmmGroupPlan qmm_group_plan(int fmt, int64_t N, int64_t K, int64_t E, int64_t B) {
+QmmGroupPlan qmm_group_plan(int fmt, int64_t N, int64_t K, int64_t E, int64_t B, int cus, int tiles_req) {
   QmmGroupPlan p;
   if (fmt != MXFP4 || N < 1 || K < 32 || K % 32 != 0 || E < 1 || B < 1) return p;
-  p.row_blocks = (int)((N + GQ_ROWS - 1) / GQ_ROWS);
-  p.scale_table = K / 32 <= GQ_STB / GQ_ROWS;
+  p.scale_table = K / 32 <= GQ_STB;
+  // 192-row workgroups (scales from the table, chunks of 48 activation
+  // rows) unless their rounds of the CUs' two workgroup slots cost more
+  // than the 128-row ones' (a 192-row workgroup takes less than 1.5 times as
+  // long: each staged activation block serves 192 weight rows), and where an
+  // expert has at most ~40 rows on average (more would often take a second
+  // chunk, streaming its weights again).  The grid has E workgroups per row
+  // block; those of experts without rows exit at once, so this counts the
+  // most it can hold.  MI355X, gpt-oss MoE at T=256 (32 experts, 1024
+  // entries): gate/up 2880 x 2 rows and down 2880 rows, 152 -> 135 us for
+  // both launches (down alone on 192 rows: 142).
+  const int64_t slots = 2 * (int64_t)(cus > 1 ? cus : 1);
+  auto rounds = [&](int64_t rows) { return (((N + rows - 1) / rows) * E + slots - 1) / slots; };
+  p.tiles = 2;
+  if (tiles_req == 3 || (tiles_req != 2 && p.scale_table && B <= 40 * E && rounds(192) * 3 <= rounds(128) * 2))
+    p.tiles = 3;
+  p.row_blocks = (int)((N + 64 * p.tiles - 1) / (64 * p.tiles));
   // buffer offsets are 32-bit and 0x80000000 marks a dead lane
-  p.ok = N * (K / 2) < ((int64_t)1 << 31) && (int64_t)GQ_MC * K * 2 < ((int64_t)1 << 31) && E <= 65535 &&
+  p.ok = N * (K / 2) < ((int64_t)1 << 31) && (int64_t)GQ_MCMAX * K * 2 < ((int64_t)1 << 31) && E <= 65535 &&
          p.row_blocks <= 65535 && B * K * 2 < ((int64_t)1 << 40);
   return p;
 }
 
 hipError_t qmm_group_launch(const QmmGroupArgs& a, const QmmGroupPlan& p, hipStream_t stream) {
   if (!p.ok) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)p.row_blocks, (unsigned)a.E);
   // the LDS scale table's direct loads need their source aligned to the
   // load width: the scales' base and every expert's N * K / 32 bytes
   const uintptr_t sb = reinterpret_cast<uintptr_t>(a.scales);
   const int64_t eb = (int64_t)a.N * (a.K / 32);
-  if (p.scale_table && sb % 16 == 0 && eb % 16 == 0)
-    hipLaunchKernelGGL(qmm_group_mxfp4_kernel<16>, grid, dim3(GQ_NT), 0, stream, a);
-  else if (p.scale_table && sb % 4 == 0 && eb % 4 == 0)
-    hipLaunchKernelGGL(qmm_group_mxfp4_kernel<4>, grid, dim3(GQ_NT), 0, stream, a);
-  else
-    hipLaunchKernelGGL(qmm_group_mxfp4_kernel<0>, grid, dim3(GQ_NT), 0, stream, a);
+  const int scl = !p.scale_table ? 0 : (sb % 16 == 0 && eb % 16 == 0) ? 16 : (sb % 4 == 0 && eb % 4 == 0) ? 4 : 0;
+  const int tiles = scl ? p.tiles : 2;  // 192-row workgroups need the table
+  const dim3 grid((unsigned)((a.N + 64 * tiles - 1) / (64 * tiles)), (unsigned)a.E);
+  if (tiles == 3 && scl == 16) hipLaunchKernelGGL((qmm_group_mxfp4_kernel<16, 3>), grid, dim3(GQ_NT), 0, stream, a);
+  else if (tiles == 3) hipLaunchKernelGGL((qmm_group_mxfp4_kernel<4, 3>), grid, dim3(GQ_NT), 0, stream, a);
+  else if (scl == 16) hipLaunchKernelGGL((qmm_group_mxfp4_kernel<16, 2>), grid, dim3(GQ_NT), 0, stream, a);
+  else if (scl == 4) hipLaunchKernelGGL((qmm_group_mxfp4_kernel<4, 2>), grid, dim3(GQ_NT), 0, stream, a);
+  else hipLaunchKernelGGL((qmm_group_mxfp4_kernel<0, 2>), grid, dim3(GQ_NT), 0, stream, a);
   return hipGetLastError();
 }
 

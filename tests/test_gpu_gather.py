@@ -394,3 +394,27 @@ def test_sorted_grouped_scale_table(monkeypatch, N, K):
     setknob(monkeypatch, "MLXQ_GATHER_SCALE_TABLE", "0")
     per_block = host_u16(mq.gather_qmm(X, W, S, None, None, R, True, 32, 4, "mxfp4", sorted_indices=True))
     np.testing.assert_array_equal(got, per_block)
+
+
+@pytest.mark.parametrize("N,K", [(2880, 2880), (200, 2880), (516, 96), (256, 4096), (130, 96), (256, 4160)])
+def test_sorted_grouped_192_row_blocks(monkeypatch, N, K):
+    # 192-row workgroups (3 weight tiles per wave, chunks of 48 activation
+    # rows, scales from the LDS table) against 128-row ones
+    # (MLXQ_GATHER_TILES=3 / 2): the same MFMA sequence per output, so the
+    # same bits.  512 entries over 8 experts put ~64 rows on an expert, so
+    # chunks of 48 repeat; partial last row blocks (200, 516, 130 rows); 130 x
+    # 96 and K = 4160 have no scale table and keep 128-row workgroups.
+    announce("gather_sorted_grouped_192", N, K)
+    E, B = 8, 512
+    rhs = np.sort(np.random.default_rng(2990 + N + K).integers(0, E, B))
+    wq, sc = mx_experts(E, N, K, 2991 + N + K)
+    x = orc.normal_bf16((B, 1, K), 1.0, 2992 + N + K)
+    X, W, S = dev_bf16(x), dev_u32(wq), dev_u8(sc)
+    R = torch.from_numpy(rhs.astype(np.int32)).cuda()
+    outs = {}
+    for tiles in ("2", "3"):
+        setknob(monkeypatch, "MLXQ_GATHER_TILES", tiles)
+        outs[tiles] = host_u16(mq.gather_qmm(X, W, S, None, None, R, True, 32, 4, "mxfp4", sorted_indices=True))
+    np.testing.assert_array_equal(outs["3"], outs["2"])
+    want = orc.gather_qmm_t(x, wq, sc, None, np.arange(B, dtype=np.uint32), rhs.astype(np.uint32), mode="mxfp4")
+    assert max_rel(outs["3"], want) <= TOL
