@@ -869,7 +869,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build runs the quantized-matmul kernels on a single "
-              "MI355X (multi-GPU sharding is described in DESIGN.md, not run).", file=sys.stderr)
+              "MI355X; sharding across GPUs is a design, not a run.", file=sys.stderr)
         sys.exit(2)
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)

@@ -1,7 +1,7 @@
 """ctypes binding of ``libmlxq.so`` (the C ABI in ``include/mlxq.h``).
 
-This is the same binding a Python caller of the reference's FFI would write;
-the Rust equivalent lives in INTEGRATION.md.  Loading fails loudly when the
+This is the same binding a Python caller of the reference's FFI would write
+(the Rust crate under ``rust/mlxq-sys`` binds the same symbols).  Loading fails loudly when the
 library has not been built: there is no fallback path.
 """
 from __future__ import annotations

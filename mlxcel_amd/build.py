@@ -6,6 +6,7 @@ Objects go to ``mlxcel_amd/_build/``; the library to ``mlxcel_amd/libmlxq.so``.
 from __future__ import annotations
 
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -27,7 +28,7 @@ COMMON = [
     "-std=c++17",
     "-fPIC",
     "-x", "hip",
-    # packed-FP32 VALU forms are kept out of every kernel
+    # no packed-FP32 VALU instructions (v_pk_fma_f32 and kin) in any kernel
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
@@ -115,6 +116,81 @@ def _verify_group_ring_waits() -> None:
         raise RuntimeError(f"qmm_group ring check: instantiations {sorted(seen)}")
 
 
+_MFMA4 = "v_mfma_f32_4x4x4_16b_bf16"
+_REG = re.compile(r"\b([va])(?:\[(\d+):(\d+)\]|(\d+)\b)")
+
+
+def _regs(operand_text: str) -> set:
+    """The VGPRs / AGPRs an operand list names, as (file, index) pairs."""
+    out = set()
+    for kind, lo, hi, one in _REG.findall(operand_text):
+        a, b = (int(lo), int(hi)) if lo else (int(one), int(one))
+        out |= {(kind, k) for k in range(a, b + 1)}
+    return out
+
+
+def check_b4_mfma_chains(asm_text: str) -> int:
+    """qmv_b4.hip writes its 4x4x4 MFMA accumulation chains as inline
+    assembly, which the compiler's hazard recognizer does not see, so the
+    wait states and register ties are the kernel's own.  Checks them in AMD
+    assembly text: each MFMA's destination is disjoint from its A and B
+    operands and its C operand is 0 or the destination itself; an `s_nop` of
+    at least 1 (2 wait states) sits right before it; and after a chain's last
+    MFMA, s_nop wait states add up to 16 before any other instruction names a
+    destination register or the basic block ends.  Returns the number of
+    MFMAs checked; raises RuntimeError at the first violation."""
+    code = [l.split(";")[0].strip() for l in asm_text.splitlines()]
+    code = [l for l in code if l and not l.startswith(".")]
+    block_end = ("s_branch", "s_cbranch", "s_setpc", "s_endpgm")
+    count = 0
+    for i, ins in enumerate(code):
+        if not ins.startswith(_MFMA4):
+            continue
+        count += 1
+        ops = [o.strip() for o in ins[len(_MFMA4):].split(",")]
+        d, a, b, c = (_regs(o) for o in ops[:4])
+        where = f"qmv_b4 MFMA chain check, instruction {count} ({ins})"
+        if d & (a | b):
+            raise RuntimeError(f"{where}: destination overlaps A or B")
+        if ops[3] != "0" and c != d:
+            raise RuntimeError(f"{where}: C operand is neither 0 nor the destination")
+        nop = re.fullmatch(r"s_nop (\d+)", code[i - 1])
+        if not nop or int(nop.group(1)) < 1:
+            raise RuntimeError(f"{where}: preceded by '{code[i - 1]}', not s_nop >= 1")
+        waits = 0
+        for nxt in code[i + 1:]:
+            m = re.fullmatch(r"s_nop (\d+)", nxt)
+            if m:
+                waits += int(m.group(1)) + 1
+                continue
+            ends = nxt.endswith(":") or nxt.startswith(block_end)
+            if not ends and not (_regs(nxt) & d):
+                continue
+            if nxt.startswith(_MFMA4):
+                o2 = [o.strip() for o in nxt[len(_MFMA4):].split(",")]
+                if _regs(o2[0]) == d and _regs(o2[3]) == d:
+                    break  # the chain goes on
+            if waits < 16:
+                raise RuntimeError(f"{where}: result reached '{nxt}' after {waits} wait states (needs 16)")
+            break
+    if count == 0:
+        raise RuntimeError("qmv_b4 MFMA chain check: no 4x4x4 MFMA found in the assembly")
+    return count
+
+
+B4_ASM = os.path.join(BUILD, "qmv_b4.device.s")
+
+
+def _verify_b4_mfma_chains() -> None:
+    """Builds qmv_b4.hip's AMD assembly and checks its MFMA chains."""
+    src = os.path.join(CSRC, "qmv_b4.hip")
+    cmd = [HIPCC, *COMMON, "--cuda-device-only", "-S", src, "-o", B4_ASM]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc -S failed for qmv_b4.hip:\n{r.stderr}")
+    check_b4_mfma_chains(open(B4_ASM).read())
+
+
 def build(verbose: bool = True) -> str:
     """Compile every source and link libmlxq.so; always rebuilds."""
     if not os.path.exists(HIPCC) and shutil.which("hipcc") is None:
@@ -130,6 +206,7 @@ def build(verbose: bool = True) -> str:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
     _verify_group_ring_waits()
+    _verify_b4_mfma_chains()
     bobjs = [_compile(k, v) for k, v in BENCH_SOURCES.items()]
     tmp = BENCH_LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *bobjs]
