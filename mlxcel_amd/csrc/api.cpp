@@ -539,7 +539,9 @@ struct Knobs {
   int mid_win = 0;  // mid-size kernel: windows per workgroup (4 or 8; 0: planner)
   int gather_scale_table = 1;  // grouped sorted gather: scales staged in LDS where they fit (0: per block)
   int gather_tiles = 0;  // grouped sorted gather: 2 or 3 weight tiles per wave (0: planner)
-  std::string qmv_kernel;  // "", "rs", "b4", "mid", "mr", "fr", "mfma"
+  int qmv_kq = 1;  // K split over a workgroup's waves for matrices of one round of 16/32-row blocks (0: off)
+  int kq_t = 0;    // its 16-row tiles per workgroup (1-4; 0: planner)
+  std::string qmv_kernel;  // "", "rs", "b4", "mid", "mr", "kq", "fr", "mfma"
 };
 
 int env_int(const char* name, int dflt) {
@@ -572,6 +574,8 @@ const Knobs* read_knobs() {
   k->mid_win = env_int("MLXQ_QMV_MID_WIN", 0);
   k->gather_scale_table = env_int("MLXQ_GATHER_SCALE_TABLE", 1);
   k->gather_tiles = env_int("MLXQ_GATHER_TILES", 0);
+  k->qmv_kq = env_int("MLXQ_QMV_KQ", 1);
+  k->kq_t = env_int("MLXQ_QMV_KQ_T", 0);
   const char* v = std::getenv("MLXQ_QMV_KERNEL");
   k->qmv_kernel = v ? v : "";
   return k;
@@ -768,7 +772,7 @@ Skinny skinny_choice(int rows, int fmt = mlxq::AFF4, int64_t K = 0) {
 bool use_mid(int rows, int fmt, int64_t K) {
   if (fmt == mlxq::MXFP4 || rows > 16) return false;
   const std::string& k = knobs().qmv_kernel;
-  if (k == "mid" || k == "mr") return true;
+  if (k == "mid" || k == "mr" || k == "kq") return true;
   if (!k.empty()) return false;
   if (knobs().qmv_mid == 0) return false;
   (void)K;
@@ -1208,6 +1212,17 @@ DenseRoute dense_route(const QmmSpec& sp, int64_t rows, int cus) {
       return r;
     }
   }
+  // Matrices that fit one round of the CUs in 16- or 32-row workgroups
+  // (q / k / v / o at 7-8B shapes): every workgroup walks the whole of K
+  // with the K windows split over its waves, so no second launch adds K
+  // ranges.
+  if (forced == "kq" || (forced.empty() && knobs().qmv_kq != 0 && rows >= kMidMinRows)) {
+    r.mr = mlxq::qmv_kq_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, knobs().kq_t);
+    if (r.mr.ok) {
+      r.kind = DR_MR;
+      return r;
+    }
+  }
   r.mid = mlxq::qmv_mid_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, knobs().mid_win);
   if (r.mid.ok) r.kind = DR_MID;
   return r;
@@ -1270,7 +1285,8 @@ bool try_multi_mid(const std::vector<QmmSpec>& sp, int n, const mlxq_array* x, c
     if (r[i].kind == DR_OTHER || r[i].kind != r[0].kind) return false;
     if (r[i].kind == DR_MR) {
       const mlxq::QmvMrPlan &a = r[i].mr, &b = r[0].mr;
-      if (a.s != b.s || a.na != b.na || a.xr != b.xr || a.rk != b.rk || a.ring != b.ring || a.lds != b.lds)
+      if (a.s != b.s || a.na != b.na || a.xr != b.xr || a.rk != b.rk || a.ring != b.ring || a.lds != b.lds ||
+          (a.t > 0) != (b.t > 0))
         return false;
     } else {
       const mlxq::QmvMidPlan &a = r[i].mid, &b = r[0].mid;
@@ -1284,7 +1300,30 @@ bool try_multi_mid(const std::vector<QmmSpec>& sp, int n, const mlxq_array* x, c
   // Qwen3-8B gate + up, 4-bit g64: 16 rows 27.8 -> 24.6 us, 8 rows 19.2 ->
   // 18.3).  Each output then has the mid-size kernel's bits (those of single
   // calls with MLXQ_QMV_MR=0), within tolerance of the single calls'.
-  if (r[0].kind == DR_MR && knobs().qmv_kernel.empty() && use_mid((int)rows, fmt, sp[0].K)) {
+  // K split over the waves: one tile count for all projections, the
+  // fewest whose blocks together fit one round of the CUs (else the
+  // projections run one by one).
+  if (r[0].kind == DR_MR && r[0].mr.t > 0) {
+    const int t_req = knobs().kq_t;
+    bool planned = false;
+    for (int t = 1; t <= 4; t++) {
+      if (planned || (mlxq::kq_tiles_ok(t_req) && t != t_req)) continue;
+      int64_t blocks = 0;
+      bool ok = true;
+      std::vector<DenseRoute> m(r);
+      for (int i = 0; i < n && ok; i++) {
+        m[i].mr = mlxq::qmv_kq_plan(fmt, sp[i].gs, sp[i].N, sp[i].K, (int)rows, cus, t, 0);
+        ok = m[i].mr.ok && m[i].mr.lds == m[0].mr.lds;
+        blocks += m[i].mr.row_blocks;
+      }
+      if (ok && (blocks <= cus || mlxq::kq_tiles_ok(t_req))) {
+        r = m;
+        planned = true;
+      }
+    }
+    if (!planned) return false;
+  }
+  if (r[0].kind == DR_MR && r[0].mr.t == 0 && knobs().qmv_kernel.empty() && use_mid((int)rows, fmt, sp[0].K)) {
     int64_t mr_blocks = 0;
     for (int i = 0; i < n; i++) mr_blocks += r[i].mr.row_blocks;
     if (mr_blocks > cus) {

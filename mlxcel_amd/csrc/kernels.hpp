@@ -283,12 +283,19 @@ struct QmvMrPlan {
   int xr = 8;          // activation rows staged (8 or 16)
   int rk = 1024;       // K positions per staged range
   int ring = 8;        // windows of weight loads in flight (4, 8 or 16)
-  int row_blocks = 0;  // workgroups (64 weight rows each)
+  int row_blocks = 0;  // workgroups (64 weight rows each; 16 t with t > 0)
+  int t = 0;           // 0: qmv_mr_kernel; 1-4: qmv_kq_kernel with t 16-row tiles per workgroup
+  int nw = 8;          // qmv_kq_kernel: waves per workgroup
   size_t lds = 0;
 };
 // force: plan even when the matrix has too few rows to fill the CUs;
 // ring_req: 4, 8 or 16 forces the weight ring depth in windows (0: planner)
 QmvMrPlan qmv_mr_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int cus, bool force, int ring_req);
+// K split over the waves of a workgroup of 16 t rows (qmv_kq_kernel): t_req
+// in 1-4 forces the tiles per workgroup; 0 takes the fewest that fit one
+// round of the CUs (none: not planned).  Launched by qmv_mr_launch.
+bool kq_tiles_ok(int t);
+QmvMrPlan qmv_kq_plan(int fmt, int gs, int64_t N, int64_t K, int rows, int cus, int t_req, int nw_req = 0);
 hipError_t qmv_mr_launch(int fmt, const QmvMrArgs& a, const QmvMrPlan& p, hipStream_t stream);
 
 // Expert-sorted gather (qmm_group.hip), mxfp4, one activation row per index

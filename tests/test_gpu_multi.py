@@ -172,7 +172,7 @@ def test_gate_up_past_one_round_takes_mid(monkeypatch, M):
     # 5-16 rows: gate and up alone each take the whole-row kernel (192
     # 64-row blocks, one round of the CUs), but together 384 blocks: the one
     # launch runs the split-K mid-size kernel instead, so each output is
-    # bitwise a single call's on that kernel (MLXQ_QMV_MR=0) and within
+    # bitwise a single call's on that kernel (MLXQ_QMV_MR=0 MLXQ_QMV_KQ=0) and within
     # tolerance of the oracle and of the whole-row single calls
     announce("multi_gate_up_mid", M)
     K = 4096
@@ -180,6 +180,7 @@ def test_gate_up_past_one_round_takes_mid(monkeypatch, M):
     sets = affine_sets([12288, 12288], K, 4, 64, 1950)
     multi, single_mr = run_both(x, sets, 64, 4)
     setknob(monkeypatch, "MLXQ_QMV_MR", "0")
+    setknob(monkeypatch, "MLXQ_QMV_KQ", "0")  # single calls on the split-K kernel
     _, single_mid = run_both(x, sets, 64, 4)
     for i in range(2):
         np.testing.assert_array_equal(multi[i], single_mid[i], err_msg=f"projection {i}")
