@@ -1212,11 +1212,14 @@ DenseRoute dense_route(const QmmSpec& sp, int64_t rows, int cus) {
       return r;
     }
   }
-  // Matrices that fit one round of the CUs in 16- or 32-row workgroups
-  // (q / k / v / o at 7-8B shapes): every workgroup walks the whole of K
-  // with the K windows split over its waves, so no second launch adds K
-  // ranges.
-  if (forced == "kq" || (forced.empty() && knobs().qmv_kq != 0 && rows >= kMidMinRows)) {
+  // Matrices that fit one round of the CUs in workgroups of 16-64 rows
+  // (q / k / v / o / down at 7-8B shapes): every workgroup walks the whole
+  // of K with the K windows split over its waves, so no second launch adds
+  // K ranges.  Not past 8 rows over rows longer than 12288 (MI355X, 4-bit
+  // g64, 16 rows: Qwen3-8B down K = 12288 15.3 us vs 17.0 on the split-K
+  // kernel, Llama-3-8B down K = 14336 19.3 vs 17.8).
+  if (forced == "kq" ||
+      (forced.empty() && knobs().qmv_kq != 0 && rows >= kMidMinRows && (rows <= 8 || sp.K <= 12288))) {
     r.mr = mlxq::qmv_kq_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, knobs().kq_t);
     if (r.mr.ok) {
       r.kind = DR_MR;
