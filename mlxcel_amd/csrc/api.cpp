@@ -1195,12 +1195,18 @@ DenseRoute dense_route(const QmmSpec& sp, int64_t rows, int cus) {
   DenseRoute r;
   const int fmt = fmt_of(sp.mode, sp.bits);
   if (rows < 1 || rows > 16) return r;
-  const bool mr_small = rows >= 3 && rows < kMidMinRows && fmt == mlxq::AFF4 && knobs().qmv_mr != 0 &&
-                        knobs().qmv_kernel.empty() &&
-                        mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, false, 0).ok;
-  if (!mr_small && !use_mid((int)rows, fmt, sp.K)) return r;
   const std::string& forced = knobs().qmv_kernel;
-  if (forced == "mr" || (knobs().qmv_mr != 0 && forced.empty())) {
+  const bool mr_fits = mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, false, 0).ok;
+  const bool mr_small = rows >= 3 && rows < kMidMinRows && fmt == mlxq::AFF4 && knobs().qmv_mr != 0 &&
+                        forced.empty() && mr_fits;
+  // 3-4 rows over matrices with too few rows for the whole-row kernel: the
+  // K-split-over-waves kernel below (MI355X, Qwen3-8B, 4-bit g64, 3-4 rows:
+  // o 5.9 us vs 7.8 on the block-MFMA kernel, q/k/v in one launch 7.8 vs
+  // 23.2 as three, down 11.3 vs 11.8 on row streaming; at 2 rows row
+  // streaming stays faster: 4.7 vs 5.9)
+  const bool kq_small = rows >= 3 && rows < kMidMinRows && forced.empty() && knobs().qmv_kq != 0 && !mr_fits;
+  if (!mr_small && !kq_small && !use_mid((int)rows, fmt, sp.K)) return r;
+  if (!kq_small && (forced == "mr" || (knobs().qmv_mr != 0 && forced.empty()))) {
     r.mr = mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, forced == "mr", knobs().mr_ring);
     // The whole-row kernel holds one 64-row block per CU at a time: past one
     // round of the CUs the split-K mid-size kernel is faster where it applies
@@ -1218,7 +1224,7 @@ DenseRoute dense_route(const QmmSpec& sp, int64_t rows, int cus) {
   // K ranges.  Not past 8 rows over rows longer than 12288 (MI355X, 4-bit
   // g64, 16 rows: Qwen3-8B down K = 12288 15.3 us vs 17.0 on the split-K
   // kernel, Llama-3-8B down K = 14336 19.3 vs 17.8).
-  if (forced == "kq" ||
+  if (forced == "kq" || kq_small ||
       (forced.empty() && knobs().qmv_kq != 0 && rows >= kMidMinRows && (rows <= 8 || sp.K <= 12288))) {
     r.mr = mlxq::qmv_kq_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, knobs().kq_t);
     if (r.mr.ok) {
@@ -1226,6 +1232,7 @@ DenseRoute dense_route(const QmmSpec& sp, int64_t rows, int cus) {
       return r;
     }
   }
+  if (kq_small) return r;  // not planned: the 1-4-row kernels
   r.mid = mlxq::qmv_mid_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, knobs().mid_win);
   if (r.mid.ok) r.kind = DR_MID;
   return r;
