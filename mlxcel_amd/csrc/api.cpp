@@ -1199,12 +1199,15 @@ DenseRoute dense_route(const QmmSpec& sp, int64_t rows, int cus) {
   const bool mr_fits = mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, false, 0).ok;
   const bool mr_small = rows >= 3 && rows < kMidMinRows && fmt == mlxq::AFF4 && knobs().qmv_mr != 0 &&
                         forced.empty() && mr_fits;
-  // 3-4 rows over matrices with too few rows for the whole-row kernel: the
-  // K-split-over-waves kernel below (MI355X, Qwen3-8B, 4-bit g64, 3-4 rows:
-  // o 5.9 us vs 7.8 on the block-MFMA kernel, q/k/v in one launch 7.8 vs
-  // 23.2 as three, down 11.3 vs 11.8 on row streaming; at 2 rows row
-  // streaming stays faster: 4.7 vs 5.9)
-  const bool kq_small = rows >= 3 && rows < kMidMinRows && forced.empty() && knobs().qmv_kq != 0 && !mr_fits;
+  // 3-4 rows, 4-bit codes, rows up to 12288 long, over matrices with too few
+  // rows for the whole-row kernel: the K-split-over-waves kernel below
+  // (MI355X, Qwen3-8B, g64, 3-4 rows: o 5.9 us vs 7.8 on the block-MFMA
+  // kernel, q/k/v in one launch 7.8 vs 23.2 as three, down K = 12288 11.3 vs
+  // 11.8 on row streaming; row streaming stays faster at 2 rows, o 4.7 vs
+  // 5.9, over Llama-3-8B down, K = 14336, 4 rows 12.9 vs 13.5, and with
+  // 8-bit codes there, 18.2 vs 21.7)
+  const bool kq_small = rows >= 3 && rows < kMidMinRows && forced.empty() && knobs().qmv_kq != 0 && !mr_fits &&
+                        fmt == mlxq::AFF4 && sp.K <= 12288;
   if (!mr_small && !kq_small && !use_mid((int)rows, fmt, sp.K)) return r;
   if (!kq_small && (forced == "mr" || (knobs().qmv_mr != 0 && forced.empty()))) {
     r.mr = mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, forced == "mr", knobs().mr_ring);
