@@ -747,6 +747,21 @@ enum class Skinny { FR, RS, B4, MFMA };
 // vs 40).
 constexpr int kMidMinRows = 5;
 
+// Row counts the default route gives the K-split-over-waves kernel over a
+// matrix too small for the whole-row one: 5-8 rows at any K; 9-16 rows and,
+// with 4-bit codes, 3-4 rows over at most 12 staged ranges (rows up to 12288
+// long with 4-bit codes, 6144 with 8-bit).  MI355X, g64, against the split-K
+// kernel: 16 rows Qwen3-8B down K = 12288 4-bit 15.3 us vs 17.0, 8-bit
+// 20.5 vs 19.9, Llama-3-8B down K = 14336 4-bit 19.3 vs 17.8; 3-4 rows over
+// Llama-3-8B down row streaming stays faster (4-bit 4 rows 12.9 vs 13.5,
+// 8-bit 18.2 vs 21.7).
+bool kq_default_rows(int fmt, int64_t rows, int64_t K) {
+  const bool few_ranges = K * (fmt == mlxq::AFF8 ? 8 : 4) <= 12288 * 4;
+  if (rows >= kMidMinRows && rows <= 8) return true;
+  if (rows > 8 && rows <= 16) return few_ranges;
+  return rows >= 3 && rows < kMidMinRows && fmt == mlxq::AFF4 && few_ranges;
+}
+
 // Defaults measured at the Llama-3-8B MLP shapes (gate K=4096, down
 // K=14336): row-streaming up to 4 rows; block-MFMA for 5-8 rows of 8-bit
 // and mxfp4 codes, and of 4-bit codes with K <= 8192; the MFMA kernel
@@ -1103,6 +1118,39 @@ bool try_mr_f16(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, con
   return true;
 }
 
+// float16 over matrices with too few rows for the whole-row kernel: the
+// K-split-over-waves kernel at the bfloat16 route's row counts
+// (kq_default_rows; any row count when MLXQ_QMV_KERNEL=kq).
+bool try_kq_f16(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const mlxq_array* scales,
+                const mlxq_array* biases, mlxq_array* out, int64_t rows, hipStream_t stream) {
+  const bool forced = knobs().qmv_kernel == "kq";
+  if (!f16_affine(sp, x, scales, biases) || rows < 1 || rows > 16) return false;
+  const int fmt = fmt_of(sp.mode, sp.bits);
+  const int cus = device_info(current_device()).cus;
+  if (!forced) {
+    if (knobs().qmv_kq == 0 || !knobs().qmv_kernel.empty()) return false;
+    if (!kq_default_rows(fmt, rows, sp.K)) return false;
+    if (rows < kMidMinRows && mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, false, 0).ok) return false;
+  }
+  const mlxq::QmvMrPlan kp = mlxq::qmv_kq_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, knobs().kq_t);
+  if (!kp.ok) return false;
+  mlxq::QmvMrArgs m{};
+  m.x = static_cast<const uint16_t*>(x->data);
+  m.w = static_cast<const uint32_t*>(w->data);
+  m.scales = static_cast<const uint16_t*>(scales->data);
+  m.biases = static_cast<const uint16_t*>(biases->data);
+  m.out = static_cast<uint16_t*>(out->data);
+  m.M = (int)rows;
+  m.N = (int)sp.N;
+  m.K = (int)sp.K;
+  int shift = 0;
+  while ((1 << shift) < sp.gs) shift++;
+  m.gs_shift = shift;
+  m.xt = 1;
+  hip_check(mlxq::qmv_mr_launch(fmt, m, kp, stream), "qmv_kq launch");
+  return true;
+}
+
 // float16, 5-16 rows (any row count when MLXQ_QMV_KERNEL=mid), other
 // matrices: the split-K mid-size kernel (down M=8: vs 84 us on the general
 // kernel).
@@ -1199,15 +1247,13 @@ DenseRoute dense_route(const QmmSpec& sp, int64_t rows, int cus) {
   const bool mr_fits = mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, false, 0).ok;
   const bool mr_small = rows >= 3 && rows < kMidMinRows && fmt == mlxq::AFF4 && knobs().qmv_mr != 0 &&
                         forced.empty() && mr_fits;
-  // 3-4 rows, 4-bit codes, rows up to 12288 long, over matrices with too few
-  // rows for the whole-row kernel: the K-split-over-waves kernel below
-  // (MI355X, Qwen3-8B, g64, 3-4 rows: o 5.9 us vs 7.8 on the block-MFMA
-  // kernel, q/k/v in one launch 7.8 vs 23.2 as three, down K = 12288 11.3 vs
-  // 11.8 on row streaming; row streaming stays faster at 2 rows, o 4.7 vs
-  // 5.9, over Llama-3-8B down, K = 14336, 4 rows 12.9 vs 13.5, and with
-  // 8-bit codes there, 18.2 vs 21.7)
+  // 3-4 rows over matrices with too few rows for the whole-row kernel: the
+  // K-split-over-waves kernel below where kq_default_rows allows (MI355X,
+  // Qwen3-8B, 4-bit g64, 3-4 rows: o 5.9 us vs 7.8 on the block-MFMA kernel,
+  // q/k/v in one launch 7.8 vs 23.2 as three, down K = 12288 11.3 vs 11.8 on
+  // row streaming; row streaming stays faster at 2 rows, o 4.7 vs 5.9)
   const bool kq_small = rows >= 3 && rows < kMidMinRows && forced.empty() && knobs().qmv_kq != 0 && !mr_fits &&
-                        fmt == mlxq::AFF4 && sp.K <= 12288;
+                        kq_default_rows(fmt, rows, sp.K);
   if (!mr_small && !kq_small && !use_mid((int)rows, fmt, sp.K)) return r;
   if (!kq_small && (forced == "mr" || (knobs().qmv_mr != 0 && forced.empty()))) {
     r.mr = mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, forced == "mr", knobs().mr_ring);
@@ -1224,11 +1270,9 @@ DenseRoute dense_route(const QmmSpec& sp, int64_t rows, int cus) {
   // Matrices that fit one round of the CUs in workgroups of 16-64 rows
   // (q / k / v / o / down at 7-8B shapes): every workgroup walks the whole
   // of K with the K windows split over its waves, so no second launch adds
-  // K ranges.  Not past 8 rows over rows longer than 12288 (MI355X, 4-bit
-  // g64, 16 rows: Qwen3-8B down K = 12288 15.3 us vs 17.0 on the split-K
-  // kernel, Llama-3-8B down K = 14336 19.3 vs 17.8).
+  // K ranges; the row counts of kq_default_rows.
   if (forced == "kq" || kq_small ||
-      (forced.empty() && knobs().qmv_kq != 0 && rows >= kMidMinRows && (rows <= 8 || sp.K <= 12288))) {
+      (forced.empty() && knobs().qmv_kq != 0 && rows >= kMidMinRows && kq_default_rows(fmt, rows, sp.K))) {
     r.mr = mlxq::qmv_kq_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, knobs().kq_t);
     if (r.mr.ok) {
       r.kind = DR_MR;
@@ -1433,6 +1477,7 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
     View wv{w};
     const bool dense = wv.ndim() == 2 && sp.small_w;  // the float16 routes use buffer resources too
     if (dense && try_mr_f16(sp, x, w, scales, biases, out, rows_total, stream)) return;
+    if (dense && try_kq_f16(sp, x, w, scales, biases, out, rows_total, stream)) return;
     if (dense && try_rs_f16(sp, x, w, scales, biases, out, rows_total, stream)) return;
     if (dense && try_mid_f16(sp, x, w, scales, biases, out, rows_total, stream, ss)) return;
     if (dense && try_qmm_f16(sp, x, w, scales, biases, out, rows_total, stream, ss)) return;

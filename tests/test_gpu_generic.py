@@ -317,11 +317,43 @@ def test_float16_split_k_mid_decode(monkeypatch, bits, gs, M):
     check(y, og.qmm(xv, wqn, sv, bv, True, gs, bits), "float16")
 
 
+@pytest.mark.parametrize("bits,gs", [(4, 32), (4, 64), (4, 128), (8, 32), (8, 64), (8, 128)])
+@pytest.mark.parametrize("M", [1, 3, 5, 8, 12, 16])
+def test_float16_k_split_over_waves_decode(monkeypatch, bits, gs, M):
+    # the K-split-over-waves kernel's float16 instantiation (MLXQ_QMV_KERNEL=kq
+    # forces it), K = 3072: three or six staged ranges, a partial last block
+    setknob(monkeypatch, "MLXQ_QMV_KERNEL", "kq")
+    announce("f16_kq", bits, gs, M)
+    (x, wq, s, b), (xv, wqn, sv, bv) = case(M, 200, 3072, bits, gs, "float16", "float16", True, 3550 + M + bits + gs)
+    y = mq.quantized_matmul(x, wq, s, b, True, gs, bits)
+    check(y, og.qmm(xv, wqn, sv, bv, True, gs, bits), "float16")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M", [3, 5, 8, 16])
+def test_float16_kq_default_route_bitwise(monkeypatch, bits, M):
+    # 5-16 float16 rows (3-4 with 4-bit codes) against the Qwen3-8B o shape
+    # (4096 x 4096: too few blocks for the whole-row kernel) take the
+    # K-split-over-waves kernel by default: bitwise the forced kernel at 1-4
+    # tiles per workgroup (8-bit at 3 rows: the row-streaming kernel)
+    announce("f16_kq_default", bits, M)
+    (x, wq, s, b), (xv, wqn, sv, bv) = case(M, 4096, 4096, bits, 64, "float16", "float16", True, 3580 + M + bits)
+    y = mq.quantized_matmul(x, wq, s, b, True, 64, bits)
+    check(y, og.qmm(xv, wqn, sv, bv, True, 64, bits), "float16")
+    if bits == 8 and M < 5:
+        return
+    setknob(monkeypatch, "MLXQ_QMV_KERNEL", "kq")
+    for t in ("1", "2", "3", "4"):
+        setknob(monkeypatch, "MLXQ_QMV_KQ_T", t)
+        assert torch.equal(y, mq.quantized_matmul(x, wq, s, b, True, 64, bits)), t
+
+
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("M", [5, 16])
 def test_float16_mid_decode_default_route(bits, M):
     # 5-16 float16 rows against the down shape (4096 rows: too few blocks for
-    # the whole-row kernel) take the split-K mid kernel by default
+    # the whole-row kernel) take the K-split-over-waves kernel at up to 8 rows
+    # and the split-K mid kernel past 8 rows over rows longer than 12288
     announce("f16_mid_default", bits, M)
     (x, wq, s, b), (xv, wqn, sv, bv) = case(M, 4096, 14336, bits, 64, "float16", "float16", True, 3600 + M + bits)
     y = mq.quantized_matmul(x, wq, s, b, True, 64, bits)

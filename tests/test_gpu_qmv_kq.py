@@ -1,13 +1,15 @@
 """GPU parity of the K-split-over-waves decode kernel (qmv_kq_kernel in
 qmv_mr.hip: 1-16 activation rows against one affine 4/8-bit weight matrix
-of few rows; a workgroup owns 16 or 32 weight rows over the whole of K and
-its four waves split every staged range's windows) against the oracle's
+of few rows; a workgroup owns 16-64 weight rows over the whole of K and
+its eight waves split every staged range's windows) against the oracle's
 restatement of MLX's `_qmm_t` (overlays/cpu/mlx/backend/cpu/quantized.cpp:
 199-257), max|y - y_ref| / max|y_ref| <= 1e-2.
 
 Forced with MLXQ_QMV_KERNEL=kq (MLXQ_QMV_KQ_T=1|2|3|4 sets the 16-row
 tiles per workgroup); the default route takes it at 5-16 rows for matrices
-whose blocks of up to 64 rows fit one round of the CUs.  Shapes reach every compiled variant:
+whose blocks of up to 64 rows fit one round of the CUs (past 8 rows over
+at most 12 staged ranges; 3-4 rows with 4-bit codes).  Shapes reach every
+compiled variant:
 group slots per window S in {1, 2, 4}, 1 and 2 A tiles, 8 and 16 staged
 activation rows, 1 and 2 tiles per workgroup, one, two and an odd number of
 staged K ranges (the last loop turn multiplies zeros), a partial last row
@@ -81,15 +83,17 @@ def test_kq_tiles_per_workgroup_bitwise(monkeypatch, bits, M):
 @pytest.mark.parametrize("N,K", [(4096, 4096), (4096, 12288)])
 def test_kq_qwen3_8b_shapes_default_route(monkeypatch, bits, M, N, K):
     # o (4096 x 4096) and down (4096 x 12288) of the Qwen3-8B shape on the
-    # default route: bitwise the forced kernel's result, within tolerance of
-    # the oracle and of the split-K kernel
+    # default route: this kernel past 8 rows only over at most 12 staged
+    # ranges (8-bit down at 16 rows: 24, the split-K kernel); bitwise the
+    # forced kernel's result, within tolerance of the oracle and of the other
     announce("kq_qwen3", bits, M, N, K)
     x, wq, s, b = affine_case(M, N, K, 64, bits, 5600 + M + bits + K)
     y = run(x, wq, s, b, 64, bits)
-    setknob(monkeypatch, "MLXQ_QMV_KERNEL", "kq")
+    routed, other = ("kq", "mid") if M <= 8 or K * bits <= 12288 * 4 else ("mid", "kq")
+    setknob(monkeypatch, "MLXQ_QMV_KERNEL", routed)
     np.testing.assert_array_equal(y, run(x, wq, s, b, 64, bits))
     assert max_rel(y, orc.qmm_t_affine(x, wq, s, b, 64, bits)) <= TOL
-    setknob(monkeypatch, "MLXQ_QMV_KERNEL", "mid")
+    setknob(monkeypatch, "MLXQ_QMV_KERNEL", other)
     assert max_rel(y, run(x, wq, s, b, 64, bits)) <= TOL
 
 
