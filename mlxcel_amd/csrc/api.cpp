@@ -519,6 +519,37 @@ void* workspace(int dev, hipStream_t stream, size_t bytes, const ScratchSrc& src
   return grow_workspace(w, bytes);
 }
 
+// Stream-K counters of a stream (slot 3): mlxq::kSplitCounters words,
+// zeroed on the stream when allocated; every launch that uses them leaves
+// them zero.
+void alloc_counters(Workspace& w, hipStream_t stream) {
+  grow_workspace(w, (size_t)mlxq::kSplitCounters * sizeof(uint32_t));
+  hip_check(hipMemsetAsync(w.data, 0, w.bytes, stream), "hipMemsetAsync (stream-K counters)");
+}
+
+// The prefill plan of a dense call: stream-K only where its partials and
+// counters can be had without allocating under a capture, and not for the
+// no-allocation entry point (its fixed scratch is small); otherwise the plan
+// without it.
+mlxq::QmmPlan prefill_plan(int fmt, int gs, int64_t rows, int64_t N, int64_t K, int dev, hipStream_t stream,
+                           const ScratchSrc& ss, int tile_req, int ksplit_req, int mix, int streamk,
+                           uint32_t** cnt) {
+  *cnt = nullptr;
+  const int cus = device_info(dev).cus;
+  mlxq::QmmPlan qp = mlxq::qmm_plan(fmt, gs, rows, N, K, cus, tile_req, ksplit_req, mix, ss.fixed ? 0 : streamk);
+  if (qp.sk_len <= 0) return qp;
+  std::lock_guard<std::mutex> lk(g_mu);
+  const bool capturing = stream_capturing(stream);
+  Workspace& w = g_ws[{dev, stream, 0}];
+  Workspace& c = g_ws[{dev, stream, 3}];
+  const bool ok = qp.sk_wgs <= mlxq::kSplitCounters &&
+                  (!capturing || (w.bytes >= (size_t)mlxq::qmm_sk_bytes(qp) && c.data));
+  if (!ok) return mlxq::qmm_plan(fmt, gs, rows, N, K, cus, tile_req, ksplit_req, mix, 0);
+  if (!c.data) alloc_counters(c, stream);
+  *cnt = static_cast<uint32_t*>(c.data);
+  return qp;
+}
+
 // Rows from which a dense quantized_matmul runs the prefill GEMM (qmm.hip):
 // at 9-16 rows its 128 x 128 tiles already beat the skinny kernels on
 // MI355X (MLXQ_QMM_MIN_ROWS overrides, for tests and measurements).
@@ -541,6 +572,8 @@ struct Knobs {
   int gather_tiles = 0;  // grouped sorted gather: 2 or 3 weight tiles per wave (0: planner)
   int qmv_kq = 1;  // K split over a workgroup's waves for matrices of one round of 16/32-row blocks (0: off)
   int kq_t = 0;    // its 16-row tiles per workgroup (1-4; 0: planner)
+  int qmm_streamk = 1;  // prefill: stream-K plan for a part-full last round of 256 x 256 tiles (0: off)
+  int sk_fallback = 0;  // stream-K: every cut tile's head computes its tail itself (tests)
   std::string qmv_kernel;  // "", "rs", "b4", "mid", "mr", "kq", "fr", "mfma"
 };
 
@@ -576,6 +609,8 @@ const Knobs* read_knobs() {
   k->gather_tiles = env_int("MLXQ_GATHER_TILES", 0);
   k->qmv_kq = env_int("MLXQ_QMV_KQ", 1);
   k->kq_t = env_int("MLXQ_QMV_KQ_T", 0);
+  k->qmm_streamk = env_int("MLXQ_QMM_STREAMK", 1);
+  k->sk_fallback = env_int("MLXQ_QMM_SK_FALLBACK", 0);
   const char* v = std::getenv("MLXQ_QMV_KERNEL");
   k->qmv_kernel = v ? v : "";
   return k;
@@ -1194,8 +1229,9 @@ bool try_qmm_f16(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, co
   const int fmt = fmt_of(sp.mode, sp.bits);
   const int dev = current_device();
   const int tile_req = knobs().qmm_tile >= 4 ? knobs().qmm_tile : -1;
-  const mlxq::QmmPlan qp = mlxq::qmm_plan(fmt, sp.gs, rows, sp.N, sp.K, device_info(dev).cus, tile_req,
-                                          knobs().qmm_ksplit, knobs().qmm_mix);
+  uint32_t* cnt = nullptr;
+  const mlxq::QmmPlan qp = prefill_plan(fmt, sp.gs, rows, sp.N, sp.K, dev, stream, ss, tile_req, knobs().qmm_ksplit,
+                                        knobs().qmm_mix, knobs().qmm_streamk, &cnt);
   if (!qp.ok || qp.tile < 4) return false;
   mlxq::QmmArgs q{};
   q.x = static_cast<const uint16_t*>(x->data);
@@ -1215,6 +1251,11 @@ bool try_qmm_f16(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, co
   q.xt = 1;
   if (qp.ksplit > 1)
     q.ws = reinterpret_cast<float*>(workspace(dev, stream, (size_t)qp.ksplit * rows * sp.N * sizeof(float), ss));
+  if (qp.sk_len > 0) {
+    q.ws = reinterpret_cast<float*>(workspace(dev, stream, (size_t)mlxq::qmm_sk_bytes(qp), ss));
+    q.cnt = cnt;
+    q.sk_fallback = knobs().sk_fallback;
+  }
   hip_check(mlxq::qmm_launch(fmt, q, qp, stream), "qmm launch");
   return true;
 }
@@ -1522,8 +1563,9 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
     // prefill: one GEMM over all rows (every leading dim of x folds into rows)
     const int dev = current_device();
     // MLXQ_QMM_TILE / MLXQ_QMM_KSPLIT: A/B overrides of the tile shape and K split
-    const mlxq::QmmPlan qp = mlxq::qmm_plan(fmt, sp.gs, rows_total, sp.N, sp.K, device_info(dev).cus,
-                                            knobs().qmm_tile, knobs().qmm_ksplit, knobs().qmm_mix);
+    uint32_t* cnt = nullptr;
+    const mlxq::QmmPlan qp = prefill_plan(fmt, sp.gs, rows_total, sp.N, sp.K, dev, stream, ss, knobs().qmm_tile,
+                                          knobs().qmm_ksplit, knobs().qmm_mix, knobs().qmm_streamk, &cnt);
     if (qp.ok) {
       mlxq::QmmArgs q{};
       q.x = a.x;
@@ -1543,6 +1585,11 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
       if (qp.ksplit > 1)
         q.ws = reinterpret_cast<float*>(
             workspace(dev, stream, (size_t)qp.ksplit * rows_total * sp.N * sizeof(float), ss));
+      if (qp.sk_len > 0) {
+        q.ws = reinterpret_cast<float*>(workspace(dev, stream, (size_t)mlxq::qmm_sk_bytes(qp), ss));
+        q.cnt = cnt;
+        q.sk_fallback = knobs().sk_fallback;
+      }
       hip_check(mlxq::qmm_launch(fmt, q, qp, stream), "qmm launch");
       return;
     }
@@ -2059,6 +2106,10 @@ mlxq_status mlxq_workspace_reserve(size_t bytes, void* stream_) {
       if (stream_capturing(stream)) unsupported("mlxq_workspace_reserve: the stream is being captured");
       grow_workspace(w, bytes);
     }
+    // and the stream-K counters (slot 3), so a capture after the reserve can
+    // take the stream-K prefill plan where the reserve covers its partials
+    Workspace& c = g_ws[{dev, stream, 3}];
+    if (!c.data && !stream_capturing(stream)) alloc_counters(c, stream);
   });
 }
 

@@ -197,6 +197,13 @@ constexpr int log2i(int v) { return v <= 1 ? 0 : 1 + log2i(v / 2); }
 // 2 GiB): bounds-checked buffer loads at it return 0.
 constexpr uint32_t kDeadOfs = 0x80000000u;
 
+// Cache-policy bit sc1 of buffer loads and stores (agent scope): stores
+// write through the XCD's L2 and loads are not served from a stale L2 line
+// of another XCD's data; the bits of relaxed agent-scope atomic loads and
+// stores, so data shared between workgroups on different XCDs needs no L2
+// writeback or invalidate.
+constexpr int kAgentScope = 16;
+
 // Raw buffer resource over [base, base + bytes): loads past the end return 0.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);

@@ -337,6 +337,10 @@ hipError_t qmv_fr_launch(int fmt, int gs, const QmvArgs& a, int nseg, const QmvF
 
 // Prefill GEMM (qmm.hip): y[M, N] = x[M, K] @ dequant(w)[N, K]^T, 256 x 128
 // output tiles, K split across workgroups when the grid is short.
+// Stream-K counter words a launch may use (the caller's zeroed array holds
+// at least this many).
+constexpr int kSplitCounters = 1 << 16;
+
 struct QmmArgs {
   const uint16_t* x;       // bf16 [M, K]
   const uint32_t* w;       // packed codes [N, K*bits/32]
@@ -363,6 +367,15 @@ struct QmmArgs {
   int tiles_m, tiles_n, m_fast;
   int xt;                  // 16-bit type of x / scales / biases / out: 0 bfloat16, 1 float16 (tile kernel, affine)
   int ldo;                 // row stride of out in elements (0: N); tile kernel without a K split
+  // Stream-K (tile kernel, 256 x 256): workgroup b takes K-steps
+  // [b sk_len, (b + 1) sk_len) of all tiles' steps laid end to end; a tile
+  // split between two workgroups meets through fp32 partials in ws
+  // (2 x gridDim.x x 256 x 256) and the per-boundary counters cnt
+  // (gridDim.x, zero between launches).  sk_fallback forces the path a head
+  // takes when its tail has not arrived (tests).
+  int sk_len;
+  int sk_fallback;
+  uint32_t* cnt;
 };
 struct QmmPlan {
   bool ok = false;
@@ -377,15 +390,21 @@ struct QmmPlan {
   // whole rounds of the CUs, then [n_first, N) on the narrower tile2
   // (tiles_n2 tiles along N) in one round.  tiles_n is the first launch's.
   int tile2 = -1, n_first = 0, tiles_n2 = 0;
+  // Stream-K (sk_len > 0): sk_wgs workgroups of sk_len K-steps each.
+  int sk_len = 0, sk_wgs = 0;
 };
+// Counter words and fp32 partial bytes a stream-K plan needs.
+inline int64_t qmm_sk_counters(const QmmPlan& p) { return p.sk_len > 0 ? p.sk_wgs : 0; }
+inline int64_t qmm_sk_bytes(const QmmPlan& p) { return p.sk_len > 0 ? (int64_t)2 * p.sk_wgs * 256 * 256 * 4 : 0; }
 // rows of x per output tile of a tile code (0 if unknown)
 int qmm_tile_rows(int tile);
 // Grouped gather: tiles along N for `tile`; tiles_m = segments is set by the caller.
 QmmPlan qmm_plan_grouped(int fmt, int gs, int64_t N, int64_t K, int tile);
 // tile_req / ksplit_req < 0 (or 0 for ksplit) choose by shape.
-// mix: allow the two-launch plan (tile2) when neither tile nor split is requested.
+// mix: allow the two-launch plan (tile2) when neither tile nor split is requested;
+// streamk: allow the stream-K plan there (it takes precedence).
 QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus, int tile_req, int ksplit_req,
-                 int mix = 1);
+                 int mix = 1, int streamk = 0);
 hipError_t qmm_launch(int fmt, const QmmArgs& a, const QmmPlan& p, hipStream_t stream);
 // out[i] = bf16(sum over z < ks of ws[z * n + i]) (qmv.hip)
 // out (16-bit type xt: 0 bfloat16, 1 float16) = sum over ks fp32 partials, in split order

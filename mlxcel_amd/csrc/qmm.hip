@@ -314,7 +314,7 @@ constexpr int kValuPerMfma = 6;
 // XT: 16-bit type of x, scales, biases and result (0 bfloat16, 1 float16:
 // weights dequantized to float16(s * q + b), products on the float16 MFMA;
 // affine only).
-template <int FMT, int BM, int BN, int NWM, int NWN, int XT>
+template <int FMT, int BM, int BN, int NWM, int NWN, int XT, bool SK = false>
 __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs a) {
   constexpr int NT = 64 * NWM * NWN;         // threads
   constexpr int TM = BM / NWM, TN = BN / NWN;  // wave tile
@@ -353,26 +353,30 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
   const int wm = wave / NWN, wn = wave % NWN;
   const int M = a.M, N = a.N, K = a.K;
 
-  // ---- workgroup -> (split, tile): XCD-contiguous runs --------------------
-  const int T = a.tiles_m * a.tiles_n;
-  const int G = T * a.ksplit;
-  int b = blockIdx.x;
-  {
-    const int q = G >> 3, r = G & 7, x = b & 7, j = b >> 3;
-    b = x < r ? x * (q + 1) + j : r * (q + 1) + (x - r) * q + j;
-  }
-  const int z = b / T, tt = b - z * T;
-  const int tm = a.m_fast ? tt % a.tiles_m : tt / a.tiles_n;
-  const int tn = a.m_fast ? tt / a.tiles_m : tt % a.tiles_n;
-  const int n0 = tn * BN;
-  const int nks = a.ksteps_per_split;
-  const int ks0 = z * nks;
-  const int ks1 = min(ks0 + nks, K / BK);
+  // Accumulators and the placement of the piece last run (the epilogues'
+  // inputs).
+  f32x16 acc[FM][FN];
+  const int fr = lane & 31;
+  int m0 = 0, rows = 0, r0 = 0, n0 = 0;
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++)
+#pragma unroll
+        for (int q = 0; q < 16; q++) acc[i][j][q] = 0.f;
+  };
 
-  int m0 = tm * BM, rows = min(BM, M - m0), r0 = 0;
+  // K-steps [ks0, ks1) of output tile (tm, tn) into acc (from zero).  The LDS
+  // buffers are free on entry (the previous piece's epilogue has passed a
+  // barrier behind its last LDS read) and after return hold nothing live.
+  auto run_piece = [&](int tm, int tn, int ks0, int ks1) __attribute__((always_inline)) {
+  n0 = tn * BN;
+  m0 = tm * BM;
+  rows = min(BM, M - m0);
+  r0 = 0;
   int64_t wbase = 0, sbase = 0;
-  if (a.seg) {
-    if (tm >= (int)a.nseg_dev[0]) return;
+  if (a.seg) {  // the caller has checked tm < nseg
     const int expert = (int)a.seg[3 * tm];
     r0 = (int)a.seg[3 * tm + 1];
     rows = (int)a.seg[3 * tm + 2];
@@ -562,19 +566,12 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
     }
   };
 
-  f32x16 acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; i++)
-#pragma unroll
-    for (int j = 0; j < FN; j++)
-#pragma unroll
-      for (int q = 0; q < 16; q++) acc[i][j][q] = 0.f;
+  zero_acc();
 
   // fragment of 32 x 32 x 16: lane holds row/column (lane % 32), k 8 * (lane / 32) .. + 8;
   // slice s reads logical chunk 2 s + lane / 32 of its row, stored at that ^
   // swz(row); fragment tile i's rows are 32 i + fr past a multiple of 64, so
   // swz(row) = (fr & 7) ^ (fr >> 3) ^ 4 (i & 1)
-  const int fr = lane & 31;
   const int c0 = (lane >> 5) ^ (fr & 7) ^ (fr >> 3);
   const int arow = (wm * TM + fr) * RS, brow = (wn * TN + fr) * RS;
   static_assert(TM % 64 == 0 && TN % 64 == 0, "wave tiles start at multiples of 64 rows");
@@ -681,6 +678,8 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
     }
   }
 
+  };
+
   // ---- epilogue ---------------------------------------------------------------
   // The products ran as (weights, activations), so block (i, j) of a lane
   // holds activation row m = wm TM + 32 i + (lane % 32) and weight columns
@@ -689,9 +688,9 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
   // 16-byte chunk c of a row at c ^ (row % chunks per row), and leaves as
   // 16-byte row pieces (per-element stores of the accumulators took ~8%
   // longer at M = 2048).  fp32 split-K partials go one wave row at a time.
-  const bool split = a.ksplit > 1;
   auto out_row = [&](int tr) -> int64_t { return a.seg ? (int64_t)a.orows[r0 + tr] : (int64_t)(m0 + tr); };
-  if (!split) {
+  // the tile's result, rounded to the 16-bit type
+  auto store_out = [&]() {
     constexpr int CPR = BN / 8;  // 16-byte chunks per row (8 values)
     uint16_t* ot = reinterpret_cast<uint16_t*>(stage);
 #pragma unroll
@@ -722,7 +721,9 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
         for (int e = 0; e < 8 && n + e < N; e++) dst[e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
       }
     }
-  } else {
+  };
+  // split z's fp32 partials of the tile, [z][M][N] in the workspace
+  auto store_partials = [&](int z) {
     constexpr int CPR = BN / 4;  // 16-byte chunks per row (4 fp32)
     float* ot = reinterpret_cast<float*>(stage);
     const bool vec = (N & 3) == 0;
@@ -756,7 +757,147 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
         }
       }
     }
+  };
+
+  // ---- stream-K (256 x 256 tiles on 8 waves, affine codes) -----------------
+  // Workgroup b (XCD-contiguous runs of b, as below) takes K-steps
+  // [b L, (b + 1) L) of the tiles' steps laid end to end, tile by tile, in
+  // pieces.  With L at least a tile's K, a run starts with at most one tail
+  // (the end of a tile whose head ends the previous run), then whole tiles,
+  // then at most one head.  The tail comes first in its run and the head
+  // last in the other, so the tail has normally been written long before
+  // the head needs it: the tail's workgroup stores its fp32 accumulators
+  // (agent scope, written through L2), waits for the stores and adds 1 to
+  // the boundary's counter; the head's workgroup adds 1 too and, if the tail
+  // was there, adds the saved tail to its accumulators (agent-scope loads)
+  // and stores the tile.  If the tail was not there yet (its workgroup has
+  // not run), the head saves its own accumulators, computes the tail itself
+  // from zero and adds the saved head: the same one fp32 addition per
+  // output, so the same bits.  Whoever arrives second puts the counter back
+  // to 0.  No workgroup waits for another.
+  if constexpr (SK) {
+    static_assert(BM == 256 && BN == 256 && NWM * NWN == 8 && AFF, "stream-K: 256 x 256 tiles, 8 waves, affine codes");
+    {
+      __shared__ uint32_t sk_old;
+      const int P = gridDim.x;
+      int b = blockIdx.x;
+      {
+        const int q = P >> 3, r = P & 7, x = b & 7, j = b >> 3;
+        b = x < r ? x * (q + 1) + j : r * (q + 1) + (x - r) * q + j;
+      }
+      const int nks = K / BK;
+      const int64_t steps = (int64_t)a.tiles_m * a.tiles_n * nks;
+      int64_t g = (int64_t)b * a.sk_len;
+      const int64_t g1 = min(steps, g + (int64_t)a.sk_len);
+      constexpr int NQ = FM * FN * 4;  // 16-byte accumulator pieces per lane
+      // partials: region 0 the tails, region 1 the heads a fallback saves;
+      // slot k is the tile cut by the boundary between runs k - 1 and k;
+      // piece idx of (wave, lane) at [region][k][wave][idx][lane] (16 bytes)
+      const __amdgpu_buffer_rsrc_t pr = buffer_rsrc(a.ws, (uint32_t)((int64_t)2 * P * BM * BN * 4));
+      auto piece_off = [&](int region, int k, int idx) -> uint32_t {
+        return (uint32_t)((((((int64_t)region * P + k) * (NT / 64) + wave) * NQ + idx) * 64 + lane) * 16);
+      };
+      auto save = [&](int region, int k) {
+#pragma unroll
+        for (int idx = 0; idx < NQ; idx++) {
+          const int i = idx / (FN * 4), j = (idx / 4) % FN, q = idx % 4;
+          const f32x4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), pr, piece_off(region, k, idx), 0,
+                                                 kAgentScope);
+        }
+      };
+      auto add_saved = [&](int region, int k) {
+        constexpr int HB = NQ / 4;  // a quarter of the pieces' loads in flight at a time
+#pragma unroll
+        for (int h = 0; h < NQ / HB; h++) {
+          f32x4 v[HB];
+#pragma unroll
+          for (int u = 0; u < HB; u++)
+            v[u] = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, piece_off(region, k, h * HB + u), 0, kAgentScope));
+#pragma unroll
+          for (int u = 0; u < HB; u++) {
+            const int idx = h * HB + u, i = idx / (FN * 4), j = (idx / 4) % FN, q = idx % 4;
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[i][j][4 * q + e] += v[u][e];
+          }
+        }
+      };
+      auto arrive = [&](int k) -> uint32_t {
+        __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+        __syncthreads();
+        if (t == 0) sk_old = __hip_atomic_fetch_add(a.cnt + k, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        return sk_old;
+      };
+      auto reset = [&](int k) {
+        if (t == 0) __hip_atomic_store(a.cnt + k, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      };
+      int fb_tile = -1, fb_ks = 0;
+      for (;;) {
+        int tile, ks0, ks1, mode;  // 0 whole tile, 1 tail, 2 head, 3 a fallback's tail
+        if (fb_tile >= 0) {
+          tile = fb_tile;
+          ks0 = fb_ks;
+          ks1 = nks;
+          mode = 3;
+        } else if (g < g1) {
+          tile = (int)(g / nks);
+          ks0 = (int)(g - (int64_t)tile * nks);
+          ks1 = (int)min((int64_t)nks, ks0 + (g1 - g));
+          mode = ks0 > 0 ? 1 : (ks1 < nks ? 2 : 0);
+          g += ks1 - ks0;
+        } else {
+          break;
+        }
+        const int tm = a.m_fast ? tile % a.tiles_m : tile / a.tiles_n;
+        const int tn = a.m_fast ? tile / a.tiles_m : tile % a.tiles_n;
+        run_piece(tm, tn, ks0, ks1);
+        if (mode == 0) {
+          store_out();
+        } else if (mode == 1) {
+          save(0, b);
+          if (arrive(b) == 1u) reset(b);
+        } else if (mode == 2) {
+          const bool tail_there = arrive(b + 1) == 1u;
+          if (tail_there) reset(b + 1);
+          if (tail_there && !a.sk_fallback) {
+            add_saved(0, b + 1);
+            store_out();
+          } else {
+            save(1, b + 1);
+            fb_tile = tile;
+            fb_ks = ks1;
+          }
+        } else {
+          __builtin_amdgcn_s_waitcnt(0);  // the saved head has completed
+          add_saved(1, b + 1);
+          store_out();
+          fb_tile = -1;
+        }
+        __syncthreads();  // the epilogue's LDS reads are done before the next piece stages
+      }
+      return;
+    }
   }
+
+  // ---- workgroup -> (split, tile): XCD-contiguous runs --------------------
+  const int T = a.tiles_m * a.tiles_n;
+  const int G = T * a.ksplit;
+  int b = blockIdx.x;
+  {
+    const int q = G >> 3, r = G & 7, x = b & 7, j = b >> 3;
+    b = x < r ? x * (q + 1) + j : r * (q + 1) + (x - r) * q + j;
+  }
+  const int z = b / T, tt = b - z * T;
+  const int tm = a.m_fast ? tt % a.tiles_m : tt / a.tiles_n;
+  const int tn = a.m_fast ? tt / a.tiles_m : tt % a.tiles_n;
+  if (a.seg && tm >= (int)a.nseg_dev[0]) return;
+  const int nks = a.ksteps_per_split;
+  const int ks0 = z * nks;
+  run_piece(tm, tn, ks0, min(ks0 + nks, K / BK));
+  if (a.ksplit > 1) store_partials(z);
+  else store_out();
 }
 
 // ---- host ------------------------------------------------------------------
@@ -775,7 +916,7 @@ bool is_tile_kernel(int tile) { return tile >= 4; }
 int qmm_tile_rows(int tile) { return tile >= 0 && tile < kTiles ? kBM[tile] : 0; }
 
 QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus, int tile_req, int ksplit_req,
-                 int mix) {
+                 int mix, int streamk) {
   QmmPlan p;
   const int bits = fmt == AFF8 ? 8 : 4;
   if (K % BK != 0 || K % gs != 0 || M <= 0 || N <= 0) return p;
@@ -834,6 +975,27 @@ QmmPlan qmm_plan(int fmt, int gs, int64_t M, int64_t N, int64_t K, int num_cus, 
   // gate/up K=4096: M=1280-1536 x N=14336 202 us vs 233, M=2048 x N=12288
   // 214 vs 234).  A 256 x 192 tail for M=2048 x N=14336 measured slower
   // than the second 256 x 256 round (246 vs 240), so none is planned there.
+  // Stream-K: one workgroup per CU takes an equal run of the 256 x 256
+  // tiles' K-steps laid end to end, so a last round holding only a few tiles
+  // does not leave the other CUs idle; a tile cut by a run boundary meets
+  // through one fp32 partial.  Runs of at least a tile's K plus 8 steps keep
+  // a cut tile's tail (the start of the next run) well ahead of its head
+  // (the end of this run).  Taken when the last round holds at most 1/8 of
+  // the CUs' tiles: the runs start their tiles at different K-steps, so
+  // workgroups that share operands no longer read them from L2 at the same
+  // time, which costs ~30% per step (MI355X, K=4096, 4-bit: 12288 x 1536
+  // rows, 1.125 rounds, 170.5 us vs 196.6 on the two-launch plan; 14336 x
+  // 2048 rows, 1.75 rounds, 269 vs 233).  streamk > 1 forces that run length.
+  if (streamk && tile_req < 0 && ksplit_req <= 0 && p.tile == 4 && p.ksplit == 1 && tiles > num_cus &&
+      fmt != MXFP4 && (streamk > 1 || (tiles < 2 * (int64_t)num_cus && (tiles - num_cus) * 8 <= num_cus))) {
+    const int64_t steps = tiles * nks;
+    const int64_t len = streamk > 1 ? streamk : (steps + num_cus - 1) / num_cus;
+    if (len >= nks + 8 && len < ((int64_t)1 << 30) && (steps + len - 1) / len <= num_cus) {
+      p.sk_len = (int)len;
+      p.sk_wgs = (int)((steps + len - 1) / len);
+      return p;
+    }
+  }
   if (mix && tile_req < 0 && ksplit_req <= 0 && p.tile == 4 && p.ksplit == 1 && tiles > num_cus) {
     const int64_t nb = (tiles / num_cus) * num_cus / p.tiles_m;  // 256-wide column tiles in whole rounds
     const int64_t n1 = nb * kBN[4];
@@ -863,6 +1025,14 @@ void qmm_tile_launch1(const QmmArgs& a, int tile, int ksplit, hipStream_t stream
 
 template <int FMT, int XT>
 void qmm_tile_launch(const QmmArgs& a, const QmmPlan& p, hipStream_t stream) {
+  if (p.sk_len > 0) {
+    QmmArgs ak = a;
+    ak.sk_len = p.sk_len;
+    if constexpr (FMT != MXFP4)
+      hipLaunchKernelGGL((qmm_tile_kernel<FMT, 256, 256, 2, 4, XT, true>), dim3((unsigned)p.sk_wgs), dim3(512), 0,
+                         stream, ak);
+    return;
+  }
   if (p.tile2 < 0) {
     qmm_tile_launch1<FMT, XT>(a, p.tile, p.ksplit, stream);
     return;
@@ -930,10 +1100,12 @@ hipError_t qmm_launch(int fmt, const QmmArgs& a_in, const QmmPlan& p, hipStream_
   if (!p.ok) return hipErrorInvalidValue;
   // float16: affine codes on the 32x32-MFMA tile kernel only
   if (a_in.xt != 0 && (fmt == MXFP4 || !is_tile_kernel(p.tile))) return hipErrorInvalidValue;
+  if (p.sk_len > 0 && (p.tile != 4 || !a_in.ws || !a_in.cnt || a_in.seg || fmt == MXFP4)) return hipErrorInvalidValue;
   QmmArgs a = a_in;
   a.tiles_m = p.tiles_m;
   a.tiles_n = p.tiles_n;
   a.m_fast = p.m_fast;
+  if (p.sk_len <= 0) a.sk_len = 0;
   switch (fmt) {
     case AFF4: qmm_launch_fmt<AFF4>(a, p, stream); break;
     case AFF8: qmm_launch_fmt<AFF8>(a, p, stream); break;
