@@ -100,9 +100,13 @@ typedef struct mlxq_array {
 /* Grows `stream`'s workspace on the current device to at least `bytes`, both
  * the kernel scratch and the staging buffer that holds row-contiguous copies
  * of strided or misaligned operands (each at least `bytes`), so a capture of
- * calls needing at most that much of either allocates nothing.  Also resolves
- * the device address of mlxq_quantized_matmul_noalloc's fixed scratch.  No
- * counterpart in the reference (MLX allocates inside each eval). */
+ * calls needing at most that much of either allocates nothing.  Also
+ * allocates the stream's stream-K counters (256 KiB) and resolves the device
+ * address of mlxq_quantized_matmul_noalloc's fixed scratch.  A captured
+ * prefill call whose stream-K plan needs more scratch than the stream holds
+ * (2 x CUs x 256 KiB, 128 MiB on MI355X) takes the plan without stream-K
+ * instead of allocating.  No counterpart in the reference (MLX allocates
+ * inside each eval). */
 mlxq_status mlxq_workspace_reserve(size_t bytes, void* stream);
 
 /* Bytes of device memory held by the workspaces (current and replaced
