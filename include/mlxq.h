@@ -101,7 +101,7 @@ typedef struct mlxq_array {
  * the kernel scratch and the staging buffer that holds row-contiguous copies
  * of strided or misaligned operands (each at least `bytes`), so a capture of
  * calls needing at most that much of either allocates nothing.  Also
- * allocates the stream's stream-K counters (256 KiB) and resolves the device
+ * allocates the stream's stream-K counters (1 MiB) and resolves the device
  * address of mlxq_quantized_matmul_noalloc's fixed scratch.  A captured
  * prefill call whose stream-K plan needs more scratch than the stream holds
  * (2 x CUs x 256 KiB, 128 MiB on MI355X) takes the plan without stream-K
