@@ -425,18 +425,44 @@ __global__ __launch_bounds__(64 * NWM * NWN) void qmm_tile_kernel(const QmmArgs 
   const uint32_t srow_off = (n0 + t < N && sload) ? (uint32_t)(n0 + t) * (uint32_t)GR * (AFF ? 2u : 1u) : kDeadOfs;
   // Scale rows need not be 16-byte aligned (K / gs groups per row, e.g. 90
   // e8m0 bytes): a chunk is read as 5 dwords from the dword boundary below
-  // and realigned by the byte offset in registers.
+  // and realigned by the byte offset in registers.  The buffer's bounds
+  // check zeroes a dword that reaches past the end as a whole, so where the
+  // scale rows end inside a dword (N x K / gs elements not a multiple of 4
+  // bytes) the last row's last chunk is read element by element: only the
+  // bytes past the end read 0.
   const uint32_t sal = srow_off & 3u;
+  const uint32_t sbytes = (uint32_t)((int64_t)N * GR * (AFF ? 2 : 1));
   u32x4 sc_r = {0u, 0u, 0u, 0u}, bi_r = {0u, 0u, 0u, 0u};
   uint32_t sc_x = 0u, bi_x = 0u;
+  auto dword_by_elements = [&](const __amdgpu_buffer_rsrc_t& r, uint32_t o) -> uint32_t {
+    if constexpr (AFF)
+      return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, o, 0, 0) |
+             ((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, o + 2u, 0, 0) << 16);
+    else
+      return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, o, 0, 0) |
+             ((uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, o + 1u, 0, 0) << 8) |
+             ((uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, o + 2u, 0, 0) << 16) |
+             ((uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, o + 3u, 0, 0) << 24);
+  };
   auto chunk_load = [&](int c) {
     if (sload) {
       const uint32_t o = (srow_off & ~3u) + (uint32_t)c * 16u;
-      sc_r = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, o, 0, 0));
-      sc_x = __builtin_amdgcn_raw_buffer_load_b32(sr, o + 16u, 0, 0);
-      if constexpr (AFF) {
-        bi_r = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(br, o, 0, 0));
-        bi_x = __builtin_amdgcn_raw_buffer_load_b32(br, o + 16u, 0, 0);
+      if (o < sbytes && o + 20u > sbytes) {
+        sc_r = u32x4{dword_by_elements(sr, o), dword_by_elements(sr, o + 4u), dword_by_elements(sr, o + 8u),
+                     dword_by_elements(sr, o + 12u)};
+        sc_x = dword_by_elements(sr, o + 16u);
+        if constexpr (AFF) {
+          bi_r = u32x4{dword_by_elements(br, o), dword_by_elements(br, o + 4u), dword_by_elements(br, o + 8u),
+                       dword_by_elements(br, o + 12u)};
+          bi_x = dword_by_elements(br, o + 16u);
+        }
+      } else {
+        sc_r = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, o, 0, 0));
+        sc_x = __builtin_amdgcn_raw_buffer_load_b32(sr, o + 16u, 0, 0);
+        if constexpr (AFF) {
+          bi_r = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(br, o, 0, 0));
+          bi_x = __builtin_amdgcn_raw_buffer_load_b32(br, o + 16u, 0, 0);
+        }
       }
     }
   };

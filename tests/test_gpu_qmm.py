@@ -136,3 +136,38 @@ def test_two_launch_tail_round_bitwise(monkeypatch, mode, M, N):
     ref = x.float() @ wd.t()
     err = float((mixed.float() - ref).abs().max() / ref.abs().max())
     assert err <= TOL, err
+
+
+@pytest.mark.parametrize("tile", [-1, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("mode,gs,N,K", [("affine4", 64, 579, 2880), ("affine8", 128, 631, 5504),
+                                         ("affine4", 64, 243, 1344), ("mxfp4", 32, 695, 64),
+                                         ("mxfp4", 32, 1215, 1344), ("float16", 64, 469, 2624)])
+def test_scale_rows_ending_inside_a_dword(monkeypatch, tile, mode, gs, N, K):
+    # N odd and K / gs odd (or 1-byte mxfp4 scales): the scale and bias
+    # buffers end inside a dword, which a bounds-checked dword load would
+    # read as 0 whole; the last weight row's last groups must still count
+    # (every output column, the last one included, against the oracle)
+    setknob(monkeypatch, "MLXQ_QMM_TILE", str(tile))
+    announce("qmm_scale_tail", tile, mode, gs, N, K)
+    M = 40
+    if mode == "mxfp4":
+        x, wq, sc = mxfp4_case(M, N, K, 3300 + N)
+        y = host_u16(mq.quantized_matmul(dev_bf16(x), dev_u32(wq), dev_u8(sc), None, True, 32, 4, "mxfp4"))
+        want = orc.fp_qmm_t_mxfp4(x, wq, sc)
+    elif mode == "float16":
+        g = torch.Generator().manual_seed(3400 + N)
+        xv = torch.randn(M, K, generator=g).to(torch.float16)
+        w = (torch.randn(N, K, generator=g) * 0.02).to(torch.float16).cuda()
+        wq_, s_, b_ = mq.quantize(w, gs, 4)
+        yt = mq.quantized_matmul(xv.cuda(), wq_, s_, b_, True, gs, 4).float()
+        ref = xv.float().cuda() @ mq.dequantize(wq_, s_, b_, gs, 4).float().t()
+        col = (yt[:, -1] - ref[:, -1]).abs().max() / ref.abs().max()
+        assert float(col) <= TOL and float((yt - ref).abs().max() / ref.abs().max()) <= TOL
+        return
+    else:
+        bits = 8 if mode == "affine8" else 4
+        x, wq, s, b = affine_case(M, N, K, gs, bits, 3500 + N)
+        y = host_u16(mq.quantized_matmul(dev_bf16(x), dev_u32(wq), dev_bf16(s), dev_bf16(b), True, gs, bits))
+        want = orc.qmm_t_affine(x, wq, s, b, gs, bits)
+    assert max_rel(y[:, -1:], want[:, -1:]) <= TOL
+    assert max_rel(y, want) <= TOL
