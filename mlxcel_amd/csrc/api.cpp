@@ -1629,6 +1629,18 @@ void run_quantized_matmul(const QmmSpec& sp, const mlxq_array* x, const mlxq_arr
     const int64_t M = xv.dim(-2);
     int64_t nb = 1;
     for (auto d : wb) nb *= d;
+    // so do batches whose rows' activation tile does not fit the skinny
+    // kernel's LDS (e.g. 64 rows of 4-bit g128 codes)
+    if (M > 16) {
+      int nw, pf;
+      qmv_shape_choice(sp.N, sp.K, nw, pf);
+      const mlxq::QmvPlan qp = mlxq::qmv_plan(fmt, sp.gs, sp.N, sp.K, (int)M, (int)nb,
+                                              device_info(current_device()).cus, nw, pf);
+      if (qp.lds > mlxq::kQmvLdsMax) {
+        run_gen_batched(sp, x, w, scales, biases, out, stream, ss);
+        return;
+      }
+    }
     a.E = (int)nb;
     a.X = (int)nb;
     a.w_expert_stride = wv.dim(-2) * wv.dim(-1);
@@ -1811,14 +1823,23 @@ void gather_run(GatherSpec& g, const mlxq_array* x, const mlxq_array* w, const m
     const mlxq::QmmPlan qp =
         mlxq::qmm_plan_grouped(fmt, sp.gs, sp.N, sp.K, per_expert <= 64 ? 3 : (per_expert <= 128 ? 2 : 0));
     const bool use_qmm = qp.ok && X * M * sp.K * 2 < ((int64_t)1 << 31);
-    // K not a multiple of 64: the MFMA skinny kernel over the same grouping
-    const int cap_rows = use_qmm ? qp.rows_per_tile : (int)std::min<int64_t>(cap, rows);
-    const int64_t maxseg = rows / cap_rows + std::min<int64_t>(E, B) + 1;
+    // K not a multiple of 64: the MFMA skinny kernel over the same grouping,
+    // in segments of fewer rows where the activation tile would not fit in
+    // LDS (e.g. 64 rows of 4-bit g128 codes)
+    int cap_rows = use_qmm ? qp.rows_per_tile : (int)std::min<int64_t>(cap, rows);
+    auto segs = [&](int cr) { return rows / cr + std::min<int64_t>(E, B) + 1; };
+    int nw = 0, pf = 0;
+    if (!use_qmm) {
+      qmv_shape_choice(sp.N, sp.K, nw, pf);
+      while (cap_rows > 1 && mlxq::qmv_plan(fmt, sp.gs, sp.N, sp.K, cap_rows,
+                                            (int)std::min<int64_t>(segs(cap_rows), 65535), di.cus, nw, pf)
+                                     .lds > mlxq::kQmvLdsMax)
+        cap_rows = (cap_rows + 1) / 2;
+    }
+    const int64_t maxseg = segs(cap_rows);
     if (maxseg > 65535) unsupported("gather_qmm: too many expert segments for one launch");
     mlxq::QmvPlan p;
     if (!use_qmm) {
-      int nw, pf;
-      qmv_shape_choice(sp.N, sp.K, nw, pf);
       p = mlxq::qmv_plan(fmt, sp.gs, sp.N, sp.K, cap_rows, (int)maxseg, di.cus, nw, pf);
       if (p.lds > mlxq::kQmvLdsMax) unsupported("gather_qmm: activation tile does not fit in LDS");
     }
@@ -1975,7 +1996,12 @@ void gather_run(GatherSpec& g, const mlxq_array* x, const mlxq_array* w, const m
   mlxq::QmvPlan p;
   if (!use_rs) {
     p = mlxq::qmv_plan(fmt, sp.gs, sp.N, sp.K, (int)M, (int)B, di.cus, nw, pf);
-    if (p.lds > mlxq::kQmvLdsMax) unsupported("gather_qmm: activation tile does not fit in LDS");
+    if (p.lds > mlxq::kQmvLdsMax) {
+      // more rows per entry than the skinny kernel's LDS holds at this
+      // group size: the general kernel tiles any row count
+      run_gen(sp, x, w, scales, biases, out, M, B, X, E, &ip, stream, ScratchSrc{});
+      return;
+    }
   }
   // indices the kernels can read in place skip the index_prep launch
   const DirectIdx dl = direct_index(lhs_indices, dsh[0], g.idx_shape);

@@ -103,3 +103,28 @@ def test_batched_weights_many_rows(xbatch):
     for e in range(E):
         xe = x[e if xbatch[0] == E else 0]
         assert max_rel(got[e], orc.qmm_t_affine(xe, wq[e], s[e], b[e], 64, 4)) <= TOL
+
+
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("M", [17, 40, 64])
+def test_rows_per_matrix_over_the_skinny_lds(gs, M):
+    # batched weights and gathered matrices with 17-64 activation rows each:
+    # at 4-bit g128 the skinny kernel's activation tile of 64 rows does not
+    # fit in LDS, so those calls run on the general kernel (or in smaller
+    # row segments) instead of being refused; every group size against the
+    # oracle
+    E, N, K = 3, 200, 2048
+    announce("rows_over_lds", gs, M)
+    w = orc.normal_bf16((E, N, K), 0.02, 4400 + gs + M)
+    wq, s, b = orc.affine_quantize(w, gs, 4)
+    x = orc.normal_bf16((E, M, K), 1.0, 4401 + gs + M)
+    W, S, B_ = dev_u32(wq), dev_bf16(s), dev_bf16(b)
+    got = host_u16(mq.quantized_matmul(dev_bf16(x), W, S, B_, True, gs, 4))
+    for e in range(E):
+        assert max_rel(got[e], orc.qmm_t_affine(x[e], wq[e], s[e], b[e], gs, 4)) <= TOL
+    rhs = np.array([2, 0, 1, 2, 0], dtype=np.int32)
+    lhs = np.array([1, 1, 0, 2, 2], dtype=np.int32)
+    g = host_u16(mq.gather_qmm(dev_bf16(x), W, S, B_, torch.from_numpy(lhs).cuda(), torch.from_numpy(rhs).cuda(),
+                               True, gs, 4))
+    want = orc.gather_qmm_t(x, wq, s, b, lhs.astype(np.uint32), rhs.astype(np.uint32), gs, 4)
+    assert max_rel(g, want) <= TOL
