@@ -105,8 +105,10 @@ typedef struct mlxq_array {
  * address of mlxq_quantized_matmul_noalloc's fixed scratch.  A captured
  * prefill call whose stream-K plan needs more scratch than the stream holds
  * (2 x CUs x 256 KiB, 128 MiB on MI355X) takes the plan without stream-K
- * instead of allocating.  No counterpart in the reference (MLX allocates
- * inside each eval). */
+ * instead of allocating; its result then equals the eager call's within
+ * rounding, not bit for bit (stream-K adds a cut tile's two K pieces in
+ * fp32).  No counterpart in the reference (MLX allocates inside each
+ * eval). */
 mlxq_status mlxq_workspace_reserve(size_t bytes, void* stream);
 
 /* Bytes of device memory held by the workspaces (current and replaced
@@ -157,10 +159,13 @@ mlxq_status mlxq_quantized_matmul(const mlxq_array* x, const mlxq_array* w,
                                   const char* mode, mlxq_array* out, void* stream);
 
 /* quantized_matmul without any allocation: the same validation, kernels and
- * result bits as mlxq_quantized_matmul, but the scratch some routes need
- * (split-K partials of the 5-16-row decode kernel and of the prefill GEMM)
- * lives in a fixed 64 MiB device array of the library (one per GPU, held
- * until the process ends) instead of the per-stream workspace.  Calls that
+ * result bits as mlxq_quantized_matmul (except at the prefill shapes that
+ * take the stream-K plan, whose partials do not fit the fixed scratch: the
+ * plan without it gives the same result within rounding), but the scratch
+ * some routes need (split-K partials of the 5-16-row decode kernel and of
+ * the prefill GEMM) lives in a fixed 64 MiB device array of the library (one
+ * per GPU, held until the process ends) instead of the per-stream
+ * workspace.  Calls that
  * would need more return MLXQ_ENOMEM with the size in mlxq_last_error().
  * Every call on one GPU shares that array: calls that overlap in time on one
  * GPU (several streams, threads or replays of graphs in flight together) race.
