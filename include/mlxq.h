@@ -203,7 +203,11 @@ int32_t mlxq_quantized_matmul_matches_dense_gemm(const mlxq_array* x, const mlxq
  * group_size, bits, mode) for i < n, 1 <= n <= 4, every w[i] 2-D and of the
  * same format.  Results are bit for bit those of n mlxq_quantized_matmul
  * calls; at decode row counts the n projections run as one launch that reads
- * x once.  `biases` (the array of pointers) may be NULL for mxfp4.  No
+ * x once.  One exception: at 5-16 rows, where the projections' 64-row
+ * blocks together exceed one round of the CUs while each alone fits (gate +
+ * up of 2 x 12288 rows on MI355X), the one launch takes the split-K kernel
+ * and the separate calls the whole-row kernel, so the results agree within
+ * rounding, not bit for bit.  `biases` (the array of pointers) may be NULL for mxfp4.  No
  * counterpart in the MLX op layer: it replaces the fused q/k/v and gate/up
  * GEMV launches of the reference's native decode path
  * (src/lib/mlxcel-xla/csrc/qmv4.hip:265-387, src/native_qmv.rs:250-330). */
