@@ -205,11 +205,12 @@ int32_t mlxq_quantized_matmul_matches_dense_gemm(const mlxq_array* x, const mlxq
  * calls; at decode row counts the n projections run as one launch that reads
  * x once.  One exception: at 5-16 rows, where the projections' 64-row
  * blocks together exceed one round of the CUs while each alone fits (gate +
- * up of 2 x 12288 rows on MI355X), the one launch takes the split-K kernel
- * and the separate calls the whole-row kernel, so the results agree within
- * rounding, not bit for bit.  `biases` (the array of pointers) may be NULL for mxfp4.  No
- * counterpart in the MLX op layer: it replaces the fused q/k/v and gate/up
- * GEMV launches of the reference's native decode path
+ * up of 2 x 12288 rows with 4-bit codes on MI355X), the one launch takes
+ * the split-K kernel and the separate calls the whole-row kernel, so the
+ * results agree within rounding, not bit for bit.  `biases` (the array of
+ * pointers) may be NULL for mxfp4.  No counterpart in the MLX op layer: it
+ * replaces the fused q/k/v and gate/up GEMV launches of the reference's
+ * native decode path
  * (src/lib/mlxcel-xla/csrc/qmv4.hip:265-387, src/native_qmv.rs:250-330). */
 mlxq_status mlxq_quantized_matmul_multi(const mlxq_array* x, int32_t n, const mlxq_array* const* w,
                                         const mlxq_array* const* scales,

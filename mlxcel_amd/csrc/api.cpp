@@ -1133,9 +1133,14 @@ bool try_mr_f16(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, con
   const int64_t min_rows = sp.bits == 4 ? 3 : kMidMinRows;
   if (!forced && (rows < min_rows || knobs().qmv_mr == 0 || !knobs().qmv_kernel.empty())) return false;
   const int fmt = fmt_of(sp.mode, sp.bits);
-  const mlxq::QmvMrPlan rp = mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, device_info(current_device()).cus,
-                                               forced, knobs().mr_ring);
+  const int cus = device_info(current_device()).cus;
+  const mlxq::QmvMrPlan rp = mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, forced, knobs().mr_ring);
   if (!rp.ok) return false;
+  // past one round of the CUs, 4-bit codes take the split-K kernel where it
+  // applies, as bfloat16 calls do
+  if (!forced && fmt == mlxq::AFF4 && rp.row_blocks > cus && use_mid((int)rows, fmt, sp.K) &&
+      mlxq::qmv_mid_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, knobs().mid_win).ok)
+    return false;
   mlxq::QmvMrArgs m{};
   m.x = static_cast<const uint16_t*>(x->data);
   m.w = static_cast<const uint32_t*>(w->data);
@@ -1299,10 +1304,14 @@ DenseRoute dense_route(const QmmSpec& sp, int64_t rows, int cus) {
   if (!kq_small && (forced == "mr" || (knobs().qmv_mr != 0 && forced.empty()))) {
     r.mr = mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, forced == "mr", knobs().mr_ring);
     // The whole-row kernel holds one 64-row block per CU at a time: past one
-    // round of the CUs the split-K mid-size kernel is faster where it applies
-    // (MI355X, 4-bit g64 K=4096: 151936 rows, 2374 blocks, 16 rows 133 ->
-    // 124 us, 8 rows 88.7 -> 85.6; 12288 rows, 192 blocks, stays whole-row)
-    if (r.mr.ok && !(forced.empty() && r.mr.row_blocks > cus && use_mid((int)rows, fmt, sp.K) &&
+    // round of the CUs the split-K mid-size kernel is faster for 4-bit codes
+    // where it applies (MI355X, 4-bit g64 K=4096: 151936 rows, 2374 blocks,
+    // 16 rows 133 -> 124 us, 8 rows 88.7 -> 85.6; 12288 rows, 192 blocks,
+    // stays whole-row); 8-bit codes stay whole-row at any size (151936
+    // rows: 5 rows 131 us vs 175 on the split-K kernel, 16 rows 155 vs 194;
+    // 24576 rows 29.4 vs 33.0)
+    if (r.mr.ok && !(forced.empty() && fmt == mlxq::AFF4 && r.mr.row_blocks > cus &&
+                     use_mid((int)rows, fmt, sp.K) &&
                      mlxq::qmv_mid_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, knobs().mid_win).ok)) {
       r.kind = DR_MR;
       return r;
@@ -1394,10 +1403,11 @@ bool try_multi_mid(const std::vector<QmmSpec>& sp, int n, const mlxq_array* x, c
   // The whole-row kernel runs one 64-row block per CU at a time: where the
   // projections' blocks together need more than one round of the CUs
   // (gate + up, 2 x 12288 rows: 384 blocks), the split-K mid-size kernel
-  // takes the launch instead, if it covers every projection alike (MI355X,
-  // Qwen3-8B gate + up, 4-bit g64: 16 rows 27.8 -> 24.6 us, 8 rows 19.2 ->
-  // 18.3).  Each output then has the mid-size kernel's bits (those of single
-  // calls with MLXQ_QMV_MR=0), within tolerance of the single calls'.
+  // takes the launch instead for 4-bit codes, if it covers every projection
+  // alike (MI355X, Qwen3-8B gate + up, 4-bit g64: 16 rows 27.8 -> 24.6 us,
+  // 8 rows 19.2 -> 18.3; 8-bit codes stay whole-row, 16 rows 31.7 us vs
+  // 34.8).  Each output then has the mid-size kernel's bits (those of
+  // single calls with MLXQ_QMV_MR=0), within tolerance of the single calls'.
   // K split over the waves: one tile count for all projections, the
   // fewest whose blocks together fit one round of the CUs (else the
   // projections run one by one).
@@ -1421,7 +1431,8 @@ bool try_multi_mid(const std::vector<QmmSpec>& sp, int n, const mlxq_array* x, c
     }
     if (!planned) return false;
   }
-  if (r[0].kind == DR_MR && r[0].mr.t == 0 && knobs().qmv_kernel.empty() && use_mid((int)rows, fmt, sp[0].K)) {
+  if (r[0].kind == DR_MR && r[0].mr.t == 0 && knobs().qmv_kernel.empty() && fmt == mlxq::AFF4 &&
+      use_mid((int)rows, fmt, sp[0].K)) {
     int64_t mr_blocks = 0;
     for (int i = 0; i < n; i++) mr_blocks += r[i].mr.row_blocks;
     if (mr_blocks > cus) {

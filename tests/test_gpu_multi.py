@@ -188,6 +188,39 @@ def test_gate_up_past_one_round_takes_mid(monkeypatch, M):
         assert max_rel(multi[i], orc.qmm_t_affine(x, *sets[i], 64, 4)) <= TOL
 
 
+@pytest.mark.parametrize("M", [5, 8, 16])
+def test_gate_up_past_one_round_8bit_stays_whole_row(M):
+    # 8-bit codes keep the whole-row kernel past one round of the CUs (it is
+    # the faster there), alone and in one launch: bitwise the single calls
+    announce("multi_gate_up_8bit_mr", M)
+    K = 4096
+    x = orc.normal_bf16((M, K), 1.0, 1960 + M)
+    check(x, affine_sets([12288, 12288], K, 8, 64, 1970), 64, 8)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M", [5, 16])
+def test_tall_matrix_route_by_code_width(monkeypatch, bits, M):
+    # a 151936-row matrix (the LM head shape, 2374 blocks of 64 rows) at
+    # 5-16 rows: 8-bit codes on the whole-row kernel, 4-bit on the split-K
+    # kernel; bitwise the forced kernel of its width, within tolerance of the
+    # oracle on a slice of rows
+    announce("tall_route", bits, M)
+    K, N = 4096, 151936
+    g = torch.Generator(device="cuda").manual_seed(1980 + bits + M)
+    w = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    wq, s, b = mq.quantize(w, 64, bits)
+    del w
+    y = host_u16(mq.quantized_matmul(x, wq, s, b, True, 64, bits))
+    setknob(monkeypatch, "MLXQ_QMV_KERNEL", "mr" if bits == 8 else "mid")
+    np.testing.assert_array_equal(y, host_u16(mq.quantized_matmul(x, wq, s, b, True, 64, bits)))
+    rows = slice(0, 4096)
+    ref = x.float() @ mq.dequantize(wq[rows], s[rows], b[rows], 64, bits).float().t()
+    got = torch.from_numpy(y[:, rows].astype(np.int16)).view(torch.bfloat16).float().cuda()
+    assert float((got - ref).abs().max() / ref.abs().max()) <= TOL
+
+
 @pytest.mark.parametrize("gs", [32, 128])
 def test_mid_one_launch_ragged(gs):
     # ragged widths (partial 128-row blocks, widths not a multiple of 4: the
