@@ -808,9 +808,11 @@ Skinny skinny_choice(int rows, int fmt = mlxq::AFF4, int64_t K = 0) {
   if (k == "rs") return rows <= 4 ? Skinny::RS : Skinny::MFMA;
   if (k == "fr") return rows <= 2 ? Skinny::FR : Skinny::MFMA;
   if (k == "b4") return rows <= 16 ? Skinny::B4 : Skinny::MFMA;
-  // 3-4 rows over short affine rows (one 16-piece chunk per wave): the
-  // block-MFMA kernel with 32 weight rows per workgroup is ~4% faster
-  if (rows >= 3 && rows <= 4 && fmt != mlxq::MXFP4 && K * (fmt == mlxq::AFF8 ? 8 : 4) <= 16384) return Skinny::B4;
+  // 3-4 rows over short affine rows (less than one 16-piece chunk per
+  // wave): the block-MFMA kernel with 32 weight rows per workgroup is faster
+  // (MI355X, 4-bit 2880 x 2880, 3 rows: 6.6 us vs 7.7); at K = 4096 row
+  // streaming is (1024 x 4096: 4.3 vs 6.9; 4096 x 4096: 6.7 vs 7.9)
+  if (rows >= 3 && rows <= 4 && fmt != mlxq::MXFP4 && K * (fmt == mlxq::AFF8 ? 8 : 4) < 16384) return Skinny::B4;
   if (rows <= 4) return Skinny::RS;
   if (rows <= 8 && (fmt != mlxq::AFF4 || K <= 8192)) return Skinny::B4;
   return Skinny::MFMA;
@@ -1137,10 +1139,15 @@ bool try_mr_f16(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, con
   const mlxq::QmvMrPlan rp = mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, forced, knobs().mr_ring);
   if (!rp.ok) return false;
   // past one round of the CUs, 4-bit codes take the split-K kernel where it
-  // applies, as bfloat16 calls do
+  // applies, and at 9-16 rows the K-split-over-waves kernel where its tiles
+  // fit one round three to a workgroup, as bfloat16 calls do
   if (!forced && fmt == mlxq::AFF4 && rp.row_blocks > cus && use_mid((int)rows, fmt, sp.K) &&
       mlxq::qmv_mid_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, knobs().mid_win).ok)
     return false;
+  if (!forced && fmt == mlxq::AFF4 && rows > 8 && knobs().qmv_kq != 0 && kq_default_rows(fmt, rows, sp.K)) {
+    const mlxq::QmvMrPlan kp = mlxq::qmv_kq_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, knobs().kq_t);
+    if (kp.ok && kp.t <= 3) return false;
+  }
   mlxq::QmvMrArgs m{};
   m.x = static_cast<const uint16_t*>(x->data);
   m.w = static_cast<const uint32_t*>(w->data);
@@ -1285,12 +1292,39 @@ struct DenseRoute {
   mlxq::QmvMidPlan mid;
 };
 
-DenseRoute dense_route(const QmmSpec& sp, int64_t rows, int cus) {
+// single: a call of its own (false for the projections of a fused launch,
+// whose kernels must agree).
+DenseRoute dense_route(const QmmSpec& sp, int64_t rows, int cus, bool single = true) {
   DenseRoute r;
   const int fmt = fmt_of(sp.mode, sp.bits);
   if (rows < 1 || rows > 16) return r;
   const std::string& forced = knobs().qmv_kernel;
-  const bool mr_fits = mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, false, 0).ok;
+  const mlxq::QmvMrPlan mr0 = mlxq::qmv_mr_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, false, 0);
+  const bool mr_fits = mr0.ok;
+  // Single calls of 4-bit codes (MI355X, g64, K=4096, graph-timed):
+  // - 3-4 rows past one round of the CUs: the split-K kernel (151936 rows:
+  //   78.3 us vs 84.3 whole-row at 3 rows, 79.4 vs 85.4 at 4);
+  // - 9-16 rows over a matrix whose 16-row tiles fit one round three to a
+  //   workgroup: the K-split-over-waves kernel (12288 rows: 12 rows 12.6 us
+  //   vs 14.2 whole-row, 16 rows 12.9 vs 14.5; 14336 rows need four tiles
+  //   per workgroup and stay whole-row, 14.9 vs 14.5).
+  if (single && forced.empty() && fmt == mlxq::AFF4 && knobs().qmv_mr != 0) {
+    if (rows >= 3 && rows < kMidMinRows && mr_fits && mr0.row_blocks > cus && knobs().qmv_mid != 0) {
+      r.mid = mlxq::qmv_mid_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, knobs().mid_win);
+      if (r.mid.ok) {
+        r.kind = DR_MID;
+        return r;
+      }
+    }
+    if (rows > 8 && mr_fits && knobs().qmv_kq != 0 && kq_default_rows(fmt, rows, sp.K)) {
+      const mlxq::QmvMrPlan kp = mlxq::qmv_kq_plan(fmt, sp.gs, sp.N, sp.K, (int)rows, cus, knobs().kq_t);
+      if (kp.ok && kp.t <= 3) {
+        r.mr = kp;
+        r.kind = DR_MR;
+        return r;
+      }
+    }
+  }
   const bool mr_small = rows >= 3 && rows < kMidMinRows && fmt == mlxq::AFF4 && knobs().qmv_mr != 0 &&
                         forced.empty() && mr_fits;
   // 3-4 rows over matrices with too few rows for the whole-row kernel: the
@@ -1388,7 +1422,7 @@ bool try_multi_mid(const std::vector<QmmSpec>& sp, int n, const mlxq_array* x, c
   std::vector<DenseRoute> r;
   for (int i = 0; i < n; i++) {
     if (sp[i].N == 0 || sp[i].K != sp[0].K || sp[i].gs != sp[0].gs) return false;
-    r.push_back(dense_route(sp[i], rows, cus));
+    r.push_back(dense_route(sp[i], rows, cus, false));
     if (r[i].kind == DR_OTHER || r[i].kind != r[0].kind) return false;
     if (r[i].kind == DR_MR) {
       const mlxq::QmvMrPlan &a = r[i].mr, &b = r[0].mr;
@@ -2267,7 +2301,7 @@ mlxq_status mlxq_quantized_matmul_multi(const mlxq_array* x, int32_t n, const ml
     mp.n = n;
     for (int i = 0; i < n && fused; i++) {
       // a projection that alone would take a mid-size kernel is not fused here
-      if (sp[i].N == 0 || dense_route(sp[i], rows, device_info(current_device()).cus).kind != DR_OTHER)
+      if (sp[i].N == 0 || dense_route(sp[i], rows, device_info(current_device()).cus, false).kind != DR_OTHER)
         fused = false;
       const mlxq::QmvRsPlan p =
           mlxq::qmv_rs_plan(fmt, sp[i].gs, sp[i].N, sp[i].K, (int)rows, knobs().qmv_r);

@@ -157,3 +157,47 @@ def test_kq_uncovered_shapes_fall_back(kq, M, K, gs, bits):
     announce("kq_fallback", M, K, gs, bits)
     x, wq, s, b = affine_case(M, 96, K, gs, bits, 5950 + M)
     assert max_rel(run(x, wq, s, b, gs, bits), orc.qmm_t_affine(x, wq, s, b, gs, bits)) <= TOL
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("M", [9, 12, 16])
+@pytest.mark.parametrize("N,kernel", [(12288, "kq"), (14336, "mr")])
+def test_single_tall_matrix_9_16_rows_route(monkeypatch, dtype, M, N, kernel):
+    # a single 4-bit call at 9-16 rows: 12288 rows (768 tiles of 16, three
+    # to a workgroup fill one round) take this kernel, 14336 rows (four to a
+    # workgroup) the whole-row one; bitwise that forced kernel, within
+    # tolerance of a float32 product of the dequantized weights
+    announce("single_tall_route", dtype, M, N, kernel)
+    K = 4096
+    dt = torch.float16 if dtype == "float16" else torch.bfloat16
+    g = torch.Generator(device="cuda").manual_seed(6000 + M + N)
+    w = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(dt)
+    x = torch.randn(M, K, device="cuda", generator=g).to(dt)
+    wq, s, b = mq.quantize(w, 64, 4)
+    y = host_u16(mq.quantized_matmul(x, wq, s, b, True, 64, 4))
+    setknob(monkeypatch, "MLXQ_QMV_KERNEL", kernel)
+    np.testing.assert_array_equal(y, host_u16(mq.quantized_matmul(x, wq, s, b, True, 64, 4)))
+    ref = x.float() @ mq.dequantize(wq, s, b, 64, 4).float().t()
+    got = torch.from_numpy(y.astype(np.int16)).view(dt).float().cuda()
+    assert float((got - ref).abs().max() / ref.abs().max()) <= TOL
+
+
+@pytest.mark.parametrize("M", [3, 4])
+def test_lm_head_3_4_rows_takes_split_k(monkeypatch, M):
+    # 4-bit, 151936 rows (2374 blocks of 64: past one round of the CUs) at
+    # 3-4 rows: the split-K kernel, bitwise its forced result
+    announce("lm_head_3_4_route", M)
+    K, N = 4096, 151936
+    g = torch.Generator(device="cuda").manual_seed(6100 + M)
+    w = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    wq, s, b = mq.quantize(w, 64, 4)
+    del w
+    y = host_u16(mq.quantized_matmul(x, wq, s, b, True, 64, 4))
+    setknob(monkeypatch, "MLXQ_QMV_KERNEL", "mid")
+    np.testing.assert_array_equal(y, host_u16(mq.quantized_matmul(x, wq, s, b, True, 64, 4)))
+    rows = slice(0, 4096)
+    ref = x.float() @ mq.dequantize(wq[rows], s[rows], b[rows], 64, 4).float().t()
+    got = torch.from_numpy(y[:, rows].astype(np.int16)).view(torch.bfloat16).float().cuda()
+    assert float((got - ref).abs().max() / ref.abs().max()) <= TOL
+
