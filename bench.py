@@ -271,6 +271,53 @@ def n_sweep(iters=240):
     return {"rows": rows, "fit": fit}
 
 
+def route_audit(bits_list=(4, 8), rows_list=(1, 2, 3, 4, 5, 8, 12, 16)):
+    """Decode routing audit: the default route beside every kernel the
+    library can be forced to (MLXQ_QMV_KERNEL), at 7-8B projection shapes,
+    the gpt-oss expert shape and a 151936-row LM head; 4/8-bit g64, graph
+    timing over enough weight copies to stream from HBM.  A row whose best
+    kernel beats the default by 5% or more is marked."""
+    from mlxcel_amd import _lib
+    shapes = [(4096, 4096), (1024, 4096), (12288, 4096), (4096, 12288), (14336, 4096), (4096, 14336),
+              (2880, 2880), (151936, 4096)]
+    kernels = ["", "rs", "b4", "mr", "kq", "mid", "mfma"]
+    saved = os.environ.get("MLXQ_QMV_KERNEL")
+    res = []
+    for bits in bits_list:
+        for N, K in shapes:
+            L = max(2, min(64, int(2.4 * MALL_BYTES / (N * K * bits // 8)) + 1))
+            ws = [make_affine(N, K, bits, 64, 500 + i) for i in range(L)]
+            for M in rows_list:
+                x = randn_bf16((M, K), 7)
+                out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+                row = {"bits": bits, "N": N, "K": K, "M": M}
+                for k in kernels:
+                    os.environ.pop("MLXQ_QMV_KERNEL", None)
+                    if k:
+                        os.environ["MLXQ_QMV_KERNEL"] = k
+                    _lib.load().mlxq_reload_options()
+                    try:
+                        g = capture(lambda: [mq.quantized_matmul(x, *w, True, 64, bits, out=out) for w in ws])
+                    except (RuntimeError, ValueError):  # a forced kernel that does not take this shape
+                        row[k or "default"] = None
+                        continue
+                    row[k or "default"] = round(timed_graphs([g], 6, 1, SETTLE_MS) * 1e3 / L, 2)
+                    del g
+                best = min((k for k in kernels[1:] if row[k] is not None), key=lambda k: row[k])
+                row["best"] = best
+                row["default_vs_best"] = round(row["default"] / row[best], 3)
+                res.append(row)
+                print(("!! " if row["default_vs_best"] > 1 / 0.95 else "   ") + json.dumps(row),
+                      file=sys.stderr, flush=True)
+            del ws
+            torch.cuda.empty_cache()
+    os.environ.pop("MLXQ_QMV_KERNEL", None)
+    if saved is not None:
+        os.environ["MLXQ_QMV_KERNEL"] = saved
+    _lib.load().mlxq_reload_options()
+    return res
+
+
 def copy_ceiling():
     n = 1 << 30
     src = torch.empty(n, dtype=torch.uint8, device="cuda")
@@ -860,7 +907,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--extras", default="copy,c1,sweep,qmm,gather,moe,e2e,general",
                     help="comma-separated extra sections: copy, c1, sweep, qmm, gather, moe, e2e, general "
-                         "(and nsweep, not in the default set)")
+                         "(and nsweep, routes, not in the default set)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run 5 copies of 256 MiB and 5 gate launches, eager, for rocprofv3 --pmc")
@@ -919,6 +966,8 @@ def main():
             extra["c1_qmv_4096"] = c1_qmv(with_cpu=not args.no_cpu)
         if "nsweep" in want:
             extra["qmv_n_sweep"] = n_sweep()
+        if "routes" in want:
+            extra["qmv_route_audit"] = route_audit()
         if "sweep" in want:
             extra["qmv_sweep"] = qmv_sweep()
         if "qmm" in want:
