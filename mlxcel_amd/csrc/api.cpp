@@ -564,6 +564,7 @@ struct Knobs {
   int qmv_mr = 1;  // whole-row mid-size kernel where it applies (0: off)
   int mr_ring = 0;  // its weight ring depth in windows (0: planner)
   int gen_ks = 0;  // K splits of the general kernel (0: planner)
+  int gen_qmv = 1;  // 0: 1-2-row general calls stay on the tile kernel
   int gather_sorted = 1, gather_group = -1, gather_runs = 2, gather_direct = 1;
   int red_vec = 0;  // outputs per thread of the mid-size kernel's split-K reduction (0: default)
   int qmm_mix = 1;  // prefill: two-launch plan for a part-full last round of tiles (0: off)
@@ -598,6 +599,7 @@ const Knobs* read_knobs() {
   k->qmv_mr = env_int("MLXQ_QMV_MR", 1);
   k->mr_ring = env_int("MLXQ_MR_RING", 0);
   k->gen_ks = env_int("MLXQ_GEN_KS", 0);
+  k->gen_qmv = env_int("MLXQ_GEN_QMV", 1);
   k->gather_sorted = env_int("MLXQ_GATHER_SORTED", 1);
   k->gather_group = env_int("MLXQ_GATHER_GROUP", -1);
   k->gather_runs = env_int("MLXQ_GATHER_RUNS", 2);
@@ -994,13 +996,17 @@ void run_gen(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const 
   if (nseg == 0 || M == 0 || sp.N == 0) return;
   if (sp.K == 0) unsupported("quantized_matmul: K == 0");
   const int dev = current_device();
-  const mlxq::GenPlan p = mlxq::gen_plan(M, sp.N, sp.K, nseg, device_info(dev).cus, knobs().gen_ks);
-  if (!p.ok) unsupported("quantized matmul: too many row tiles or segments for one launch");
+  // 1-2 rows with transpose=true and affine codes: the decode kernel (one
+  // wave per 8 weight rows, no K split); otherwise the tile kernel
+  const bool dec = knobs().gen_qmv != 0 && knobs().gen_ks <= 0 &&
+                   sp.mode == AFFINE && biases != nullptr && mlxq::qmv_gen_fits(mlxq::GEN_AFFINE, sp.transpose, M, sp.N, sp.K, nseg, sp.bits);
+  const mlxq::GenPlan p = dec ? mlxq::GenPlan{} : mlxq::gen_plan(M, sp.N, sp.K, nseg, device_info(dev).cus, knobs().gen_ks);
+  if (!dec && !p.ok) unsupported("quantized matmul: too many row tiles or segments for one launch");
   const int tc = gen_type(sp.out_dtype);
   const int64_t out_elems = nseg * M * sp.N;
   auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
   const size_t idx_bytes = ip ? al((size_t)nseg * 2 * sizeof(uint32_t)) : 0;
-  const size_t part_bytes = p.ks > 1 ? (size_t)p.ks * out_elems * sizeof(float) : 0;
+  const size_t part_bytes = !dec && p.ks > 1 ? (size_t)p.ks * out_elems * sizeof(float) : 0;
   char* base = idx_bytes + part_bytes ? static_cast<char*>(workspace(dev, stream, idx_bytes + part_bytes, ss))
                                       : nullptr;
   mlxq::GenArgs a{};
@@ -1036,6 +1042,10 @@ void run_gen(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const 
   a.w_expert_stride = wv.dim(-2) * wv.dim(-1);
   a.s_expert_stride = sv.dim(-2) * sv.dim(-1);
   a.out_elems = out_elems;
+  if (dec) {
+    hip_check(mlxq::qmv_gen_launch(a, tc, nseg, stream), "qmv_gen launch");
+    return;
+  }
   hip_check(mlxq::qmm_gen_launch(a, p, tc, sp.transpose, nseg, stream), "qmm_gen launch");
   if (p.ks > 1) hip_check(mlxq::launch_gen_reduce(a.ws, out->data, out_elems, p.ks, tc, stream), "reduce launch");
 }

@@ -308,6 +308,140 @@ __global__ __launch_bounds__(256) void gen_reduce_kernel(const float* ws, void* 
   else static_cast<uint16_t*>(out)[i] = __builtin_bit_cast(uint16_t, (_Float16)s);
 }
 
+// ---- decode: 1-2 rows, transpose=true, affine ------------------------------
+//
+// The general path's decode shapes (codes of 1-8 bits, or float32
+// activations) as a row-streaming GEMV instead of the tile kernel: a wave
+// owns R weight rows; lane l takes the 32-position pieces l, l + 64, ... of
+// every row.  A piece is BITS consecutive words (the reference's
+// little-endian bit stream, quantized.cpp:107-137) inside one quantization
+// group, so per piece and row
+//   y += s * sum_j q_j x_j + b * sum_j x_j
+// with the codes widened exactly to fp32 and every product and sum in fp32
+// (the reference's qmv formulation, qmv_tiled_kernel.hip:29-128).  The
+// activation piece (32 values per row) is converted once and serves the R
+// rows.  Lane partials meet in a butterfly over the wave; no LDS, no
+// barriers, one launch.
+constexpr int kGenQmvRows = 8;  // weight rows per wave
+constexpr int kGenQmvWaves = 4;
+
+template <int XT>
+__device__ __forceinline__ void load32_as_f32(const void* p, int64_t i, float (&v)[32]) {
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    float t[8];
+    load8_as_f32(p, i + 8 * q, XT, t);
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[8 * q + j] = t[j];
+  }
+}
+
+// load_as_f32 without branches on the element type (two 16-bit loads, the
+// second one repeating the first for 16-bit types), so that the loads of
+// several rows can be issued together
+__device__ __forceinline__ float load_as_f32_flat(const void* p, int64_t i, int dt) {
+  const uint16_t* h = static_cast<const uint16_t*>(p);
+  const bool wide = dt == GEN_F32;
+  const uint32_t lo = h[wide ? 2 * i : i], hi = h[wide ? 2 * i + 1 : i];
+  const float f16v = (float)__builtin_bit_cast(_Float16, (uint16_t)lo);
+  const float v16 = dt == GEN_BF16 ? __uint_as_float(lo << 16) : f16v;
+  return wide ? __uint_as_float(lo | (hi << 16)) : v16;
+}
+
+// code j of a piece held in w[0 .. BITS-1]
+template <int BITS>
+__device__ __forceinline__ uint32_t piece_code(const uint32_t (&w)[BITS], int j) {
+  const int o = j * BITS, i = o >> 5, sh = o & 31;
+  uint32_t v = w[i] >> sh;
+  if (sh + BITS > 32) v |= w[i + 1] << (32 - sh);
+  return v & ((1u << BITS) - 1u);
+}
+
+template <int BITS, int XT, int MR>
+__global__ __launch_bounds__(256) void qmv_gen_kernel(const GenArgs a, int tc) {
+  constexpr int R = kGenQmvRows;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int seg = blockIdx.y;
+  const int n0 = (blockIdx.x * kGenQmvWaves + wave) * R;
+  if (n0 >= a.N) return;  // wave-uniform; the kernel has no barriers
+  const int N = a.N, K = a.K, M = a.M;
+  const int xb = a.lhs ? (int)min(a.lhs[seg], (uint32_t)(a.X - 1)) : (a.X > 1 ? seg : 0);
+  const int eb = a.rhs ? (int)min(a.rhs[seg], (uint32_t)(a.E - 1)) : (a.E > 1 ? seg : 0);
+  const uint32_t* W = a.w + (int64_t)eb * a.w_expert_stride;
+  const int64_t sofs = (int64_t)eb * a.s_expert_stride;
+  const int64_t rw = (int64_t)(K >> 5) * BITS;  // words per weight row
+  const int G = K >> a.gs_shift;
+  const int nch = K >> 5;
+
+  float acc[MR][R];
+#pragma unroll
+  for (int m = 0; m < MR; m++)
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[m][r] = 0.f;
+
+  for (int c = lane; c < nch; c += 64) {
+    float xv[MR][32], sx[MR];
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      if (m < M) {
+        load32_as_f32<XT>(a.x, ((int64_t)xb * M + m) * K + (int64_t)c * 32, xv[m]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 32; j++) xv[m][j] = 0.f;
+      }
+      float t = 0.f;
+#pragma unroll
+      for (int j = 0; j < 32; j++) t += xv[m][j];
+      sx[m] = t;
+    }
+    // all R rows' loads first (rows past N read row N-1 and are not
+    // stored), so their latencies overlap
+    const int g = (c * 32) >> a.gs_shift;
+    uint32_t w[R][BITS];
+    float sv[R], bv[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const int n = min(n0 + r, N - 1);
+      const uint32_t* wp = W + (int64_t)n * rw + (int64_t)c * BITS;
+#pragma unroll
+      for (int t = 0; t < BITS; t++) w[r][t] = wp[t];
+      sv[r] = load_as_f32_flat(a.scales, sofs + (int64_t)n * G + g, a.s_dtype);
+      bv[r] = load_as_f32_flat(a.biases, sofs + (int64_t)n * G + g, a.b_dtype);
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      float qx[MR];
+#pragma unroll
+      for (int m = 0; m < MR; m++) qx[m] = 0.f;
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
+        const float q = (float)piece_code<BITS>(w[r], j);
+#pragma unroll
+        for (int m = 0; m < MR; m++) qx[m] = __builtin_fmaf(q, xv[m][j], qx[m]);
+      }
+#pragma unroll
+      for (int m = 0; m < MR; m++) acc[m][r] = __builtin_fmaf(sv[r], qx[m], __builtin_fmaf(bv[r], sx[m], acc[m][r]));
+    }
+  }
+
+#pragma unroll
+  for (int m = 0; m < MR; m++) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      float v = acc[m][r];
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+      const int n = n0 + r;
+      if (lane == 0 && m < M && n < N) {
+        const int64_t o = ((int64_t)seg * M + m) * N + n;
+        if (tc == GEN_F32) static_cast<float*>(a.out)[o] = v;
+        else if (tc == GEN_BF16) static_cast<uint16_t*>(a.out)[o] = (uint16_t)f32_to_bf16_bits(v);
+        else static_cast<uint16_t*>(a.out)[o] = __builtin_bit_cast(uint16_t, (_Float16)v);
+      }
+    }
+  }
+}
+
 // ---- host ------------------------------------------------------------------
 
 GenPlan gen_plan(int64_t M, int64_t N, int64_t K, int64_t nseg, int cus, int ks_req) {
@@ -357,6 +491,35 @@ hipError_t qmm_gen_launch(const GenArgs& a0, const GenPlan& p, int tc, bool tran
   GEN_CASE(GEN_F32, 16, false)
   GEN_CASE(GEN_F32, 64, false)
 #undef GEN_CASE
+  return hipErrorInvalidValue;
+}
+
+bool qmv_gen_fits(int mode, bool transpose, int64_t M, int64_t N, int64_t K, int64_t nseg, int bits) {
+  return mode == GEN_AFFINE && transpose && M >= 1 && M <= 2 && K % 32 == 0 && K > 0 && nseg <= 65535 &&
+         (N + kGenQmvRows * kGenQmvWaves - 1) / (kGenQmvRows * kGenQmvWaves) <= 0x7FFFFFFF &&
+         ((bits >= 1 && bits <= 6) || bits == 8);
+}
+
+hipError_t qmv_gen_launch(const GenArgs& a, int tc, int64_t nseg, hipStream_t stream) {
+  if (!qmv_gen_fits(a.mode, true, a.M, a.N, a.K, nseg, a.bits)) return hipErrorInvalidValue;
+  const int64_t per_wg = kGenQmvRows * kGenQmvWaves;
+  const dim3 grid((unsigned)((a.N + per_wg - 1) / per_wg), (unsigned)nseg), block(64 * kGenQmvWaves);
+#define QG_CASE(B_, X_, MR_)                                                                  \
+  if (a.bits == B_ && a.x_dtype == X_ && (a.M <= 1) == (MR_ == 1)) {                          \
+    hipLaunchKernelGGL((qmv_gen_kernel<B_, X_, MR_>), grid, block, 0, stream, a, tc);         \
+    return hipGetLastError();                                                                 \
+  }
+#define QG_BITS(X_, MR_) \
+  QG_CASE(1, X_, MR_) QG_CASE(2, X_, MR_) QG_CASE(3, X_, MR_) QG_CASE(4, X_, MR_) \
+  QG_CASE(5, X_, MR_) QG_CASE(6, X_, MR_) QG_CASE(8, X_, MR_)
+  QG_BITS(GEN_BF16, 1)
+  QG_BITS(GEN_BF16, 2)
+  QG_BITS(GEN_F16, 1)
+  QG_BITS(GEN_F16, 2)
+  QG_BITS(GEN_F32, 1)
+  QG_BITS(GEN_F32, 2)
+#undef QG_BITS
+#undef QG_CASE
   return hipErrorInvalidValue;
 }
 
