@@ -997,7 +997,7 @@ void run_gen(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const 
   if (sp.K == 0) unsupported("quantized_matmul: K == 0");
   const int dev = current_device();
   // 1-2 rows with transpose=true and affine codes: the decode kernel (one
-  // wave per 8 weight rows, no K split); otherwise the tile kernel
+  // wave per 4 weight rows, no K split); otherwise the tile kernel
   const bool dec = knobs().gen_qmv != 0 && knobs().gen_ks <= 0 &&
                    sp.mode == AFFINE && biases != nullptr && mlxq::qmv_gen_fits(mlxq::GEN_AFFINE, sp.transpose, M, sp.N, sp.K, nseg, sp.bits);
   const mlxq::GenPlan p = dec ? mlxq::GenPlan{} : mlxq::gen_plan(M, sp.N, sp.K, nseg, device_info(dev).cus, knobs().gen_ks);

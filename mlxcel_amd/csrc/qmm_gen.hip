@@ -322,7 +322,7 @@ __global__ __launch_bounds__(256) void gen_reduce_kernel(const float* ws, void* 
 // activation piece (32 values per row) is converted once and serves the R
 // rows.  Lane partials meet in a butterfly over the wave; no LDS, no
 // barriers, one launch.
-constexpr int kGenQmvRows = 8;  // weight rows per wave
+constexpr int kGenQmvRows = 4;  // weight rows per wave
 constexpr int kGenQmvWaves = 4;
 
 template <int XT>
