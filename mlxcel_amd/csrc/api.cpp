@@ -1000,13 +1000,21 @@ void run_gen(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const 
   // wave per 4 weight rows, no K split); otherwise the tile kernel
   const bool dec = knobs().gen_qmv != 0 && knobs().gen_ks <= 0 &&
                    sp.mode == AFFINE && biases != nullptr && mlxq::qmv_gen_fits(mlxq::GEN_AFFINE, sp.transpose, M, sp.N, sp.K, nseg, sp.bits);
-  const mlxq::GenPlan p = dec ? mlxq::GenPlan{} : mlxq::gen_plan(M, sp.N, sp.K, nseg, device_info(dev).cus, knobs().gen_ks);
-  if (!dec && !p.ok) unsupported("quantized matmul: too many row tiles or segments for one launch");
+  // the same for transpose=false: column pieces over K ranges
+  const mlxq::GenTPlan tp = knobs().gen_qmv != 0 && knobs().gen_ks <= 0 && sp.mode == AFFINE && biases != nullptr &&
+                                    !sp.transpose
+                                ? mlxq::qmv_gen_t_plan(M, sp.N, sp.K, nseg, sp.bits, mlxq::GEN_AFFINE, device_info(dev).cus)
+                                : mlxq::GenTPlan{};
+  const bool dect = tp.ok;
+  const mlxq::GenPlan p = dec || dect ? mlxq::GenPlan{}
+                                      : mlxq::gen_plan(M, sp.N, sp.K, nseg, device_info(dev).cus, knobs().gen_ks);
+  if (!dec && !dect && !p.ok) unsupported("quantized matmul: too many row tiles or segments for one launch");
   const int tc = gen_type(sp.out_dtype);
   const int64_t out_elems = nseg * M * sp.N;
   auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
   const size_t idx_bytes = ip ? al((size_t)nseg * 2 * sizeof(uint32_t)) : 0;
-  const size_t part_bytes = !dec && p.ks > 1 ? (size_t)p.ks * out_elems * sizeof(float) : 0;
+  const int parts = dect ? tp.ks : dec ? 1 : p.ks;
+  const size_t part_bytes = parts > 1 ? (size_t)parts * out_elems * sizeof(float) : 0;
   char* base = idx_bytes + part_bytes ? static_cast<char*>(workspace(dev, stream, idx_bytes + part_bytes, ss))
                                       : nullptr;
   mlxq::GenArgs a{};
@@ -1044,6 +1052,11 @@ void run_gen(const QmmSpec& sp, const mlxq_array* x, const mlxq_array* w, const 
   a.out_elems = out_elems;
   if (dec) {
     hip_check(mlxq::qmv_gen_launch(a, tc, nseg, stream), "qmv_gen launch");
+    return;
+  }
+  if (dect) {
+    hip_check(mlxq::qmv_gen_t_launch(a, tp, tc, nseg, stream), "qmv_gen_t launch");
+    if (tp.ks > 1) hip_check(mlxq::launch_gen_reduce(a.ws, out->data, out_elems, tp.ks, tc, stream), "reduce launch");
     return;
   }
   hip_check(mlxq::qmm_gen_launch(a, p, tc, sp.transpose, nseg, stream), "qmm_gen launch");

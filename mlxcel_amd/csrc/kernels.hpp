@@ -160,6 +160,18 @@ hipError_t launch_gen_reduce(const float* ws, void* out, int64_t n, int ks, int 
 // biases too); tc is the result type.
 bool qmv_gen_fits(int mode, bool transpose, int64_t M, int64_t N, int64_t K, int64_t nseg, int bits);
 hipError_t qmv_gen_launch(const GenArgs& a, int tc, int64_t nseg, hipStream_t stream);
+// transpose=false decode (qmm_gen.hip): 1-2 rows, affine codes of 1-6 or 8
+// bits, N a multiple of 32; workgroups of 8 waves over 64 column pieces of
+// 32 and one K range of `kper` code rows; ks > 1 ranges write fp32 partials
+// ([ks][out_elems] in a.ws) for launch_gen_reduce.
+struct GenTPlan {
+  bool ok = false;
+  int blocks = 0;  // workgroups along N
+  int ks = 1;      // K ranges
+  int kper = 0;    // code rows per range
+};
+GenTPlan qmv_gen_t_plan(int64_t M, int64_t N, int64_t K, int64_t nseg, int bits, int mode, int cus);
+hipError_t qmv_gen_t_launch(const GenArgs& a, const GenTPlan& p, int tc, int64_t nseg, hipStream_t stream);
 // dequantize for every element type (dequant.hip): affine codes of 2-8 bits
 // with scales/biases of type ts, or mxfp4 (mode GEN_MXFP4) to float16/float32;
 // `to` is the output type.  K a multiple of 32.

@@ -442,6 +442,104 @@ __global__ __launch_bounds__(256) void qmv_gen_kernel(const GenArgs a, int tc) {
   }
 }
 
+// transpose=false decode (W is [K][N], codes packed along N): lane l of a
+// workgroup owns the 32-column piece blockIdx.x * 64 + l, i.e. 32 fp32 sums
+// per activation row, over the code rows k of the workgroup's K range; the 8
+// waves take every 8th row, kGenQmvtRows rows at a time with all their loads
+// issued first (rows past the range read the range's last row and count with
+// x = 0).  Per row and piece: s * x_k and b * x_k once, then 32 FMAs; the
+// bias part is one running sum per piece.  The waves' sums meet in LDS in a
+// fixed order; several K ranges leave fp32 partials for gen_reduce_kernel.
+constexpr int kGenQmvtWaves = 8;
+constexpr int kGenQmvtRows = 4;
+
+template <int BITS, int XT, int MR>
+__global__ __launch_bounds__(512) void qmv_gen_t_kernel(const GenArgs a, int tc, int kper) {
+  __shared__ float red[kGenQmvtWaves][32][64];
+  constexpr int U = kGenQmvtRows;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int seg = blockIdx.z, kz = blockIdx.y;
+  const int N = a.N, K = a.K, M = a.M;
+  const int npc = N >> 5;
+  const int pc = blockIdx.x * 64 + lane;
+  const int pcl = min(pc, npc - 1);
+  const int xb = a.lhs ? (int)min(a.lhs[seg], (uint32_t)(a.X - 1)) : (a.X > 1 ? seg : 0);
+  const int eb = a.rhs ? (int)min(a.rhs[seg], (uint32_t)(a.E - 1)) : (a.E > 1 ? seg : 0);
+  const uint32_t* W = a.w + (int64_t)eb * a.w_expert_stride;
+  const int64_t sofs = (int64_t)eb * a.s_expert_stride;
+  const int64_t rw = (int64_t)npc * BITS;  // words per code row
+  const int Gn = N >> a.gs_shift;
+  const int g = (pcl * 32) >> a.gs_shift;
+  const int k0 = kz * kper, k1 = min(K, k0 + kper);
+
+  float acc[MR][32], bsum[MR];
+#pragma unroll
+  for (int m = 0; m < MR; m++) {
+    bsum[m] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) acc[m][j] = 0.f;
+  }
+  for (int kb = k0 + wave * U; kb < k1; kb += kGenQmvtWaves * U) {  // wave-uniform
+    uint32_t w[U][BITS];
+    float sv[U], bv[U], xk[U][MR];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int k = min(kb + u, k1 - 1);
+      const uint32_t* wp = W + (int64_t)k * rw + (int64_t)pcl * BITS;
+#pragma unroll
+      for (int t = 0; t < BITS; t++) w[u][t] = wp[t];
+      sv[u] = load_as_f32_flat(a.scales, sofs + (int64_t)k * Gn + g, a.s_dtype);
+      bv[u] = load_as_f32_flat(a.biases, sofs + (int64_t)k * Gn + g, a.b_dtype);
+#pragma unroll
+      for (int m = 0; m < MR; m++) {
+        const float xv = load_as_f32(a.x, ((int64_t)xb * M + min(m, M - 1)) * K + k, XT);
+        xk[u][m] = kb + u < k1 ? xv : 0.f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      float xs[MR];
+#pragma unroll
+      for (int m = 0; m < MR; m++) {
+        xs[m] = xk[u][m] * sv[u];
+        bsum[m] = __builtin_fmaf(xk[u][m], bv[u], bsum[m]);
+      }
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
+        const float q = (float)piece_code<BITS>(w[u], j);
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[m][j] = __builtin_fmaf(xs[m], q, acc[m][j]);
+      }
+    }
+  }
+
+  const int64_t n_out = (int64_t)seg * M * N;
+#pragma unroll
+  for (int m = 0; m < MR; m++) {
+    if (m > 0) __syncthreads();  // the previous row's sums have been read
+#pragma unroll
+    for (int j = 0; j < 32; j++) red[wave][j][lane ^ j] = acc[m][j] + bsum[m];  // lane ^ j: no bank conflicts below
+    __syncthreads();
+    // 512 threads x 4 of the workgroup's 2048 (piece, column) sums
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int e = threadIdx.x + 512 * i;
+      const int l = e >> 5, j = e & 31;  // consecutive threads: one piece's columns
+      float t = 0.f;
+#pragma unroll
+      for (int v = 0; v < kGenQmvtWaves; v++) t += red[v][j][l ^ j];
+      const int p = blockIdx.x * 64 + l;
+      if (p < npc && m < M) {
+        const int64_t o = n_out + (int64_t)m * N + p * 32 + j;
+        if (a.ws) a.ws[(int64_t)kz * a.out_elems + o] = t;
+        else if (tc == GEN_F32) static_cast<float*>(a.out)[o] = t;
+        else if (tc == GEN_BF16) static_cast<uint16_t*>(a.out)[o] = (uint16_t)f32_to_bf16_bits(t);
+        else static_cast<uint16_t*>(a.out)[o] = __builtin_bit_cast(uint16_t, (_Float16)t);
+      }
+    }
+  }
+}
+
 // ---- host ------------------------------------------------------------------
 
 GenPlan gen_plan(int64_t M, int64_t N, int64_t K, int64_t nseg, int cus, int ks_req) {
@@ -520,6 +618,46 @@ hipError_t qmv_gen_launch(const GenArgs& a, int tc, int64_t nseg, hipStream_t st
   QG_BITS(GEN_F32, 2)
 #undef QG_BITS
 #undef QG_CASE
+  return hipErrorInvalidValue;
+}
+
+GenTPlan qmv_gen_t_plan(int64_t M, int64_t N, int64_t K, int64_t nseg, int bits, int mode, int cus) {
+  GenTPlan p;
+  if (mode != GEN_AFFINE || M < 1 || M > 2 || N % 32 != 0 || N <= 0 || K <= 0 || nseg > 65535 ||
+      !((bits >= 1 && bits <= 6) || bits == 8))
+    return p;
+  p.blocks = (int)((N / 32 + 63) / 64);
+  // about two workgroups per CU, each K range a whole number of the 8
+  // waves' 4-row steps
+  const int64_t step = kGenQmvtWaves * kGenQmvtRows;
+  int64_t ks = std::max<int64_t>(1, (2LL * cus + p.blocks * nseg - 1) / (p.blocks * nseg));
+  int64_t kper = (K + ks - 1) / ks;
+  kper = std::max<int64_t>(step, (kper + step - 1) / step * step);
+  p.kper = (int)kper;
+  p.ks = (int)((K + kper - 1) / kper);
+  p.ok = p.ks <= 65535;
+  return p;
+}
+
+hipError_t qmv_gen_t_launch(const GenArgs& a, const GenTPlan& p, int tc, int64_t nseg, hipStream_t stream) {
+  if (!p.ok || (p.ks > 1) != (a.ws != nullptr)) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)p.blocks, (unsigned)p.ks, (unsigned)nseg), block(64 * kGenQmvtWaves);
+#define QT_CASE(B_, X_, MR_)                                                                       \
+  if (a.bits == B_ && a.x_dtype == X_ && (a.M <= 1) == (MR_ == 1)) {                               \
+    hipLaunchKernelGGL((qmv_gen_t_kernel<B_, X_, MR_>), grid, block, 0, stream, a, tc, p.kper);    \
+    return hipGetLastError();                                                                      \
+  }
+#define QT_BITS(X_, MR_) \
+  QT_CASE(1, X_, MR_) QT_CASE(2, X_, MR_) QT_CASE(3, X_, MR_) QT_CASE(4, X_, MR_) \
+  QT_CASE(5, X_, MR_) QT_CASE(6, X_, MR_) QT_CASE(8, X_, MR_)
+  QT_BITS(GEN_BF16, 1)
+  QT_BITS(GEN_BF16, 2)
+  QT_BITS(GEN_F16, 1)
+  QT_BITS(GEN_F16, 2)
+  QT_BITS(GEN_F32, 1)
+  QT_BITS(GEN_F32, 2)
+#undef QT_BITS
+#undef QT_CASE
   return hipErrorInvalidValue;
 }
 

@@ -1,8 +1,10 @@
-"""GPU parity of the general path's decode kernel (`qmv_gen_kernel`,
-qmm_gen.hip): 1-2 activation rows per weight matrix, transpose=true, affine
-codes of 1-6 and 8 bits read as MLX's little-endian bit stream
-(overlays/cpu/mlx/backend/cpu/quantized.cpp:107-137), any element type of
-x / scales / biases, 2-D weights, batched weights and gather segments.
+"""GPU parity of the general path's decode kernels (qmm_gen.hip):
+`qmv_gen_kernel` (transpose=true) and `qmv_gen_t_kernel` (transpose=false,
+codes packed along N, K split over workgroups): 1-2 activation rows per
+weight matrix, affine codes of 1-6 and 8 bits read as MLX's little-endian
+bit stream (overlays/cpu/mlx/backend/cpu/quantized.cpp:107-137), any element
+type of x / scales / biases, 2-D weights, batched weights and gather
+segments.
 
 Checked against the float64 numpy restatement of MLX's CPU `_qmm_t`
 (oracle/generic.py) at max|y - y_ref| / max|y_ref| <= 1e-2 for 16-bit results
@@ -115,3 +117,54 @@ def test_gather_segments(M):
                       torch.from_numpy(rhs.astype(np.int32)).cuda(), True, gs, bits)
     want = og.gather_qmm(xv, wqn, sv, bv, lhs, rhs, True, gs, bits, "affine")
     assert _rel(y, want, "bfloat16") <= 1e-2
+
+
+# transpose=false: W is [K][N] with codes packed along N (qmv_gen_t_kernel);
+# K needs no alignment, N is a multiple of the group size.
+def _weights_t(rng, lead, K, N, bits, gs, st):
+    codes = rng.integers(0, 1 << bits, size=lead + (K, N))
+    wqn = og.pack_codes(codes, bits)
+    s, sv = _dev(rng.uniform(0.002, 0.02, size=lead + (K, N // gs)), st)
+    b, bv = _dev(rng.uniform(-0.1, 0.1, size=lead + (K, N // gs)), st)
+    return (dev_u32(wqn), s, b), (wqn, sv, bv)
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 6, 8])
+@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("xt", ["bfloat16", "float32"])
+def test_no_transpose_widths(bits, M, xt):
+    rng = np.random.default_rng(36000 + 10 * bits + M)
+    K, N, gs = 333, 2112, 64  # a partial 2048-column block, K over several ranges
+    announce("gen_qmv_t", bits, M, xt, K, N)
+    x, xv = _dev(rng.standard_normal((M, K)), xt)
+    (wq, s, b), (wqn, sv, bv) = _weights_t(rng, (), K, N, bits, gs, xt)
+    y = mq.quantized_matmul(x, wq, s, b, False, gs, bits)
+    assert _rel(y, og.qmm(xv, wqn, sv, bv, False, gs, bits), xt) <= _tol(xt)
+
+
+@pytest.mark.parametrize("K,N,gs", [(1, 32, 32), (7, 64, 64), (100, 128, 128), (4096, 4096, 64), (4096, 14336, 64)])
+def test_no_transpose_shapes_against_the_tile_kernel(monkeypatch, K, N, gs):
+    rng = np.random.default_rng(37000 + K + N)
+    bits = 4
+    announce("gen_qmv_t_vs_tile", K, N, gs)
+    x, xv = _dev(rng.standard_normal((1, K)), "bfloat16")
+    (wq, s, b), (wqn, sv, bv) = _weights_t(rng, (), K, N, bits, gs, "bfloat16")
+    y = mq.quantized_matmul(x, wq, s, b, False, gs, bits)
+    want = og.qmm(xv, wqn, sv, bv, False, gs, bits)
+    assert _rel(y, want, "bfloat16") <= 1e-2
+    setknob(monkeypatch, "MLXQ_GEN_QMV", "0")
+    y_tile = mq.quantized_matmul(x, wq, s, b, False, gs, bits)
+    assert _rel(y_tile, want, "bfloat16") <= 1e-2
+
+
+def test_no_transpose_gather():
+    rng = np.random.default_rng(38000)
+    E, X, B, K, N, bits, gs = 5, 3, 9, 200, 256, 6, 32
+    announce("gen_qmv_t_gather", E, X, B, K, N, bits)
+    x, xv = _dev(rng.standard_normal((X, 1, K)), "float16")
+    (wq, s, b), (wqn, sv, bv) = _weights_t(rng, (E,), K, N, bits, gs, "float16")
+    lhs, rhs = rng.integers(0, X, B), rng.integers(0, E, B)
+    y = mq.gather_qmm(x, wq, s, b, torch.from_numpy(lhs.astype(np.int32)).cuda(),
+                      torch.from_numpy(rhs.astype(np.int32)).cuda(), False, gs, bits)
+    want = og.gather_qmm(xv, wqn, sv, bv, lhs, rhs, False, gs, bits, "affine")
+    assert _rel(y, want, "float16") <= 1e-2
