@@ -297,12 +297,22 @@ __global__ __launch_bounds__(256) void qmm_gen_kernel(const GenArgs a) {
   }
 }
 
-// out[i] = sum over z < ks of ws[z][i] (in order), rounded to the output type
-__global__ __launch_bounds__(256) void gen_reduce_kernel(const float* ws, void* out, int64_t n, int ks, int tc) {
+// out[i] = sum over z < ks of ws[z][i] (in order), rounded to the output type;
+// the partials are loaded 8 at a time so their latencies overlap, and
+// 64-thread workgroups spread small outputs over the CUs
+__global__ __launch_bounds__(64) void gen_reduce_kernel(const float* ws, void* out, int64_t n, int ks, int tc) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   float s = 0.f;
-  for (int z = 0; z < ks; z++) s += ws[(int64_t)z * n + i];
+  int z = 0;
+  for (; z + 8 <= ks; z += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) v[u] = ws[(int64_t)(z + u) * n + i];
+#pragma unroll
+    for (int u = 0; u < 8; u++) s += v[u];
+  }
+  for (; z < ks; z++) s += ws[(int64_t)z * n + i];
   if (tc == GEN_F32) static_cast<float*>(out)[i] = s;
   else if (tc == GEN_BF16) static_cast<uint16_t*>(out)[i] = (uint16_t)f32_to_bf16_bits(s);
   else static_cast<uint16_t*>(out)[i] = __builtin_bit_cast(uint16_t, (_Float16)s);
@@ -663,8 +673,9 @@ hipError_t qmv_gen_t_launch(const GenArgs& a, const GenTPlan& p, int tc, int64_t
 
 hipError_t launch_gen_reduce(const float* ws, void* out, int64_t n, int ks, int tc, hipStream_t stream) {
   if (n <= 0) return hipSuccess;
-  const int64_t blocks = (n + 255) / 256;
-  hipLaunchKernelGGL(gen_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, ws, out, n, ks, tc);
+  const int64_t blocks = (n + 63) / 64;
+  if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(gen_reduce_kernel, dim3((unsigned)blocks), dim3(64), 0, stream, ws, out, n, ks, tc);
   return hipGetLastError();
 }
 
