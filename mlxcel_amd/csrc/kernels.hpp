@@ -154,7 +154,7 @@ GenPlan gen_plan(int64_t M, int64_t N, int64_t K, int64_t nseg, int cus, int ks_
 hipError_t qmm_gen_launch(const GenArgs& a, const GenPlan& p, int tc, bool transpose, int64_t nseg,
                           hipStream_t stream);
 hipError_t launch_gen_reduce(const float* ws, void* out, int64_t n, int ks, int tc, hipStream_t stream);
-// Decode form of the general path (qmm_gen.hip): 1-2 rows per segment,
+// Decode form of the general path (qmm_gen.hip): 1-4 rows per segment,
 // transpose=true, affine codes of 1-6 or 8 bits, K a multiple of 32; one
 // wave per 4 weight rows, no workspace.  x may be any GenType (scales and
 // biases too); tc is the result type.

@@ -603,7 +603,7 @@ hipError_t qmm_gen_launch(const GenArgs& a0, const GenPlan& p, int tc, bool tran
 }
 
 bool qmv_gen_fits(int mode, bool transpose, int64_t M, int64_t N, int64_t K, int64_t nseg, int bits) {
-  return mode == GEN_AFFINE && transpose && M >= 1 && M <= 2 && K % 32 == 0 && K > 0 && nseg <= 65535 &&
+  return mode == GEN_AFFINE && transpose && M >= 1 && M <= 4 && K % 32 == 0 && K > 0 && nseg <= 65535 &&
          (N + kGenQmvRows * kGenQmvWaves - 1) / (kGenQmvRows * kGenQmvWaves) <= 0x7FFFFFFF &&
          ((bits >= 1 && bits <= 6) || bits == 8);
 }
@@ -612,8 +612,9 @@ hipError_t qmv_gen_launch(const GenArgs& a, int tc, int64_t nseg, hipStream_t st
   if (!qmv_gen_fits(a.mode, true, a.M, a.N, a.K, nseg, a.bits)) return hipErrorInvalidValue;
   const int64_t per_wg = kGenQmvRows * kGenQmvWaves;
   const dim3 grid((unsigned)((a.N + per_wg - 1) / per_wg), (unsigned)nseg), block(64 * kGenQmvWaves);
+  const int mr = a.M <= 1 ? 1 : a.M <= 2 ? 2 : 4;  // 3 rows run as 4 (the 4th is zeros, not stored)
 #define QG_CASE(B_, X_, MR_)                                                                  \
-  if (a.bits == B_ && a.x_dtype == X_ && (a.M <= 1) == (MR_ == 1)) {                          \
+  if (a.bits == B_ && a.x_dtype == X_ && mr == MR_) {                                         \
     hipLaunchKernelGGL((qmv_gen_kernel<B_, X_, MR_>), grid, block, 0, stream, a, tc);         \
     return hipGetLastError();                                                                 \
   }
@@ -622,10 +623,13 @@ hipError_t qmv_gen_launch(const GenArgs& a, int tc, int64_t nseg, hipStream_t st
   QG_CASE(5, X_, MR_) QG_CASE(6, X_, MR_) QG_CASE(8, X_, MR_)
   QG_BITS(GEN_BF16, 1)
   QG_BITS(GEN_BF16, 2)
+  QG_BITS(GEN_BF16, 4)
   QG_BITS(GEN_F16, 1)
   QG_BITS(GEN_F16, 2)
+  QG_BITS(GEN_F16, 4)
   QG_BITS(GEN_F32, 1)
   QG_BITS(GEN_F32, 2)
+  QG_BITS(GEN_F32, 4)
 #undef QG_BITS
 #undef QG_CASE
   return hipErrorInvalidValue;

@@ -1,7 +1,7 @@
 """GPU parity of the general path's decode kernels (qmm_gen.hip):
-`qmv_gen_kernel` (transpose=true) and `qmv_gen_t_kernel` (transpose=false,
-codes packed along N, K split over workgroups): 1-2 activation rows per
-weight matrix, affine codes of 1-6 and 8 bits read as MLX's little-endian
+`qmv_gen_kernel` (transpose=true, 1-4 activation rows per weight matrix)
+and `qmv_gen_t_kernel` (transpose=false, 1-2 rows, codes packed along N, K
+split over workgroups): affine codes of 1-6 and 8 bits read as MLX's little-endian
 bit stream (overlays/cpu/mlx/backend/cpu/quantized.cpp:107-137), any element
 type of x / scales / biases, 2-D weights, batched weights and gather
 segments.
@@ -51,7 +51,7 @@ def _weights(rng, lead, N, K, bits, gs, st):
 
 
 @pytest.mark.parametrize("bits", [1, 2, 3, 5, 6])
-@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
 @pytest.mark.parametrize("gs", [32, 64, 128])
 def test_code_widths_bfloat16(bits, M, gs):
     rng = np.random.default_rng(31000 + 10 * bits + M + gs)
@@ -69,8 +69,9 @@ def test_code_widths_bfloat16(bits, M, gs):
 def test_element_types(bits, xt, st, out):
     rng = np.random.default_rng(32000 + bits)
     N, K, gs = 300, 2048, 64
-    announce("gen_qmv_types", bits, xt, st, N, K)
-    x, xv = _dev(rng.standard_normal((1, K)), xt)
+    M = 4 if bits % 2 else 1
+    announce("gen_qmv_types", bits, xt, st, M, N, K)
+    x, xv = _dev(rng.standard_normal((M, K)), xt)
     (wq, s, b), (wqn, sv, bv) = _weights(rng, (), N, K, bits, gs, st)
     y = mq.quantized_matmul(x, wq, s, b, True, gs, bits)
     assert _rel(y, og.qmm(xv, wqn, sv, bv, True, gs, bits), out) <= _tol(out)
@@ -82,7 +83,7 @@ def test_shapes_against_the_tile_kernel(monkeypatch, N, K, bits):
     rng = np.random.default_rng(33000 + N + K + bits)
     gs = 32
     announce("gen_qmv_vs_tile", bits, N, K)
-    x, xv = _dev(rng.standard_normal((2, K)), "float16")
+    x, xv = _dev(rng.standard_normal((2 if bits == 3 else 3, K)), "float16")
     (wq, s, b), (wqn, sv, bv) = _weights(rng, (), N, K, bits, gs, "float16")
     y = mq.quantized_matmul(x, wq, s, b, True, gs, bits)
     want = og.qmm(xv, wqn, sv, bv, True, gs, bits)
@@ -96,7 +97,7 @@ def test_shapes_against_the_tile_kernel(monkeypatch, N, K, bits):
 
 def test_batched_weights():
     rng = np.random.default_rng(34000)
-    E, M, N, K, bits, gs = 3, 2, 130, 512, 5, 64
+    E, M, N, K, bits, gs = 3, 4, 130, 512, 5, 64
     announce("gen_qmv_batched", E, M, N, K, bits)
     x, xv = _dev(rng.standard_normal((E, M, K)), "bfloat16")
     (wq, s, b), (wqn, sv, bv) = _weights(rng, (E,), N, K, bits, gs, "bfloat16")
@@ -105,7 +106,7 @@ def test_batched_weights():
     assert _rel(y, want, "bfloat16") <= 1e-2
 
 
-@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("M", [1, 2, 3])
 def test_gather_segments(M):
     rng = np.random.default_rng(35000 + M)
     E, X, B, N, K, bits, gs = 6, 4, 11, 96, 384, 3, 64
