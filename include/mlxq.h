@@ -148,8 +148,11 @@ const char* mlxq_version(void);
  * (x, scales, biases and result) 4/8-bit affine with transpose=true (decode
  * and prefill; its prefill dequantizes the weights to float16, as the
  * reference's dequantize + GEMM route does); every other combination runs
- * the general kernel (float16 results there also round the dequantized
- * weights to float16).  Operands of 2 GiB and more: with 2-D weights, x and
+ * the general path: affine calls of 1-4 rows per matrix with transpose=true
+ * (1-2 with transpose=false) on its row-streaming decode kernels (fp32
+ * products, no weight rounding), the rest on its tile kernel (float16
+ * results there also round the dequantized weights to float16).  Operands
+ * of 2 GiB and more: with 2-D weights, x and
  * the result run as row chunks below 2 GiB on the same kernels; a weight
  * matrix (or its scales) of 2 GiB or more runs on the general kernel.
  * Batched weights take any rows per batch. */
